@@ -1,0 +1,259 @@
+// Split-K flash-decoding for one new token per sequence over a device KV cache.
+//
+// Replaces the per-head `for t in visible` loop of attention_token
+// (reference src/engine/runtime/inference.rs:1970-2530) for every sequence of a
+// batch at once.  Work unit = (sequence, KV head, split of `split_keys` keys):
+// one workgroup reads each K/V row of its split exactly once and serves all
+// kv_mul = Hq/Hkv query heads of that KV head (GQA, kv_head = h / kv_mul,
+// inference.rs:2019).  Each workgroup leaves an online-softmax partial
+// (running max m, sum l, unnormalised o[d]) in the workspace; a combine kernel
+// merges the partials of a (sequence, head).
+//
+// Scores are kept in the log2 domain: s2 = (q.k) * score_scale * log2(e), so
+// exp(s - m) == exp2(s2 - m2) with one v_exp_f32.
+#include "gr_common.hpp"
+#include "gr_internal.hpp"
+
+namespace gr {
+
+constexpr int kDecodeThreads = 256;
+constexpr int kDecodeWaves = kDecodeThreads / 64;
+constexpr int kDecodeUnroll = 4;  // rows per row-group per iteration (memory-level parallelism)
+
+// One lane owns 16 bytes (EPL elements) of a key row; LPR lanes cover a row of
+// D elements; a wave instruction covers RPW = 64 / LPR consecutive rows.
+template <typename KV, int D>
+struct DecodeGeom {
+    static constexpr int EPL = 16 / KV::bytes;
+    static constexpr int LPR = D / EPL;
+    static constexpr int RPW = 64 / LPR;
+    static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row must map onto a wave");
+};
+
+template <typename KV, int D, int KVMUL>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const DecodeLaunch p) {
+    using G = DecodeGeom<KV, D>;
+    constexpr int EPL = G::EPL, LPR = G::LPR, RPW = G::RPW;
+    constexpr int STEP = kDecodeWaves * kDecodeUnroll * RPW;  // rows per block iteration
+
+    const int split = blockIdx.x;
+    const int g = blockIdx.y;
+    const int s = blockIdx.z;
+    const int t_begin = p.kv_start[s] + split * p.split_keys;
+    const int t_limit = p.kv_end[s];
+    if (t_begin >= t_limit) return;
+    const int t_stop = min(t_limit, t_begin + p.split_keys);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int rg = lane / LPR;   // row group within the wave
+    const int sl = lane % LPR;   // slice of the row owned by this lane
+    const int e0 = sl * EPL;
+
+    // q slices for the kv_mul heads of this KV head, pre-scaled into log2 units.
+    const float qscale = p.score_scale * kLog2e;
+    float qv[KVMUL][EPL];
+#pragma unroll
+    for (int j = 0; j < KVMUL; j++) {
+        const float* qh = p.q + ((size_t)s * p.n_heads + (size_t)g * KVMUL + j) * D + e0;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) qv[j][e] = qh[e] * qscale;
+    }
+
+    float m[KVMUL], l[KVMUL], o[KVMUL][EPL];
+#pragma unroll
+    for (int j = 0; j < KVMUL; j++) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[j][e] = 0.0f;
+    }
+
+    const char* kbase = (const char*)p.k_cache +
+                        ((size_t)s * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
+    const char* vbase = (const char*)p.v_cache +
+                        ((size_t)s * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
+    const size_t row_bytes = (size_t)p.row_stride * KV::bytes;
+
+    for (int tb = t_begin; tb < t_stop; tb += STEP) {
+        uint4 kraw[kDecodeUnroll], vraw[kDecodeUnroll];
+        bool valid[kDecodeUnroll];
+#pragma unroll
+        for (int u = 0; u < kDecodeUnroll; u++) {
+            const int t = tb + (wave * kDecodeUnroll + u) * RPW + rg;
+            valid[u] = t < t_stop;
+            const int tt = valid[u] ? t : t_begin;  // clamp: never read past the split
+            kraw[u] = *(const uint4*)(kbase + (size_t)tt * row_bytes);
+            vraw[u] = *(const uint4*)(vbase + (size_t)tt * row_bytes);
+        }
+        float sc[kDecodeUnroll][KVMUL];
+#pragma unroll
+        for (int u = 0; u < kDecodeUnroll; u++) {
+            float kf[EPL];
+            unpack16<KV>(kraw[u], kf);
+#pragma unroll
+            for (int j = 0; j < KVMUL; j++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc = fmaf(qv[j][e], kf[e], acc);
+                sc[u][j] = acc;
+            }
+        }
+        // Reduce partial dots across the LPR lanes of a row (butterfly: every
+        // lane of the row group ends with the full score).
+#pragma unroll
+        for (int u = 0; u < kDecodeUnroll; u++)
+#pragma unroll
+            for (int j = 0; j < KVMUL; j++) {
+                float v = wave_sum<LPR>(sc[u][j]);
+                sc[u][j] = valid[u] ? v : -INFINITY;
+            }
+#pragma unroll
+        for (int j = 0; j < KVMUL; j++) {
+            float mx = m[j];
+#pragma unroll
+            for (int u = 0; u < kDecodeUnroll; u++) mx = fmaxf(mx, sc[u][j]);
+            // mx is finite whenever any row of this group was valid.
+            const float alpha = (mx == -INFINITY) ? 1.0f : exp2f(m[j] - mx);
+            float lsum = l[j] * alpha;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[j][e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < kDecodeUnroll; u++) {
+                const float pu = (sc[u][j] == -INFINITY) ? 0.0f : exp2f(sc[u][j] - mx);
+                lsum += pu;
+                sc[u][j] = pu;
+            }
+            l[j] = lsum;
+            m[j] = mx;
+        }
+#pragma unroll
+        for (int u = 0; u < kDecodeUnroll; u++) {
+            float vf[EPL];
+            unpack16<KV>(vraw[u], vf);
+#pragma unroll
+            for (int j = 0; j < KVMUL; j++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++) o[j][e] = fmaf(sc[u][j], vf[e], o[j][e]);
+        }
+    }
+
+    // Merge the RPW row groups of the wave (lanes with equal `sl`).
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+        for (int j = 0; j < KVMUL; j++) {
+            const float m_o = shfl_xor(m[j], off);
+            const float l_o = shfl_xor(l[j], off);
+            const float mx = fmaxf(m[j], m_o);
+            const float a = (m[j] == -INFINITY) ? 0.0f : exp2f(m[j] - mx);
+            const float b = (m_o == -INFINITY) ? 0.0f : exp2f(m_o - mx);
+            l[j] = l[j] * a + l_o * b;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const float oo = shfl_xor(o[j][e], off);
+                o[j][e] = o[j][e] * a + oo * b;
+            }
+            m[j] = mx;
+        }
+    }
+
+    // Merge the waves through LDS; wave 0 writes the partial.
+    __shared__ float sh_m[kDecodeWaves][KVMUL];
+    __shared__ float sh_l[kDecodeWaves][KVMUL];
+    __shared__ float sh_o[kDecodeWaves][KVMUL][D];
+    if (rg == 0) {
+#pragma unroll
+        for (int j = 0; j < KVMUL; j++) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) sh_o[wave][j][e0 + e] = o[j][e];
+            if (sl == 0) {
+                sh_m[wave][j] = m[j];
+                sh_l[wave][j] = l[j];
+            }
+        }
+    }
+    __syncthreads();
+    // Thread layout for the final merge: KVMUL*D outputs spread over the block.
+    const int n_splits = p.n_splits;
+    for (int idx = threadIdx.x; idx < KVMUL * D; idx += kDecodeThreads) {
+        const int j = idx / D;
+        const int i = idx % D;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; w++) mx = fmaxf(mx, sh_m[w][j]);
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; w++) {
+            const float a = (sh_m[w][j] == -INFINITY) ? 0.0f : exp2f(sh_m[w][j] - mx);
+            lt += sh_l[w][j] * a;
+            ot += sh_o[w][j][i] * a;
+        }
+        const int h = g * KVMUL + j;
+        const size_t part = ((size_t)s * p.n_heads + h) * n_splits + split;
+        p.ws_o[part * D + i] = ot;
+        if (i == 0) {
+            p.ws_ml[part * 2 + 0] = mx;
+            p.ws_ml[part * 2 + 1] = lt;
+        }
+    }
+}
+
+// Merge the split partials of one (sequence, head): out = sum_s o_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
+template <int D>
+__global__ __launch_bounds__(D) void decode_combine_kernel(const DecodeLaunch p) {
+    const int h = blockIdx.x;
+    const int s = blockIdx.y;
+    const int i = threadIdx.x;
+    const int len = p.kv_end[s] - p.kv_start[s];
+    const int nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
+    const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
+    float mx = -INFINITY;
+    for (int k = 0; k < nv; k++) mx = fmaxf(mx, p.ws_ml[(base + k) * 2]);
+    float lt = 0.0f, ot = 0.0f;
+    for (int k = 0; k < nv; k++) {
+        const float mk = p.ws_ml[(base + k) * 2];
+        const float a = (mk == -INFINITY) ? 0.0f : exp2f(mk - mx);
+        lt += p.ws_ml[(base + k) * 2 + 1] * a;
+        ot += p.ws_o[(base + k) * D + i] * a;
+    }
+    p.out[((size_t)s * p.n_heads + h) * D + i] = lt > 0.0f ? ot * (1.0f / lt) : 0.0f;
+}
+
+template <typename KV, int D>
+static hipError_t launch_kvmul(const DecodeLaunch& p, int kv_mul, hipStream_t st) {
+    dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
+    switch (kv_mul) {
+        case 1: decode_split_kernel<KV, D, 1><<<grid, kDecodeThreads, 0, st>>>(p); break;
+        case 2: decode_split_kernel<KV, D, 2><<<grid, kDecodeThreads, 0, st>>>(p); break;
+        case 4: decode_split_kernel<KV, D, 4><<<grid, kDecodeThreads, 0, st>>>(p); break;
+        case 8: decode_split_kernel<KV, D, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+        default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    decode_combine_kernel<D><<<dim3(p.n_heads, p.n_seq), D, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+template <typename KV>
+static hipError_t launch_dim(const DecodeLaunch& p, int kv_mul, hipStream_t st) {
+    switch (p.head_dim) {
+        case 64: return launch_kvmul<KV, 64>(p, kv_mul, st);
+        case 128: return launch_kvmul<KV, 128>(p, kv_mul, st);
+        case 256: return launch_kvmul<KV, 256>(p, kv_mul, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st) {
+    const int kv_mul = p.n_heads / p.n_kv_heads;
+    switch (p.kv_dtype) {
+        case GR_DTYPE_F32: return launch_dim<F32>(p, kv_mul, st);
+        case GR_DTYPE_F16: return launch_dim<F16>(p, kv_mul, st);
+        case GR_DTYPE_BF16: return launch_dim<BF16>(p, kv_mul, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace gr

@@ -1,0 +1,21 @@
+// Host-side helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "gr_attn.h"
+
+namespace gr {
+
+// Record `fmt` as this thread's last error and return `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+void clear_error();
+size_t align_up(size_t x, size_t a);
+
+int check_decode_shape_only(const gr_decode_args* a);
+int decode_enqueue(const gr_decode_args* a, hipStream_t st);
+size_t decode_ws_bytes(const gr_decode_args* a);
+
+}  // namespace gr

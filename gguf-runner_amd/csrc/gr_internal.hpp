@@ -1,0 +1,96 @@
+// Launch descriptors shared between the C-ABI layer (api.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gr {
+
+// Split-K decode.  Partials: ws_o [n_seq][n_heads][n_splits][head_dim],
+// ws_ml [n_seq][n_heads][n_splits][2] = (m, l) in log2 units.
+struct DecodeLaunch {
+    int n_seq, n_heads, n_kv_heads, head_dim, kv_dtype;
+    int split_keys, n_splits;
+    float score_scale;
+    const float* q;
+    const void* k_cache;
+    const void* v_cache;
+    int64_t seq_stride, row_stride;
+    const int32_t* kv_start;
+    const int32_t* kv_end;
+    float* out;
+    float* ws_o;
+    float* ws_ml;
+};
+
+hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);
+
+// Per-token Q/K/V preparation: optional QK RMSNorm (math.rs:164-184), RoPE
+// (inference.rs:1817-1874), Gemma q scale, then
+//   K, V rows -> cache (dtype `cache_dtype`) at rows pos0 + i,
+//   Q rows -> q_out (f32, or 16-bit `q_out_dtype`) multiplied by q_out_scale.
+struct QkvPrepLaunch {
+    int n_tokens, n_heads, n_kv_heads, head_dim;
+    int in_dtype;          // dtype of q/k/v inputs
+    const int32_t* pos;    // [n_tokens] positions (device), or nullptr -> pos0 + i
+    int64_t pos0;
+    int rope_mode, rope_dim;
+    float rope_scale;
+    const float* rope_freqs;
+    const float* q_norm;
+    const float* k_norm;
+    float eps;
+    int gemma_q_scale;
+    const void* q;
+    const void* k;
+    const void* v;
+    int64_t q_row_stride, kv_row_stride;  // input row strides (elements)
+    void* q_out;
+    int q_out_dtype;
+    float q_out_scale;
+    void* k_cache;
+    void* v_cache;
+    int cache_dtype;
+    const int32_t* cache_row;   // [n_tokens] destination row per token (device), or nullptr -> pos
+    int64_t cache_seq_stride;   // elements, used with cache_seq
+    const int32_t* cache_seq;   // [n_tokens] sequence slot per token, or nullptr -> 0
+    int64_t cache_row_stride;
+};
+
+hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);
+
+// Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
+// [m][n_heads][d] already multiplied by score_scale*log2(e).
+struct PrefillLaunch {
+    int n_tokens, n_heads, n_kv_heads, head_dim, dtype;
+    int64_t base_pos;
+    int window;
+    const void* q;
+    const void* k_cache;
+    const void* v_cache;
+    int64_t cache_row_stride;
+    float* out;
+};
+
+hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st);
+
+// Gated DeltaNet.
+struct DeltaNetLaunch {
+    int n_tokens, n_heads, head_dim, in_dtype, l2norm;
+    float eps;
+    const void* q;
+    const void* k;
+    const void* v;
+    const float* gate;
+    const float* beta;
+    float* state;
+    float* out;
+    float* ws;   // chunked algorithm workspace
+    int chunk;
+};
+
+hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st);
+hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st);
+size_t deltanet_chunked_ws_bytes(int n_tokens, int n_heads, int head_dim, int chunk);
+
+}  // namespace gr

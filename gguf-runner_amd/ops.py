@@ -1,0 +1,84 @@
+"""Device-pointer entry points of libgr_attn for torch tensors resident in HBM.
+
+torch is used only for device memory and the stream handle; every computation
+is a HIP kernel of libgr_attn.so reached through the C ABI (see ffi.py).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import ffi
+
+_DT = {torch.float32: ffi.DTYPE_F32, torch.float16: ffi.DTYPE_F16, torch.bfloat16: ffi.DTYPE_BF16}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("libgr_attn device entry points take device tensors")
+    return t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256) + 256, dtype=torch.uint8, device=device)
+
+
+def _aligned(ws: torch.Tensor) -> int:
+    p = ws.data_ptr()
+    return (p + 255) // 256 * 256
+
+
+class DecodeCall:
+    """A prepared gr_decode_attention call (args + workspace), reusable for timing.
+
+    q [n_seq][Hq][d] f32; k_cache/v_cache [n_seq][seq_len][Hkv][d] (f32/f16/bf16);
+    kv_start/kv_end int32 [n_seq]; out [n_seq][Hq][d] f32.
+    """
+
+    def __init__(self, q, k_cache, v_cache, kv_start, kv_end, out, *, max_kv_len,
+                 score_scale=None, split_keys=0):
+        n_seq, n_heads, d = q.shape
+        _, seq_len, n_kv, d2 = k_cache.shape
+        assert d2 == d and v_cache.shape == k_cache.shape and out.shape == q.shape
+        assert q.dtype == torch.float32 and out.dtype == torch.float32
+        assert kv_start.dtype == torch.int32 and kv_end.dtype == torch.int32
+        assert k_cache.is_contiguous() and v_cache.is_contiguous() and q.is_contiguous()
+        self._keep = (q, k_cache, v_cache, kv_start, kv_end, out)
+        a = ffi.DecodeArgs()
+        a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim = n_seq, n_heads, n_kv, d
+        a.kv_dtype = _DT[k_cache.dtype]
+        a.split_keys = split_keys
+        a.max_kv_len = int(max_kv_len)
+        a.score_scale = 1.0 / math.sqrt(d) if score_scale is None else float(score_scale)
+        a.q, a.k_cache, a.v_cache = _ptr(q), _ptr(k_cache), _ptr(v_cache)
+        a.seq_stride = seq_len * n_kv * d
+        a.row_stride = n_kv * d
+        a.kv_start, a.kv_end, a.out = _ptr(kv_start), _ptr(kv_end), _ptr(out)
+        L = ffi.lib()
+        nbytes = L.gr_decode_workspace_size(ctypes.byref(a))
+        self.ws = _workspace(nbytes, q.device)
+        a.workspace = _aligned(self.ws)
+        self.args = a
+
+    def __call__(self, stream=None) -> None:
+        ffi.check(ffi.lib().gr_decode_attention(ctypes.byref(self.args), _stream(stream)))
+
+
+def decode_attention(q, k_cache, v_cache, kv_start, kv_end, *, max_kv_len=None, score_scale=None,
+                     split_keys=0, out=None):
+    if out is None:
+        out = torch.empty_like(q)
+    if max_kv_len is None:
+        max_kv_len = int((kv_end - kv_start).max().item())
+    DecodeCall(q, k_cache, v_cache, kv_start, kv_end, out, max_kv_len=max_kv_len,
+               score_scale=score_scale, split_keys=split_keys)()
+    return out

@@ -1,0 +1,548 @@
+/*
+ * oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A CPU restatement of gguf-runner's attention hot path, used as the parity
+ * checker for the HIP kernels and as the CPU baseline leg of bench.py.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline may load it; the
+ * product library (libgr_attn.so) never links or calls anything here.
+ *
+ * Each function follows the x86_64 branch of the cited Rust function in
+ * /root/reference (gguf-runner v0.7.0).  The reference cannot be built here
+ * (no Rust toolchain), so this file is the oracle; tests/test_oracle_*.py pin
+ * it against the reference's own unit-test constants and against closed forms.
+ *
+ * Arithmetic fidelity notes:
+ *  - Built with -ffp-contract=off: the reference's scalar loops are compiled by
+ *    rustc/LLVM without FMA contraction, so a*b+c stays two roundings.
+ *  - axpy_inplace (quant.rs:1069-1080) dispatches to the AVX2-FMA kernel on
+ *    x86 (quant.rs:1023-1047, 1049-1067); it is restated with fmaf().
+ *  - libm expf/powf/cosf/sinf/sqrtf are the host glibc ones, like Rust's
+ *    f32::{exp,powf,cos,sin,sqrt} on linux-x86_64.
+ *  - Parallel-over-heads (rayon, inference.rs:2002-2007) is restated with
+ *    OpenMP; every head is computed by one thread in the same order as the
+ *    serial branch, so results do not depend on the thread count.
+ *
+ * Parity pinning status is recorded per function in the comment above it.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_BF16 2
+#define ORC_Q8 3
+
+/* ---------------------------------------------------------------- dtypes */
+
+/* IEEE binary16 -> f32 (exact).  Same semantics as fp16_to_fp32,
+ * src/engine/io/gguf.rs:27-61. */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do {
+                e++;
+                man <<= 1;
+            } while ((man & 0x400u) == 0);
+            man &= 0x3ff;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* bfloat16 -> f32 (exact), gguf.rs:63-70. */
+float orc_bf16_to_f32(uint16_t b) {
+    uint32_t bits = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static inline float load_kv(const void* base, size_t idx, int fmt) {
+    switch (fmt) {
+        case ORC_F16: return orc_f16_to_f32(((const uint16_t*)base)[idx]);
+        case ORC_BF16: return orc_bf16_to_f32(((const uint16_t*)base)[idx]);
+        case ORC_Q8: return (float)((const int8_t*)base)[idx];
+        default: return ((const float*)base)[idx];
+    }
+}
+
+/* ---------------------------------------------------------------- RoPE */
+
+/* Frequency table, inference.rs:1590-1609:
+ *   freq_i = 1 / theta^((2i) as f32 / rope_dim as f32)
+ * Pinned by: tests/test_oracle_rope.py (reference constants 4098-4118 with
+ * unit frequencies; closed form against float64). */
+void orc_rope_freqs(float theta, int rope_dim, float* freqs) {
+    int half = rope_dim / 2;
+    for (int i = 0; i < half; i++) {
+        freqs[i] = 1.0f / powf(theta, (float)(i * 2) / (float)rope_dim);
+    }
+}
+
+/* rebuild_rope_cache, inference.rs:1485-1523, text positions (the position
+ * plan is [pos;3] for text, 1498-1501):
+ *   val = (pos as f32 * freq) * frequency_scale;  cos = val.cos(); sin = val.sin()
+ * Pinned by: reference test inference.rs:4098-4118 (cos 8/sin 8/cos 1/sin 1). */
+void orc_rope_cache(const float* freqs, int half, int64_t pos, float scale, float* cos_out,
+                    float* sin_out) {
+    for (int i = 0; i < half; i++) {
+        float val = ((float)pos * freqs[i]) * scale;
+        cos_out[i] = cosf(val);
+        sin_out[i] = sinf(val);
+    }
+}
+
+/* apply_rope_qk, inference.rs:1817-1874.
+ * neox != 0: half-split pairs (i, i+rope_half) per head, 1829-1852
+ *            (Gemma3 / Qwen2 / Qwen3 / Qwen3VL / Qwen3MoE / Qwen3Next);
+ * neox == 0: adjacent pairs over the flat q vector, k rotated while i < kv_dim,
+ *            1853-1869 (Llama).
+ * gemma_q_scale != 0: q *= attn_scale afterwards, 1871-1873.
+ * Pinned by: reference tests 4098-4118 and 4133-4182 (pairing, partial tail),
+ * pair-norm invariant, pos 0 identity. */
+void orc_apply_rope_qk(float* q, float* k, int n_heads, int n_kv_heads, int head_size, int rope_half,
+                       const float* cos_t, const float* sin_t, int neox, int gemma_q_scale,
+                       float attn_scale) {
+    int q_dim = n_heads * head_size;
+    int kv_dim = n_kv_heads * head_size;
+    if (neox) {
+        int pair_offset = rope_half;
+        for (int h = 0; h < n_heads; h++) {
+            int hs = h * head_size;
+            for (int i = 0; i < rope_half; i++) {
+                float fcr = cos_t[i], fci = sin_t[i];
+                float v0 = q[hs + i], v1 = q[hs + i + pair_offset];
+                q[hs + i] = v0 * fcr - v1 * fci;
+                q[hs + i + pair_offset] = v0 * fci + v1 * fcr;
+            }
+        }
+        for (int h = 0; h < n_kv_heads; h++) {
+            int hs = h * head_size;
+            for (int i = 0; i < rope_half; i++) {
+                float fcr = cos_t[i], fci = sin_t[i];
+                float v0 = k[hs + i], v1 = k[hs + i + pair_offset];
+                k[hs + i] = v0 * fcr - v1 * fci;
+                k[hs + i + pair_offset] = v0 * fci + v1 * fcr;
+            }
+        }
+    } else {
+        for (int i = 0; i < q_dim; i += 2) {
+            int head_dim_idx = (i % head_size) / 2;
+            float fcr = cos_t[head_dim_idx], fci = sin_t[head_dim_idx];
+            int rotn = i < kv_dim ? 2 : 1;
+            for (int v = 0; v < rotn; v++) {
+                float* vec = v == 0 ? q : k;
+                float v0 = vec[i], v1 = vec[i + 1];
+                vec[i] = v0 * fcr - v1 * fci;
+                vec[i + 1] = v0 * fci + v1 * fcr;
+            }
+        }
+    }
+    if (gemma_q_scale) {
+        for (int i = 0; i < q_dim; i++) q[i] *= attn_scale;
+    }
+}
+
+/* rmsnorm_per_head_gemma_inplace, math.rs:164-184 (QK-norm, applied by
+ * qkv_bias_and_norm, inference.rs:2535-2572):
+ *   ss = sum(x^2)/d + eps;  x_j = w_j * ((1/sqrt(ss)) * x_j)
+ * Pinned by: closed form (unit RMS with w = 1) in tests/test_oracle_misc.py. */
+void orc_rmsnorm_per_head(float* x, const float* weight, int n_heads, int head_size, float eps) {
+    for (int h = 0; h < n_heads; h++) {
+        int hs = h * head_size;
+        float ss = 0.0f;
+        for (int j = 0; j < head_size; j++) ss += x[hs + j] * x[hs + j];
+        ss /= (float)head_size;
+        ss += eps;
+        float inv = 1.0f / sqrtf(ss);
+        for (int j = 0; j < head_size; j++) x[hs + j] = weight[j] * (inv * x[hs + j]);
+    }
+}
+
+/* ---------------------------------------------------------------- Q8 KV codec */
+
+/* quantize_row_q8, x86 branch, inference.rs:249-268.  Rust f32::round is
+ * half-away-from-zero == C roundf.  Pinned by closed form + tie cases. */
+void orc_quantize_row_q8(const float* src, int n, int8_t* dst, float* scale_out) {
+    float max_abs = 0.0f;
+    for (int i = 0; i < n; i++) max_abs = fmaxf(max_abs, fabsf(src[i]));
+    if (max_abs == 0.0f) {
+        *scale_out = 1.0f;
+        memset(dst, 0, (size_t)n);
+        return;
+    }
+    float inv = 127.0f / max_abs;
+    *scale_out = max_abs / 127.0f;
+    for (int i = 0; i < n; i++) {
+        float r = roundf(src[i] * inv);
+        if (r < -127.0f) r = -127.0f;
+        if (r > 127.0f) r = 127.0f;
+        dst[i] = (int8_t)r;
+    }
+}
+
+/* ---------------------------------------------------------------- softmax */
+
+/* softmax, x86 branch, math.rs:263-280. */
+void orc_softmax(float* x, int size) {
+    float max_val = x[0];
+    for (int i = 1; i < size; i++)
+        if (x[i] > max_val) max_val = x[i];
+    float sum = 0.0f;
+    for (int i = 0; i < size; i++) {
+        x[i] = expf(x[i] - max_val);
+        sum += x[i];
+    }
+    float inv_sum = 1.0f / sum;
+    for (int i = 0; i < size; i++) x[i] *= inv_sum;
+}
+
+/* ---------------------------------------------------------------- attention */
+
+/* Row dot / axpy.  Q8: dot_q8_row / axpy_q8_row scalar x86 branches,
+ * inference.rs:1337-1366:  acc += q * (c * scale);  scaled = a*scale; d += scaled*c.
+ * Raw storage (f32/f16/bf16): the same loops with the exact dequantiser
+ * (scale == 1 removed): acc += q * c;  d += a * c. */
+static inline float row_dot(const float* q, const void* cache, size_t off, int n, int fmt,
+                            float scale) {
+    float acc = 0.0f;
+    if (fmt == ORC_Q8) {
+        const int8_t* c = (const int8_t*)cache + off;
+        for (int i = 0; i < n; i++) acc += q[i] * ((float)c[i] * scale);
+    } else {
+        for (int i = 0; i < n; i++) acc += q[i] * load_kv(cache, off + (size_t)i, fmt);
+    }
+    return acc;
+}
+
+static inline void row_axpy(float* dst, float a, const void* cache, size_t off, int n, int fmt,
+                            float scale) {
+    if (fmt == ORC_Q8) {
+        const int8_t* c = (const int8_t*)cache + off;
+        float scaled = a * scale;
+        for (int i = 0; i < n; i++) dst[i] += scaled * (float)c[i];
+    } else {
+        for (int i = 0; i < n; i++) dst[i] += a * load_kv(cache, off + (size_t)i, fmt);
+    }
+}
+
+/* One query head of attention_token, inference.rs:2008-2284 (the per-head
+ * closure; the serial branch 2290-2528 computes the same thing).
+ *   online == 0: two-pass: scores -> softmax (math.rs:263-280) -> axpy (2175-2283)
+ *   online == 1: online-softmax fusion used iff online_attn_fusion (2048-2174):
+ *                running max from -inf, rescale exp(m_old - m_new) applied to acc
+ *                and sum only when sum > 0, final *(1/sum) when sum > 0. */
+static void attention_head(const float* q_head, float* xb_head, float* att_head, int head_size,
+                           const void* key_cache, const void* value_cache, int fmt,
+                           const float* key_scale, const float* value_scale, size_t layer_row_base,
+                           size_t kv_dim, size_t kv_head_offset, size_t vis_start, size_t vis_end,
+                           float attn_scale, int apply_attn_scale, int online) {
+    if (online) {
+        for (int i = 0; i < head_size; i++) xb_head[i] = 0.0f;
+        float max_score = -INFINITY;
+        float score_sum = 0.0f;
+        for (size_t t = vis_start; t < vis_end; t++) {
+            size_t t_row = layer_row_base + t;
+            size_t row_offset = t_row * kv_dim + kv_head_offset;
+            float score = row_dot(q_head, key_cache, row_offset, head_size, fmt,
+                                  fmt == ORC_Q8 ? key_scale[t_row] : 1.0f);
+            if (apply_attn_scale) score *= attn_scale;
+            if (score > max_score) {
+                if (score_sum > 0.0f) {
+                    float rescale = expf(max_score - score);
+                    for (int i = 0; i < head_size; i++) xb_head[i] *= rescale;
+                    score_sum *= rescale;
+                }
+                max_score = score;
+            }
+            float weight = expf(score - max_score);
+            score_sum += weight;
+            row_axpy(xb_head, weight, value_cache, row_offset, head_size, fmt,
+                     fmt == ORC_Q8 ? value_scale[t_row] : 1.0f);
+        }
+        if (score_sum > 0.0f) {
+            float inv = 1.0f / score_sum;
+            for (int i = 0; i < head_size; i++) xb_head[i] *= inv;
+        }
+    } else {
+        size_t n = vis_end - vis_start;
+        for (size_t t = vis_start; t < vis_end; t++) {
+            size_t t_row = layer_row_base + t;
+            size_t row_offset = t_row * kv_dim + kv_head_offset;
+            float score = row_dot(q_head, key_cache, row_offset, head_size, fmt,
+                                  fmt == ORC_Q8 ? key_scale[t_row] : 1.0f);
+            if (apply_attn_scale) score *= attn_scale;
+            att_head[t - vis_start] = score;
+        }
+        orc_softmax(att_head, (int)n);
+        for (int i = 0; i < head_size; i++) xb_head[i] = 0.0f;
+        for (size_t t = vis_start; t < vis_end; t++) {
+            size_t t_row = layer_row_base + t;
+            size_t row_offset = t_row * kv_dim + kv_head_offset;
+            row_axpy(xb_head, att_head[t - vis_start], value_cache, row_offset, head_size, fmt,
+                     fmt == ORC_Q8 ? value_scale[t_row] : 1.0f);
+        }
+    }
+}
+
+/* attention_token, inference.rs:1970-2530, for one (layer, pos).
+ * The KV cache is indexed like RunState's: element (row t_row, kv head g, i) at
+ * t_row*kv_dim + g*head_size + i with t_row = layer_row_base + t (1880-1882).
+ * GQA: kv_head = h / kv_mul (2019).  Visible keys [vis_start, vis_end) come from
+ * LanguageAttentionPolicy::visible_keys (attention.rs:74-96).
+ * att must hold n_heads * att_stride floats (att_stride >= vis_end - vis_start).
+ * n_threads > 1 parallelises over heads like the rayon branch (2002-2007).
+ * Pinned by: fp64 closed form + special cases in tests/test_oracle_attention.py. */
+void orc_attention_token(const float* q, float* xb, float* att, size_t att_stride, int n_heads,
+                         int n_kv_heads, int head_size, const void* key_cache,
+                         const void* value_cache, int fmt, const float* key_scale,
+                         const float* value_scale, size_t layer_row_base, size_t vis_start,
+                         size_t vis_end, float attn_scale, int apply_attn_scale, int online,
+                         int n_threads) {
+    int kv_mul = n_heads / n_kv_heads;
+    size_t kv_dim = (size_t)n_kv_heads * (size_t)head_size;
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1) if (n_threads > 1)
+    for (int h = 0; h < n_heads; h++) {
+        int kv_head = h / kv_mul;
+        attention_head(q + (size_t)h * head_size, xb + (size_t)h * head_size,
+                       att + (size_t)h * att_stride, head_size, key_cache, value_cache, fmt,
+                       key_scale, value_scale, layer_row_base, kv_dim,
+                       (size_t)kv_head * head_size, vis_start, vis_end, attn_scale,
+                       apply_attn_scale, online);
+    }
+}
+
+/* LanguageAttentionPolicy::visible_keys, attention.rs:74-96 (text tokens):
+ * end = query + 1; start = window ? end.saturating_sub(window) : 0.
+ * window == 0 encodes "None" (global layer).  Pinned by attention.rs:171-172
+ * and the window semantics comment types.rs:614-616. */
+void orc_visible_keys(int64_t window, int64_t query, int64_t* start, int64_t* end) {
+    int64_t e = query + 1;
+    int64_t s = 0;
+    if (window > 0) s = e > window ? e - window : 0;
+    *start = s;
+    *end = e;
+}
+
+/* ---------------------------------------------------------------- per-token layer driver */
+
+/* Round one f32 to the raw storage format (the raw-mode "kv_write_token"):
+ * f16 / bf16 use IEEE round-to-nearest-even like fp32_to_fp16 / fp32_to_bf16,
+ * src/engine/io/gguf.rs:72-117. */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
+    if (ax < 0x38800000u) {                                   /* subnormal / zero in f16 */
+        if (ax < 0x33000000u) return (uint16_t)sign;          /* < half the smallest subnormal */
+        uint32_t man = (ax & 0x7fffffu) | 0x800000u;
+        int e = (int)(ax >> 23);
+        int shift = 126 - e; /* 113 - e + 13 */
+        uint32_t r = man >> shift;
+        uint32_t rem = man & ((1u << shift) - 1);
+        uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (r & 1))) r++;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((ax - 0x38000000u) >> 13);
+    uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1))) r++;
+    return (uint16_t)(sign | r);
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    uint32_t lsb = (x >> 16) & 1u;
+    x += 0x7fffu + lsb;
+    return (uint16_t)(x >> 16);
+}
+
+static void store_kv(void* base, size_t idx, int fmt, float v) {
+    switch (fmt) {
+        case ORC_F16: ((uint16_t*)base)[idx] = orc_f32_to_f16(v); break;
+        case ORC_BF16: ((uint16_t*)base)[idx] = orc_f32_to_bf16(v); break;
+        default: ((float*)base)[idx] = v; break;
+    }
+}
+
+/* The serial prefill loop of transformer_prefill_batch, inference.rs:2981-3017,
+ * for the attention part of one layer and one sequence, raw KV storage:
+ *   per token i (pos = base_pos + i):  qkv_bias_and_norm (QK-norm only, 2535-2572)
+ *   -> apply_rope_qk (1817-1874) -> kv_write_token (1877-1965, raw storage)
+ *   -> attention_token (1970-2530) -> xb row.
+ * Inputs q [m][n_heads*d], k/v [m][n_kv_heads*d] are f32 (already upcast from the
+ * test's f16/bf16 buffers).  key/value_cache are [seq_len][kv_dim] of `fmt`.
+ * rope_freqs has rope_dim/2 entries for the layer (local or global table);
+ * rope_scale is the layer's frequency scale.  window 0 = global.
+ * q_norm/k_norm may be NULL (no QK-norm).  Pinned through the functions it calls
+ * plus tests/test_oracle_attention.py (fp64 closed form on the whole layer). */
+void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, float* xb_out,
+                       int m, int64_t base_pos, int n_heads, int n_kv_heads, int head_size,
+                       void* key_cache, void* value_cache, int fmt, int rope_dim, int neox,
+                       const float* rope_freqs, float rope_scale, int is_gemma3, int online,
+                       int64_t window, const float* q_norm, const float* k_norm, float eps,
+                       int n_threads) {
+    int q_dim = n_heads * head_size;
+    int kv_dim = n_kv_heads * head_size;
+    int half = rope_dim / 2;
+    float attn_scale = 1.0f / sqrtf((float)head_size);
+    float* q = (float*)malloc(sizeof(float) * (size_t)q_dim);
+    float* k = (float*)malloc(sizeof(float) * (size_t)kv_dim);
+    float* cs = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    float* sn = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
+    size_t att_stride = (size_t)(base_pos + m);
+    float* att = (float*)malloc(sizeof(float) * (size_t)n_heads * att_stride);
+    for (int i = 0; i < m; i++) {
+        int64_t pos = base_pos + i;
+        memcpy(q, q_in + (size_t)i * q_dim, sizeof(float) * (size_t)q_dim);
+        memcpy(k, k_in + (size_t)i * kv_dim, sizeof(float) * (size_t)kv_dim);
+        if (q_norm && k_norm) {
+            orc_rmsnorm_per_head(q, q_norm, n_heads, head_size, eps);
+            orc_rmsnorm_per_head(k, k_norm, n_kv_heads, head_size, eps);
+        }
+        if (half > 0) {
+            orc_rope_cache(rope_freqs, half, pos, rope_scale, cs, sn);
+            orc_apply_rope_qk(q, k, n_heads, n_kv_heads, head_size, half, cs, sn, neox, is_gemma3,
+                              attn_scale);
+        } else if (is_gemma3) {
+            for (int j = 0; j < q_dim; j++) q[j] *= attn_scale;
+        }
+        for (int j = 0; j < kv_dim; j++) {
+            store_kv(key_cache, (size_t)pos * kv_dim + j, fmt, k[j]);
+            store_kv(value_cache, (size_t)pos * kv_dim + j, fmt, v_in[(size_t)i * kv_dim + j]);
+        }
+        int64_t s, e;
+        orc_visible_keys(window, pos, &s, &e);
+        orc_attention_token(q, xb_out + (size_t)i * q_dim, att, att_stride, n_heads, n_kv_heads,
+                            head_size, key_cache, value_cache, fmt, NULL, NULL, 0, (size_t)s,
+                            (size_t)e, attn_scale, !is_gemma3, online, n_threads);
+    }
+    free(q);
+    free(k);
+    free(cs);
+    free(sn);
+    free(att);
+}
+
+/* ---------------------------------------------------------------- gated DeltaNet */
+
+/* axpy_inplace on x86 with AVX2+FMA, quant.rs:1023-1047 + 1069-1080:
+ * elements in 8/16-wide blocks use fused multiply-add; a tail (n % 8) uses
+ * dst += a*src with two roundings. */
+static inline void axpy_inplace(float* dst, float a, const float* src, int n) {
+    int n_fma = n - n % 8;
+    int i = 0;
+    for (; i < n_fma; i++) dst[i] = fmaf(src[i], a, dst[i]);
+    for (; i < n; i++) dst[i] += a * src[i];
+}
+
+static inline float finite_or_zero(float x) { return isfinite(x) ? x : 0.0f; }
+
+/* qwen3next_state_head_step, math.rs:492-546 (gated delta rule, one head).
+ * state_h is [d][d] row-major, S[j][i] (j = key dim row, i = value dim col).
+ * Pinned by: delta-rule retrieval invariant, beta=0 pure decay, fp64 brute force
+ * (tests/test_oracle_deltanet.py). */
+void orc_deltanet_head_step(float* state_h, float* out_h, const float* q, const float* k,
+                            const float* v, float g, float beta, int d) {
+    float* kv_mem = (float*)malloc(sizeof(float) * (size_t)d);
+    float* delta = (float*)malloc(sizeof(float) * (size_t)d);
+    for (int x = 0; x < d * d; x++) state_h[x] *= g; /* scale_slice_inplace */
+    for (int i = 0; i < d; i++) kv_mem[i] = 0.0f;
+    for (int j = 0; j < d; j++) {
+        if (k[j] == 0.0f) continue;
+        axpy_inplace(kv_mem, k[j], state_h + (size_t)j * d, d);
+    }
+    for (int i = 0; i < d; i++) {
+        kv_mem[i] = finite_or_zero(kv_mem[i]);
+        delta[i] = finite_or_zero((v[i] - kv_mem[i]) * beta);
+    }
+    for (int j = 0; j < d; j++) {
+        if (k[j] == 0.0f) continue;
+        axpy_inplace(state_h + (size_t)j * d, k[j], delta, d);
+    }
+    for (int i = 0; i < d; i++) out_h[i] = 0.0f;
+    for (int j = 0; j < d; j++) {
+        if (q[j] == 0.0f) continue;
+        axpy_inplace(out_h, q[j], state_h + (size_t)j * d, d);
+    }
+    for (int i = 0; i < d; i++)
+        if (!isfinite(out_h[i])) out_h[i] = 0.0f; /* sanitize_finite_inplace */
+    free(kv_mem);
+    free(delta);
+}
+
+/* The per-head L2 normalisation of qwen3next_linear_attention_projected_state,
+ * math.rs:833-846: q_dst = q * (1/sqrt(sum q^2 + eps)) * (1/sqrt(d)),
+ * k_dst = k * (1/sqrt(sum k^2 + eps)).  (Written as (x*inv)*scale like 844.) */
+void orc_deltanet_l2norm(float* q, float* k, int d, float eps) {
+    float q_ss = 0.0f, k_ss = 0.0f;
+    for (int i = 0; i < d; i++) {
+        q_ss += q[i] * q[i];
+        k_ss += k[i] * k[i];
+    }
+    float q_inv = 1.0f / sqrtf(q_ss + eps);
+    float k_inv = 1.0f / sqrtf(k_ss + eps);
+    float inv_scale_q = 1.0f / sqrtf((float)d);
+    for (int i = 0; i < d; i++) {
+        q[i] = finite_or_zero(q[i] * q_inv * inv_scale_q);
+        k[i] = finite_or_zero(k[i] * k_inv);
+    }
+}
+
+/* Token-serial recurrence over T tokens for n_heads heads, as the reference's
+ * prefill runs it (inference.rs:2866-2885 -> math.rs:890-934 per token).
+ * q,k,v are [T][H][d] f32 (raw, pre-normalisation when l2norm != 0),
+ * gate is [T][H] log-decay (g = exp(gate), math.rs:869-874), beta [T][H]
+ * (post-sigmoid).  state [H][d][d] is updated in place; out [T][H][d]. */
+void orc_deltanet_scan(const float* q, const float* k, const float* v, const float* gate,
+                       const float* beta, float* state, float* out, int T, int n_heads, int d,
+                       int l2norm, float eps, int n_threads) {
+    for (int t = 0; t < T; t++) {
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1) if (n_threads > 1)
+        for (int h = 0; h < n_heads; h++) {
+            size_t off = ((size_t)t * n_heads + h) * d;
+            float* qq = (float*)malloc(sizeof(float) * (size_t)d);
+            float* kk = (float*)malloc(sizeof(float) * (size_t)d);
+            memcpy(qq, q + off, sizeof(float) * (size_t)d);
+            memcpy(kk, k + off, sizeof(float) * (size_t)d);
+            if (l2norm) orc_deltanet_l2norm(qq, kk, d, eps);
+            float g = finite_or_zero(expf(gate[(size_t)t * n_heads + h]));
+            float b = finite_or_zero(beta[(size_t)t * n_heads + h]);
+            orc_deltanet_head_step(state + (size_t)h * d * d, out + off, qq, kk, v + off, g, b, d);
+            free(qq);
+            free(kk);
+        }
+    }
+}
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,244 @@
+"""ctypes wrapper of the CPU oracle (oracle.c) -- TEST INFRASTRUCTURE ONLY.
+
+Importable only from tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg.  It is the checker, never the thing measured as the product
+and never a fallback for the HIP path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+F32, F16, BF16, Q8 = 0, 1, 2, 3
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+_f = ctypes.c_float
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_f16_to_f32.restype = _f
+    L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_bf16_to_f32.restype = _f
+    L.orc_f32_to_f16.argtypes = [_f]
+    L.orc_f32_to_f16.restype = ctypes.c_uint16
+    L.orc_f32_to_bf16.argtypes = [_f]
+    L.orc_f32_to_bf16.restype = ctypes.c_uint16
+    L.orc_rope_freqs.argtypes = [_f, _i, _p]
+    L.orc_rope_cache.argtypes = [_p, _i, _i64, _f, _p, _p]
+    L.orc_apply_rope_qk.argtypes = [_p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _f]
+    L.orc_rmsnorm_per_head.argtypes = [_p, _p, _i, _i, _f]
+    L.orc_quantize_row_q8.argtypes = [_p, _i, _p, _p]
+    L.orc_softmax.argtypes = [_p, _i]
+    L.orc_attention_token.argtypes = [_p, _p, _p, _sz, _i, _i, _i, _p, _p, _i, _p, _p, _sz, _sz,
+                                      _sz, _f, _i, _i, _i]
+    L.orc_visible_keys.argtypes = [_i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
+    L.orc_prefill_layer.argtypes = [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _i, _i, _i, _p,
+                                    _f, _i, _i, _i64, _p, _p, _f, _i]
+    L.orc_deltanet_head_step.argtypes = [_p, _p, _p, _p, _p, _f, _f, _i]
+    L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
+    L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
+    L.orc_max_threads.restype = _i
+
+
+def _ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())
+
+
+def rope_freqs(theta: float, rope_dim: int) -> np.ndarray:
+    out = np.zeros(rope_dim // 2, np.float32)
+    lib().orc_rope_freqs(theta, rope_dim, _ptr(out))
+    return out
+
+
+def rope_cache(freqs: np.ndarray, pos: int, scale: float):
+    freqs = _f32(freqs)
+    c = np.zeros_like(freqs)
+    s = np.zeros_like(freqs)
+    lib().orc_rope_cache(_ptr(freqs), freqs.size, pos, scale, _ptr(c), _ptr(s))
+    return c, s
+
+
+def apply_rope_qk(q, k, n_heads, n_kv_heads, head_size, cos_t, sin_t, neox, gemma_q_scale=False,
+                  attn_scale=None):
+    """In-place on copies; returns (q, k)."""
+    q = _f32(q).copy()
+    k = _f32(k).copy()
+    cos_t = _f32(cos_t)
+    sin_t = _f32(sin_t)
+    if attn_scale is None:
+        attn_scale = float(np.float32(1.0) / np.sqrt(np.float32(head_size)))
+    lib().orc_apply_rope_qk(_ptr(q), _ptr(k), n_heads, n_kv_heads, head_size, cos_t.size,
+                            _ptr(cos_t), _ptr(sin_t), int(neox), int(gemma_q_scale), attn_scale)
+    return q, k
+
+
+def rmsnorm_per_head(x, w, n_heads, head_size, eps):
+    x = _f32(x).copy()
+    w = _f32(w)
+    lib().orc_rmsnorm_per_head(_ptr(x), _ptr(w), n_heads, head_size, eps)
+    return x
+
+
+def quantize_row_q8(src):
+    src = _f32(src)
+    dst = np.zeros(src.size, np.int8)
+    scale = np.zeros(1, np.float32)
+    lib().orc_quantize_row_q8(_ptr(src), src.size, _ptr(dst), _ptr(scale))
+    return dst, float(scale[0])
+
+
+def softmax(x):
+    x = _f32(x).copy()
+    lib().orc_softmax(_ptr(x), x.size)
+    return x
+
+
+def visible_keys(window: int, query: int):
+    s = _i64()
+    e = _i64()
+    lib().orc_visible_keys(window, query, ctypes.byref(s), ctypes.byref(e))
+    return s.value, e.value
+
+
+def attention_token(q, key_cache, value_cache, fmt, n_heads, n_kv_heads, head_size, vis_start,
+                    vis_end, *, layer_row_base=0, key_scale=None, value_scale=None,
+                    attn_scale=None, apply_attn_scale=True, online=False, n_threads=1):
+    """attention_token for one query position; caches are flat row-major
+    [rows][n_kv_heads*head_size] arrays of f32 / uint16 (f16|bf16 bits) / int8."""
+    q = _f32(q)
+    xb = np.zeros(n_heads * head_size, np.float32)
+    att_stride = max(vis_end - vis_start, 1)
+    att = np.zeros(n_heads * att_stride, np.float32)
+    if attn_scale is None:
+        attn_scale = float(np.float32(1.0) / np.sqrt(np.float32(head_size)))
+    key_cache = np.ascontiguousarray(key_cache)
+    value_cache = np.ascontiguousarray(value_cache)
+    ks = _f32(key_scale) if key_scale is not None else None
+    vs = _f32(value_scale) if value_scale is not None else None
+    lib().orc_attention_token(_ptr(q), _ptr(xb), _ptr(att), att_stride, n_heads, n_kv_heads,
+                              head_size, _ptr(key_cache), _ptr(value_cache), fmt, _ptr(ks),
+                              _ptr(vs), layer_row_base, vis_start, vis_end, attn_scale,
+                              int(apply_attn_scale), int(online), n_threads)
+    return xb
+
+
+def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope_dim, neox,
+                  rope_freqs_tab, rope_scale, is_gemma3=False, online=False, window=0,
+                  q_norm=None, k_norm=None, eps=1e-6, base_pos=0, key_cache=None,
+                  value_cache=None, n_threads=1):
+    """Token-serial prefill of one layer (inference.rs:2981-3017), raw KV mode.
+    q [m][n_heads*d], k/v [m][n_kv_heads*d] f32.  Returns (xb [m][q_dim], kcache, vcache)."""
+    q = _f32(q)
+    k = _f32(k)
+    v = _f32(v)
+    m = q.shape[0]
+    kv_dim = n_kv_heads * head_size
+    cdt = np.float32 if fmt == F32 else np.uint16
+    if key_cache is None:
+        key_cache = np.zeros((seq_len, kv_dim), cdt)
+        value_cache = np.zeros((seq_len, kv_dim), cdt)
+    xb = np.zeros((m, n_heads * head_size), np.float32)
+    freqs = _f32(rope_freqs_tab) if rope_freqs_tab is not None else None
+    qn = _f32(q_norm) if q_norm is not None else None
+    kn = _f32(k_norm) if k_norm is not None else None
+    lib().orc_prefill_layer(_ptr(q), _ptr(k), _ptr(v), _ptr(xb), m, base_pos, n_heads, n_kv_heads,
+                            head_size, _ptr(key_cache), _ptr(value_cache), fmt, rope_dim,
+                            int(neox), _ptr(freqs), rope_scale, int(is_gemma3), int(online),
+                            window, _ptr(qn), _ptr(kn), eps, n_threads)
+    return xb, key_cache, value_cache
+
+
+def deltanet_head_step(state, q, k, v, g, beta):
+    state = _f32(state).copy()
+    d = q.size
+    out = np.zeros(d, np.float32)
+    lib().orc_deltanet_head_step(_ptr(state), _ptr(out), _ptr(_f32(q)), _ptr(_f32(k)),
+                                 _ptr(_f32(v)), g, beta, d)
+    return state, out
+
+
+def deltanet_scan(q, k, v, gate, beta, state, *, l2norm=True, eps=1e-6, n_threads=1):
+    """q,k,v [T][H][d]; gate, beta [T][H]; state [H][d][d].  Returns (out, state)."""
+    q = _f32(q)
+    k = _f32(k)
+    v = _f32(v)
+    gate = _f32(gate)
+    beta = _f32(beta)
+    state = _f32(state).copy()
+    T, H, d = q.shape
+    out = np.zeros((T, H, d), np.float32)
+    lib().orc_deltanet_scan(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta), _ptr(state),
+                            _ptr(out), T, H, d, int(l2norm), eps, n_threads)
+    return out, state
+
+
+def f16_bits(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, np.float32).astype(np.float16)).view(np.uint16)
+
+
+def bf16_bits(x) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16 bit pattern (gguf.rs fp32_to_bf16 semantics)."""
+    a = np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32)
+    nan = (a & 0x7FFFFFFF) > 0x7F800000
+    r = ((a + 0x7FFF + ((a >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((a[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_to_f32(bits) -> np.ndarray:
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def upcast(bits, fmt) -> np.ndarray:
+    if fmt == F16:
+        return f16_to_f32(bits)
+    if fmt == BF16:
+        return bf16_to_f32(bits)
+    return np.asarray(bits, np.float32)
+
+
+def env_threads() -> int:
+    return int(os.environ.get("ORACLE_THREADS", "0")) or max_threads()
