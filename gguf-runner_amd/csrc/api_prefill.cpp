@@ -1,0 +1,155 @@
+// C-ABI entry points of the prefill path: validation, workspace carving, and
+// the two launches (Q/K/V prep -> cache; MFMA flash attention).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "gr_api_util.hpp"
+#include "gr_attn.h"
+#include "gr_internal.hpp"
+
+namespace gr {
+
+namespace {
+
+int check_prefill(const gr_prefill_args* a) {
+    if (!a) return fail(GR_ERR_ARG, "gr_prefill_attention: null args");
+    if (a->n_tokens < 0 || a->base_pos < 0)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: negative n_tokens/base_pos");
+    if (a->n_heads <= 0 || a->n_kv_heads <= 0 || a->n_heads % a->n_kv_heads != 0)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: n_heads %d must be a positive multiple of n_kv_heads %d",
+                    a->n_heads, a->n_kv_heads);
+    if (a->head_dim != 128 && a->head_dim != 256)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: head_dim %d unsupported (128, 256)", a->head_dim);
+    if (a->dtype != GR_DTYPE_F16 && a->dtype != GR_DTYPE_BF16)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: dtype must be f16 or bf16");
+    if (a->window < 0) return fail(GR_ERR_ARG, "gr_prefill_attention: window < 0");
+    if (a->rope_mode < GR_ROPE_NONE || a->rope_mode > GR_ROPE_NEOX)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: bad rope_mode %d", a->rope_mode);
+    if (a->rope_mode != GR_ROPE_NONE) {
+        if (a->rope_dim <= 0 || a->rope_dim > a->head_dim || (a->rope_dim & 1))
+            return fail(GR_ERR_ARG, "gr_prefill_attention: rope_dim %d must be even and in (0, head_dim]",
+                        a->rope_dim);
+        if (a->rope_mode == GR_ROPE_ADJACENT && a->rope_dim != a->head_dim)
+            return fail(GR_ERR_ARG, "gr_prefill_attention: adjacent-pair RoPE rotates whole heads (rope_dim == head_dim)");
+        if (!a->rope_freqs) return fail(GR_ERR_ARG, "gr_prefill_attention: rope_freqs is NULL");
+        if (!std::isfinite(a->rope_scale) || a->rope_scale <= 0.0f)
+            return fail(GR_ERR_ARG, "RoPE frequency scales must be finite and positive");
+    }
+    if ((a->q_norm == nullptr) != (a->k_norm == nullptr))
+        return fail(GR_ERR_ARG, "gr_prefill_attention: q_norm and k_norm must be both set or both NULL");
+    if (a->n_tokens > 0 && (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache || !a->out ||
+                            !a->workspace))
+        return fail(GR_ERR_ARG, "gr_prefill_attention: null buffer");
+    if (a->cache_row_stride < (int64_t)a->n_kv_heads * a->head_dim || (a->cache_row_stride * 2) % 16)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: cache_row_stride must be >= n_kv_heads*head_dim and 16-byte aligned");
+    if (((uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 || (uintptr_t)a->out % 16)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: cache and out must be 16-byte aligned");
+    if ((uintptr_t)a->workspace % 256)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: workspace must be 256-byte aligned");
+    return GR_OK;
+}
+
+size_t prefill_q_bytes(const gr_prefill_args* a) {
+    return align_up((size_t)a->n_tokens * a->n_heads * a->head_dim * 2, 256);
+}
+
+// bf16 carries Q as hi + lo residual pairs (two staging buffers).
+size_t prefill_ws_total(const gr_prefill_args* a) {
+    return prefill_q_bytes(a) * (a->dtype == GR_DTYPE_BF16 ? 2 : 1);
+}
+
+}  // namespace
+
+int prefill_enqueue(const gr_prefill_args* a, hipStream_t st) {
+    int rc = check_prefill(a);
+    if (rc) return rc;
+    if (a->n_tokens == 0) return GR_OK;
+    const float score_scale = a->is_gemma3 ? 1.0f : 1.0f / std::sqrt((float)a->head_dim);
+
+    QkvPrepLaunch pp{};
+    pp.n_tokens = a->n_tokens;
+    pp.n_heads = a->n_heads;
+    pp.n_kv_heads = a->n_kv_heads;
+    pp.head_dim = a->head_dim;
+    pp.in_dtype = a->dtype;
+    pp.pos = nullptr;
+    pp.pos0 = a->base_pos;
+    pp.rope_mode = a->rope_mode;
+    pp.rope_dim = a->rope_dim;
+    pp.rope_scale = a->rope_scale;
+    pp.rope_freqs = a->rope_freqs;
+    pp.q_norm = a->q_norm;
+    pp.k_norm = a->k_norm;
+    pp.eps = a->norm_eps;
+    pp.gemma_q_scale = a->is_gemma3;
+    pp.q = a->q;
+    pp.k = a->k;
+    pp.v = a->v;
+    pp.q_row_stride = (int64_t)a->n_heads * a->head_dim;
+    pp.kv_row_stride = (int64_t)a->n_kv_heads * a->head_dim;
+    pp.q_out = a->workspace;
+    pp.q_out_lo = a->dtype == GR_DTYPE_BF16 ? (char*)a->workspace + prefill_q_bytes(a) : nullptr;
+    pp.q_out_dtype = a->dtype;
+    pp.q_out_scale = score_scale * 1.4426950408889634f;
+    pp.k_cache = a->k_cache;
+    pp.v_cache = a->v_cache;
+    pp.cache_dtype = a->dtype;
+    pp.cache_row = nullptr;
+    pp.cache_seq = nullptr;
+    pp.cache_seq_stride = 0;
+    pp.cache_row_stride = a->cache_row_stride;
+    hipError_t e = launch_qkv_prep(pp, st);
+    if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention prep launch");
+
+    PrefillLaunch pf{};
+    pf.n_tokens = a->n_tokens;
+    pf.n_heads = a->n_heads;
+    pf.n_kv_heads = a->n_kv_heads;
+    pf.head_dim = a->head_dim;
+    pf.dtype = a->dtype;
+    pf.base_pos = a->base_pos;
+    pf.window = a->window;
+    pf.q = pp.q_out;
+    pf.q_lo = pp.q_out_lo;
+    pf.k_cache = a->k_cache;
+    pf.v_cache = a->v_cache;
+    pf.cache_row_stride = a->cache_row_stride;
+    pf.out = a->out;
+    e = launch_prefill(pf, st);
+    if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention launch");
+    return GR_OK;
+}
+
+size_t prefill_ws_bytes(const gr_prefill_args* a) {
+    if (!a || a->n_tokens < 0 || a->n_heads <= 0 || a->head_dim <= 0) return 0;
+    return prefill_ws_total(a);
+}
+
+int rope_freqs_host(float theta, int rope_dim, float* out) {
+    if (!out || rope_dim <= 0 || (rope_dim & 1))
+        return fail(GR_ERR_ARG, "gr_rope_freqs: rope_dim %d must be positive and even", rope_dim);
+    if (!std::isfinite(theta) || theta <= 0.0f)
+        return fail(GR_ERR_ARG, "gr_rope_freqs: theta must be finite and positive");
+    for (int i = 0; i < rope_dim / 2; i++)
+        out[i] = 1.0f / powf(theta, (float)(i * 2) / (float)rope_dim);
+    return GR_OK;
+}
+
+}  // namespace gr
+
+extern "C" {
+
+size_t gr_prefill_workspace_size(const gr_prefill_args* a) { return gr::prefill_ws_bytes(a); }
+
+int gr_prefill_attention(const gr_prefill_args* a, void* stream) {
+    gr::clear_error();
+    return gr::prefill_enqueue(a, (hipStream_t)stream);
+}
+
+int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out) {
+    gr::clear_error();
+    return gr::rope_freqs_host(theta, rope_dim, freqs_out);
+}
+
+}  // extern "C"

@@ -46,6 +46,7 @@ struct QkvPrepLaunch {
     const void* v;
     int64_t q_row_stride, kv_row_stride;  // input row strides (elements)
     void* q_out;
+    void* q_out_lo;        // 16-bit q_out only: residual x - round(x) in the same dtype, or nullptr
     int q_out_dtype;
     float q_out_scale;
     void* k_cache;
@@ -60,12 +61,14 @@ struct QkvPrepLaunch {
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);
 
 // Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
-// [m][n_heads][d] already multiplied by score_scale*log2(e).
+// [m][n_heads][d] already multiplied by score_scale*log2(e); for bf16, q_lo
+// holds the bf16 residual q - q_hi so that q_hi + q_lo carries ~16 mantissa bits.
 struct PrefillLaunch {
     int n_tokens, n_heads, n_kv_heads, head_dim, dtype;
     int64_t base_pos;
     int window;
     const void* q;
+    const void* q_lo;
     const void* k_cache;
     const void* v_cache;
     int64_t cache_row_stride;

@@ -32,9 +32,14 @@ struct Mfma32<F16> {
     static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
         return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
     }
+    static constexpr bool kSplit = false;
 };
+// bf16 keeps only 8 mantissa bits: Q and P are carried as hi + lo bf16 pairs
+// (two MFMAs per product; K and V are exact bf16 values of the cache), which
+// brings the products to ~1e-5 of an fp32 evaluation.
 template <>
 struct Mfma32<BF16> {
+    static constexpr bool kSplit = true;
     static __device__ __forceinline__ f32x16 mma(const uint4& a, const uint4& b, const f32x16& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -84,11 +89,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillLaunch
     const int64_t wpos_max = P0 + min(wr0 + 31, m - 1);
 
     // Q fragments (B operand): lane (query ln, group lg) holds d = 16 s + 8 lg .. +7.
+    constexpr bool kSplit = M::kSplit;
     uint4 qf[D / 16];
+    uint4 qfl[kSplit ? D / 16 : 1];
     {
-        const uint16_t* qrow = (const uint16_t*)p.q + ((size_t)my_row_c * p.n_heads + h) * D + 8 * lg;
+        const size_t qoff = ((size_t)my_row_c * p.n_heads + h) * D + 8 * lg;
+        const uint16_t* qrow = (const uint16_t*)p.q + qoff;
 #pragma unroll
         for (int s = 0; s < D / 16; s++) qf[s] = *(const uint4*)(qrow + 16 * s);
+        if constexpr (kSplit) {
+            const uint16_t* qrl = (const uint16_t*)p.q_lo + qoff;
+#pragma unroll
+            for (int s = 0; s < D / 16; s++) qfl[s] = *(const uint4*)(qrl + 16 * s);
+        }
     }
 
     const int last_row = min(q0 + BM, m) - 1;
@@ -187,6 +200,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillLaunch
             for (int s = 0; s < D / 16; s++) {
                 const uint4 a = *(const uint4*)(krow + 16 * s);
                 sacc[sb] = M::mma(a, qf[s], sacc[sb]);
+                if constexpr (kSplit) sacc[sb] = M::mma(a, qfl[s], sacc[sb]);
             }
         }
         // S^T register j of sub-tile sb holds key t0 + 32 sb + 8 (j/4) + 4 lg + j%4.
@@ -210,6 +224,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillLaunch
         mrow = mnew;
         float psum = 0.0f;
         uint4 pf[2][2];
+        uint4 pfl[kSplit ? 2 : 1][2];
 #pragma unroll
         for (int sb = 0; sb < 2; sb++) {
             float pv[16];
@@ -224,6 +239,20 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillLaunch
                 pf[sb][t].y = M::pack2(pv[8 * t + 2], pv[8 * t + 3]);
                 pf[sb][t].z = M::pack2(pv[8 * t + 4], pv[8 * t + 5]);
                 pf[sb][t].w = M::pack2(pv[8 * t + 6], pv[8 * t + 7]);
+            }
+            if constexpr (kSplit) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t hw[4] = {pf[sb][t].x, pf[sb][t].y, pf[sb][t].z, pf[sb][t].w};
+                    uint32_t lw[4];
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+                        const float r0 = pv[8 * t + 2 * w] - __uint_as_float(hw[w] << 16);
+                        const float r1 = pv[8 * t + 2 * w + 1] - __uint_as_float(hw[w] & 0xffff0000u);
+                        lw[w] = M::pack2(r0, r1);
+                    }
+                    pfl[sb][t] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+                }
             }
         }
         lrow = lrow * alpha + psum;
@@ -241,6 +270,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillLaunch
                     const uint2 hi = *(const uint2*)(vrow + kb + 8);
                     const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
                     o[dt] = M::mma(a, pf[sb][t], o[dt]);
+                    if constexpr (kSplit) o[dt] = M::mma(a, pfl[sb][t], o[dt]);
                 }
         }
     }

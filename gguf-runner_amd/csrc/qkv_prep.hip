@@ -106,7 +106,14 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
     if (kind == 0) {
         const size_t ob = ((size_t)i * p.n_heads + head) * D;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) store_elem(p.q_out, ob + lane + 64 * e, p.q_out_dtype, x[e] * p.q_out_scale);
+        for (int e = 0; e < EPL; e++) {
+            const float xs = x[e] * p.q_out_scale;
+            store_elem(p.q_out, ob + lane + 64 * e, p.q_out_dtype, xs);
+            if (p.q_out_lo) {
+                const float hi = load_elem(p.q_out, ob + lane + 64 * e, p.q_out_dtype);
+                store_elem(p.q_out_lo, ob + lane + 64 * e, p.q_out_dtype, xs - hi);
+            }
+        }
     } else {
         const int64_t row = p.cache_row ? (int64_t)p.cache_row[i] : pos;
         const int64_t sq = p.cache_seq ? (int64_t)p.cache_seq[i] : 0;

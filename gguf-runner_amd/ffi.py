@@ -45,6 +45,17 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", _i32), ("base_pos", _i32), ("n_heads", _i32), ("n_kv_heads", _i32),
+        ("head_dim", _i32), ("dtype", _i32), ("window", _i32), ("rope_mode", _i32),
+        ("rope_dim", _i32), ("rope_scale", _f), ("rope_freqs", _p), ("q_norm", _p),
+        ("k_norm", _p), ("norm_eps", _f), ("is_gemma3", _i32), ("q", _p), ("k", _p), ("v", _p),
+        ("k_cache", _p), ("v_cache", _p), ("cache_row_stride", _i64), ("out", _p),
+        ("workspace", _p),
+    ]
+
+
 _lib = None
 
 
@@ -69,6 +80,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_decode_workspace_size.restype = ctypes.c_size_t
     L.gr_decode_attention.argtypes = [ctypes.POINTER(DecodeArgs), _p]
     L.gr_decode_attention.restype = ctypes.c_int
+    L.gr_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs)]
+    L.gr_prefill_workspace_size.restype = ctypes.c_size_t
+    L.gr_prefill_attention.argtypes = [ctypes.POINTER(PrefillArgs), _p]
+    L.gr_prefill_attention.restype = ctypes.c_int
+    L.gr_rope_freqs.argtypes = [_f, _i32, _p]
+    L.gr_rope_freqs.restype = ctypes.c_int
 
 
 def check(rc: int) -> None:

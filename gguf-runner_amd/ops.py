@@ -82,3 +82,57 @@ def decode_attention(q, k_cache, v_cache, kv_start, kv_end, *, max_kv_len=None, 
     DecodeCall(q, k_cache, v_cache, kv_start, kv_end, out, max_kv_len=max_kv_len,
                score_scale=score_scale, split_keys=split_keys)()
     return out
+
+
+def rope_freqs(theta: float, rope_dim: int) -> list[float]:
+    """Host-computed RoPE frequency table (gr_rope_freqs, inference.rs:1590-1609)."""
+    buf = (ctypes.c_float * (rope_dim // 2))()
+    ffi.check(ffi.lib().gr_rope_freqs(float(theta), int(rope_dim), ctypes.cast(buf, ctypes.c_void_p)))
+    return list(buf)
+
+
+class PrefillCall:
+    """A prepared gr_prefill_attention call.
+
+    q [m][Hq][d], k/v [m][Hkv][d] (f16 or bf16, pre-norm, pre-RoPE);
+    k_cache/v_cache [rows][Hkv][d] of the same dtype (rows >= base_pos + m);
+    out [m][Hq][d] f32.  rope_freqs is a device f32 tensor [rope_dim/2].
+    """
+
+    def __init__(self, q, k, v, k_cache, v_cache, out, *, base_pos=0, window=0,
+                 rope_mode=ffi.ROPE_NONE, rope_dim=0, rope_scale=1.0, rope_freqs=None,
+                 q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False):
+        m, n_heads, d = q.shape
+        _, n_kv, d2 = k.shape
+        assert d2 == d and v.shape == k.shape and out.shape == (m, n_heads, d)
+        assert q.dtype == k.dtype == v.dtype == k_cache.dtype == v_cache.dtype
+        assert out.dtype == torch.float32
+        for t in (q, k, v, k_cache, v_cache, out):
+            assert t.is_contiguous()
+        self._keep = (q, k, v, k_cache, v_cache, out, rope_freqs, q_norm, k_norm)
+        a = ffi.PrefillArgs()
+        a.n_tokens, a.base_pos, a.n_heads, a.n_kv_heads, a.head_dim = m, base_pos, n_heads, n_kv, d
+        a.dtype = _DT[q.dtype]
+        a.window = int(window)
+        a.rope_mode, a.rope_dim, a.rope_scale = int(rope_mode), int(rope_dim), float(rope_scale)
+        a.rope_freqs = _ptr(rope_freqs)
+        a.q_norm, a.k_norm = _ptr(q_norm), _ptr(k_norm)
+        a.norm_eps = float(norm_eps)
+        a.is_gemma3 = int(bool(is_gemma3))
+        a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
+        a.k_cache, a.v_cache = _ptr(k_cache), _ptr(v_cache)
+        a.cache_row_stride = n_kv * d
+        a.out = _ptr(out)
+        nbytes = ffi.lib().gr_prefill_workspace_size(ctypes.byref(a))
+        self.ws = _workspace(nbytes, q.device)
+        a.workspace = _aligned(self.ws)
+        self.args = a
+
+    def __call__(self, stream=None) -> None:
+        ffi.check(ffi.lib().gr_prefill_attention(ctypes.byref(self.args), _stream(stream)))
+
+
+def prefill_attention(q, k, v, k_cache, v_cache, **kw):
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    PrefillCall(q, k, v, k_cache, v_cache, out, **kw)()
+    return out

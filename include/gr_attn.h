@@ -85,6 +85,53 @@ size_t gr_decode_workspace_size(const gr_decode_args* a);
 /* Enqueue split-K flash decoding on `stream` (a hipStream_t, NULL = default). */
 int gr_decode_attention(const gr_decode_args* a, void* stream);
 
+/* ======================================================================
+ * Prefill: a chunk of m new tokens of one sequence and one layer.
+ * Replaces the serial per-token loop of transformer_prefill_batch
+ * (inference.rs:2981-3017): for each token, qkv_bias_and_norm's QK-norm
+ * (2535-2572), apply_rope_qk (1817-1874), kv_write_token (1877-1965, raw
+ * storage) and attention_token (1970-2530).  Token i sits at position
+ * base_pos + i and sees keys [start, base_pos + i] of the cache, where
+ * start = 0 (window 0, global) or base_pos + i + 1 - window (sliding window,
+ * attention.rs:74-96).  Q/K/V are pre-norm and pre-RoPE; the post-norm,
+ * post-RoPE K and V rows are written into the cache at rows base_pos ..
+ * base_pos + m - 1.  Cache rows [0, base_pos) must hold earlier tokens.
+ * ====================================================================== */
+typedef struct gr_prefill_args {
+    int32_t n_tokens;     /* m */
+    int32_t base_pos;
+    int32_t n_heads;
+    int32_t n_kv_heads;   /* n_heads % n_kv_heads == 0 */
+    int32_t head_dim;     /* 128 or 256 */
+    int32_t dtype;        /* GR_DTYPE_F16 or GR_DTYPE_BF16: q/k/v inputs and cache */
+    int32_t window;       /* 0 = global causal, W > 0 = sliding window of W keys */
+    int32_t rope_mode;    /* gr_rope_mode; GR_ROPE_ADJACENT needs rope_dim == head_dim */
+    int32_t rope_dim;     /* rotated dims per head, even, <= head_dim */
+    float rope_scale;     /* rope_scaling.global or .local of this layer (inference.rs:1502-1506) */
+    const float* rope_freqs; /* device [rope_dim/2], see gr_rope_freqs */
+    const float* q_norm;  /* device [head_dim] QK RMSNorm weights, or NULL */
+    const float* k_norm;  /* device [head_dim], or NULL */
+    float norm_eps;       /* rms_norm_eps (1e-5 when the model gives 0, inference.rs:2539-2543) */
+    int32_t is_gemma3;    /* 1: q *= 1/sqrt(head_dim) after RoPE, scores unscaled (1871-1873, 1982) */
+    const void* q;        /* [m][n_heads][head_dim] */
+    const void* k;        /* [m][n_kv_heads][head_dim] */
+    const void* v;
+    void* k_cache;        /* [>= base_pos + m][n_kv_heads][head_dim] rows of this sequence and layer */
+    void* v_cache;
+    int64_t cache_row_stride; /* elements between cache rows (>= n_kv_heads*head_dim) */
+    float* out;           /* [m][n_heads][head_dim] f32 (s.xb rows) */
+    void* workspace;      /* gr_prefill_workspace_size() bytes, 256-byte aligned */
+} gr_prefill_args;
+
+size_t gr_prefill_workspace_size(const gr_prefill_args* a);
+int gr_prefill_attention(const gr_prefill_args* a, void* stream);
+
+/* RoPE frequency table freq_i = 1 / theta^(2i / rope_dim), i < rope_dim/2, in
+ * f32 with the host libm powf, exactly as malloc_run_state builds rope_freqs
+ * (inference.rs:1590-1609).  Host memory; copy it to the device for the
+ * device-pointer entry points. */
+int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,147 @@
+"""Prefill parity: gr_prefill_attention (Q/K/V prep + MFMA flash kernel) vs the
+CPU oracle's token-serial prefill (reference inference.rs:2981-3017: QK-norm ->
+apply_rope_qk -> kv_write_token -> attention_token per token) on identical
+seeded f16/bf16 inputs.
+
+Tolerance for the f16/bf16 MFMA path (written here, fixed before measuring):
+  |gpu - ref| <= 2e-3 + 1e-2 * |ref| elementwise.
+Cache rows: V is copied bit-exactly; post-RoPE K may differ from the oracle's
+by the rounding of the 16-bit store (1 ulp), checked at 2 ulp.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _t16(bits: np.ndarray, fmt, orc, dev):
+    dt = torch.float16 if fmt == orc.F16 else torch.bfloat16
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(dt).to(dev)
+
+
+def _bits(x, fmt, orc):
+    return orc.f16_bits(x) if fmt == orc.F16 else orc.bf16_bits(x)
+
+
+def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_scale=1.0,
+          window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6):
+    from gguf_runner_amd import ffi, ops
+    rng = np.random.default_rng(seed)
+    qb = _bits(rng.standard_normal((m, n_heads, d), dtype=np.float32), fmt, orc)
+    kb = _bits(rng.standard_normal((m, n_kv, d), dtype=np.float32), fmt, orc)
+    vb = _bits(rng.standard_normal((m, n_kv, d), dtype=np.float32), fmt, orc)
+    qn = kn = None
+    if norm:
+        qn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        kn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    freqs = orc.rope_freqs(theta, d)
+    # oracle (token-serial, raw cache of the same 16-bit format)
+    ref, kc_ref, vc_ref = orc.prefill_layer(
+        orc.upcast(qb, fmt).reshape(m, -1), orc.upcast(kb, fmt).reshape(m, -1),
+        orc.upcast(vb, fmt).reshape(m, -1), n_heads=n_heads, n_kv_heads=n_kv, head_size=d,
+        seq_len=m, fmt=fmt, rope_dim=(0 if rope_mode == ffi.ROPE_NONE else d), neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs,
+        rope_scale=rope_scale, is_gemma3=is_gemma3, window=window, q_norm=qn, k_norm=kn, eps=eps,
+        n_threads=orc.env_threads())
+    # GPU
+    q, k, v = (_t16(x, fmt, orc, dev) for x in (qb, kb, vb))
+    kc = torch.zeros((m, n_kv, d), dtype=q.dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    fr = torch.tensor(ops.rope_freqs(theta, d), dtype=torch.float32, device=dev)
+    qnt = torch.from_numpy(qn).to(dev) if norm else None
+    knt = torch.from_numpy(kn).to(dev) if norm else None
+    chunks = base_chunks or [m]
+    out = torch.empty((m, n_heads, d), dtype=torch.float32, device=dev)
+    b = 0
+    for c in chunks:
+        ops.PrefillCall(q[b:b + c].contiguous(), k[b:b + c].contiguous(), v[b:b + c].contiguous(),
+                        kc, vc, out_view := torch.empty((c, n_heads, d), dtype=torch.float32,
+                                                        device=dev),
+                        base_pos=b, window=window, rope_mode=rope_mode, rope_dim=d,
+                        rope_scale=rope_scale, rope_freqs=fr, q_norm=qnt, k_norm=knt,
+                        norm_eps=eps, is_gemma3=is_gemma3)()
+        out[b:b + c] = out_view
+        b += c
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(m, -1)
+    kc_got = kc.cpu().view(torch.int16).numpy().view(np.uint16).reshape(m, -1)
+    vc_got = vc.cpu().view(torch.int16).numpy().view(np.uint16).reshape(m, -1)
+    return got, ref, (kc_got, kc_ref), (vc_got, vc_ref)
+
+
+def _assert_close(got, ref):
+    err = np.abs(got - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), f"{bad.sum()} / {bad.size} out of tolerance; max abs {err.max():.3e}"
+
+
+def _assert_cache(kc, vc, fmt, orc):
+    kg, kr = kc
+    vg, vr = vc
+    assert np.array_equal(vg, vr), "V cache rows must be copied exactly"
+    a = orc.upcast(kg, fmt)
+    b = orc.upcast(kr, fmt)
+    ulp = 2.0 ** (-10 if fmt == orc.F16 else -7)
+    assert np.all(np.abs(a - b) <= 2 * ulp * np.maximum(np.abs(b), 2.0 ** -14)), \
+        f"K cache max diff {np.abs(a - b).max():.3e}"
+
+
+def test_config2_llama3_8b_prefill_f16(orc, dev):
+    """Config 2: 32 Q / 8 KV heads, d128, 2048 tokens, f16, adjacent-pair RoPE theta 5e5
+    fused on load, causal, fp32 accumulate, output [2048, 32, 128]."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=32, n_kv=8, d=128, fmt=orc.F16, seed=1002,
+                             rope_mode=ffi.ROPE_ADJACENT, theta=5e5)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)
+
+
+@pytest.mark.parametrize("layer", ["local", "global"])
+def test_config4_gemma3_prefill_bf16(orc, dev, layer):
+    """Config 4 (reduced length): 8 Q / 4 KV heads, d256, bf16, QK RMSNorm eps 1e-6 with
+    weights ~N(1, 0.1), NeoX RoPE; local layer theta 1e4 window 1024, global layer theta 1e6
+    x 0.125; q pre-scaled by 1/16 and scores unscaled."""
+    from gguf_runner_amd import ffi
+    local = layer == "local"
+    got, ref, kc, vc = _case(orc, dev, m=2048 if local else 1280, n_heads=8, n_kv=4, d=256,
+                             fmt=orc.BF16, seed=1004, rope_mode=ffi.ROPE_NEOX,
+                             theta=1e4 if local else 1e6, rope_scale=1.0 if local else 0.125,
+                             window=1024 if local else 0, norm=True, is_gemma3=True)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.BF16, orc)
+
+
+@pytest.mark.parametrize("chunks", [[64, 64, 72], [1, 127, 129, 3], [200]])
+def test_prefill_chunked_continuation(orc, dev, chunks):
+    """Chunks continue from base_pos over the rows earlier chunks wrote (the 64-token
+    prefill chunking of generation.rs:4869-4923), ragged m, f16 NeoX RoPE."""
+    from gguf_runner_amd import ffi
+    m = sum(chunks)
+    got, ref, kc, vc = _case(orc, dev, m=m, n_heads=8, n_kv=2, d=128, fmt=orc.F16, seed=m,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6, base_chunks=chunks)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)
+
+
+@pytest.mark.parametrize("window", [1, 7, 64, 100])
+def test_prefill_small_windows(orc, dev, window):
+    """Window edge cases: W=1 attends only to itself (out == v row), W not a tile multiple."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=300, n_heads=4, n_kv=4, d=128, fmt=orc.BF16,
+                             seed=window, rope_mode=ffi.ROPE_NEOX, theta=1e4, window=window)
+    _assert_close(got, ref)
+
+
+def test_prefill_window_one_returns_v(orc, dev):
+    """W = 1: softmax over one key is exactly 1, so the output is the V row itself."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=130, n_heads=4, n_kv=2, d=128, fmt=orc.F16, seed=5,
+                             rope_mode=ffi.ROPE_NONE, theta=1e4, window=1)
+    v = orc.upcast(vc[0], orc.F16).reshape(130, 2, 128)
+    exp = np.repeat(v, 2, axis=1).reshape(130, -1)
+    assert np.array_equal(got, exp)

@@ -1,0 +1,116 @@
+"""Pins the oracle's attention_token / prefill loop against the float64 closed form
+softmax(q K^T s) V and the special cases the mathematics fixes (CPU only).
+
+Tolerance 2e-5 * max(|x|, 1): the reference's own attention-oracle tolerance
+(src/engine/multimodal/mod.rs:724-728)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+
+def _np_attention(q, K, V, scale):
+    s = (K.astype(np.float64) @ q.astype(np.float64)) * scale
+    p = np.exp(s - s.max())
+    return (p / p.sum()) @ V.astype(np.float64)
+
+
+def _tol(x):
+    return 2e-5 * np.maximum(np.abs(x), 1.0)
+
+
+@pytest.mark.parametrize("online", [False, True])
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_attention_token_closed_form_gqa(orc, online, fmt):
+    rng = np.random.default_rng(21 + fmt)
+    H, Hk, d, L = 8, 2, 64, 300
+    q = rng.standard_normal(H * d).astype(np.float32)
+    kf = rng.standard_normal((L, Hk * d)).astype(np.float32)
+    vf = rng.standard_normal((L, Hk * d)).astype(np.float32)
+    if fmt == orc.F32:
+        kc, vc = kf, vf
+    else:
+        conv = orc.f16_bits if fmt == orc.F16 else orc.bf16_bits
+        kc, vc = conv(kf), conv(vf)
+    K = orc.upcast(kc, fmt).reshape(L, Hk, d)
+    V = orc.upcast(vc, fmt).reshape(L, Hk, d)
+    s0, s1 = 17, 250
+    out = orc.attention_token(q, kc, vc, fmt, H, Hk, d, s0, s1, online=online, n_threads=4)
+    scale = 1.0 / np.sqrt(d)
+    for h in range(H):
+        g = h // (H // Hk)  # GQA: kv_head = h / kv_mul (inference.rs:2019)
+        exp = _np_attention(q[h * d:(h + 1) * d], K[s0:s1, g], V[s0:s1, g], scale)
+        assert np.all(np.abs(out[h * d:(h + 1) * d] - exp) <= _tol(exp))
+
+
+def test_attention_token_special_cases(orc):
+    rng = np.random.default_rng(4)
+    H, d, L = 2, 32, 40
+    kc = rng.standard_normal((L, H * d)).astype(np.float32)
+    vc = rng.standard_normal((L, H * d)).astype(np.float32)
+    q = rng.standard_normal(H * d).astype(np.float32)
+    # one visible key: xb == v of that key
+    out = orc.attention_token(q, kc, vc, orc.F32, H, H, d, 9, 10)
+    assert np.array_equal(out, vc[9])
+    # q == 0: uniform weights -> mean of V over the visible range
+    out0 = orc.attention_token(np.zeros_like(q), kc, vc, orc.F32, H, H, d, 0, L)
+    assert np.allclose(out0, vc.astype(np.float64).mean(axis=0), atol=2e-6)
+    # identical keys: uniform weights too
+    kc_eq = np.repeat(kc[:1], L, axis=0)
+    out_eq = orc.attention_token(q, kc_eq, vc, orc.F32, H, H, d, 0, L)
+    assert np.allclose(out_eq, vc.astype(np.float64).mean(axis=0), atol=2e-6)
+    # apply_attn_scale off (Gemma3) equals scale 1
+    a = orc.attention_token(q, kc, vc, orc.F32, H, H, d, 0, L, apply_attn_scale=False)
+    b = orc.attention_token(q, kc, vc, orc.F32, H, H, d, 0, L, attn_scale=1.0)
+    assert np.array_equal(a, b)
+
+
+def test_attention_thread_count_invariant(orc):
+    """The rayon-style parallel branch equals the serial one bit for bit."""
+    rng = np.random.default_rng(8)
+    H, Hk, d, L = 16, 8, 128, 513
+    q = rng.standard_normal(H * d).astype(np.float32)
+    kc = rng.standard_normal((L, Hk * d)).astype(np.float32)
+    vc = rng.standard_normal((L, Hk * d)).astype(np.float32)
+    a = orc.attention_token(q, kc, vc, orc.F32, H, Hk, d, 0, L, n_threads=1)
+    b = orc.attention_token(q, kc, vc, orc.F32, H, Hk, d, 0, L, n_threads=8)
+    assert np.array_equal(a, b)
+
+
+def test_prefill_layer_closed_form_window_norm_rope(orc):
+    """The token-serial prefill (norm -> RoPE -> write -> attend) against a float64
+    restatement built from numpy primitives, local window 5, NeoX, Gemma scaling."""
+    rng = np.random.default_rng(12)
+    m, H, Hk, d, W, eps = 23, 4, 2, 32, 5, 1e-6
+    q = rng.standard_normal((m, H * d)).astype(np.float32)
+    k = rng.standard_normal((m, Hk * d)).astype(np.float32)
+    v = rng.standard_normal((m, Hk * d)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    fr = orc.rope_freqs(1e4, d)
+    out, kc, vc = orc.prefill_layer(q, k, v, n_heads=H, n_kv_heads=Hk, head_size=d, seq_len=m,
+                                    fmt=orc.F32, rope_dim=d, neox=True, rope_freqs_tab=fr,
+                                    rope_scale=1.0, is_gemma3=True, window=W, q_norm=qn,
+                                    k_norm=kn, eps=eps)
+
+    def norm(x, w, nh):
+        x = x.astype(np.float64).reshape(nh, d)
+        return (w * x / np.sqrt((x ** 2).mean(axis=1, keepdims=True) + eps))
+
+    def rope(x, pos):
+        ang = pos * fr.astype(np.float64)
+        a, b = x[:, : d // 2], x[:, d // 2:]
+        return np.concatenate([a * np.cos(ang) - b * np.sin(ang),
+                               a * np.sin(ang) + b * np.cos(ang)], axis=1)
+
+    Ks = np.stack([rope(norm(k[t], kn, Hk), t) for t in range(m)])
+    Vs = v.astype(np.float64).reshape(m, Hk, d)
+    assert np.allclose(kc.reshape(m, Hk, d), Ks, atol=2e-5)
+    for t in range(m):
+        qq = rope(norm(q[t], qn, H), t) / np.sqrt(d)
+        s0 = max(0, t + 1 - W)
+        for h in range(H):
+            g = h // (H // Hk)
+            exp = _np_attention(qq[h], Ks[s0:t + 1, g], Vs[s0:t + 1, g], 1.0)
+            got = out[t, h * d:(h + 1) * d]
+            assert np.all(np.abs(got - exp) <= 5e-5 * np.maximum(np.abs(exp), 1.0))
