@@ -1,0 +1,196 @@
+"""Benchmark of the attention hot path on one MI355X (prints ONE JSON line).
+
+Headline (`value`): split-K decode attention
+(Qwen3-30B-A3B-shaped: 16 sequences with ragged cached lengths U[1024, 32768],
+32 Q / 4 KV heads, head_dim 128, f16 KV cache), in GB/s of algorithmic KV bytes
+  bytes/step = sum_b L_b * Hkv * d * 2 (K and V) * 2 B
+with every input already resident in HBM.  A step is one gr_decode_attention
+call (split kernel + combine kernel) over the whole batch.
+
+Also reported in the same line:
+  decode_32k   -- the decode target run (all 16 sequences at 32768 keys)
+  prefill      -- config 2 (Llama-3-8B-shaped causal prefill, 2048 tokens, f16,
+                  RoPE fused) and the 8k target run, in TFLOP/s with
+                  flops = 4 * Hq * d * sum_q visible(q)
+  roofline     -- the dominant kernel (decode) against 8 TB/s HBM
+  cpu_baseline -- the CPU oracle (a C restatement of the reference's
+                  attention_token, oracle/oracle.c) timed on this host's cores on
+                  the decode workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense f16)
+METRIC = "decode attn GB/s (% of 8 TB/s) + prefill attn TFLOP/s (% MFMA), 1×MI355X"
+
+
+def _timed(fn, steps, warmup, stream):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        fn()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall * 1e3 / steps  # ms per step (events, wall)
+
+
+def decode_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
+    import torch
+    from gguf_runner_amd import ops
+    n_seq = len(lens)
+    max_len = int(max(lens))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((n_seq, n_heads, d), generator=g, device=dev, dtype=torch.float32)
+    kc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    vc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    st = torch.zeros(n_seq, dtype=torch.int32, device=dev)
+    en = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    call = ops.DecodeCall(q, kc, vc, st, en, out, max_kv_len=max_len)
+    nbytes = int(sum(lens)) * n_kv * d * 2 * 2
+    return call, nbytes, (q, kc, vc, st, en, out)
+
+
+def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
+    import torch
+    from gguf_runner_amd import ffi, ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    kc = torch.empty((S, n_kv, d), device=dev, dtype=torch.float16)
+    vc = torch.empty_like(kc)
+    out = torch.empty((S, n_heads, d), device=dev, dtype=torch.float32)
+    fr = torch.tensor(ops.rope_freqs(5e5, d), dtype=torch.float32, device=dev)
+    call = ops.PrefillCall(q, k, v, kc, vc, out, rope_mode=ffi.ROPE_ADJACENT, rope_dim=d,
+                           rope_freqs=fr)
+    flops = 4 * n_heads * d * S * (S + 1) // 2
+    return call, flops, (q, k, v, kc, vc, out, fr)
+
+
+def cpu_baseline(lens, n_heads=32, n_kv=4, d=128, budget_s=10.0):
+    """Oracle attention_token on the host cores over a bounded prefix of the decode
+    batch (whole sequences, in batch order), as the reference runs it: one sequence
+    at a time, parallel over heads."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import __graft_entry__ as ge
+    orc = ge.load_oracle()
+    threads = orc.max_threads()
+    rng = np.random.default_rng(1003)
+    done_bytes = 0
+    elapsed = 0.0
+    n_done = 0
+    for L in lens:
+        kc = orc.f16_bits(rng.standard_normal((L, n_kv * d), dtype=np.float32))
+        vc = orc.f16_bits(rng.standard_normal((L, n_kv * d), dtype=np.float32))
+        q = rng.standard_normal(n_heads * d, dtype=np.float32)
+        t0 = time.perf_counter()
+        orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
+        elapsed += time.perf_counter() - t0
+        done_bytes += L * n_kv * d * 2 * 2
+        n_done += 1
+        if elapsed >= budget_s:
+            break
+    return {"value": round(done_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax) over the first "
+                      f"{n_done} of {len(lens)} config-3 sequences ({sum(lens[:n_done])} keys), "
+                      f"{elapsed:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the attention path shards without communication (see DESIGN.md), "
+              "so no multi-GPU figure is produced", file=sys.stderr)
+        return 2
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import __graft_entry__ as ge
+    ge.load_package()
+    import torch
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+
+    rng = np.random.default_rng(1003)
+    lens = rng.integers(1024, 32768, size=16, endpoint=True).tolist()
+
+    # headline: config 3 decode (ragged)
+    dcall, dbytes, _keep_d = decode_workload(dev, lens, 3)
+    dec_ms, dec_wall = _timed(dcall, args.steps, args.warmup, stream)
+    dec_gbs = dbytes / (dec_ms * 1e-3) / 1e9
+    del _keep_d, dcall
+
+    # decode target run: all sequences at 32768 keys
+    tcall, tbytes, _keep_t = decode_workload(dev, [32768] * 16, 33)
+    t_ms, _ = _timed(tcall, args.steps, args.warmup, stream)
+    t_gbs = tbytes / (t_ms * 1e-3) / 1e9
+    del _keep_t, tcall
+
+    pre = {}
+    for S, seed in ((2048, 2), (8192, 8)):
+        pcall, flops, _keep_p = prefill_workload(dev, S, seed)
+        p_ms, _ = _timed(pcall, max(5, args.steps // 5), 2, stream)
+        tf = flops / (p_ms * 1e-3) / 1e12
+        pre[f"S{S}"] = {"tflops": round(tf, 2), "ms": round(p_ms, 4),
+                        "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                        "gflop": round(flops / 1e9, 3)}
+        del _keep_p, pcall
+
+    line = {
+        "metric": METRIC,
+        "value": round(dec_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, no checkpoint)",
+        "config": {"workload": "config 3: Qwen3-30B-A3B-shaped split-K decode, 16 seqs, ragged "
+                               "L~U[1024,32768] (seed 1003), 32 Q / 4 KV heads, d128, f16 KV",
+                   "seq_lens_sum": int(sum(lens)), "bytes_per_step": dbytes},
+        "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gr_decode_attention (split kernel + combine), hipEvent-timed"},
+        "decode_32k": {"gbs": round(t_gbs, 2), "ms": round(t_ms, 5),
+                       "frac_of_hbm": round(t_gbs / HBM_PEAK_GBS, 4), "bytes": tbytes},
+        "prefill": pre,
+        "wall_ms_per_step": round(dec_wall, 5),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(lens)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

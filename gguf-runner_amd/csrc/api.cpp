@@ -74,8 +74,11 @@ int check_decode(const gr_decode_args* a) {
         return fail(GR_ERR_ARG, "gr_decode_attention: n_heads %d not a multiple of n_kv_heads %d",
                     a->n_heads, a->n_kv_heads);
     const int kv_mul = a->n_heads / a->n_kv_heads;
-    if (kv_mul != 1 && kv_mul != 2 && kv_mul != 4 && kv_mul != 8)
-        return fail(GR_ERR_ARG, "gr_decode_attention: kv_mul %d unsupported (1,2,4,8)", kv_mul);
+    const bool pow2 = kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 8;
+    if (a->kv_dtype == GR_DTYPE_F32 ? !pow2 : (kv_mul > 16 || (a->head_dim == 64 && !pow2)))
+        return fail(GR_ERR_ARG,
+                    "gr_decode_attention: kv_mul %d unsupported (f32 KV: 1,2,4,8; 16-bit KV: <= 16)",
+                    kv_mul);
     if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
         return fail(GR_ERR_ARG, "gr_decode_attention: head_dim %d unsupported (64,128,256)",
                     a->head_dim);
@@ -123,6 +126,7 @@ int decode_enqueue(const gr_decode_args* a, hipStream_t st) {
     p.out = a->out;
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
+    p.use_mfma = 1;
     hipError_t e = launch_decode(p, st);
     if (e != hipSuccess) return hip_fail(e, "gr_decode_attention launch");
     return GR_OK;

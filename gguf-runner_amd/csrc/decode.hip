@@ -246,8 +246,23 @@ static hipError_t launch_dim(const DecodeLaunch& p, int kv_mul, hipStream_t st) 
     }
 }
 
+template <int D>
+static hipError_t launch_combine(const DecodeLaunch& p, hipStream_t st) {
+    decode_combine_kernel<D><<<dim3(p.n_heads, p.n_seq), D, 0, st>>>(p);
+    return hipGetLastError();
+}
+
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
+    if (p.use_mfma && decode_mfma_supported(p)) {
+        hipError_t e = launch_decode_mfma_split(p, st);
+        if (e != hipSuccess) return e;
+        switch (p.head_dim) {
+            case 128: return launch_combine<128>(p, st);
+            case 256: return launch_combine<256>(p, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (p.kv_dtype) {
         case GR_DTYPE_F32: return launch_dim<F32>(p, kv_mul, st);
         case GR_DTYPE_F16: return launch_dim<F16>(p, kv_mul, st);

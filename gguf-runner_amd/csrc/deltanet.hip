@@ -1,0 +1,404 @@
+// Gated DeltaNet (gated delta rule) on gfx950, fp32 state [H][d][d], S[j][i]
+// with j = key dim (row) and i = value dim (column), as in
+// qwen3next_state_head_step (reference src/engine/kernels/math.rs:492-546):
+//   S *= g;  kv_i = sum_j k_j S[j][i];  delta_i = beta (v_i - kv_i);
+//   S[j][i] += k_j delta_i;  o_i = sum_j q_j S[j][i]
+// q/k are optionally L2-normalised first (q also * 1/sqrt(d)), math.rs:833-846.
+// Columns i are independent, which is how both kernels parallelise.
+//
+// 1. deltanet_step_kernel: the recurrence token by token with a 32-column
+//    slice of the state in registers (decode, and the serial scan).
+// 2. Chunked prefill (chunk C = 64), WY form of the same recurrence:
+//      gamma_t = prod_{s<=t} g_s (in-chunk),  A[t][s] = beta_t (gamma_t/gamma_s) k_t.k_s (s<t)
+//      Delta = (I + A)^-1 [beta V - beta gamma K S0] = U - W S0
+//      O     = diag(gamma) Q S0 + (Gamma-mask . Q K^T) Delta
+//      S_C   = gamma_last S0 + Kd^T Delta,  Kd_s = (gamma_last/gamma_s) k_s
+//    deltanet_chunk_prep_kernel builds U, W, P, Qg, Kd^T per (chunk, head) in
+//    parallel; deltanet_chunk_scan_kernel carries S across chunks with the
+//    state columns split over blocks.
+#include "gr_common.hpp"
+#include "gr_internal.hpp"
+
+namespace gr {
+
+__device__ __forceinline__ float dn_load(const void* p, size_t i, int dt) {
+    if (dt == GR_DTYPE_F32) return ((const float*)p)[i];
+    const uint16_t b = ((const uint16_t*)p)[i];
+    return dt == GR_DTYPE_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+}
+
+// ------------------------------------------------------------------ recurrent step
+constexpr int kStepThreads = 256;
+constexpr int kStepCols = 32;
+
+template <int D>
+__global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const DeltaNetLaunch p) {
+    constexpr int NJG = kStepThreads / kStepCols;  // 8 row groups
+    constexpr int R = D / NJG;                     // rows per thread
+    __shared__ float qs[D], ks[D];
+    __shared__ float red[kStepThreads / 64][kStepCols];
+    const int tid = threadIdx.x;
+    const int ci = tid % kStepCols;
+    const int jg = tid / kStepCols;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int h = blockIdx.y;
+    const int i = blockIdx.x * kStepCols + ci;
+    const int H = p.n_heads;
+    float* Sh = p.state + (size_t)h * D * D;
+
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = Sh[(size_t)(jg * R + r) * D + i];
+
+    const float inv_scale_q = 1.0f / sqrtf((float)D);
+    for (int t = 0; t < p.n_tokens; t++) {
+        const size_t row = ((size_t)t * H + h) * D;
+        if (wave < 2) {
+            const void* src = wave == 0 ? p.q : p.k;
+            float x[D / 64];
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < D / 64; e++) {
+                x[e] = dn_load(src, row + lane + 64 * e, p.in_dtype);
+                ss += x[e] * x[e];
+            }
+            float* dst = wave == 0 ? qs : ks;
+            if (p.l2norm) {
+                ss = wave_sum<64>(ss);
+                const float inv = 1.0f / sqrtf(ss + p.eps);
+#pragma unroll
+                for (int e = 0; e < D / 64; e++)
+                    dst[lane + 64 * e] = finite_or_zero(wave == 0 ? x[e] * inv * inv_scale_q : x[e] * inv);
+            } else {
+#pragma unroll
+                for (int e = 0; e < D / 64; e++) dst[lane + 64 * e] = x[e];
+            }
+        }
+        const float g = finite_or_zero(expf(p.gate[(size_t)t * H + h]));
+        const float beta = finite_or_zero(p.beta[(size_t)t * H + h]);
+        const float vi = finite_or_zero(dn_load(p.v, row + i, p.in_dtype));
+        __syncthreads();
+        float part = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            s[r] *= g;
+            const float kj = ks[jg * R + r];
+            if (kj != 0.0f) part = fmaf(kj, s[r], part);
+        }
+        part += shfl_xor(part, 32);
+        if (lane < 32) red[wave][ci] = part;
+        __syncthreads();
+        float kv = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kStepThreads / 64; w++) kv += red[w][ci];
+        kv = finite_or_zero(kv);
+        const float delta = finite_or_zero((vi - kv) * beta);
+        float po = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float kj = ks[jg * R + r];
+            if (kj != 0.0f) s[r] = fmaf(kj, delta, s[r]);
+            const float qj = qs[jg * R + r];
+            if (qj != 0.0f) po = fmaf(qj, s[r], po);
+        }
+        po += shfl_xor(po, 32);
+        __syncthreads();
+        if (lane < 32) red[wave][ci] = po;
+        __syncthreads();
+        if (tid < kStepCols) {
+            float o = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kStepThreads / 64; w++) o += red[w][ci];
+            p.out[row + i] = finite_or_zero(o);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) Sh[(size_t)(jg * R + r) * D + i] = s[r];
+}
+
+// ------------------------------------------------------------------ chunked prefill
+constexpr int kChunk = 64;
+constexpr int kChunkThreads = 256;
+
+// Per (chunk, head) workspace block, floats: U, W, Qg [C][D]; KdT [D][C]; P [C][C]; gamma_last.
+template <int D>
+struct ChunkWs {
+    static constexpr size_t U = 0;
+    static constexpr size_t W = U + (size_t)kChunk * D;
+    static constexpr size_t QG = W + (size_t)kChunk * D;
+    static constexpr size_t KDT = QG + (size_t)kChunk * D;
+    static constexpr size_t P = KDT + (size_t)D * kChunk;
+    static constexpr size_t GL = P + (size_t)kChunk * kChunk;
+    static constexpr size_t SIZE = (GL + 1 + 63) / 64 * 64;
+};
+
+template <int D>
+__global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(const DeltaNetLaunch p) {
+    constexpr int C = kChunk;
+    constexpr int DS = D + 4;  // padded LDS row stride
+    extern __shared__ float smem[];
+    float* qs = smem;                   // [C][DS] normalised q
+    float* ks = qs + C * DS;            // [C][DS] normalised k
+    float* As = ks + C * DS;            // [C][C+1]
+    float* Ts = As + C * (C + 1);       // [C][C+1] (I + A)^-1
+    float* lg = Ts + C * (C + 1);       // [C] in-chunk cumulative log decay
+    float* bt = lg + C;                 // [C] beta
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int H = p.n_heads;
+    const int t0 = c * C;
+    const int Cn = min(C, p.n_tokens - t0);  // tokens in this chunk
+    float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
+
+    // 1. normalised q, k rows (zero rows past the end of the sequence)
+    const float inv_scale_q = 1.0f / sqrtf((float)D);
+    for (int r = wave; r < 2 * C; r += kChunkThreads / 64) {
+        const int t = r % C;
+        const bool isq = r < C;
+        float x[D / 64];
+        float ss = 0.0f;
+        const bool valid = t < Cn;
+        const size_t row = ((size_t)(t0 + t) * H + h) * D;
+#pragma unroll
+        for (int e = 0; e < D / 64; e++) {
+            x[e] = valid ? dn_load(isq ? p.q : p.k, row + lane + 64 * e, p.in_dtype) : 0.0f;
+            ss += x[e] * x[e];
+        }
+        float* dst = (isq ? qs : ks) + t * DS;
+        if (p.l2norm) {
+            ss = wave_sum<64>(ss);
+            const float inv = 1.0f / sqrtf(ss + p.eps);
+#pragma unroll
+            for (int e = 0; e < D / 64; e++)
+                dst[lane + 64 * e] = valid ? finite_or_zero(isq ? x[e] * inv * inv_scale_q : x[e] * inv) : 0.0f;
+        } else {
+#pragma unroll
+            for (int e = 0; e < D / 64; e++) dst[lane + 64 * e] = x[e];
+        }
+    }
+    // in-chunk cumulative log decay (inclusive) and beta; padded tokens: gate 0, beta 0
+    if (wave == 0) {
+        const bool valid = lane < Cn;
+        float gl = valid ? p.gate[(size_t)(t0 + lane) * H + h] : 0.0f;
+        // inclusive prefix sum over the 64 lanes
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_up(gl, off, 64);
+            if (lane >= off) gl += o;
+        }
+        lg[lane] = gl;
+        bt[lane] = valid ? finite_or_zero(p.beta[(size_t)(t0 + lane) * H + h]) : 0.0f;
+    }
+    __syncthreads();
+
+    // 2. A (LDS) and P (workspace): thread -> row t, 16 columns s
+    {
+        const int t = tid >> 2;
+        const int sb = (tid & 3) * 16;
+        float akk[16], aqk[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) akk[u] = aqk[u] = 0.0f;
+        for (int j = 0; j < D; j += 4) {
+            const float4 kt = *(const float4*)(ks + t * DS + j);
+            const float4 qt = *(const float4*)(qs + t * DS + j);
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const float4 kk = *(const float4*)(ks + (sb + u) * DS + j);
+                akk[u] = fmaf(kt.x, kk.x, fmaf(kt.y, kk.y, fmaf(kt.z, kk.z, fmaf(kt.w, kk.w, akk[u]))));
+                aqk[u] = fmaf(qt.x, kk.x, fmaf(qt.y, kk.y, fmaf(qt.z, kk.z, fmaf(qt.w, kk.w, aqk[u]))));
+            }
+        }
+        const float lt = lg[t];
+        const float bet = bt[t];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int s = sb + u;
+            const float decay = s <= t ? expf(lt - lg[s]) : 0.0f;
+            As[t * (C + 1) + s] = s < t ? bet * decay * akk[u] : 0.0f;
+            ws[ChunkWs<D>::P + t * C + s] = s <= t ? decay * aqk[u] : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // 3. T = (I + A)^-1 (unit lower triangular) by forward substitution, one
+    //    column per lane of wave 0, kept in LDS; waves 1-3 meanwhile write
+    //    Qg = gamma_t q_t and Kd^T[j][s] = (gamma_last / gamma_s) k_s[j].
+    const float lglast = lg[C - 1];
+    if (wave == 0) {
+        const int cc = lane;
+        for (int t = 0; t < C; t++) {
+            float acc = t == cc ? 1.0f : 0.0f;
+            for (int s2 = cc; s2 < t; s2++) acc = fmaf(-As[t * (C + 1) + s2], Ts[s2 * (C + 1) + cc], acc);
+            Ts[t * (C + 1) + cc] = t >= cc ? acc : 0.0f;
+        }
+    } else {
+        for (int e = tid - 64; e < C * D; e += kChunkThreads - 64) {
+            const int t = e / D, j = e % D;
+            ws[ChunkWs<D>::QG + e] = expf(lg[t]) * qs[t * DS + j];
+        }
+        for (int e = tid - 64; e < D * C; e += kChunkThreads - 64) {
+            const int j = e / C, s2 = e % C;
+            ws[ChunkWs<D>::KDT + e] = expf(lglast - lg[s2]) * ks[s2 * DS + j];
+        }
+    }
+    __syncthreads();
+
+    // 4. [U | W] = T [beta V | beta gamma K]: one right-hand-side column per thread,
+    //    rows in groups of 8 accumulators.
+    for (int col = tid; col < 2 * D; col += kChunkThreads) {
+        const bool isv = col < D;
+        const int cc = isv ? col : col - D;
+        float* dst = ws + (isv ? ChunkWs<D>::U : ChunkWs<D>::W);
+        for (int tb = 0; tb < C; tb += 8) {
+            float x8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) x8[u] = 0.0f;
+            for (int s2 = 0; s2 < tb + 8; s2++) {
+                float r;
+                if (isv)
+                    r = s2 < Cn ? bt[s2] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + s2) * H + h) * D + cc, p.in_dtype))
+                                : 0.0f;
+                else
+                    r = bt[s2] * expf(lg[s2]) * ks[s2 * DS + cc];
+#pragma unroll
+                for (int u = 0; u < 8; u++) x8[u] = fmaf(Ts[(tb + u) * (C + 1) + s2], r, x8[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) dst[(tb + u) * D + cc] = x8[u];
+        }
+    }
+    if (tid == 0) ws[ChunkWs<D>::GL] = expf(lglast);
+}
+
+constexpr int kScanCols = 16;
+
+template <int D>
+__global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(const DeltaNetLaunch p) {
+    constexpr int C = kChunk;
+    constexpr int NC = kScanCols;
+    __shared__ __attribute__((aligned(16))) float Ss[D][NC];
+    __shared__ __attribute__((aligned(16))) float Dl[C][NC];
+    const int tid = threadIdx.x;
+    const int h = blockIdx.y;
+    const int c0 = blockIdx.x * NC;
+    const int H = p.n_heads;
+    float* Sh = p.state + (size_t)h * D * D;
+    for (int e = tid; e < D * NC; e += kChunkThreads) Ss[e / NC][e % NC] = Sh[(size_t)(e / NC) * D + c0 + e % NC];
+    __syncthreads();
+
+    const int n_chunks = (p.n_tokens + C - 1) / C;
+    const int ta = tid >> 2;          // phase A/B: row t
+    const int ia = (tid & 3) * 4;     //            4 columns
+    const int jc = tid >> 1;          // phase C: state row j (D = 128 rows over 256 threads / 2)
+    const int ic = (tid & 1) * (NC / 2);
+    for (int c = 0; c < n_chunks; c++) {
+        const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
+        // A: Delta[t][i] = U[t][i] - sum_j W[t][j] S[j][i]
+        {
+            float4 acc = *(const float4*)(ws + ChunkWs<D>::U + ta * D + c0 + ia);
+            const float* wr = ws + ChunkWs<D>::W + ta * D;
+            for (int j = 0; j < D; j += 4) {
+                const float4 w4 = *(const float4*)(wr + j);
+                const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 sv = *(const float4*)&Ss[j + u][ia];
+                    acc.x = fmaf(-wv[u], sv.x, acc.x);
+                    acc.y = fmaf(-wv[u], sv.y, acc.y);
+                    acc.z = fmaf(-wv[u], sv.z, acc.z);
+                    acc.w = fmaf(-wv[u], sv.w, acc.w);
+                }
+            }
+            *(float4*)&Dl[ta][ia] = acc;
+        }
+        __syncthreads();
+        // B: O[t][i] = sum_j Qg[t][j] S[j][i] + sum_{s<=t} P[t][s] Delta[s][i]
+        {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float* qr = ws + ChunkWs<D>::QG + ta * D;
+            for (int j = 0; j < D; j += 4) {
+                const float4 q4 = *(const float4*)(qr + j);
+                const float qv[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 sv = *(const float4*)&Ss[j + u][ia];
+                    acc.x = fmaf(qv[u], sv.x, acc.x);
+                    acc.y = fmaf(qv[u], sv.y, acc.y);
+                    acc.z = fmaf(qv[u], sv.z, acc.z);
+                    acc.w = fmaf(qv[u], sv.w, acc.w);
+                }
+            }
+            const float* pr = ws + ChunkWs<D>::P + ta * C;
+            for (int s = 0; s <= ta; s++) {
+                const float pv = pr[s];
+                const float4 dv = *(const float4*)&Dl[s][ia];
+                acc.x = fmaf(pv, dv.x, acc.x);
+                acc.y = fmaf(pv, dv.y, acc.y);
+                acc.z = fmaf(pv, dv.z, acc.z);
+                acc.w = fmaf(pv, dv.w, acc.w);
+            }
+            const int t = c * C + ta;
+            if (t < p.n_tokens) {
+                float* o = p.out + ((size_t)t * H + h) * D + c0 + ia;
+                o[0] = finite_or_zero(acc.x);
+                o[1] = finite_or_zero(acc.y);
+                o[2] = finite_or_zero(acc.z);
+                o[3] = finite_or_zero(acc.w);
+            }
+        }
+        // C: S'[j][i] = gamma_last S[j][i] + sum_s KdT[j][s] Delta[s][i]
+        float nv[NC / 2];
+        {
+            const float gl = ws[ChunkWs<D>::GL];
+#pragma unroll
+            for (int u = 0; u < NC / 2; u++) nv[u] = gl * Ss[jc][ic + u];
+            const float* kr = ws + ChunkWs<D>::KDT + jc * C;
+            for (int s = 0; s < C; s += 4) {
+                const float4 k4 = *(const float4*)(kr + s);
+                const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+#pragma unroll
+                    for (int u = 0; u < NC / 2; u++) nv[u] = fmaf(kv[w], Dl[s + w][ic + u], nv[u]);
+            }
+        }
+        __syncthreads();  // every read of Ss / Dl for this chunk is done
+#pragma unroll
+        for (int u = 0; u < NC / 2; u++) Ss[jc][ic + u] = nv[u];
+        __syncthreads();
+    }
+    for (int e = tid; e < D * NC; e += kChunkThreads) Sh[(size_t)(e / NC) * D + c0 + e % NC] = Ss[e / NC][e % NC];
+}
+
+size_t deltanet_chunked_ws_bytes(int n_tokens, int n_heads, int head_dim, int chunk) {
+    if (head_dim != 128 || chunk != kChunk) return 0;
+    const size_t n_chunks = (size_t)(n_tokens + kChunk - 1) / kChunk;
+    return n_chunks * n_heads * ChunkWs<128>::SIZE * sizeof(float);
+}
+
+hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st) {
+    if (p.n_tokens <= 0) return hipSuccess;
+    if (p.head_dim != 128) return hipErrorInvalidValue;
+    dim3 grid(128 / kStepCols, p.n_heads);
+    deltanet_step_kernel<128><<<grid, kStepThreads, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
+    if (p.n_tokens <= 0) return hipSuccess;
+    if (p.head_dim != 128) return hipErrorInvalidValue;
+    constexpr int D = 128;
+    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + 2 * kChunk * (kChunk + 1) + 2 * kChunk) * sizeof(float);
+    hipError_t ea = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (ea != hipSuccess) return ea;
+    const int n_chunks = (p.n_tokens + kChunk - 1) / kChunk;
+    deltanet_chunk_prep_kernel<D><<<dim3(n_chunks, p.n_heads), kChunkThreads, lds, st>>>(p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    deltanet_chunk_scan_kernel<D><<<dim3(D / kScanCols, p.n_heads), kChunkThreads, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace gr

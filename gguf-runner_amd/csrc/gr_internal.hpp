@@ -21,9 +21,12 @@ struct DecodeLaunch {
     float* out;
     float* ws_o;
     float* ws_ml;
+    int use_mfma;  // 16-bit caches: MFMA split kernel (decode_mfma.hip) instead of VALU
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);
+bool decode_mfma_supported(const DecodeLaunch& p);
+hipError_t launch_decode_mfma_split(const DecodeLaunch& p, hipStream_t st);
 
 // Per-token Q/K/V preparation: optional QK RMSNorm (math.rs:164-184), RoPE
 // (inference.rs:1817-1874), Gemma q scale, then

@@ -56,6 +56,16 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class DeltaNetArgs(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", _i32), ("n_heads", _i32), ("head_dim", _i32), ("in_dtype", _i32),
+        ("l2norm", _i32), ("algo", _i32), ("eps", _f), ("q", _p), ("k", _p), ("v", _p),
+        ("gate", _p), ("beta", _p), ("state", _p), ("out", _p), ("workspace", _p),
+    ]
+
+
+DELTANET_AUTO, DELTANET_RECURRENT, DELTANET_CHUNKED = 0, 1, 2
+
 _lib = None
 
 
@@ -86,6 +96,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_prefill_attention.restype = ctypes.c_int
     L.gr_rope_freqs.argtypes = [_f, _i32, _p]
     L.gr_rope_freqs.restype = ctypes.c_int
+    L.gr_deltanet_workspace_size.argtypes = [ctypes.POINTER(DeltaNetArgs)]
+    L.gr_deltanet_workspace_size.restype = ctypes.c_size_t
+    L.gr_deltanet_attention.argtypes = [ctypes.POINTER(DeltaNetArgs), _p]
+    L.gr_deltanet_attention.restype = ctypes.c_int
 
 
 def check(rc: int) -> None:

@@ -136,3 +136,37 @@ def prefill_attention(q, k, v, k_cache, v_cache, **kw):
     out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     PrefillCall(q, k, v, k_cache, v_cache, out, **kw)()
     return out
+
+
+class DeltaNetCall:
+    """A prepared gr_deltanet_attention call.
+
+    q/k/v [T][H][d] (f32/f16/bf16); gate/beta [T][H] f32; state [H][d][d] f32
+    (updated in place); out [T][H][d] f32.
+    """
+
+    def __init__(self, q, k, v, gate, beta, state, out, *, l2norm=True, eps=1e-6,
+                 algo=ffi.DELTANET_AUTO):
+        T, H, d = q.shape
+        assert k.shape == v.shape == q.shape and q.dtype == k.dtype == v.dtype
+        assert gate.shape == beta.shape == (T, H) and gate.dtype == beta.dtype == torch.float32
+        assert state.shape == (H, d, d) and state.dtype == torch.float32
+        assert out.shape == (T, H, d) and out.dtype == torch.float32
+        for t in (q, k, v, gate, beta, state, out):
+            assert t.is_contiguous()
+        self._keep = (q, k, v, gate, beta, state, out)
+        a = ffi.DeltaNetArgs()
+        a.n_tokens, a.n_heads, a.head_dim = T, H, d
+        a.in_dtype = _DT[q.dtype]
+        a.l2norm = int(bool(l2norm))
+        a.algo = int(algo)
+        a.eps = float(eps)
+        a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
+        a.gate, a.beta, a.state, a.out = _ptr(gate), _ptr(beta), _ptr(state), _ptr(out)
+        nbytes = ffi.lib().gr_deltanet_workspace_size(ctypes.byref(a))
+        self.ws = _workspace(nbytes, q.device) if nbytes else None
+        a.workspace = _aligned(self.ws) if nbytes else None
+        self.args = a
+
+    def __call__(self, stream=None) -> None:
+        ffi.check(ffi.lib().gr_deltanet_attention(ctypes.byref(self.args), _stream(stream)))

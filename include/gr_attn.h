@@ -132,6 +132,43 @@ int gr_prefill_attention(const gr_prefill_args* a, void* stream);
  * device-pointer entry points. */
 int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out);
 
+/* ======================================================================
+ * Gated DeltaNet linear attention (Qwen3-Next / Qwen3.5 SSM layers).
+ * Per value head h and token t, with state S[h] (f32 [d][d], S[j][i]):
+ *   S *= exp(gate); kv = S^T k; delta = beta (v - kv); S += k delta^T; o = S^T q
+ * = qwen3next_state_head_step (src/engine/kernels/math.rs:492-546) applied over
+ * heads (math.rs:890-934) and tokens (the serial scan inference.rs:2866-2885).
+ * With l2norm = 1 the per-head normalisation of math.rs:833-846 is fused:
+ * q <- q / sqrt(sum q^2 + eps) / sqrt(d), k <- k / sqrt(sum k^2 + eps).
+ * q/k/v are the per-value-head rows (after the K->V head tiling, math.rs:826).
+ * ====================================================================== */
+typedef enum gr_deltanet_algo {
+    GR_DELTANET_AUTO = 0,      /* chunked for n_tokens >= 64, recurrent otherwise */
+    GR_DELTANET_RECURRENT = 1, /* token by token, state slice in registers */
+    GR_DELTANET_CHUNKED = 2    /* chunks of 64 tokens (WY form); finite inputs assumed */
+} gr_deltanet_algo;
+
+typedef struct gr_deltanet_args {
+    int32_t n_tokens;     /* T */
+    int32_t n_heads;      /* value heads H */
+    int32_t head_dim;     /* 128 */
+    int32_t in_dtype;     /* gr_dtype of q/k/v */
+    int32_t l2norm;       /* 1: fuse the q/k normalisation above */
+    int32_t algo;         /* gr_deltanet_algo */
+    float eps;            /* normalisation epsilon (rms_norm_eps) */
+    const void* q;        /* [T][H][head_dim] */
+    const void* k;
+    const void* v;
+    const float* gate;    /* [T][H] log decay: g = exp(gate) (math.rs:869-874) */
+    const float* beta;    /* [T][H] sigmoid-ed beta (math.rs:862) */
+    float* state;         /* [H][head_dim][head_dim] f32, updated in place */
+    float* out;           /* [T][H][head_dim] f32 (ssm_proj before the gated norm) */
+    void* workspace;      /* gr_deltanet_workspace_size() bytes (0 for recurrent), 256-aligned */
+} gr_deltanet_args;
+
+size_t gr_deltanet_workspace_size(const gr_deltanet_args* a);
+int gr_deltanet_attention(const gr_deltanet_args* a, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,3 +132,23 @@ def test_decode_windowed_ragged_bf16(orc, dev):
     got, ref = _run_case(orc, dev, n_heads=16, n_kv=4, d=128, starts=starts, ends=ends,
                          seq_len=5024, fmt=orc.BF16, seed=99)
     _assert_close(got, ref, orc.BF16, orc)
+
+
+@pytest.mark.parametrize("fmt_name", ["f16", "bf16"])
+@pytest.mark.parametrize("L,n_heads,n_kv", [(1, 16, 1), (31, 4, 2), (32, 12, 1), (33, 8, 8),
+                                             (129, 16, 4), (4097, 32, 4)])
+def test_decode_16bit_mfma_shapes(orc, dev, fmt_name, L, n_heads, n_kv):
+    """The MFMA split kernel (16-bit caches): tile tails, kv_mul 1..16 (incl. 12),
+    head_dim 128."""
+    fmt = orc.F16 if fmt_name == "f16" else orc.BF16
+    got, ref = _run_case(orc, dev, n_heads=n_heads, n_kv=n_kv, d=128, starts=[0], ends=[L],
+                         seq_len=L, fmt=fmt, seed=L + n_heads)
+    _assert_close(got, ref, fmt, orc)
+
+
+@pytest.mark.parametrize("fmt_name", ["f16", "bf16"])
+def test_decode_16bit_d256_window(orc, dev, fmt_name):
+    fmt = orc.F16 if fmt_name == "f16" else orc.BF16
+    got, ref = _run_case(orc, dev, n_heads=8, n_kv=4, d=256, starts=[3, 0], ends=[1500, 77],
+                         seq_len=1500, fmt=fmt, seed=256, score_scale=1.0)
+    _assert_close(got, ref, fmt, orc)
