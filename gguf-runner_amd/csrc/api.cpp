@@ -103,7 +103,10 @@ int check_decode(const gr_decode_args* a) {
 
 }  // namespace
 
-int decode_enqueue(const gr_decode_args* a, hipStream_t st) {
+int decode_enqueue(const gr_decode_args* a, hipStream_t st) { return decode_enqueue_ex(a, nullptr, st); }
+
+// seq_slot: optional device map from batch entry to cache sequence slot.
+int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st) {
     int rc = check_decode(a);
     if (rc) return rc;
     const DecodePlan pl = plan_decode(a);
@@ -123,6 +126,7 @@ int decode_enqueue(const gr_decode_args* a, hipStream_t st) {
     p.row_stride = a->row_stride;
     p.kv_start = a->kv_start;
     p.kv_end = a->kv_end;
+    p.seq_slot = seq_slot;
     p.out = a->out;
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);

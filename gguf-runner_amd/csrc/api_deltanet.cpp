@@ -57,6 +57,7 @@ int deltanet_enqueue(const gr_deltanet_args* a, hipStream_t st) {
     p.out = a->out;
     p.ws = (float*)a->workspace;
     p.chunk = 64;
+    p.gate_is_log = 1;
     hipError_t e = use_chunked(a) ? launch_deltanet_chunked(p, st) : launch_deltanet_scan(p, st);
     if (e != hipSuccess) return hip_fail(e, "gr_deltanet_attention launch");
     return GR_OK;

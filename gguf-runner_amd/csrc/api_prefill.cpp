@@ -61,7 +61,9 @@ size_t prefill_ws_total(const gr_prefill_args* a) {
 
 }  // namespace
 
-int prefill_enqueue(const gr_prefill_args* a, hipStream_t st) {
+// in_dtype: element type of a->q / a->k / a->v (the public entry point uses
+// a->dtype; the run-state path stages the reference's f32 rows directly).
+int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     int rc = check_prefill(a);
     if (rc) return rc;
     if (a->n_tokens == 0) return GR_OK;
@@ -72,7 +74,7 @@ int prefill_enqueue(const gr_prefill_args* a, hipStream_t st) {
     pp.n_heads = a->n_heads;
     pp.n_kv_heads = a->n_kv_heads;
     pp.head_dim = a->head_dim;
-    pp.in_dtype = a->dtype;
+    pp.in_dtype = in_dtype;
     pp.pos = nullptr;
     pp.pos0 = a->base_pos;
     pp.rope_mode = a->rope_mode;
@@ -144,7 +146,7 @@ size_t gr_prefill_workspace_size(const gr_prefill_args* a) { return gr::prefill_
 
 int gr_prefill_attention(const gr_prefill_args* a, void* stream) {
     gr::clear_error();
-    return gr::prefill_enqueue(a, (hipStream_t)stream);
+    return gr::prefill_enqueue_ex(a, a ? a->dtype : 0, (hipStream_t)stream);
 }
 
 int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out) {

@@ -1,0 +1,713 @@
+// Run-state entry points: the device-resident counterpart of the reference's
+// RunState (src/engine/types.rs:745-809) and the functions that read and
+// write it.  Each entry point takes the reference's host f32 rows, stages them
+// on the state's stream, runs the kernels and returns once the results are
+// back in host memory (the Rust call sites are synchronous).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "gr_api_util.hpp"
+#include "gr_attn.h"
+#include "gr_internal.hpp"
+
+struct gr_run_state {
+    gr_attn_config cfg{};
+    std::vector<int32_t> windows;      // [n_layers], 0 = global
+    std::vector<uint8_t> norm_present;  // [n_layers]
+    bool has_norm = false;
+    int device = 0;
+    int d = 0, kv_dim = 0, q_dim = 0, rope_dim = 0;
+    float eps = 1e-5f;
+    hipStream_t stream = nullptr;
+    void* k_cache = nullptr;
+    void* v_cache = nullptr;
+    size_t seq_stride = 0;    // elements between sequence slots
+    size_t layer_stride = 0;  // elements between layers
+    float* freqs = nullptr;
+    float* freqs_swa = nullptr;
+    float* qn = nullptr;
+    float* kn = nullptr;
+    float* ssm = nullptr;
+    size_t ssm_layer = 0;  // floats per layer
+    void* stage = nullptr;
+    size_t stage_bytes = 0;
+};
+
+namespace gr {
+
+namespace {
+
+int elem_bytes(int dt) { return dt == GR_DTYPE_F32 ? 4 : 2; }
+
+// RAII: make the state's device current for the duration of a call.
+struct DeviceScope {
+    int prev = -1;
+    explicit DeviceScope(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceScope() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Staging arena: grows (never shrinks) and is carved per call.
+struct Carve {
+    char* base;
+    size_t off = 0;
+    explicit Carve(void* b) : base((char*)b) {}
+    template <typename T>
+    T* take(size_t n) {
+        T* p = (T*)(base + off);
+        off = align_up(off + n * sizeof(T), 256);
+        return p;
+    }
+};
+
+int ensure_stage(gr_run_state* s, size_t bytes) {
+    if (bytes <= s->stage_bytes) return GR_OK;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "staging resize sync");
+    if (s->stage) (void)hipFree(s->stage);
+    s->stage = nullptr;
+    s->stage_bytes = 0;
+    const size_t want = align_up(bytes + bytes / 4, 1 << 20);
+    e = hipMalloc(&s->stage, want);
+    if (e != hipSuccess) return fail(GR_ERR_OOM, "unable to allocate %zu bytes of device staging", want);
+    s->stage_bytes = want;
+    return GR_OK;
+}
+
+int h2d(gr_run_state* s, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return GR_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "host to device copy");
+}
+
+int d2h_sync(gr_run_state* s, void* dst, const void* src, size_t bytes) {
+    hipError_t e = bytes ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "device to host copy");
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
+}
+
+// is_swa_layer, inference.rs:1821-1825.
+bool is_swa_layer(const gr_run_state* s, int l) {
+    if (s->windows.empty()) {
+        const int P = s->cfg.swa_pattern;
+        return P > 0 && (l % P < P - 1);
+    }
+    return s->windows[l] > 0;
+}
+
+// visible_keys, attention.rs:74-96 (text tokens).
+void visible(const gr_run_state* s, int l, int64_t pos, int32_t* start, int32_t* end) {
+    const int64_t e = pos + 1;
+    const int64_t w = s->windows.empty() ? 0 : s->windows[l];
+    *start = (int32_t)(w > 0 && e > w ? e - w : 0);
+    *end = (int32_t)e;
+}
+
+int check_layer(const gr_run_state* s, int l) {
+    if (!s) return fail(GR_ERR_ARG, "null run state");
+    if (l < 0 || l >= s->cfg.n_layers)
+        return fail(GR_ERR_RANGE, "layer %d outside [0, %d)", l, s->cfg.n_layers);
+    return GR_OK;
+}
+
+int check_pos(const gr_run_state* s, int seq, int64_t pos, int64_t count) {
+    if (seq < 0 || seq >= s->cfg.n_seq)
+        return fail(GR_ERR_RANGE, "sequence slot %d outside [0, %d)", seq, s->cfg.n_seq);
+    if (pos < 0 || count < 0 || pos + count > s->cfg.seq_len)
+        return fail(GR_ERR_RANGE, "batched prefill range exceeds context (%lld + %lld > %d)",
+                    (long long)pos, (long long)count, s->cfg.seq_len);
+    return GR_OK;
+}
+
+void* layer_k(gr_run_state* s, int l) { return (char*)s->k_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
+void* layer_v(gr_run_state* s, int l) { return (char*)s->v_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
+
+// Prep launch for one layer: QK-norm and/or RoPE as requested.
+QkvPrepLaunch prep_for(gr_run_state* s, int l, int n_tokens, bool norm, bool rope) {
+    QkvPrepLaunch p{};
+    p.n_tokens = n_tokens;
+    p.n_heads = s->cfg.n_heads;
+    p.n_kv_heads = s->cfg.n_kv_heads;
+    p.head_dim = s->d;
+    p.in_dtype = GR_DTYPE_F32;
+    const bool swa = is_swa_layer(s, l);
+    p.rope_mode = rope ? s->cfg.rope_mode : GR_ROPE_NONE;
+    p.rope_dim = s->rope_dim;
+    p.rope_freqs = (s->cfg.is_gemma3 && swa) ? s->freqs_swa : s->freqs;
+    p.rope_scale = swa ? s->cfg.rope_scale_local : s->cfg.rope_scale_global;
+    if (norm && s->has_norm && s->norm_present[l]) {
+        p.q_norm = s->qn + (size_t)l * s->d;
+        p.k_norm = s->kn + (size_t)l * s->d;
+    }
+    p.eps = s->eps;
+    p.gemma_q_scale = rope ? s->cfg.is_gemma3 : 0;
+    p.q_row_stride = s->q_dim;
+    p.kv_row_stride = s->kv_dim;
+    p.q_out_dtype = GR_DTYPE_F32;
+    p.q_out_scale = 1.0f;
+    p.cache_dtype = s->cfg.kv_dtype;
+    p.cache_row_stride = s->kv_dim;
+    return p;
+}
+
+float score_scale(const gr_run_state* s) { return s->cfg.is_gemma3 ? 1.0f : 1.0f / std::sqrt((float)s->d); }
+
+int validate_config(const gr_attn_config* c) {
+    if (!c) return fail(GR_ERR_ARG, "null config");
+    const float scales[2] = {c->rope_scale_global, c->rope_scale_local};
+    for (float sc : scales)
+        if (!std::isfinite(sc) || sc <= 0.0f) return fail(GR_ERR_ARG, "RoPE frequency scales must be finite and positive");
+    if (c->layer_windows) {
+        for (int l = 0; l < c->n_layers; l++)
+            if (c->layer_windows[l] < 0)
+                return fail(GR_ERR_ARG, "attention policy requires one positive window or global entry per layer");
+    }
+    if (c->n_layers <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 || c->seq_len <= 0 || c->n_seq <= 0)
+        return fail(GR_ERR_ARG, "n_layers, n_heads, n_kv_heads, seq_len and n_seq must be positive");
+    if (c->n_heads % c->n_kv_heads)
+        return fail(GR_ERR_ARG, "n_heads %d is not a multiple of n_kv_heads %d", c->n_heads, c->n_kv_heads);
+    if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
+        return fail(GR_ERR_ARG, "head_dim %d unsupported (64, 128, 256)", c->head_dim);
+    if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_BF16) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
+    if (c->rope_mode < GR_ROPE_NONE || c->rope_mode > GR_ROPE_NEOX) return fail(GR_ERR_ARG, "bad rope_mode %d", c->rope_mode);
+    const int rd = c->rope_dim > 0 ? c->rope_dim : c->head_dim;
+    if (rd > c->head_dim || (rd & 1)) return fail(GR_ERR_ARG, "rope_dim %d must be even and <= head_dim", rd);
+    if (c->rope_mode == GR_ROPE_ADJACENT && rd != c->head_dim)
+        return fail(GR_ERR_ARG, "adjacent-pair RoPE rotates whole heads (rope_dim == head_dim)");
+    if (c->rope_mode != GR_ROPE_NONE && (!std::isfinite(c->rope_theta) || c->rope_theta <= 0.0f))
+        return fail(GR_ERR_ARG, "rope_theta must be finite and positive");
+    if ((c->q_norm == nullptr) != (c->k_norm == nullptr))
+        return fail(GR_ERR_ARG, "q_norm and k_norm must be both set or both NULL");
+    if (c->ssm_n_heads < 0 || (c->ssm_n_heads > 0 && c->ssm_head_dim != 128))
+        return fail(GR_ERR_ARG, "DeltaNet state needs ssm_head_dim 128");
+    return GR_OK;
+}
+
+}  // namespace
+
+int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st);
+int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st);
+int deltanet_enqueue(const gr_deltanet_args* a, hipStream_t st);
+size_t deltanet_ws(const gr_deltanet_args* a);
+
+}  // namespace gr
+
+using namespace gr;
+
+extern "C" {
+
+int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out) {
+    clear_error();
+    if (!out) return fail(GR_ERR_ARG, "null output pointer");
+    *out = nullptr;
+    int rc = validate_config(cfg);
+    if (rc) return rc;
+    gr_run_state* s = new gr_run_state();
+    s->cfg = *cfg;
+    s->cfg.layer_windows = nullptr;
+    s->cfg.q_norm = s->cfg.k_norm = nullptr;
+    s->cfg.qk_norm_present = nullptr;
+    if (cfg->layer_windows) s->windows.assign(cfg->layer_windows, cfg->layer_windows + cfg->n_layers);
+    s->d = cfg->head_dim;
+    s->kv_dim = cfg->n_kv_heads * cfg->head_dim;
+    s->q_dim = cfg->n_heads * cfg->head_dim;
+    s->rope_dim = cfg->rope_dim > 0 ? cfg->rope_dim : cfg->head_dim;
+    s->eps = cfg->rms_norm_eps > 0.0f ? cfg->rms_norm_eps : 1e-5f;
+    s->has_norm = cfg->q_norm != nullptr;
+    s->norm_present.assign(cfg->n_layers, s->has_norm ? 1 : 0);
+    if (s->has_norm && cfg->qk_norm_present)
+        for (int l = 0; l < cfg->n_layers; l++) s->norm_present[l] = cfg->qk_norm_present[l] ? 1 : 0;
+    (void)hipGetDevice(&s->device);
+
+    auto cleanup_fail = [&](int code) {
+        gr_free_run_state(s);
+        return code;
+    };
+    hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return cleanup_fail(hip_fail(e, "stream create"));
+    s->seq_stride = (size_t)cfg->seq_len * s->kv_dim;
+    s->layer_stride = s->seq_stride * cfg->n_seq;
+    const size_t cache_bytes = s->layer_stride * cfg->n_layers * elem_bytes(cfg->kv_dtype);
+    if (hipMalloc(&s->k_cache, cache_bytes) != hipSuccess || hipMalloc(&s->v_cache, cache_bytes) != hipSuccess)
+        return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate KV cache (%zu bytes each); reduce --context-size", cache_bytes));
+    (void)hipMemsetAsync(s->k_cache, 0, cache_bytes, s->stream);
+    (void)hipMemsetAsync(s->v_cache, 0, cache_bytes, s->stream);
+
+    // RoPE tables (inference.rs:1590-1609), host powf.
+    const int half = s->rope_dim / 2;
+    std::vector<float> f(half > 0 ? half : 1), fs(half > 0 ? half : 1);
+    if (cfg->rope_mode != GR_ROPE_NONE) {
+        const float swa_theta = cfg->rope_theta_swa > 0.0f ? cfg->rope_theta_swa : 10000.0f;
+        for (int i = 0; i < half; i++) {
+            f[i] = 1.0f / powf(cfg->rope_theta, (float)(i * 2) / (float)s->rope_dim);
+            fs[i] = 1.0f / powf(swa_theta, (float)(i * 2) / (float)s->rope_dim);
+        }
+    }
+    if (hipMalloc(&s->freqs, f.size() * 4) != hipSuccess || hipMalloc(&s->freqs_swa, fs.size() * 4) != hipSuccess)
+        return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate RoPE tables"));
+    (void)hipMemcpyAsync(s->freqs, f.data(), f.size() * 4, hipMemcpyHostToDevice, s->stream);
+    (void)hipMemcpyAsync(s->freqs_swa, fs.data(), fs.size() * 4, hipMemcpyHostToDevice, s->stream);
+    if (s->has_norm) {
+        const size_t nb = (size_t)cfg->n_layers * s->d * 4;
+        if (hipMalloc(&s->qn, nb) != hipSuccess || hipMalloc(&s->kn, nb) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate QK-norm weights"));
+        (void)hipMemcpyAsync(s->qn, cfg->q_norm, nb, hipMemcpyHostToDevice, s->stream);
+        (void)hipMemcpyAsync(s->kn, cfg->k_norm, nb, hipMemcpyHostToDevice, s->stream);
+    }
+    if (cfg->ssm_n_heads > 0) {
+        s->ssm_layer = (size_t)cfg->ssm_n_heads * cfg->ssm_head_dim * cfg->ssm_head_dim;
+        const size_t nb = s->ssm_layer * cfg->n_layers * 4;
+        if (hipMalloc(&s->ssm, nb) != hipSuccess) return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate SSM state"));
+        (void)hipMemsetAsync(s->ssm, 0, nb, s->stream);
+    }
+    e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return cleanup_fail(hip_fail(e, "run state initialisation"));
+    *out = s;
+    return GR_OK;
+}
+
+void gr_free_run_state(gr_run_state* s) {
+    if (!s) return;
+    DeviceScope ds(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    for (void* p : {s->k_cache, s->v_cache, (void*)s->freqs, (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn,
+                    (void*)s->ssm, s->stage})
+        if (p) (void)hipFree(p);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+}
+
+static int norm_or_rope(gr_run_state* s, int32_t layer, int64_t pos, float* q, float* k, bool norm, bool rope) {
+    int rc = check_layer(s, layer);
+    if (rc) return rc;
+    if (!q || !k) return fail(GR_ERR_ARG, "null q/k");
+    if (norm && !(s->has_norm && s->norm_present[layer])) return GR_OK;  // no QK-norm weights: no-op
+    DeviceScope dsc(s->device);
+    rc = ensure_stage(s, 4 * ((size_t)s->q_dim * 2 + (size_t)s->kv_dim * 2) + 4096);
+    if (rc) return rc;
+    Carve cv(s->stage);
+    float* qin = cv.take<float>(s->q_dim);
+    float* kin = cv.take<float>(s->kv_dim);
+    float* qout = cv.take<float>(s->q_dim);
+    float* kout = cv.take<float>(s->kv_dim);
+    float* vdump = cv.take<float>(s->kv_dim);
+    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim)) || (rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim))) return rc;
+    QkvPrepLaunch p = prep_for(s, layer, 1, norm, rope);
+    p.pos0 = pos;
+    p.q = qin;
+    p.k = kin;
+    p.v = kin;
+    p.q_out = qout;
+    p.k_cache = kout;
+    p.v_cache = vdump;
+    p.cache_dtype = GR_DTYPE_F32;
+    p.cache_row_stride = 0;  // single row: ignore the position as a row index
+    hipError_t e = launch_qkv_prep(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    if ((rc = d2h_sync(s, q, qout, 4 * (size_t)s->q_dim))) return rc;
+    return d2h_sync(s, k, kout, 4 * (size_t)s->kv_dim);
+}
+
+int gr_qkv_norm(gr_run_state* s, int32_t layer, float* q, float* k) {
+    clear_error();
+    return norm_or_rope(s, layer, 0, q, k, true, false);
+}
+
+int gr_apply_rope_qk(gr_run_state* s, int32_t layer, int64_t pos, float* q, float* k) {
+    clear_error();
+    if (pos < 0) return fail(GR_ERR_RANGE, "negative position");
+    return norm_or_rope(s, layer, pos, q, k, false, true);
+}
+
+int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* k, const float* v) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, pos, 1))) return rc;
+    if (!k || !v) return fail(GR_ERR_ARG, "null k/v");
+    DeviceScope dsc(s->device);
+    if ((rc = ensure_stage(s, 8 * (size_t)s->kv_dim + 1024))) return rc;
+    Carve cv(s->stage);
+    float* kin = cv.take<float>(s->kv_dim);
+    float* vin = cv.take<float>(s->kv_dim);
+    if ((rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim)) || (rc = h2d(s, vin, v, 4 * (size_t)s->kv_dim))) return rc;
+    QkvPrepLaunch p = prep_for(s, layer, 1, false, false);
+    p.pos0 = pos;
+    p.q = kin;
+    p.k = kin;
+    p.v = vin;
+    p.q_out = nullptr;
+    p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    hipError_t e = launch_qkv_prep(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "kv write launch");
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
+}
+
+// Decode n queries whose prepared f32 q rows are at qdev; entry b reads cache
+// slot slots[b] (or `seq` for all when slots_dev is null) with visible range
+// [starts[b], ends[b]).
+static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, const int32_t* slots_dev, int seq,
+                      const std::vector<int32_t>& starts, const std::vector<int32_t>& ends, float* xb_dev,
+                      Carve& cv) {
+    int32_t* se = cv.take<int32_t>(2 * (size_t)n);
+    std::vector<int32_t> host(2 * (size_t)n);
+    int max_len = 1;
+    for (int b = 0; b < n; b++) {
+        host[b] = starts[b];
+        host[n + b] = ends[b];
+        max_len = std::max(max_len, ends[b] - starts[b]);
+    }
+    int rc = h2d(s, se, host.data(), host.size() * 4);
+    if (rc) return rc;
+    gr_decode_args a{};
+    a.n_seq = n;
+    a.n_heads = s->cfg.n_heads;
+    a.n_kv_heads = s->cfg.n_kv_heads;
+    a.head_dim = s->d;
+    a.kv_dtype = s->cfg.kv_dtype;
+    a.split_keys = 0;
+    a.max_kv_len = max_len;
+    a.score_scale = score_scale(s);
+    a.q = qdev;
+    const size_t eb = elem_bytes(s->cfg.kv_dtype);
+    a.k_cache = (char*)layer_k(s, layer) + (slots_dev ? 0 : (size_t)seq * s->seq_stride * eb);
+    a.v_cache = (char*)layer_v(s, layer) + (slots_dev ? 0 : (size_t)seq * s->seq_stride * eb);
+    a.seq_stride = slots_dev ? (int64_t)s->seq_stride : 0;
+    a.row_stride = s->kv_dim;
+    a.kv_start = se;
+    a.kv_end = se + n;
+    a.out = xb_dev;
+    const size_t ws = decode_ws_bytes(&a);
+    a.workspace = cv.take<char>(ws + 256);
+    return decode_enqueue_ex(&a, slots_dev, s->stream);
+}
+
+int gr_attention_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* q, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, pos, 1))) return rc;
+    if (!q || !xb) return fail(GR_ERR_ARG, "null q/xb");
+    DeviceScope dsc(s->device);
+    int32_t st, en;
+    visible(s, layer, pos, &st, &en);
+    gr_decode_args probe{};
+    probe.n_seq = 1;
+    probe.n_heads = s->cfg.n_heads;
+    probe.n_kv_heads = s->cfg.n_kv_heads;
+    probe.head_dim = s->d;
+    probe.max_kv_len = en - st;
+    if ((rc = ensure_stage(s, 8 * (size_t)s->q_dim + decode_ws_bytes(&probe) + 4096))) return rc;
+    Carve cv(s->stage);
+    float* qin = cv.take<float>(s->q_dim);
+    float* xo = cv.take<float>(s->q_dim);
+    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim))) return rc;
+    if ((rc = run_decode(s, layer, 1, qin, nullptr, seq, {st}, {en}, xo, cv))) return rc;
+    return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
+}
+
+int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* q,
+                             const float* k, const float* v, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, pos, 1))) return rc;
+    if (!q || !k || !v || !xb) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    int32_t st, en;
+    visible(s, layer, pos, &st, &en);
+    gr_decode_args probe{};
+    probe.n_seq = 1;
+    probe.n_heads = s->cfg.n_heads;
+    probe.n_kv_heads = s->cfg.n_kv_heads;
+    probe.head_dim = s->d;
+    probe.max_kv_len = en - st;
+    if ((rc = ensure_stage(s, 4 * (3 * (size_t)s->q_dim + 2 * (size_t)s->kv_dim) + decode_ws_bytes(&probe) + 8192)))
+        return rc;
+    Carve cv(s->stage);
+    float* qin = cv.take<float>(s->q_dim);
+    float* kin = cv.take<float>(s->kv_dim);
+    float* vin = cv.take<float>(s->kv_dim);
+    float* qp = cv.take<float>(s->q_dim);
+    float* xo = cv.take<float>(s->q_dim);
+    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim)) || (rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim)) ||
+        (rc = h2d(s, vin, v, 4 * (size_t)s->kv_dim)))
+        return rc;
+    QkvPrepLaunch p = prep_for(s, layer, 1, true, true);
+    p.pos0 = pos;
+    p.q = qin;
+    p.k = kin;
+    p.v = vin;
+    p.q_out = qp;
+    p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    hipError_t e = launch_qkv_prep(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    if ((rc = run_decode(s, layer, 1, qp, nullptr, seq, {st}, {en}, xo, cv))) return rc;
+    return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
+}
+
+int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
+                               const float* q, const float* k, const float* v, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, base_pos, m))) return rc;
+    if (m == 0) return GR_OK;
+    if (!q || !k || !v || !xb) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const size_t qb = 4 * (size_t)m * s->q_dim, kb = 4 * (size_t)m * s->kv_dim;
+    const bool mfma = s->cfg.kv_dtype != GR_DTYPE_F32 && (s->d == 128 || s->d == 256);
+    const int64_t w = s->windows.empty() ? 0 : s->windows[layer];
+    std::vector<int32_t> starts(m), ends(m);
+    int max_len = 1;
+    for (int i = 0; i < m; i++) {
+        visible(s, layer, base_pos + i, &starts[i], &ends[i]);
+        max_len = std::max(max_len, ends[i] - starts[i]);
+    }
+    gr_decode_args probe{};
+    probe.n_seq = m;
+    probe.n_heads = s->cfg.n_heads;
+    probe.n_kv_heads = s->cfg.n_kv_heads;
+    probe.head_dim = s->d;
+    probe.max_kv_len = max_len;
+    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb;
+    if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
+    Carve cv(s->stage);
+    float* qin = cv.take<float>((size_t)m * s->q_dim);
+    float* kin = cv.take<float>((size_t)m * s->kv_dim);
+    float* vin = cv.take<float>((size_t)m * s->kv_dim);
+    float* xo = cv.take<float>((size_t)m * s->q_dim);
+    if ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb))) return rc;
+    const size_t eb = elem_bytes(s->cfg.kv_dtype);
+    void* kc = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * eb;
+    void* vc = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * eb;
+    if (mfma) {
+        gr_prefill_args a{};
+        a.n_tokens = m;
+        a.base_pos = (int32_t)base_pos;
+        a.n_heads = s->cfg.n_heads;
+        a.n_kv_heads = s->cfg.n_kv_heads;
+        a.head_dim = s->d;
+        a.dtype = s->cfg.kv_dtype;
+        a.window = (int32_t)w;
+        a.rope_mode = s->cfg.rope_mode;
+        a.rope_dim = s->rope_dim;
+        const bool swa = is_swa_layer(s, layer);
+        a.rope_scale = swa ? s->cfg.rope_scale_local : s->cfg.rope_scale_global;
+        a.rope_freqs = (s->cfg.is_gemma3 && swa) ? s->freqs_swa : s->freqs;
+        if (s->has_norm && s->norm_present[layer]) {
+            a.q_norm = s->qn + (size_t)layer * s->d;
+            a.k_norm = s->kn + (size_t)layer * s->d;
+        }
+        a.norm_eps = s->eps;
+        a.is_gemma3 = s->cfg.is_gemma3;
+        a.q = qin;
+        a.k = kin;
+        a.v = vin;
+        a.k_cache = kc;
+        a.v_cache = vc;
+        a.cache_row_stride = s->kv_dim;
+        a.out = xo;
+        a.workspace = cv.take<char>(2 * qb);
+        if ((rc = prefill_enqueue_ex(&a, GR_DTYPE_F32, s->stream))) return rc;
+    } else {
+        float* qp = cv.take<float>((size_t)m * s->q_dim);
+        QkvPrepLaunch p = prep_for(s, layer, m, true, true);
+        p.pos0 = base_pos;
+        p.q = qin;
+        p.k = kin;
+        p.v = vin;
+        p.q_out = qp;
+        p.k_cache = kc;
+        p.v_cache = vc;
+        hipError_t e = launch_qkv_prep(p, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "prep launch");
+        if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) return rc;
+    }
+    return d2h_sync(s, xb, xo, qb);
+}
+
+int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32_t* seqs, const int64_t* pos,
+                          const float* q, const float* k, const float* v, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc) return rc;
+    if (n <= 0) return n == 0 ? GR_OK : fail(GR_ERR_ARG, "n < 0");
+    if (!seqs || !pos || !q || !k || !v || !xb) return fail(GR_ERR_ARG, "null buffer");
+    std::vector<int32_t> starts(n), ends(n), pos32(n);
+    int max_len = 1;
+    for (int b = 0; b < n; b++) {
+        if ((rc = check_pos(s, seqs[b], pos[b], 1))) return rc;
+        visible(s, layer, pos[b], &starts[b], &ends[b]);
+        pos32[b] = (int32_t)pos[b];
+        max_len = std::max(max_len, ends[b] - starts[b]);
+    }
+    DeviceScope dsc(s->device);
+    gr_decode_args probe{};
+    probe.n_seq = n;
+    probe.n_heads = s->cfg.n_heads;
+    probe.n_kv_heads = s->cfg.n_kv_heads;
+    probe.head_dim = s->d;
+    probe.max_kv_len = max_len;
+    const size_t qb = 4 * (size_t)n * s->q_dim, kb = 4 * (size_t)n * s->kv_dim;
+    if ((rc = ensure_stage(s, 3 * qb + 2 * kb + decode_ws_bytes(&probe) + 16 * (size_t)n + 16384))) return rc;
+    Carve cv(s->stage);
+    float* qin = cv.take<float>((size_t)n * s->q_dim);
+    float* kin = cv.take<float>((size_t)n * s->kv_dim);
+    float* vin = cv.take<float>((size_t)n * s->kv_dim);
+    float* qp = cv.take<float>((size_t)n * s->q_dim);
+    float* xo = cv.take<float>((size_t)n * s->q_dim);
+    int32_t* slot_d = cv.take<int32_t>(n);
+    int32_t* pos_d = cv.take<int32_t>(n);
+    if ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)) ||
+        (rc = h2d(s, slot_d, seqs, 4 * (size_t)n)) || (rc = h2d(s, pos_d, pos32.data(), 4 * (size_t)n)))
+        return rc;
+    QkvPrepLaunch p = prep_for(s, layer, n, true, true);
+    p.pos = pos_d;
+    p.q = qin;
+    p.k = kin;
+    p.v = vin;
+    p.q_out = qp;
+    p.k_cache = layer_k(s, layer);
+    p.v_cache = layer_v(s, layer);
+    p.cache_seq = slot_d;
+    p.cache_seq_stride = (int64_t)s->seq_stride;
+    hipError_t e = launch_qkv_prep(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    if ((rc = run_decode(s, layer, n, qp, slot_d, 0, starts, ends, xo, cv))) return rc;
+    return d2h_sync(s, xb, xo, qb);
+}
+
+static int check_ssm(gr_run_state* s, int layer) {
+    int rc = check_layer(s, layer);
+    if (rc) return rc;
+    if (!s->ssm) return fail(GR_ERR_ARG, "run state has no SSM state (ssm_n_heads == 0)");
+    return GR_OK;
+}
+
+int gr_qwen3next_state_step(gr_run_state* s, int32_t layer, const float* q, const float* k, const float* v,
+                            const float* g, const float* beta, float* out) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!q || !k || !v || !g || !beta || !out) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const int H = s->cfg.ssm_n_heads, D = s->cfg.ssm_head_dim;
+    const size_t rb = 4 * (size_t)H * D;
+    if ((rc = ensure_stage(s, 4 * rb + 8 * (size_t)H + 4096))) return rc;
+    Carve cv(s->stage);
+    float* qd = cv.take<float>((size_t)H * D);
+    float* kd = cv.take<float>((size_t)H * D);
+    float* vd = cv.take<float>((size_t)H * D);
+    float* od = cv.take<float>((size_t)H * D);
+    float* gd = cv.take<float>(H);
+    float* bd = cv.take<float>(H);
+    if ((rc = h2d(s, qd, q, rb)) || (rc = h2d(s, kd, k, rb)) || (rc = h2d(s, vd, v, rb)) ||
+        (rc = h2d(s, gd, g, 4 * (size_t)H)) || (rc = h2d(s, bd, beta, 4 * (size_t)H)))
+        return rc;
+    DeltaNetLaunch p{};
+    p.n_tokens = 1;
+    p.n_heads = H;
+    p.head_dim = D;
+    p.in_dtype = GR_DTYPE_F32;
+    p.l2norm = 0;
+    p.eps = s->eps;
+    p.q = qd;
+    p.k = kd;
+    p.v = vd;
+    p.gate = gd;
+    p.beta = bd;
+    p.state = s->ssm + (size_t)layer * s->ssm_layer;
+    p.out = od;
+    p.gate_is_log = 0;
+    hipError_t e = launch_deltanet_scan(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "deltanet step launch");
+    return d2h_sync(s, out, od, rb);
+}
+
+int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float* q, const float* k,
+                         const float* v, const float* gate, const float* beta, float* out) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (T < 0) return fail(GR_ERR_ARG, "T < 0");
+    if (T == 0) return GR_OK;
+    if (!q || !k || !v || !gate || !beta || !out) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const int H = s->cfg.ssm_n_heads, D = s->cfg.ssm_head_dim;
+    const size_t rb = 4 * (size_t)T * H * D, gb = 4 * (size_t)T * H;
+    gr_deltanet_args a{};
+    a.n_tokens = T;
+    a.n_heads = H;
+    a.head_dim = D;
+    a.in_dtype = GR_DTYPE_F32;
+    a.l2norm = 1;
+    a.algo = GR_DELTANET_AUTO;
+    a.eps = s->eps;
+    const size_t ws = deltanet_ws(&a);
+    if ((rc = ensure_stage(s, 4 * rb + 2 * gb + ws + 8192))) return rc;
+    Carve cv(s->stage);
+    float* qd = cv.take<float>((size_t)T * H * D);
+    float* kd = cv.take<float>((size_t)T * H * D);
+    float* vd = cv.take<float>((size_t)T * H * D);
+    float* od = cv.take<float>((size_t)T * H * D);
+    float* gd = cv.take<float>((size_t)T * H);
+    float* bd = cv.take<float>((size_t)T * H);
+    if ((rc = h2d(s, qd, q, rb)) || (rc = h2d(s, kd, k, rb)) || (rc = h2d(s, vd, v, rb)) ||
+        (rc = h2d(s, gd, gate, gb)) || (rc = h2d(s, bd, beta, gb)))
+        return rc;
+    a.q = qd;
+    a.k = kd;
+    a.v = vd;
+    a.gate = gd;
+    a.beta = bd;
+    a.state = s->ssm + (size_t)layer * s->ssm_layer;
+    a.out = od;
+    a.workspace = ws ? cv.take<char>(ws) : nullptr;
+    if ((rc = deltanet_enqueue(&a, s->stream))) return rc;
+    return d2h_sync(s, out, od, rb);
+}
+
+int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows, void* k_out,
+                    void* v_out) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, row0, n_rows))) return rc;
+    DeviceScope dsc(s->device);
+    const size_t eb = elem_bytes(s->cfg.kv_dtype);
+    const size_t off = ((size_t)seq * s->seq_stride + (size_t)row0 * s->kv_dim) * eb;
+    const size_t nb = (size_t)n_rows * s->kv_dim * eb;
+    if (k_out && (rc = d2h_sync(s, k_out, (char*)layer_k(s, layer) + off, nb))) return rc;
+    if (v_out && (rc = d2h_sync(s, v_out, (char*)layer_v(s, layer) + off, nb))) return rc;
+    return GR_OK;
+}
+
+int gr_read_ssm_state(gr_run_state* s, int32_t layer, float* out) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!out) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    return d2h_sync(s, out, s->ssm + (size_t)layer * s->ssm_layer, 4 * s->ssm_layer);
+}
+
+int gr_write_ssm_state(gr_run_state* s, int32_t layer, const float* in) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!in) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    if ((rc = h2d(s, s->ssm + (size_t)layer * s->ssm_layer, in, 4 * s->ssm_layer))) return rc;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
+}
+
+}  // extern "C"

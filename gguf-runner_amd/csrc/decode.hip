@@ -70,9 +70,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     }
 
     const char* kbase = (const char*)p.k_cache +
-                        ((size_t)s * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
+                        ((size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
     const char* vbase = (const char*)p.v_cache +
-                        ((size_t)s * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
+                        ((size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D + e0) * KV::bytes;
     const size_t row_bytes = (size_t)p.row_stride * KV::bytes;
 
     for (int tb = t_begin; tb < t_stop; tb += STEP) {

@@ -10,8 +10,10 @@
 // Each wave streams its own 32-key tiles (keys split between the 4 waves of
 // the workgroup, next tile prefetched into registers while the current one is
 // processed) and keeps its own online-softmax state; the waves merge in LDS.
-// bf16 carries Q and P as hi + lo pairs (two MFMAs per product), as in
-// prefill.hip, so the result stays within ~1e-5 of an fp32 evaluation.
+// Q and P are carried as hi + lo 16-bit pairs (two MFMAs per product; K and V
+// are exact 16-bit cache values), so the scores and weights keep ~fp32
+// precision even for large unscaled logits.  Decode is HBM-bound with the
+// matrix cores mostly idle, so the second MFMA costs no time.
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -25,7 +27,7 @@ template <typename DT>
 struct Mfma16;
 template <>
 struct Mfma16<F16> {
-    static constexpr bool kSplit = false;
+    static constexpr bool kSplit = true;
     static __device__ __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
                                                       __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
@@ -103,8 +105,8 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         }
     }
 
-    const uint16_t* kc = (const uint16_t*)p.k_cache + (size_t)s * p.seq_stride + (size_t)g * D;
-    const uint16_t* vc = (const uint16_t*)p.v_cache + (size_t)s * p.seq_stride + (size_t)g * D;
+    const uint16_t* kc = (const uint16_t*)p.k_cache + (size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D;
+    const uint16_t* vc = (const uint16_t*)p.v_cache + (size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D;
     const int64_t rs = p.row_stride;
 
     uint4 kr[2][KS];

@@ -74,7 +74,8 @@ __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const Delta
                 for (int e = 0; e < D / 64; e++) dst[lane + 64 * e] = x[e];
             }
         }
-        const float g = finite_or_zero(expf(p.gate[(size_t)t * H + h]));
+        const float gv = p.gate[(size_t)t * H + h];
+        const float g = finite_or_zero(p.gate_is_log ? expf(gv) : gv);
         const float beta = finite_or_zero(p.beta[(size_t)t * H + h]);
         const float vi = finite_or_zero(dn_load(p.v, row + i, p.in_dtype));
         __syncthreads();

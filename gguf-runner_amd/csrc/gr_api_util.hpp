@@ -16,6 +16,7 @@ size_t align_up(size_t x, size_t a);
 
 int check_decode_shape_only(const gr_decode_args* a);
 int decode_enqueue(const gr_decode_args* a, hipStream_t st);
+int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st);
 size_t decode_ws_bytes(const gr_decode_args* a);
 
 }  // namespace gr

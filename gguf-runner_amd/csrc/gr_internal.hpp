@@ -18,6 +18,7 @@ struct DecodeLaunch {
     int64_t seq_stride, row_stride;
     const int32_t* kv_start;
     const int32_t* kv_end;
+    const int32_t* seq_slot;  // [n_seq] cache sequence slot of batch entry s, or nullptr (= s)
     float* out;
     float* ws_o;
     float* ws_ml;
@@ -93,6 +94,7 @@ struct DeltaNetLaunch {
     float* out;
     float* ws;   // chunked algorithm workspace
     int chunk;
+    int gate_is_log;  // 1: g = exp(gate[t][h]); 0: gate already holds the decay factor g
 };
 
 hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st);

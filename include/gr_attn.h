@@ -169,6 +169,99 @@ typedef struct gr_deltanet_args {
 size_t gr_deltanet_workspace_size(const gr_deltanet_args* a);
 int gr_deltanet_attention(const gr_deltanet_args* a, void* stream);
 
+/* ======================================================================
+ * Run state: device-resident KV cache, DeltaNet state and stream of one
+ * RunState (src/engine/types.rs:745-809).  The entry points below take the
+ * reference's own host buffers (s.q, s.k, s.v, s.xb as f32 rows) and return
+ * when the results are back in host memory, so each one replaces the body of
+ * the cited Rust function.  Device layout of the cache, per layer l and
+ * sequence slot s: row t of kv_dim = n_kv_heads*head_dim elements at
+ * ((l*n_seq + s)*seq_len + t)*kv_dim (the reference's (l*seq_len + t)*kv_dim,
+ * inference.rs:1880-1882, with a slot index for batched decode).
+ * ====================================================================== */
+typedef struct gr_run_state gr_run_state;
+
+typedef struct gr_attn_config {
+    int32_t n_layers;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t seq_len;            /* cache rows per sequence (Config::seq_len) */
+    int32_t n_seq;              /* sequence slots, one reference RunState each (>= 1) */
+    int32_t kv_dtype;           /* gr_dtype of the device KV cache (raw storage) */
+    int32_t rope_mode;          /* gr_rope_mode (NEOX for Gemma3/Qwen2/Qwen3*, ADJACENT for Llama) */
+    int32_t rope_dim;           /* rotated dims, 0 -> head_dim (vendors/mod.rs:1015-1019) */
+    float rope_theta;
+    float rope_theta_swa;       /* <= 0 -> 10000 (inference.rs:1595-1599) */
+    float rope_scale_global;    /* RopeScalingPolicy::global */
+    float rope_scale_local;     /* RopeScalingPolicy::local */
+    const int32_t* layer_windows; /* [n_layers] or NULL: window per layer, 0 = global
+                                   * (LanguageAttentionPolicy::layer_windows, types.rs:614-621) */
+    int32_t swa_pattern;        /* Config::swa_pattern, for is_swa_layer without layer_windows (1821-1825) */
+    int32_t is_gemma3;          /* SWA RoPE table, q *= 1/sqrt(d), unscaled scores (1871-1873, 1982) */
+    int32_t online_attn_fusion; /* accepted for parity; the device path is always online split-K */
+    float rms_norm_eps;         /* <= 0 -> 1e-5 (inference.rs:2539-2543) */
+    const float* q_norm;        /* host [n_layers][head_dim] QK-norm weights, or NULL */
+    const float* k_norm;        /* host [n_layers][head_dim], or NULL */
+    const uint8_t* qk_norm_present; /* host [n_layers] or NULL (= every layer when q_norm is set) */
+    int32_t ssm_n_heads;        /* DeltaNet value heads, 0 = no SSM state */
+    int32_t ssm_head_dim;       /* 128 */
+} gr_attn_config;
+
+/* malloc_run_state_with_kv_cache_format (inference.rs:1529-1748): validates
+ * like 1533-1546 ("RoPE frequency scales must be finite and positive", one
+ * positive window or global entry per layer), builds the RoPE tables
+ * (1590-1609) and allocates the device cache, SSM state and stream. */
+int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out);
+void gr_free_run_state(gr_run_state* s);
+
+/* qkv_bias_and_norm's per-head QK RMSNorm (inference.rs:2535-2572 ->
+ * math.rs:164-184), in place on host q [n_heads*head_dim], k [n_kv_heads*head_dim]. */
+int gr_qkv_norm(gr_run_state* s, int32_t layer, float* q, float* k);
+/* apply_rope_qk (inference.rs:1817-1874), in place on host q and k. */
+int gr_apply_rope_qk(gr_run_state* s, int32_t layer, int64_t pos, float* q, float* k);
+/* kv_write_token (inference.rs:1877-1965), raw storage: k, v -> cache row (layer, seq, pos). */
+int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* k,
+                      const float* v);
+/* attention_token (inference.rs:1970-2530): q (post-RoPE) -> xb over the
+ * visible keys of (layer, pos) (attention.rs:74-96). */
+int gr_attention_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* q,
+                       float* xb);
+/* The four calls of layer_attention_token_staged (inference.rs:3499-3507)
+ * fused into one device pass: QK-norm, RoPE, KV write and attention. */
+int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos,
+                             const float* q, const float* k, const float* v, float* xb);
+/* The per-token attention loop of transformer_prefill_batch
+ * (inference.rs:2981-3017) for m tokens at base_pos..base_pos+m-1:
+ * q [m][n_heads*head_dim], k/v [m][kv_dim] pre-norm, pre-RoPE; xb [m][q_dim]. */
+int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos,
+                               int32_t m, const float* q, const float* k, const float* v,
+                               float* xb);
+/* One decode step for n sequences at once (one token each, sequence slot
+ * seqs[b] at position pos[b]): the per-sequence calls of
+ * layer_attention_token_staged batched into one launch. */
+int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32_t* seqs,
+                          const int64_t* pos, const float* q, const float* k, const float* v,
+                          float* xb);
+/* qwen3next_state_head_step over all value heads for one token
+ * (math.rs:890-934): q, k already normalised, g the decay factor
+ * (ssm_gate_exp), beta the sigmoid-ed gate; q/k/v/out [ssm_n_heads*ssm_head_dim]. */
+int gr_qwen3next_state_step(gr_run_state* s, int32_t layer, const float* q, const float* k,
+                            const float* v, const float* g, const float* beta, float* out);
+/* The serial SSM prefill recurrence (inference.rs:2866-2885) for T tokens on the
+ * chunk-64 device path: q/k raw (normalised in-kernel as math.rs:833-846),
+ * gate the log decay, rows [T][ssm_n_heads*ssm_head_dim]. */
+int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float* q,
+                         const float* k, const float* v, const float* gate, const float* beta,
+                         float* out);
+/* Host copies of device state (for checks and snapshots): `n_rows` cache rows
+ * of (layer, seq) starting at row0 as raw kv_dtype elements, and the SSM state
+ * of a layer (f32 [ssm_n_heads][d][d]). */
+int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
+                    void* k_out, void* v_out);
+int gr_read_ssm_state(gr_run_state* s, int32_t layer, float* out);
+int gr_write_ssm_state(gr_run_state* s, int32_t layer, const float* in);
+
 #ifdef __cplusplus
 }
 #endif
