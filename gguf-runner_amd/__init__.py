@@ -8,4 +8,4 @@ identifier: __graft_entry__.load_package() registers it in sys.modules as
 """
 from . import ffi  # noqa: F401
 
-__all__ = ["ffi", "ops"]
+__all__ = ["ffi", "ops", "runtime"]

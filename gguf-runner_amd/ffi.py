@@ -66,6 +66,18 @@ class DeltaNetArgs(ctypes.Structure):
 
 DELTANET_AUTO, DELTANET_RECURRENT, DELTANET_CHUNKED = 0, 1, 2
 
+
+class AttnConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", _i32), ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32),
+        ("seq_len", _i32), ("n_seq", _i32), ("kv_dtype", _i32), ("rope_mode", _i32),
+        ("rope_dim", _i32), ("rope_theta", _f), ("rope_theta_swa", _f),
+        ("rope_scale_global", _f), ("rope_scale_local", _f), ("layer_windows", _p),
+        ("swa_pattern", _i32), ("is_gemma3", _i32), ("online_attn_fusion", _i32),
+        ("rms_norm_eps", _f), ("q_norm", _p), ("k_norm", _p), ("qk_norm_present", _p),
+        ("ssm_n_heads", _i32), ("ssm_head_dim", _i32),
+    ]
+
 _lib = None
 
 
@@ -100,6 +112,28 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_deltanet_workspace_size.restype = ctypes.c_size_t
     L.gr_deltanet_attention.argtypes = [ctypes.POINTER(DeltaNetArgs), _p]
     L.gr_deltanet_attention.restype = ctypes.c_int
+    ip = ctypes.c_int
+    L.gr_malloc_run_state.argtypes = [ctypes.POINTER(AttnConfig), ctypes.POINTER(_p)]
+    L.gr_malloc_run_state.restype = ip
+    L.gr_free_run_state.argtypes = [_p]
+    L.gr_free_run_state.restype = None
+    L.gr_qkv_norm.argtypes = [_p, _i32, _p, _p]
+    L.gr_apply_rope_qk.argtypes = [_p, _i32, _i64, _p, _p]
+    L.gr_kv_write_token.argtypes = [_p, _i32, _i32, _i64, _p, _p]
+    L.gr_attention_token.argtypes = [_p, _i32, _i32, _i64, _p, _p]
+    L.gr_attention_layer_token.argtypes = [_p, _i32, _i32, _i64, _p, _p, _p, _p]
+    L.gr_prefill_attention_chunk.argtypes = [_p, _i32, _i32, _i64, _i32, _p, _p, _p, _p]
+    L.gr_decode_layer_batch.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
+    L.gr_qwen3next_state_step.argtypes = [_p, _i32, _p, _p, _p, _p, _p, _p]
+    L.gr_qwen3next_prefill.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
+    L.gr_read_kv_rows.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
+    L.gr_read_ssm_state.argtypes = [_p, _i32, _p]
+    L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
+    for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
+              "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_decode_layer_batch",
+              "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
+              "gr_read_ssm_state", "gr_write_ssm_state"):
+        getattr(L, n).restype = ip
 
 
 def check(rc: int) -> None:

@@ -33,3 +33,45 @@ def test_abi_version_and_error_path(pkg):
     rc = L.gr_decode_attention(ctypes.byref(a), None)
     assert rc == ffi.GR_ERR_ARG
     assert b"multiple" in L.gr_last_error()
+
+
+def test_malloc_run_state_rejects_invalid_rope_scales(pkg):
+    """inference.rs:4120-4131 (rope_scaling_rejects_invalid_runtime_policies): scales
+    0, -1, NaN, inf are refused before any device allocation (runs without a GPU)."""
+    from gguf_runner_amd import ffi, runtime
+    for scale in (0.0, -1.0, float("nan"), float("inf")):
+        for glob in (True, False):
+            p = runtime.Config(n_layers=1, n_heads=1, n_kv_heads=1, head_dim=64, seq_len=8,
+                               rope_scale_global=scale if glob else 1.0,
+                               rope_scale_local=1.0 if glob else scale)
+            try:
+                runtime.malloc_run_state(p)
+            except ffi.GrError as e:
+                assert e.code == ffi.GR_ERR_ARG
+                assert "RoPE frequency scales must be finite and positive" in str(e)
+            else:
+                raise AssertionError("invalid scale accepted")
+
+
+def test_malloc_run_state_rejects_bad_windows_and_shapes(pkg):
+    from gguf_runner_amd import ffi, runtime
+    bad = [dict(layer_windows=[1024, -1]), dict(n_kv_heads=3), dict(head_dim=96),
+           dict(rope_mode=ffi.ROPE_ADJACENT, rope_dim=32)]
+    for kw in bad:
+        base = dict(n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, seq_len=8)
+        base.update(kw)
+        try:
+            runtime.malloc_run_state(runtime.Config(**base))
+        except ffi.GrError as e:
+            assert e.code == ffi.GR_ERR_ARG
+        else:
+            raise AssertionError(f"accepted {kw}")
+
+
+def test_rope_freqs_match_oracle_bitwise(pkg, orc):
+    """gr_rope_freqs and the oracle both restate inference.rs:1590-1609 with host powf."""
+    import numpy as np
+    from gguf_runner_amd import ops
+    for theta, dim in ((5e5, 128), (1e4, 256), (1e6, 64)):
+        a = np.array(ops.rope_freqs(theta, dim), np.float32)
+        assert np.array_equal(a, orc.rope_freqs(theta, dim))

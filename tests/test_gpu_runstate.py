@@ -1,0 +1,208 @@
+"""The run-state entry points (the drop-ins for the reference's Rust call sites)
+against the CPU oracle and against the reference's own unit-test constants."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+ATOL_16, RTOL_16 = 2e-3, 1e-2
+
+
+def test_rope_scaling_switches_local_and_global_layers_at_the_same_position(dev):
+    """inference.rs:4098-4118 through gr_apply_rope_qk: adjacent pairs, layer 0 local
+    (window 1024, scale 1) -> angle 8, layer 1 global (scale 0.125) -> angle 1."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = rt.Config(n_layers=2, n_heads=1, n_kv_heads=1, head_dim=64, seq_len=16,
+                  rope_mode=ffi.ROPE_ADJACENT, rope_theta=10_000.0, layer_windows=[1024, None],
+                  rope_scale_global=0.125)
+    s = rt.malloc_run_state(p)
+    for layer, angle in [(0, 8.0), (1, 1.0), (0, 8.0)]:
+        s.q.fill(0.0)
+        s.k.fill(0.0)
+        s.q[0] = 1.0
+        s.k[0] = 1.0
+        rt.apply_rope_qk(p, s, layer, 8)
+        for values in (s.q, s.k):
+            assert abs(values[0] - math.cos(angle)) < 1e-7
+            assert abs(values[1] - math.sin(angle)) < 1e-7
+
+
+def test_neox_rope_partial_tail_through_device(dev, orc):
+    """NeoX pairing with rope_dim < head_dim leaves the tail untouched (4133-4182) and
+    matches the oracle's apply_rope_qk to 1 ulp-level."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = rt.Config(n_layers=1, n_heads=2, n_kv_heads=1, head_dim=256, rope_dim=64, seq_len=8,
+                  rope_mode=ffi.ROPE_NEOX, rope_theta=1e6)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(0)
+    q0 = rng.standard_normal(p.q_dim).astype(np.float32)
+    k0 = rng.standard_normal(p.kv_dim).astype(np.float32)
+    s.q[:] = q0
+    s.k[:] = k0
+    rt.apply_rope_qk(p, s, 0, 5)
+    c, sn = orc.rope_cache(orc.rope_freqs(1e6, 64), 5, 1.0)
+    qr, kr = orc.apply_rope_qk(q0, k0, 2, 1, 256, c, sn, neox=True)
+    assert np.allclose(s.q, qr, atol=1e-6) and np.allclose(s.k, kr, atol=1e-6)
+    assert np.array_equal(s.q.reshape(2, 256)[:, 64:], q0.reshape(2, 256)[:, 64:])
+
+
+def _qwen3_config(rt, ffi, kv_dtype, n_seq=1, seq_len=256):
+    rng = np.random.default_rng(42)
+    return rt.Config(n_layers=2, n_heads=16, n_kv_heads=8, head_dim=128, seq_len=seq_len,
+                     n_seq=n_seq, kv_dtype=kv_dtype, rope_mode=ffi.ROPE_NEOX, rope_theta=1e6,
+                     rms_norm_eps=1e-6,
+                     q_norm=(1 + 0.1 * rng.standard_normal((2, 128))).astype(np.float32),
+                     k_norm=(1 + 0.1 * rng.standard_normal((2, 128))).astype(np.float32))
+
+
+def test_layer_token_loop_matches_oracle_f32(dev, orc):
+    """Qwen3-0.6B-shaped layer (16 Q / 8 KV heads, d128, QK-norm, NeoX theta 1e6, f32
+    KV): gr_attention_layer_token per token == the oracle's token-serial prefill loop
+    (inference.rs:2981-3017) within 1e-5."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, ffi.DTYPE_F32)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(1)
+    m, layer = 97, 1
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    got = np.zeros((m, p.q_dim), np.float32)
+    for t in range(m):
+        s.q[:], s.k[:], s.v[:] = q[t], k[t], v[t]
+        rt.attention_layer_token(p, s, layer, t)
+        got[t] = s.xb
+    ref, kc, vc = orc.prefill_layer(q, k, v, n_heads=16, n_kv_heads=8, head_size=128,
+                                    seq_len=m, fmt=orc.F32, rope_dim=128, neox=True,
+                                    rope_freqs_tab=orc.rope_freqs(1e6, 128), rope_scale=1.0,
+                                    q_norm=p.q_norm[layer], k_norm=p.k_norm[layer], eps=1e-6,
+                                    n_threads=orc.env_threads())
+    assert float(np.abs(got - ref).max()) <= TOL_F32
+    kd, vd = rt.read_kv_rows(p, s, layer, 0, m)
+    assert np.allclose(kd, kc, atol=1e-6) and np.array_equal(vd, vc)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1, 2])
+def test_chunked_prefill_equals_sequential(dev, orc, kv_dtype):
+    """Analogue of image_positions_preserve_chunked_prefill_kv_rows_and_decode_results
+    (inference.rs:4184-4284): 64-token chunked prefill writes the same KV rows as the
+    token-by-token path, and the attention outputs agree."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, kv_dtype)
+    s_seq = rt.malloc_run_state(p)
+    s_chk = rt.malloc_run_state(p)
+    rng = np.random.default_rng(2)
+    m, layer = 150, 0
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    seq_out = np.zeros((m, p.q_dim), np.float32)
+    for t in range(m):
+        s_seq.q[:], s_seq.k[:], s_seq.v[:] = q[t], k[t], v[t]
+        rt.attention_layer_token(p, s_seq, layer, t)
+        seq_out[t] = s_seq.xb
+    chk = []
+    for b in range(0, m, 64):
+        chk.append(rt.prefill_attention_chunk(p, s_chk, layer, b, q[b:b + 64], k[b:b + 64],
+                                              v[b:b + 64]))
+    chk = np.concatenate(chk)
+    k1, v1 = rt.read_kv_rows(p, s_seq, layer, 0, m)
+    k2, v2 = rt.read_kv_rows(p, s_chk, layer, 0, m)
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    err = np.abs(chk - seq_out)
+    if kv_dtype == ffi.DTYPE_F32:
+        assert float(err.max()) <= TOL_F32
+    else:
+        assert not (err > ATOL_16 + RTOL_16 * np.abs(seq_out)).any(), err.max()
+
+
+def test_decode_layer_batch_equals_per_sequence(dev):
+    """One batched decode launch over 3 sequence slots == per-slot layer tokens."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, ffi.DTYPE_F16, n_seq=3, seq_len=300)
+    s_a = rt.malloc_run_state(p)
+    s_b = rt.malloc_run_state(p)
+    rng = np.random.default_rng(3)
+    lens = [40, 250, 7]
+    layer = 1
+    for seq, L in enumerate(lens):
+        q = rng.standard_normal((L, p.q_dim)).astype(np.float32)
+        k = rng.standard_normal((L, p.kv_dim)).astype(np.float32)
+        v = rng.standard_normal((L, p.kv_dim)).astype(np.float32)
+        for st in (s_a, s_b):
+            rt.prefill_attention_chunk(p, st, layer, 0, q, k, v, seq=seq)
+    qn = rng.standard_normal((3, p.q_dim)).astype(np.float32)
+    kn = rng.standard_normal((3, p.kv_dim)).astype(np.float32)
+    vn = rng.standard_normal((3, p.kv_dim)).astype(np.float32)
+    batch = rt.decode_layer_batch(p, s_a, layer, [0, 1, 2], lens, qn, kn, vn)
+    for seq, L in enumerate(lens):
+        s_b.q[:], s_b.k[:], s_b.v[:] = qn[seq], kn[seq], vn[seq]
+        rt.attention_layer_token(p, s_b, layer, L, seq=seq)
+        assert np.allclose(batch[seq], s_b.xb, atol=1e-6)
+
+
+def test_errors_follow_reference_messages(dev):
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, ffi.DTYPE_F16, seq_len=64)
+    s = rt.malloc_run_state(p)
+    z = np.zeros((10, p.q_dim), np.float32)
+    zk = np.zeros((10, p.kv_dim), np.float32)
+    with pytest.raises(ffi.GrError, match="exceeds context"):
+        rt.prefill_attention_chunk(p, s, 0, 60, z, zk, zk)
+    with pytest.raises(ffi.GrError, match="layer"):
+        rt.attention_token(p, s, 5, 0)
+
+
+def test_qwen3next_state_step_matches_oracle(dev, orc):
+    """gr_qwen3next_state_step over 16 heads x 20 tokens == qwen3next_state_head_step
+    (math.rs:492-546) on the oracle, g given as the decay factor."""
+    from gguf_runner_amd import runtime as rt
+    H, d = 16, 128
+    p = rt.Config(n_layers=1, n_heads=1, n_kv_heads=1, head_dim=128, seq_len=8,
+                  ssm_n_heads=H, ssm_head_dim=d)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(4)
+    S = (0.1 * rng.standard_normal((H, d, d))).astype(np.float32)
+    rt.write_ssm_state(p, s, 0, S)
+    for t in range(20):
+        q = rng.standard_normal((H, d)).astype(np.float32)
+        k = rng.standard_normal((H, d)).astype(np.float32)
+        q /= np.linalg.norm(q, axis=1, keepdims=True) * np.sqrt(d)
+        k /= np.linalg.norm(k, axis=1, keepdims=True)
+        v = rng.standard_normal((H, d)).astype(np.float32)
+        g = np.exp(rng.uniform(-0.1, 0, H)).astype(np.float32)
+        beta = rng.uniform(0, 1, H).astype(np.float32)
+        out = rt.qwen3next_state_step(p, s, 0, q, k, v, g, beta).reshape(H, d)
+        for h in range(H):
+            s_new, o = orc.deltanet_head_step(S[h].reshape(-1), q[h], k[h], v[h], float(g[h]),
+                                              float(beta[h]))
+            S[h] = s_new.reshape(d, d)
+            assert float(np.abs(out[h] - o).max()) <= TOL_F32
+    assert float(np.abs(rt.read_ssm_state(p, s, 0) - S).max()) <= TOL_F32
+
+
+def test_qwen3next_prefill_matches_oracle_scan(dev, orc):
+    from gguf_runner_amd import runtime as rt
+    H, d, T = 8, 128, 300
+    p = rt.Config(n_layers=2, n_heads=1, n_kv_heads=1, head_dim=128, seq_len=8,
+                  ssm_n_heads=H, ssm_head_dim=d, rms_norm_eps=1e-6)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((T, H, d)).astype(np.float32)
+    k = rng.standard_normal((T, H, d)).astype(np.float32)
+    v = rng.standard_normal((T, H, d)).astype(np.float32)
+    gate = rng.uniform(-0.1, 0, (T, H)).astype(np.float32)
+    beta = rng.uniform(0, 1, (T, H)).astype(np.float32)
+    out = rt.qwen3next_prefill(p, s, 1, q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1),
+                               gate, beta).reshape(T, H, d)
+    ref, Sref = orc.deltanet_scan(q, k, v, gate, beta, np.zeros((H, d, d), np.float32),
+                                  eps=1e-6, n_threads=orc.env_threads())
+    assert float(np.abs(out - ref).max()) <= TOL_F32
+    assert float(np.abs(rt.read_ssm_state(p, s, 1) - Sref).max()) <= TOL_F32
