@@ -96,25 +96,80 @@ def cpu_baseline(lens, n_heads=32, n_kv=4, d=128, budget_s=10.0):
     orc = ge.load_oracle()
     threads = orc.max_threads()
     rng = np.random.default_rng(1003)
+    # one KV buffer sized for the longest sequence, reused (the timed region is the
+    # attention itself, not the data generation)
+    Lmax = max(lens)
+    kc = orc.f16_bits(rng.standard_normal((Lmax, n_kv * d), dtype=np.float32))
+    vc = orc.f16_bits(rng.standard_normal((Lmax, n_kv * d), dtype=np.float32))
+    q = rng.standard_normal(n_heads * d, dtype=np.float32)
     done_bytes = 0
     elapsed = 0.0
     n_done = 0
-    for L in lens:
-        kc = orc.f16_bits(rng.standard_normal((L, n_kv * d), dtype=np.float32))
-        vc = orc.f16_bits(rng.standard_normal((L, n_kv * d), dtype=np.float32))
-        q = rng.standard_normal(n_heads * d, dtype=np.float32)
+    keys = 0
+    while elapsed < budget_s and n_done < 64 * len(lens):
+        L = lens[n_done % len(lens)]
         t0 = time.perf_counter()
         orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
         elapsed += time.perf_counter() - t0
         done_bytes += L * n_kv * d * 2 * 2
+        keys += L
         n_done += 1
-        if elapsed >= budget_s:
-            break
     return {"value": round(done_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax) over the first "
-                      f"{n_done} of {len(lens)} config-3 sequences ({sum(lens[:n_done])} keys), "
-                      f"{elapsed:.2f} s"}
+            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax, parallel over "
+                      f"heads) on {n_done} config-3 sequences in batch order, cycling "
+                      f"({keys} keys, {elapsed:.2f} s)"}
+
+
+def deltanet_workload(dev, T, seed, H=16, d=128):
+    """Config 5: bf16 q/k/v ~N(0,1) (L2-normed in-kernel), beta = sigmoid(N(0,1)),
+    log-decay ~U(-0.1, 0), fp32 state; chunk-64 prefill."""
+    import torch
+    from gguf_runner_amd import ffi, ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((T, H, d), generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn((T, H, d), generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn((T, H, d), generator=g, device=dev, dtype=torch.bfloat16)
+    beta = torch.sigmoid(torch.randn((T, H), generator=g, device=dev))
+    gate = -0.1 * torch.rand((T, H), generator=g, device=dev)
+    state = torch.zeros((H, d, d), device=dev)
+    out = torch.empty((T, H, d), device=dev)
+    algo = ffi.DELTANET_CHUNKED if T >= 64 else ffi.DELTANET_RECURRENT
+    call = ops.DeltaNetCall(q, k, v, gate, beta, state, out, algo=algo)
+    return call, (q, k, v, beta, gate, state, out)
+
+
+def run_one(args, dev, stream, lens) -> int:
+    """A single workload, for rocprofv3 runs; prints one short JSON line."""
+    import torch
+    res = {"only": args.only, "steps": args.steps}
+    if args.only in ("decode3", "decode32k"):
+        ls = lens if args.only == "decode3" else [32768] * 16
+        call, nbytes, keep = decode_workload(dev, ls, 3)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+    elif args.only in ("prefill2k", "prefill8k"):
+        S = 2048 if args.only == "prefill2k" else 8192
+        call, flops, keep = prefill_workload(dev, S, 8)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "deltanet":
+        pcall, keep = deltanet_workload(dev, 4096, 5)
+        ms, _ = _timed(pcall, args.steps, args.warmup, stream)
+        dcall, keep2 = deltanet_workload(dev, 1, 6)
+        dms, _ = _timed(dcall, args.steps, args.warmup, stream)
+        res.update(prefill_ms=ms, prefill_tok_s=4096 / (ms * 1e-3), decode_step_ms=dms,
+                   decode_state_gbs=2 * 16 * 128 * 128 * 4 / (dms * 1e-3) / 1e9)
+    else:  # copy: calibration of the HBM byte counters with a plain 1 GiB device copy
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        a.fill_(1.0)
+        ms, _ = _timed(lambda: b.copy_(a), args.steps, args.warmup, stream)
+        res.update(ms=ms, bytes_read=a.numel() * 4, bytes_written=b.numel() * 4,
+                   gbs=2 * a.numel() * 4 / (ms * 1e-3) / 1e9)
+    print(json.dumps(res), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -123,6 +178,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="all",
+                    choices=["all", "decode3", "decode32k", "prefill2k", "prefill8k", "deltanet",
+                             "copy"],
+                    help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -139,6 +198,9 @@ def main() -> int:
 
     rng = np.random.default_rng(1003)
     lens = rng.integers(1024, 32768, size=16, endpoint=True).tolist()
+
+    if args.only != "all":
+        return run_one(args, dev, stream, lens)
 
     # headline: config 3 decode (ragged)
     dcall, dbytes, _keep_d = decode_workload(dev, lens, 3)
