@@ -199,25 +199,67 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     }
 }
 
-// Merge the split partials of one (sequence, head): out = sum_s o_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
+// Merge the split partials of one (sequence, head), one wavefront each:
+//   out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),  M = max_s m_s.
+// Lanes first cover splits (weights), then dimensions (weighted sums, splits
+// unrolled by 4 so the partial loads are in flight together).
+constexpr int kCombineWaves = 4;
+
 template <int D>
-__global__ __launch_bounds__(D) void decode_combine_kernel(const DecodeLaunch p) {
-    const int h = blockIdx.x;
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(const DecodeLaunch p) {
+    __shared__ float wts[kCombineWaves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = blockIdx.x * kCombineWaves + wave;
     const int s = blockIdx.y;
-    const int i = threadIdx.x;
+    if (h >= p.n_heads) return;
     const int len = p.kv_end[s] - p.kv_start[s];
     const int nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
     const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
+    float* out = p.out + ((size_t)s * p.n_heads + h) * D;
+    // pass 1: global max and denominator, lanes over splits
     float mx = -INFINITY;
-    for (int k = 0; k < nv; k++) mx = fmaxf(mx, p.ws_ml[(base + k) * 2]);
-    float lt = 0.0f, ot = 0.0f;
-    for (int k = 0; k < nv; k++) {
+    for (int k = lane; k < nv; k += 64) mx = fmaxf(mx, p.ws_ml[(base + k) * 2]);
+    mx = wave_max<64>(mx);
+    float lt = 0.0f;
+    for (int k = lane; k < nv; k += 64) {
         const float mk = p.ws_ml[(base + k) * 2];
-        const float a = (mk == -INFINITY) ? 0.0f : exp2f(mk - mx);
-        lt += p.ws_ml[(base + k) * 2 + 1] * a;
-        ot += p.ws_o[(base + k) * D + i] * a;
+        lt += p.ws_ml[(base + k) * 2 + 1] * (mk == -INFINITY ? 0.0f : exp2f(mk - mx));
     }
-    p.out[((size_t)s * p.n_heads + h) * D + i] = lt > 0.0f ? ot * (1.0f / lt) : 0.0f;
+    lt = wave_sum<64>(lt);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    // pass 2: weighted sum of o, lanes over dimensions; weights staged per 64 splits
+    constexpr int EPL = D / 64;
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; e++) acc[e] = 0.0f;
+    for (int k0 = 0; k0 < nv; k0 += 64) {
+        const int k = k0 + lane;
+        float wk = 0.0f;
+        if (k < nv) {
+            const float mk = p.ws_ml[(base + k) * 2];
+            wk = mk == -INFINITY ? 0.0f : exp2f(mk - mx);
+        }
+        wts[wave][lane] = wk;
+        __builtin_amdgcn_wave_barrier();
+        const int kn = min(64, nv - k0);
+        int kk = 0;
+        for (; kk + 4 <= kn; kk += 4) {
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const float* op = p.ws_o + (base + k0 + kk) * D + lane + 64 * e;
+                const float a0 = op[0], a1 = op[D], a2 = op[2 * D], a3 = op[3 * D];
+                acc[e] += wts[wave][kk] * a0 + wts[wave][kk + 1] * a1 + wts[wave][kk + 2] * a2 +
+                          wts[wave][kk + 3] * a3;
+            }
+        }
+        for (; kk < kn; kk++)
+#pragma unroll
+            for (int e = 0; e < EPL; e++)
+                acc[e] += wts[wave][kk] * p.ws_o[(base + k0 + kk) * D + lane + 64 * e];
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e++) out[lane + 64 * e] = acc[e] * inv;
 }
 
 template <typename KV, int D>
@@ -232,7 +274,8 @@ static hipError_t launch_kvmul(const DecodeLaunch& p, int kv_mul, hipStream_t st
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    decode_combine_kernel<D><<<dim3(p.n_heads, p.n_seq), D, 0, st>>>(p);
+    decode_combine_kernel<D><<<dim3((p.n_heads + kCombineWaves - 1) / kCombineWaves, p.n_seq),
+                               64 * kCombineWaves, 0, st>>>(p);
     return hipGetLastError();
 }
 
@@ -248,7 +291,8 @@ static hipError_t launch_dim(const DecodeLaunch& p, int kv_mul, hipStream_t st) 
 
 template <int D>
 static hipError_t launch_combine(const DecodeLaunch& p, hipStream_t st) {
-    decode_combine_kernel<D><<<dim3(p.n_heads, p.n_seq), D, 0, st>>>(p);
+    decode_combine_kernel<D><<<dim3((p.n_heads + kCombineWaves - 1) / kCombineWaves, p.n_seq),
+                               64 * kCombineWaves, 0, st>>>(p);
     return hipGetLastError();
 }
 

@@ -1,4 +1,4 @@
-// Per-token Q/K/V preparation on the device, one wavefront per head row:
+// Per-token Q/K/V preparation on the device (one workgroup per token):
 //   qkv_bias_and_norm's QK RMSNorm  (reference inference.rs:2535-2572 -> math.rs:164-184)
 //   apply_rope_qk                   (inference.rs:1817-1874; angle as rebuild_rope_cache 1485-1523)
 //   Gemma3 q *= 1/sqrt(head_dim)    (inference.rs:1871-1873)
@@ -13,122 +13,156 @@ namespace gr {
 constexpr int kPrepThreads = 256;
 constexpr int kPrepRowsPerBlock = kPrepThreads / 64;
 
-__device__ __forceinline__ float load_elem(const void* base, size_t idx, int dt) {
-    if (dt == GR_DTYPE_F32) return ((const float*)base)[idx];
-    const uint16_t b = ((const uint16_t*)base)[idx];
-    return dt == GR_DTYPE_F16 ? f16_to_f32(b) : bf16_to_f32(b);
+// 8 consecutive elements (one 16-byte chunk of a 16-bit row, two of an f32 row).
+__device__ __forceinline__ void load8(const void* base, size_t idx, int dt, float* v) {
+    if (dt == GR_DTYPE_F32) {
+        const float4 a = *(const float4*)((const float*)base + idx);
+        const float4 b = *(const float4*)((const float*)base + idx + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        return;
+    }
+    const uint4 u = *(const uint4*)((const uint16_t*)base + idx);
+    if (dt == GR_DTYPE_F16) unpack16<F16>(u, v);
+    else unpack16<BF16>(u, v);
 }
 
-__device__ __forceinline__ void store_elem(void* base, size_t idx, int dt, float v) {
-    if (dt == GR_DTYPE_F32)
-        ((float*)base)[idx] = v;
-    else
-        ((uint16_t*)base)[idx] = dt == GR_DTYPE_F16 ? f32_to_f16(v) : f32_to_bf16(v);
+__device__ __forceinline__ void store8(void* base, size_t idx, int dt, const float* v) {
+    if (dt == GR_DTYPE_F32) {
+        *(float4*)((float*)base + idx) = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)((float*)base + idx + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        return;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint16_t lo = dt == GR_DTYPE_F16 ? f32_to_f16(v[2 * k]) : f32_to_bf16(v[2 * k]);
+        const uint16_t hi = dt == GR_DTYPE_F16 ? f32_to_f16(v[2 * k + 1]) : f32_to_bf16(v[2 * k + 1]);
+        w[k] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *(uint4*)((uint16_t*)base + idx) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Row r of the launch: token i = r / rows_per_token, then Q heads, K heads, V heads.
+// One workgroup per token.  The token's RoPE cos/sin (rope_dim/2 values, the
+// rebuild_rope_cache angle (pos*freq)*scale) are computed once into LDS; then
+// each lane owns 8 consecutive elements of a head row, LPR = D/8 lanes cover a
+// row and a wave processes 64/LPR rows at once: Q heads, K heads, V heads.
 template <int D>
 __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLaunch p) {
-    constexpr int EPL = D / 64;  // elements per lane
-    __shared__ float row_buf[kPrepRowsPerBlock][D];
+    constexpr int LPR = D / 8;        // lanes per row
+    constexpr int RPW = 64 / LPR;     // rows per wave step
+    __shared__ float row_buf[kPrepRowsPerBlock][RPW][D];
+    __shared__ float cs_t[D / 2], sn_t[D / 2];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    const int rsub = lane / LPR;      // row of this lane within the wave step
+    const int c8 = (lane % LPR) * 8;  // first element owned by this lane
+    const int i = blockIdx.x;
     const int rows_per_token = p.n_heads + 2 * p.n_kv_heads;
-    const long total = (long)p.n_tokens * rows_per_token;
-    const long r = (long)blockIdx.x * kPrepRowsPerBlock + wave;
-    const bool active = r < total;
-    const long rr = active ? r : 0;
-    const int i = (int)(rr / rows_per_token);
-    const int hr = (int)(rr % rows_per_token);
-    const int kind = hr < p.n_heads ? 0 : (hr < p.n_heads + p.n_kv_heads ? 1 : 2);  // q, k, v
-    const int head = kind == 0 ? hr : (kind == 1 ? hr - p.n_heads : hr - p.n_heads - p.n_kv_heads);
-    const bool skip_q = (kind == 0 && p.q_out == nullptr);
-
-    float x[EPL];
-    const void* src = kind == 0 ? p.q : (kind == 1 ? p.k : p.v);
-    const int64_t rs = kind == 0 ? p.q_row_stride : p.kv_row_stride;
-    const size_t base = (size_t)i * rs + (size_t)head * D;
-#pragma unroll
-    for (int e = 0; e < EPL; e++) x[e] = active && !skip_q ? load_elem(src, base + lane + 64 * e, p.in_dtype) : 0.0f;
-
     const int64_t pos = p.pos ? (int64_t)p.pos[i] : p.pos0 + i;
-
-    if (kind != 2) {
-        // QK RMSNorm: ss = sum(x^2)/d + eps; x = w * ((1/sqrt(ss)) * x).
-        const float* w = kind == 0 ? p.q_norm : p.k_norm;
-        if (w) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) ss += x[e] * x[e];
-            ss = wave_sum<64>(ss);
-            ss = ss / (float)D + p.eps;
-            const float inv = 1.0f / sqrtf(ss);
-#pragma unroll
-            for (int e = 0; e < EPL; e++) x[e] = w[lane + 64 * e] * (inv * x[e]);
-        }
-    }
-    // Stage the row so that RoPE can pair elements held by other lanes.
-#pragma unroll
-    for (int e = 0; e < EPL; e++) row_buf[wave][lane + 64 * e] = x[e];
-    __syncthreads();
-    if (kind != 2 && p.rope_mode != GR_ROPE_NONE) {
-        const int half = p.rope_dim / 2;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            const int idx = lane + 64 * e;
-            int fi, partner;
-            bool first;
-            if (p.rope_mode == GR_ROPE_NEOX) {
-                if (idx >= p.rope_dim) continue;  // partial RoPE: tail untouched
-                first = idx < half;
-                fi = first ? idx : idx - half;
-                partner = first ? idx + half : idx - half;
-            } else {
-                first = (idx & 1) == 0;
-                fi = idx >> 1;
-                partner = idx ^ 1;
-            }
-            const float val = ((float)pos * p.rope_freqs[fi]) * p.rope_scale;
+    const bool rope = p.rope_mode != GR_ROPE_NONE;
+    const int half = p.rope_dim / 2;
+    if (rope) {
+        for (int f = threadIdx.x; f < half; f += kPrepThreads) {
+            const float val = ((float)pos * p.rope_freqs[f]) * p.rope_scale;
             float sn, cs;
             sincosf(val, &sn, &cs);
-            const float mine = row_buf[wave][idx];
-            const float other = row_buf[wave][partner];
-            // (v0, v1) -> (v0*c - v1*s, v0*s + v1*c)
-            x[e] = first ? mine * cs - other * sn : other * sn + mine * cs;
+            cs_t[f] = cs;
+            sn_t[f] = sn;
         }
     }
-    if (kind == 0 && p.gemma_q_scale) {
-        const float sc = 1.0f / sqrtf((float)D);
+    __syncthreads();
+    float* rb = row_buf[wave][rsub];
+    const int64_t row = p.cache_row ? (int64_t)p.cache_row[i] : pos;
+    const int64_t sq = p.cache_seq ? (int64_t)p.cache_seq[i] : 0;
+
+    for (int hr0 = wave * RPW; hr0 < rows_per_token; hr0 += kPrepRowsPerBlock * RPW) {
+        const int hr = hr0 + rsub;
+        const bool valid = hr < rows_per_token;
+        const int hrc = valid ? hr : rows_per_token - 1;
+        const int kind = hrc < p.n_heads ? 0 : (hrc < p.n_heads + p.n_kv_heads ? 1 : 2);  // q, k, v
+        const int head = kind == 0 ? hrc : (kind == 1 ? hrc - p.n_heads : hrc - p.n_heads - p.n_kv_heads);
+        const bool skip = !valid || (kind == 0 && p.q_out == nullptr);
+        const void* src = kind == 0 ? p.q : (kind == 1 ? p.k : p.v);
+        const int64_t rs = kind == 0 ? p.q_row_stride : p.kv_row_stride;
+        float x[8];
+        if (!skip) load8(src, (size_t)i * rs + (size_t)head * D + c8, p.in_dtype, x);
+        else
 #pragma unroll
-        for (int e = 0; e < EPL; e++) x[e] *= sc;
-    }
-    if (!active || skip_q) return;
-    if (kind == 0) {
-        const size_t ob = ((size_t)i * p.n_heads + head) * D;
+            for (int e = 0; e < 8; e++) x[e] = 0.0f;
+        if (kind != 2) {
+            // QK RMSNorm: ss = sum(x^2)/d + eps; x = w * ((1/sqrt(ss)) * x).
+            const float* w = kind == 0 ? p.q_norm : p.k_norm;
+            float ss = 0.0f;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            const float xs = x[e] * p.q_out_scale;
-            store_elem(p.q_out, ob + lane + 64 * e, p.q_out_dtype, xs);
-            if (p.q_out_lo) {
-                const float hi = load_elem(p.q_out, ob + lane + 64 * e, p.q_out_dtype);
-                store_elem(p.q_out_lo, ob + lane + 64 * e, p.q_out_dtype, xs - hi);
+            for (int e = 0; e < 8; e++) ss += x[e] * x[e];
+            ss = wave_sum<LPR>(ss);  // lanes of other rows never mix: groups are LPR-aligned
+            if (w) {
+                const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = w[c8 + e] * (inv * x[e]);
+            }
+            if (rope) {
+                if (p.rope_mode == GR_ROPE_ADJACENT) {
+                    // pairs (2j, 2j+1) sit inside the lane's 8 elements
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const int fi = (c8 + e) >> 1;
+                        const float cs = cs_t[fi], sn = sn_t[fi];
+                        const float v0 = x[e], v1 = x[e + 1];
+                        x[e] = v0 * cs - v1 * sn;
+                        x[e + 1] = v0 * sn + v1 * cs;
+                    }
+                } else {
+                    // NeoX pairs (i, i + rope_dim/2) live in other lanes: stage the row
+#pragma unroll
+                    for (int e = 0; e < 8; e++) rb[c8 + e] = x[e];
+                    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const int idx = c8 + e;
+                        if (idx >= p.rope_dim) continue;  // partial RoPE: tail untouched
+                        const bool first = idx < half;
+                        const int fi = first ? idx : idx - half;
+                        const float other = rb[first ? idx + half : idx - half];
+                        const float cs = cs_t[fi], sn = sn_t[fi];
+                        // (v0, v1) -> (v0*c - v1*s, v0*s + v1*c)
+                        x[e] = first ? x[e] * cs - other * sn : other * sn + x[e] * cs;
+                    }
+                    __builtin_amdgcn_wave_barrier();  // reads done before the next rows' stores
+                }
+            }
+            if (kind == 0 && p.gemma_q_scale) {
+                const float sc = 1.0f / sqrtf((float)D);
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] *= sc;
             }
         }
-    } else {
-        const int64_t row = p.cache_row ? (int64_t)p.cache_row[i] : pos;
-        const int64_t sq = p.cache_seq ? (int64_t)p.cache_seq[i] : 0;
-        void* dst = kind == 1 ? p.k_cache : p.v_cache;
-        const size_t ob = (size_t)sq * p.cache_seq_stride + (size_t)row * p.cache_row_stride +
-                          (size_t)head * D;
+        if (skip) continue;
+        if (kind == 0) {
+            const size_t ob = ((size_t)i * p.n_heads + head) * D + c8;
+            float xs[8];
 #pragma unroll
-        for (int e = 0; e < EPL; e++) store_elem(dst, ob + lane + 64 * e, p.cache_dtype, x[e]);
+            for (int e = 0; e < 8; e++) xs[e] = x[e] * p.q_out_scale;
+            store8(p.q_out, ob, p.q_out_dtype, xs);
+            if (p.q_out_lo) {
+                float hi[8], lo[8];
+                load8(p.q_out, ob, p.q_out_dtype, hi);
+#pragma unroll
+                for (int e = 0; e < 8; e++) lo[e] = xs[e] - hi[e];
+                store8(p.q_out_lo, ob, p.q_out_dtype, lo);
+            }
+        } else {
+            void* dst = kind == 1 ? p.k_cache : p.v_cache;
+            const size_t ob = (size_t)sq * p.cache_seq_stride + (size_t)row * p.cache_row_stride +
+                              (size_t)head * D + c8;
+            store8(dst, ob, p.cache_dtype, x);
+        }
     }
 }
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st) {
-    const long rows = (long)p.n_tokens * (p.n_heads + 2 * p.n_kv_heads);
-    const unsigned blocks = (unsigned)((rows + kPrepRowsPerBlock - 1) / kPrepRowsPerBlock);
-    if (blocks == 0) return hipSuccess;
+    if (p.n_tokens <= 0) return hipSuccess;
+    const unsigned blocks = (unsigned)p.n_tokens;
     switch (p.head_dim) {
         case 64: qkv_prep_kernel<64><<<blocks, kPrepThreads, 0, st>>>(p); break;
         case 128: qkv_prep_kernel<128><<<blocks, kPrepThreads, 0, st>>>(p); break;
