@@ -39,6 +39,11 @@ def _timed(fn, steps, warmup, stream):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    # settle clocks and TLBs on freshly allocated buffers: at least ~0.2 s of work
+    t_end = time.perf_counter() + 0.2
+    while time.perf_counter() < t_end:
+        fn()
+        torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()

@@ -48,16 +48,24 @@ struct Mfma16<BF16> {
 
 constexpr int kMdThreads = 256;
 constexpr int kMdWaves = kMdThreads / 64;
-constexpr int kMdTile = 32;  // keys per wave iteration
 
-template <typename DT, int D>
+// Raise a row's reference maximum only when a tile exceeds it by more than
+// this (log2 units); P = 2^(s - m_ref) <= 2^8 meanwhile and O needs no rescale.
+constexpr float kMdLazyRescale = 8.0f;
+
+// NSUB groups of 32 keys per wave iteration.  1 is used: with 2, the d128
+// kernel needs 300 registers (one wave per SIMD) and measured slower than two
+// waves per SIMD streaming 32-key tiles.
+template <typename DT, int D, int NSUB>
 __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLaunch p) {
     using M = Mfma16<DT>;
     constexpr bool kSplit = M::kSplit;
+    constexpr int TILE = 32 * NSUB;              // keys per wave iteration
+    constexpr int NS16 = TILE / 16;              // 16-key score sub-tiles
     constexpr int DC = D / 8;                    // 16-byte chunks per row
     constexpr int KS = D / 32;                   // MFMA k-steps over d
-    constexpr int VTASK = (kMdTile / 4) * DC / 64;  // 4-key x 16-byte V tasks per lane
-    constexpr int VS = kMdTile + 4;              // V^T row stride (elements)
+    constexpr int VTASK = (TILE / 4) * DC / 64;  // 4-key x 16-byte V tasks per lane
+    constexpr int VS = TILE + 4;                 // V^T row stride (elements)
     static_assert(VTASK >= 1, "tile");
 
     // LDS: per-wave V^T tiles during the key loop, then (aliased) the wave merge.
@@ -105,17 +113,36 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         }
     }
 
-    const uint16_t* kc = (const uint16_t*)p.k_cache + (size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D;
-    const uint16_t* vc = (const uint16_t*)p.v_cache + (size_t)(p.seq_slot ? p.seq_slot[s] : s) * p.seq_stride + (size_t)g * D;
+    const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
+    const uint16_t* kc = (const uint16_t*)p.k_cache + slot * p.seq_stride + (size_t)g * D;
+    const uint16_t* vc = (const uint16_t*)p.v_cache + slot * p.seq_stride + (size_t)g * D;
     const int64_t rs = p.row_stride;
 
-    uint4 kr[2][KS];
+    uint4 kr[NS16][KS];
     uint4 vr[VTASK][4];
     auto load_tile = [&](int t0) {
+        if (t0 + TILE <= t_stop) {  // whole tile inside the split: plain strided rows
+            const uint16_t* kt = kc + (int64_t)t0 * rs + 8 * g4;
+            const uint16_t* vtp = vc + (int64_t)t0 * rs;
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++) {
-            int key = t0 + 16 * sb + l16;
-            key = key < t_stop ? key : t_stop - 1;
+            for (int sb = 0; sb < NS16; sb++) {
+                const uint16_t* row = kt + (int64_t)(16 * sb + l16) * rs;
+#pragma unroll
+                for (int k = 0; k < KS; k++) kr[sb][k] = *(const uint4*)(row + 32 * k);
+            }
+#pragma unroll
+            for (int u = 0; u < VTASK; u++) {
+                const int task = lane + 64 * u;
+                const int dc = task % DC, kg = task / DC;
+                const uint16_t* v0 = vtp + (int64_t)(4 * kg) * rs + 8 * dc;
+#pragma unroll
+                for (int r = 0; r < 4; r++) vr[u][r] = *(const uint4*)(v0 + r * rs);
+            }
+            return;
+        }
+#pragma unroll
+        for (int sb = 0; sb < NS16; sb++) {
+            const int key = min(t0 + 16 * sb + l16, t_stop - 1);
             const uint16_t* row = kc + (int64_t)key * rs + 8 * g4;
 #pragma unroll
             for (int k = 0; k < KS; k++) kr[sb][k] = *(const uint4*)(row + 32 * k);
@@ -126,8 +153,7 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
             const int dc = task % DC, kg = task / DC;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                int key = t0 + 4 * kg + r;
-                key = key < t_stop ? key : t_stop - 1;
+                const int key = min(t0 + 4 * kg + r, t_stop - 1);
                 vr[u][r] = *(const uint4*)(vc + (int64_t)key * rs + 8 * dc);
             }
         }
@@ -138,11 +164,11 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     for (int dt = 0; dt < D / 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrow = -1e30f, lrow = 0.0f;
 
-    const int n_tiles = (t_stop - t_begin + kMdTile - 1) / kMdTile;
+    const int n_tiles = (t_stop - t_begin + TILE - 1) / TILE;
     int it = wave;
-    if (it < n_tiles) load_tile(t_begin + it * kMdTile);
+    if (it < n_tiles) load_tile(t_begin + it * TILE);
     for (; it < n_tiles; it += kMdWaves) {
-        const int t0 = t_begin + it * kMdTile;
+        const int t0 = t_begin + it * TILE;
         // V tile -> LDS, transposed: Vt[d][key]
 #pragma unroll
         for (int u = 0; u < VTASK; u++) {
@@ -166,70 +192,81 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
                 *(uint2*)(vt + (8 * dc + dd) * VS + 4 * kg) = make_uint2(lo, hi);
             }
         }
-        // scores for the two 16-key sub-tiles
-        f32x4 sacc[2];
+        // scores for the 16-key sub-tiles
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 sacc[NS16];
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++) {
-            sacc[sb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int sb = 0; sb < NS16; sb++) {
 #pragma unroll
             for (int k = 0; k < KS; k++) {
-                sacc[sb] = M::mma(kr[sb][k], qf[k], sacc[sb]);
+                sacc[sb] = M::mma(kr[sb][k], qf[k], k == 0 ? zero : sacc[sb]);
                 if constexpr (kSplit) sacc[sb] = M::mma(kr[sb][k], qfl[k], sacc[sb]);
             }
         }
         // prefetch the wave's next tile while this one is finished
-        if (it + kMdWaves < n_tiles) load_tile(t_begin + (it + kMdWaves) * kMdTile);
+        if (it + kMdWaves < n_tiles) load_tile(t_begin + (it + kMdWaves) * TILE);
 
         // S^T register j of sub-tile sb holds key t0 + 16 sb + 4 g4 + j (query l16).
-        float mx = -INFINITY;
+        float sv[4 * NS16];
+        const bool tail = t0 + TILE > t_stop;
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++)
+        for (int sb = 0; sb < NS16; sb++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int key = t0 + 16 * sb + 4 * g4 + j;
-                const float sv = key < t_stop ? sacc[sb][j] : -INFINITY;
-                sacc[sb][j] = sv;
-                mx = fmaxf(mx, sv);
+                sv[4 * sb + j] = (!tail || key < t_stop) ? sacc[sb][j] : -INFINITY;
             }
+        float mx = sv[0];
+#pragma unroll
+        for (int e = 1; e < 4 * NS16; e++) mx = fmaxf(mx, sv[e]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(mrow, mx);
-        const float alpha = exp2f(mrow - mnew);
-        mrow = mnew;
-        float pv[8];
+        if (__any(mx > mrow + kMdLazyRescale)) {
+            const float mnew = fmaxf(mrow, mx);
+            const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+            mrow = mnew;
+            lrow *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < D / 16; dt++) o[dt] *= alpha;
+        }
+        float pv[4 * NS16];
         float psum = 0.0f;
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                pv[4 * sb + j] = exp2f(sacc[sb][j] - mnew);
-                psum += pv[4 * sb + j];
-            }
-        lrow = lrow * alpha + psum;
-        // B operand P^T: k-slot r <-> key 16 (r / 4) + 4 g4 + r % 4 (matches pv order)
-        uint32_t ph[4], pl[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const uint16_t h0 = M::cvt(pv[2 * w]), h1 = M::cvt(pv[2 * w + 1]);
-            ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-            if constexpr (kSplit)
-                pl[w] = (uint32_t)M::cvt(pv[2 * w] - M::back(h0)) |
-                        ((uint32_t)M::cvt(pv[2 * w + 1] - M::back(h1)) << 16);
+        for (int e = 0; e < 4 * NS16; e++) {
+            pv[e] = __builtin_amdgcn_exp2f(sv[e] - mrow);
+            psum += pv[e];
         }
-        const uint4 pf = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-        const uint4 pfl = kSplit ? make_uint4(pl[0], pl[1], pl[2], pl[3]) : pf;
+        lrow += psum;
+        // B operand P^T per 32-key k-step kk: k-slot r <-> key 32 kk + 16 (r/4) + 4 g4 + r%4
+        uint4 pf[NSUB], pfl[kSplit ? NSUB : 1];
+#pragma unroll
+        for (int kk = 0; kk < NSUB; kk++) {
+            uint32_t ph[4], pl[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float a0 = pv[8 * kk + 2 * w], a1 = pv[8 * kk + 2 * w + 1];
+                const uint16_t h0 = M::cvt(a0), h1 = M::cvt(a1);
+                ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                if constexpr (kSplit)
+                    pl[w] = (uint32_t)M::cvt(a0 - M::back(h0)) | ((uint32_t)M::cvt(a1 - M::back(h1)) << 16);
+            }
+            pf[kk] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+            if constexpr (kSplit) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        }
         // LDS operations of one wave complete in issue order, so the V^T reads
         // below see this wave's stores; the barrier only pins the compiler's order.
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int dt = 0; dt < D / 16; dt++) {
-            o[dt] *= alpha;
             const uint16_t* vrow = vt + (16 * dt + l16) * VS + 4 * g4;
-            const uint2 lo = *(const uint2*)(vrow);
-            const uint2 hi = *(const uint2*)(vrow + 16);
-            const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            o[dt] = M::mma(a, pf, o[dt]);
-            if constexpr (kSplit) o[dt] = M::mma(a, pfl, o[dt]);
+#pragma unroll
+            for (int kk = 0; kk < NSUB; kk++) {
+                const uint2 lo = *(const uint2*)(vrow + 32 * kk);
+                const uint2 hi = *(const uint2*)(vrow + 32 * kk + 16);
+                const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                o[dt] = M::mma(a, pf[kk], o[dt]);
+                if constexpr (kSplit) o[dt] = M::mma(a, pfl[kk], o[dt]);
+            }
         }
         __builtin_amdgcn_wave_barrier();  // V^T reads done before the next tile overwrites it
     }
@@ -277,8 +314,8 @@ template <typename DT>
 static hipError_t launch_mfma_dt(const DecodeLaunch& p, hipStream_t st) {
     dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
     switch (p.head_dim) {
-        case 128: decode_mfma_kernel<DT, 128><<<grid, kMdThreads, 0, st>>>(p); break;
-        case 256: decode_mfma_kernel<DT, 256><<<grid, kMdThreads, 0, st>>>(p); break;
+        case 128: decode_mfma_kernel<DT, 128, 1><<<grid, kMdThreads, 0, st>>>(p); break;
+        case 256: decode_mfma_kernel<DT, 256, 1><<<grid, kMdThreads, 0, st>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
