@@ -140,10 +140,11 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     extern __shared__ float smem[];
     float* qs = smem;                   // [C][DS] normalised q
     float* ks = qs + C * DS;            // [C][DS] normalised k
-    float* As = ks + C * DS;            // [C][C+1]
-    float* Ts = As + C * (C + 1);       // [C][C+1] (I + A)^-1
-    float* lg = Ts + C * (C + 1);       // [C] in-chunk cumulative log decay
+    constexpr int AS = C + 4;           // A row stride (16-byte aligned rows)
+    float* As = ks + C * DS;            // [C][AS] strictly lower-triangular A
+    float* lg = As + C * AS;            // [C] in-chunk cumulative log decay
     float* bt = lg + C;                 // [C] beta
+    float* gm = bt + C;                 // [C] gamma_t = exp(lg[t])
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x, h = blockIdx.y;
@@ -189,6 +190,7 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
             if (lane >= off) gl += o;
         }
         lg[lane] = gl;
+        gm[lane] = expf(gl);
         bt[lane] = valid ? finite_or_zero(p.beta[(size_t)(t0 + lane) * H + h]) : 0.0f;
     }
     __syncthreads();
@@ -216,57 +218,62 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
         for (int u = 0; u < 16; u++) {
             const int s = sb + u;
             const float decay = s <= t ? expf(lt - lg[s]) : 0.0f;
-            As[t * (C + 1) + s] = s < t ? bet * decay * akk[u] : 0.0f;
+            As[t * AS + s] = s < t ? bet * decay * akk[u] : 0.0f;
             ws[ChunkWs<D>::P + t * C + s] = s <= t ? decay * aqk[u] : 0.0f;
         }
     }
     __syncthreads();
 
-    // 3. T = (I + A)^-1 (unit lower triangular) by forward substitution, one
-    //    column per lane of wave 0, kept in LDS; waves 1-3 meanwhile write
-    //    Qg = gamma_t q_t and Kd^T[j][s] = (gamma_last / gamma_s) k_s[j].
+    // 3. Qg = gamma_t q_t and Kd^T[j][s] = (gamma_last / gamma_s) k_s[j]
     const float lglast = lg[C - 1];
-    if (wave == 0) {
-        const int cc = lane;
-        for (int t = 0; t < C; t++) {
-            float acc = t == cc ? 1.0f : 0.0f;
-            for (int s2 = cc; s2 < t; s2++) acc = fmaf(-As[t * (C + 1) + s2], Ts[s2 * (C + 1) + cc], acc);
-            Ts[t * (C + 1) + cc] = t >= cc ? acc : 0.0f;
-        }
-    } else {
-        for (int e = tid - 64; e < C * D; e += kChunkThreads - 64) {
-            const int t = e / D, j = e % D;
-            ws[ChunkWs<D>::QG + e] = expf(lg[t]) * qs[t * DS + j];
-        }
-        for (int e = tid - 64; e < D * C; e += kChunkThreads - 64) {
-            const int j = e / C, s2 = e % C;
-            ws[ChunkWs<D>::KDT + e] = expf(lglast - lg[s2]) * ks[s2 * DS + j];
-        }
+    for (int e = tid; e < C * D; e += kChunkThreads) {
+        const int t = e / D, j = e % D;
+        ws[ChunkWs<D>::QG + e] = gm[t] * qs[t * DS + j];
     }
-    __syncthreads();
+    for (int e = tid; e < D * C; e += kChunkThreads) {
+        const int j = e / C, s2 = e % C;
+        ws[ChunkWs<D>::KDT + e] = expf(lglast - lg[s2]) * ks[s2 * DS + j];
+    }
 
-    // 4. [U | W] = T [beta V | beta gamma K]: one right-hand-side column per thread,
-    //    rows in groups of 8 accumulators.
+    // 4. [U | W] = (I + A)^-1 [beta V | beta gamma K] by blocked forward
+    //    substitution, one right-hand-side column per thread: 4 blocks of 16 rows;
+    //    block b first subtracts A[b][b'] X[b'] for the earlier blocks (read back
+    //    from this thread's own column of the workspace), then solves its unit
+    //    lower-triangular 16x16 diagonal block in registers.
+    constexpr int RB = 16;
     for (int col = tid; col < 2 * D; col += kChunkThreads) {
         const bool isv = col < D;
         const int cc = isv ? col : col - D;
         float* dst = ws + (isv ? ChunkWs<D>::U : ChunkWs<D>::W);
-        for (int tb = 0; tb < C; tb += 8) {
-            float x8[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) x8[u] = 0.0f;
-            for (int s2 = 0; s2 < tb + 8; s2++) {
-                float r;
-                if (isv)
-                    r = s2 < Cn ? bt[s2] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + s2) * H + h) * D + cc, p.in_dtype))
-                                : 0.0f;
-                else
-                    r = bt[s2] * expf(lg[s2]) * ks[s2 * DS + cc];
+        for (int b = 0; b < C / RB; b++) {
+            float x[RB];
 #pragma unroll
-                for (int u = 0; u < 8; u++) x8[u] = fmaf(Ts[(tb + u) * (C + 1) + s2], r, x8[u]);
+            for (int tt = 0; tt < RB; tt++) {
+                const int t = b * RB + tt;
+                x[tt] = isv ? (t < Cn ? bt[t] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + t) * H + h) * D + cc, p.in_dtype))
+                                      : 0.0f)
+                            : bt[t] * gm[t] * ks[t * DS + cc];
+            }
+            for (int bp = 0; bp < b; bp++) {
+                float xp[RB];
+#pragma unroll
+                for (int ss = 0; ss < RB; ss++) xp[ss] = dst[(bp * RB + ss) * D + cc];
+#pragma unroll
+                for (int tt = 0; tt < RB; tt++) {
+                    const float* arow = As + (b * RB + tt) * AS + bp * RB;
+#pragma unroll
+                    for (int ss = 0; ss < RB; ss++) x[tt] = fmaf(-arow[ss], xp[ss], x[tt]);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 8; u++) dst[(tb + u) * D + cc] = x8[u];
+            for (int tt = 0; tt < RB; tt++) {
+                const float* arow = As + (b * RB + tt) * AS + b * RB;
+#pragma unroll
+                for (int ss = 0; ss < tt; ss++) x[tt] = fmaf(-arow[ss], x[ss], x[tt]);
+            }
+#pragma unroll
+            for (int tt = 0; tt < RB; tt++) dst[(b * RB + tt) * D + cc] = x[tt];
         }
     }
     if (tid == 0) ws[ChunkWs<D>::GL] = expf(lglast);
@@ -390,7 +397,7 @@ hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     if (p.head_dim != 128) return hipErrorInvalidValue;
     constexpr int D = 128;
-    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + 2 * kChunk * (kChunk + 1) + 2 * kChunk) * sizeof(float);
+    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 3 * kChunk) * sizeof(float);
     hipError_t ea = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ea != hipSuccess) return ea;
