@@ -56,6 +56,20 @@ def _timed(fn, steps, warmup, stream):
     return ev0.elapsed_time(ev1) / steps, wall * 1e3 / steps  # ms per step (events, wall)
 
 
+def measured_traffic(name="decode_mfma_f16_d128_config3.md"):
+    """HBM bytes per decode call from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE of both kernels, calibrated against a plain copy), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_call:"):
+                    return int(float(ln.split(":")[1]))
+    except OSError:
+        pass
+    return None
+
+
 def decode_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
     import torch
     from gguf_runner_amd import ops
@@ -246,7 +260,8 @@ def main() -> int:
                                "L~U[1024,32768] (seed 1003), 32 Q / 4 KV heads, d128, f16 KV",
                    "seq_lens_sum": int(sum(lens)), "bytes_per_step": dbytes},
         "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "kernel": "gr_decode_attention (split kernel + combine), hipEvent-timed"},
         "decode_32k": {"gbs": round(t_gbs, 2), "ms": round(t_ms, 5),
                        "frac_of_hbm": round(t_gbs / HBM_PEAK_GBS, 4), "bytes": tbytes},
