@@ -9,6 +9,7 @@ call (split kernel + combine kernel) over the whole batch.
 
 Also reported in the same line:
   decode_32k   -- the decode target run (all 16 sequences at 32768 keys)
+  decode_32k_q8 -- the same over a Q8 cache (int8 rows + one f32 scale per row)
   prefill      -- config 2 (Llama-3-8B-shaped causal prefill, 2048 tokens, f16,
                   RoPE fused) and the 8k target run, in TFLOP/s with
                   flops = 4 * Hq * d * sum_q visible(q)
@@ -86,6 +87,31 @@ def decode_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
     call = ops.DecodeCall(q, kc, vc, st, en, out, max_kv_len=max_len)
     nbytes = int(sum(lens)) * n_kv * d * 2 * 2
     return call, nbytes, (q, kc, vc, st, en, out)
+
+
+def decode_q8_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128, block=False):
+    """Config-3 shape over a Q8 cache (int8 codes ~U[-127, 127], f32 scales)."""
+    import torch
+    from gguf_runner_amd import ops
+    n_seq = len(lens)
+    max_len = int(max(lens))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((n_seq, n_heads, d), generator=g, device=dev, dtype=torch.float32)
+    kc = torch.randint(-127, 128, (n_seq, max_len, n_kv, d), generator=g, device=dev,
+                       dtype=torch.int8)
+    vc = torch.randint(-127, 128, (n_seq, max_len, n_kv, d), generator=g, device=dev,
+                       dtype=torch.int8)
+    per = n_kv * d // 32 if block else 1
+    ks = torch.rand((n_seq, max_len, per), generator=g, device=dev) * 0.02 + 0.01
+    vs = torch.rand((n_seq, max_len, per), generator=g, device=dev) * 0.02 + 0.01
+    st = torch.zeros(n_seq, dtype=torch.int32, device=dev)
+    en = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    call = ops.DecodeCall(q, kc, vc, st, en, out, max_kv_len=max_len, k_scale=ks, v_scale=vs,
+                          q8_block=block)
+    nbytes = int(sum(lens)) * (n_kv * d * 2 + 2 * per * 4)
+    return call, nbytes, (q, kc, vc, ks, vs, st, en, out)
 
 
 def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
@@ -168,6 +194,11 @@ def run_one(args, dev, stream, lens) -> int:
         call, nbytes, keep = decode_workload(dev, ls, 3)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+    elif args.only in ("decode32k_q8", "decode32k_q8b"):
+        call, nbytes, keep = decode_q8_workload(dev, [32768] * 16, 34,
+                                                block=args.only.endswith("b"))
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
     elif args.only in ("prefill2k", "prefill8k"):
         S = 2048 if args.only == "prefill2k" else 8192
         call, flops, keep = prefill_workload(dev, S, 8)
@@ -198,8 +229,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "prefill2k", "prefill8k", "deltanet",
-                             "copy"],
+                    choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b",
+                             "prefill2k", "prefill8k", "deltanet", "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -233,6 +264,12 @@ def main() -> int:
     t_gbs = tbytes / (t_ms * 1e-3) / 1e9
     del _keep_t, tcall
 
+    # the same target run over a Q8 cache (row scales, the reference's Q8 format)
+    qcall, qbytes, _keep_q = decode_q8_workload(dev, [32768] * 16, 34)
+    q_ms, _ = _timed(qcall, args.steps, args.warmup, stream)
+    q_gbs = qbytes / (q_ms * 1e-3) / 1e9
+    del _keep_q, qcall
+
     pre = {}
     for S, seed in ((2048, 2), (8192, 8)):
         pcall, flops, _keep_p = prefill_workload(dev, S, seed)
@@ -265,6 +302,8 @@ def main() -> int:
                      "kernel": "gr_decode_attention (split kernel + combine), hipEvent-timed"},
         "decode_32k": {"gbs": round(t_gbs, 2), "ms": round(t_ms, 5),
                        "frac_of_hbm": round(t_gbs / HBM_PEAK_GBS, 4), "bytes": tbytes},
+        "decode_32k_q8": {"gbs": round(q_gbs, 2), "ms": round(q_ms, 5),
+                          "frac_of_hbm": round(q_gbs / HBM_PEAK_GBS, 4), "bytes": qbytes},
         "prefill": pre,
         "wall_ms_per_step": round(dec_wall, 5),
     }

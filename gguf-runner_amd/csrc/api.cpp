@@ -77,13 +77,27 @@ int check_decode(const gr_decode_args* a) {
     const bool pow2 = kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 8;
     if (a->kv_dtype == GR_DTYPE_F32 ? !pow2 : (kv_mul > 16 || (a->head_dim == 64 && !pow2)))
         return fail(GR_ERR_ARG,
-                    "gr_decode_attention: kv_mul %d unsupported (f32 KV: 1,2,4,8; 16-bit KV: <= 16)",
+                    "gr_decode_attention: kv_mul %d unsupported (f32 KV: 1,2,4,8; 16-bit / Q8 KV: <= 16)",
                     kv_mul);
     if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
         return fail(GR_ERR_ARG, "gr_decode_attention: head_dim %d unsupported (64,128,256)",
                     a->head_dim);
-    if (a->kv_dtype < GR_DTYPE_F32 || a->kv_dtype > GR_DTYPE_BF16)
+    if (a->kv_dtype < GR_DTYPE_F32 || a->kv_dtype > GR_DTYPE_Q8)
         return fail(GR_ERR_ARG, "gr_decode_attention: bad kv_dtype %d", a->kv_dtype);
+    if (a->kv_dtype == GR_DTYPE_Q8) {
+        if (a->head_dim != 128 && a->head_dim != 256)
+            return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs head_dim 128 or 256");
+        if (!a->k_scale || !a->v_scale)
+            return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs k_scale and v_scale");
+        if (a->q8_block &&
+            (((uintptr_t)a->k_scale | (uintptr_t)a->v_scale) % 16 != 0 || a->scale_row_stride % 4 != 0 ||
+             a->scale_seq_stride % 4 != 0 || a->scale_row_stride < (int64_t)a->n_kv_heads * a->head_dim / 32))
+            return fail(GR_ERR_ARG,
+                        "gr_decode_attention: Q8 block scales need 16-byte aligned scale arrays and "
+                        "strides (multiples of 4 floats, row stride >= kv_dim/32)");
+        if (a->scale_row_stride < 0 || a->scale_seq_stride < 0)
+            return fail(GR_ERR_ARG, "gr_decode_attention: negative scale stride");
+    }
     if (a->max_kv_len <= 0) return fail(GR_ERR_ARG, "gr_decode_attention: max_kv_len must be > 0");
     if (a->split_keys < 0) return fail(GR_ERR_ARG, "gr_decode_attention: split_keys < 0");
     if (!a->q || !a->k_cache || !a->v_cache || !a->kv_start || !a->kv_end || !a->out ||
@@ -92,7 +106,7 @@ int check_decode(const gr_decode_args* a) {
     if (a->row_stride < (int64_t)a->n_kv_heads * a->head_dim)
         return fail(GR_ERR_ARG, "gr_decode_attention: row_stride %lld < n_kv_heads*head_dim",
                     (long long)a->row_stride);
-    const int eb = a->kv_dtype == GR_DTYPE_F32 ? 4 : 2;
+    const int eb = a->kv_dtype == GR_DTYPE_F32 ? 4 : (a->kv_dtype == GR_DTYPE_Q8 ? 1 : 2);
     if (((uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 != 0 ||
         (a->row_stride * eb) % 16 != 0 || (a->seq_stride * eb) % 16 != 0)
         return fail(GR_ERR_ARG, "gr_decode_attention: caches and strides must be 16-byte aligned");
@@ -131,6 +145,13 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
     p.use_mfma = 1;
+    if (a->kv_dtype == GR_DTYPE_Q8) {
+        p.k_scale = a->k_scale;
+        p.v_scale = a->v_scale;
+        p.scale_seq_stride = a->scale_seq_stride;
+        p.scale_row_stride = a->scale_row_stride;
+        p.q8_block = a->q8_block ? 1 : 0;
+    }
     hipError_t e = launch_decode(p, st);
     if (e != hipSuccess) return hip_fail(e, "gr_decode_attention launch");
     return GR_OK;

@@ -26,6 +26,11 @@ struct gr_run_state {
     void* v_cache = nullptr;
     size_t seq_stride = 0;    // elements between sequence slots
     size_t layer_stride = 0;  // elements between layers
+    // Q8 cache: key_cache_scale / value_cache_scale, sc_per_row scales per row
+    // (1, or kv_dim/32 in block mode), same [layer][slot][row] order as the cache.
+    float* k_scale = nullptr;
+    float* v_scale = nullptr;
+    size_t sc_per_row = 0, sc_seq_stride = 0, sc_layer_stride = 0;
     float* freqs = nullptr;
     float* freqs_swa = nullptr;
     float* qn = nullptr;
@@ -40,7 +45,7 @@ namespace gr {
 
 namespace {
 
-int elem_bytes(int dt) { return dt == GR_DTYPE_F32 ? 4 : 2; }
+int elem_bytes(int dt) { return dt == GR_DTYPE_F32 ? 4 : (dt == GR_DTYPE_Q8 ? 1 : 2); }
 
 // RAII: make the state's device current for the duration of a call.
 struct DeviceScope {
@@ -131,6 +136,53 @@ int check_pos(const gr_run_state* s, int seq, int64_t pos, int64_t count) {
 void* layer_k(gr_run_state* s, int l) { return (char*)s->k_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
 void* layer_v(gr_run_state* s, int l) { return (char*)s->v_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
 
+bool is_q8(const gr_run_state* s) { return s->cfg.kv_dtype == GR_DTYPE_Q8; }
+
+// Extra staging bytes a K/V write of n rows needs (Q8: f32 rows before quantising).
+size_t q8_stage_bytes(const gr_run_state* s, size_t n) { return is_q8(s) ? 8 * n * s->kv_dim + 512 : 0; }
+
+// Run the prep kernel and store its K/V rows into layer `l`'s cache.  Raw
+// storage: the prep kernel writes the cache itself (p.k_cache / p.v_cache set by
+// the caller, sequence slot `seq` already folded into them unless p.cache_seq is
+// given).  Q8: the prep kernel writes f32 rows to staging and the Q8 write
+// kernel quantises them into the cache rows (kv_write_token, inference.rs:1886-1917).
+int prep_and_store(gr_run_state* s, int l, int seq, QkvPrepLaunch p, Carve& cv) {
+    hipError_t e;
+    if (!is_q8(s)) {
+        e = launch_qkv_prep(p, s->stream);
+        return e == hipSuccess ? GR_OK : hip_fail(e, "prep launch");
+    }
+    float* kst = cv.take<float>((size_t)p.n_tokens * s->kv_dim);
+    float* vst = cv.take<float>((size_t)p.n_tokens * s->kv_dim);
+    Q8WriteLaunch w{};
+    w.n_rows = p.n_tokens;
+    w.kv_dim = s->kv_dim;
+    w.block = s->cfg.q8_block_scales ? 1 : 0;
+    w.k_rows = kst;
+    w.v_rows = vst;
+    const size_t so = p.cache_seq ? 0 : (size_t)seq;
+    w.k_cache = (int8_t*)layer_k(s, l) + so * s->seq_stride;
+    w.v_cache = (int8_t*)layer_v(s, l) + so * s->seq_stride;
+    w.k_scale = s->k_scale + (size_t)l * s->sc_layer_stride + so * s->sc_seq_stride;
+    w.v_scale = s->v_scale + (size_t)l * s->sc_layer_stride + so * s->sc_seq_stride;
+    w.cache_seq_stride = (int64_t)s->seq_stride;
+    w.cache_row_stride = s->kv_dim;
+    w.scale_seq_stride = (int64_t)s->sc_seq_stride;
+    w.scale_row_stride = (int64_t)s->sc_per_row;
+    w.cache_row = p.cache_row ? p.cache_row : p.pos;
+    w.cache_seq = p.cache_seq;
+    w.row0 = p.pos0;
+    p.k_cache = kst;
+    p.v_cache = vst;
+    p.cache_dtype = GR_DTYPE_F32;
+    p.cache_row_stride = s->kv_dim;
+    p.cache_by_index = 1;
+    e = launch_qkv_prep(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    e = launch_q8_write(w, s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "q8 kv write launch");
+}
+
 // Prep launch for one layer: QK-norm and/or RoPE as requested.
 QkvPrepLaunch prep_for(gr_run_state* s, int l, int n_tokens, bool norm, bool rope) {
     QkvPrepLaunch p{};
@@ -177,7 +229,9 @@ int validate_config(const gr_attn_config* c) {
         return fail(GR_ERR_ARG, "n_heads %d is not a multiple of n_kv_heads %d", c->n_heads, c->n_kv_heads);
     if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "head_dim %d unsupported (64, 128, 256)", c->head_dim);
-    if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_BF16) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
+    if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_Q8) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
+    if (c->kv_dtype == GR_DTYPE_Q8 && c->head_dim != 128 && c->head_dim != 256)
+        return fail(GR_ERR_ARG, "Q8 KV cache needs head_dim 128 or 256");
     if (c->rope_mode < GR_ROPE_NONE || c->rope_mode > GR_ROPE_NEOX) return fail(GR_ERR_ARG, "bad rope_mode %d", c->rope_mode);
     const int rd = c->rope_dim > 0 ? c->rope_dim : c->head_dim;
     if (rd > c->head_dim || (rd & 1)) return fail(GR_ERR_ARG, "rope_dim %d must be even and <= head_dim", rd);
@@ -241,6 +295,16 @@ int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out) {
         return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate KV cache (%zu bytes each); reduce --context-size", cache_bytes));
     (void)hipMemsetAsync(s->k_cache, 0, cache_bytes, s->stream);
     (void)hipMemsetAsync(s->v_cache, 0, cache_bytes, s->stream);
+    if (cfg->kv_dtype == GR_DTYPE_Q8) {
+        s->sc_per_row = cfg->q8_block_scales ? (size_t)s->kv_dim / 32 : 1;
+        s->sc_seq_stride = (size_t)cfg->seq_len * s->sc_per_row;
+        s->sc_layer_stride = s->sc_seq_stride * cfg->n_seq;
+        const size_t sb = s->sc_layer_stride * cfg->n_layers * 4;
+        if (hipMalloc(&s->k_scale, sb) != hipSuccess || hipMalloc(&s->v_scale, sb) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate KV scale buffers (%zu bytes each)", sb));
+        (void)hipMemsetAsync(s->k_scale, 0, sb, s->stream);
+        (void)hipMemsetAsync(s->v_scale, 0, sb, s->stream);
+    }
 
     // RoPE tables (inference.rs:1590-1609), host powf.
     const int half = s->rope_dim / 2;
@@ -279,8 +343,8 @@ void gr_free_run_state(gr_run_state* s) {
     if (!s) return;
     DeviceScope ds(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
-    for (void* p : {s->k_cache, s->v_cache, (void*)s->freqs, (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn,
-                    (void*)s->ssm, s->stage})
+    for (void* p : {s->k_cache, s->v_cache, (void*)s->k_scale, (void*)s->v_scale, (void*)s->freqs,
+                    (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn, (void*)s->ssm, s->stage})
         if (p) (void)hipFree(p);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
@@ -334,7 +398,7 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
     if (rc || (rc = check_pos(s, seq, pos, 1))) return rc;
     if (!k || !v) return fail(GR_ERR_ARG, "null k/v");
     DeviceScope dsc(s->device);
-    if ((rc = ensure_stage(s, 8 * (size_t)s->kv_dim + 1024))) return rc;
+    if ((rc = ensure_stage(s, 8 * (size_t)s->kv_dim + q8_stage_bytes(s, 1) + 1024))) return rc;
     Carve cv(s->stage);
     float* kin = cv.take<float>(s->kv_dim);
     float* vin = cv.take<float>(s->kv_dim);
@@ -347,9 +411,8 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
     p.q_out = nullptr;
     p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
     p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
-    hipError_t e = launch_qkv_prep(p, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "kv write launch");
-    e = hipStreamSynchronize(s->stream);
+    if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
+    hipError_t e = hipStreamSynchronize(s->stream);
     return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
 }
 
@@ -387,6 +450,14 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
     a.kv_start = se;
     a.kv_end = se + n;
     a.out = xb_dev;
+    if (is_q8(s)) {
+        const size_t so = slots_dev ? 0 : (size_t)seq * s->sc_seq_stride;
+        a.k_scale = s->k_scale + (size_t)layer * s->sc_layer_stride + so;
+        a.v_scale = s->v_scale + (size_t)layer * s->sc_layer_stride + so;
+        a.scale_seq_stride = slots_dev ? (int64_t)s->sc_seq_stride : 0;
+        a.scale_row_stride = (int64_t)s->sc_per_row;
+        a.q8_block = s->cfg.q8_block_scales ? 1 : 0;
+    }
     const size_t ws = decode_ws_bytes(&a);
     a.workspace = cv.take<char>(ws + 256);
     return decode_enqueue_ex(&a, slots_dev, s->stream);
@@ -430,7 +501,8 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
     probe.max_kv_len = en - st;
-    if ((rc = ensure_stage(s, 4 * (3 * (size_t)s->q_dim + 2 * (size_t)s->kv_dim) + decode_ws_bytes(&probe) + 8192)))
+    if ((rc = ensure_stage(s, 4 * (3 * (size_t)s->q_dim + 2 * (size_t)s->kv_dim) + decode_ws_bytes(&probe) +
+                                  q8_stage_bytes(s, 1) + 8192)))
         return rc;
     Carve cv(s->stage);
     float* qin = cv.take<float>(s->q_dim);
@@ -449,8 +521,7 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     p.q_out = qp;
     p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
     p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
-    hipError_t e = launch_qkv_prep(p, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
     if ((rc = run_decode(s, layer, 1, qp, nullptr, seq, {st}, {en}, xo, cv))) return rc;
     return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
 }
@@ -464,7 +535,8 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
     if (!q || !k || !v || !xb) return fail(GR_ERR_ARG, "null buffer");
     DeviceScope dsc(s->device);
     const size_t qb = 4 * (size_t)m * s->q_dim, kb = 4 * (size_t)m * s->kv_dim;
-    const bool mfma = s->cfg.kv_dtype != GR_DTYPE_F32 && (s->d == 128 || s->d == 256);
+    const bool mfma = (s->cfg.kv_dtype == GR_DTYPE_F16 || s->cfg.kv_dtype == GR_DTYPE_BF16) &&
+                      (s->d == 128 || s->d == 256);
     const int64_t w = s->windows.empty() ? 0 : s->windows[layer];
     std::vector<int32_t> starts(m), ends(m);
     int max_len = 1;
@@ -478,7 +550,7 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
     probe.max_kv_len = max_len;
-    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb;
+    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m);
     if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
     Carve cv(s->stage);
     float* qin = cv.take<float>((size_t)m * s->q_dim);
@@ -528,8 +600,7 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
         p.q_out = qp;
         p.k_cache = kc;
         p.v_cache = vc;
-        hipError_t e = launch_qkv_prep(p, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "prep launch");
+        if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
         if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) return rc;
     }
     return d2h_sync(s, xb, xo, qb);
@@ -558,7 +629,9 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     probe.head_dim = s->d;
     probe.max_kv_len = max_len;
     const size_t qb = 4 * (size_t)n * s->q_dim, kb = 4 * (size_t)n * s->kv_dim;
-    if ((rc = ensure_stage(s, 3 * qb + 2 * kb + decode_ws_bytes(&probe) + 16 * (size_t)n + 16384))) return rc;
+    if ((rc = ensure_stage(s, 3 * qb + 2 * kb + decode_ws_bytes(&probe) + 16 * (size_t)n + q8_stage_bytes(s, n) +
+                                  16384)))
+        return rc;
     Carve cv(s->stage);
     float* qin = cv.take<float>((size_t)n * s->q_dim);
     float* kin = cv.take<float>((size_t)n * s->kv_dim);
@@ -580,8 +653,7 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     p.v_cache = layer_v(s, layer);
     p.cache_seq = slot_d;
     p.cache_seq_stride = (int64_t)s->seq_stride;
-    hipError_t e = launch_qkv_prep(p, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "prep launch");
+    if ((rc = prep_and_store(s, layer, 0, p, cv))) return rc;
     if ((rc = run_decode(s, layer, n, qp, slot_d, 0, starts, ends, xo, cv))) return rc;
     return d2h_sync(s, xb, xo, qb);
 }
@@ -687,6 +759,20 @@ int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, i
     const size_t nb = (size_t)n_rows * s->kv_dim * eb;
     if (k_out && (rc = d2h_sync(s, k_out, (char*)layer_k(s, layer) + off, nb))) return rc;
     if (v_out && (rc = d2h_sync(s, v_out, (char*)layer_v(s, layer) + off, nb))) return rc;
+    return GR_OK;
+}
+
+int gr_read_kv_scales(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
+                      float* k_scale_out, float* v_scale_out) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, row0, n_rows))) return rc;
+    if (!is_q8(s)) return fail(GR_ERR_ARG, "run state has no Q8 KV cache (kv_dtype %d)", s->cfg.kv_dtype);
+    DeviceScope dsc(s->device);
+    const size_t off = (size_t)layer * s->sc_layer_stride + (size_t)seq * s->sc_seq_stride + (size_t)row0 * s->sc_per_row;
+    const size_t nb = (size_t)n_rows * s->sc_per_row * 4;
+    if (k_scale_out && (rc = d2h_sync(s, k_scale_out, s->k_scale + off, nb))) return rc;
+    if (v_scale_out && (rc = d2h_sync(s, v_scale_out, s->v_scale + off, nb))) return rc;
     return GR_OK;
 }
 

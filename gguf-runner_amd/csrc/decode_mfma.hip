@@ -1,4 +1,4 @@
-// Split-K flash decoding on gfx950 MFMA for 16-bit (f16 / bf16) KV caches.
+// Split-K flash decoding on gfx950 MFMA for 16-bit (f16 / bf16) and Q8 KV caches.
 //
 // Same work split and partial format as decode.hip (one workgroup per
 // (sequence, KV head, split); partials merged by decode_combine_kernel), but
@@ -14,6 +14,16 @@
 // are exact 16-bit cache values), so the scores and weights keep ~fp32
 // precision even for large unscaled logits.  Decode is HBM-bound with the
 // matrix cores mostly idle, so the second MFMA costs no time.
+//
+// Q8 caches (KvCacheFormat::Q8, reference inference.rs:1337-1483): int8 codes
+// are exact in f16, so K and V tiles are widened to f16 in registers and the
+// same f16 MFMAs run; the f32 scales are applied outside the products:
+//   row scales    score *= k_scale[t];  P[t] *= v_scale[t] before the PV product
+//   block scales  one QK MFMA chain per 32-element block (an MFMA k-step is
+//                 exactly one block), scaled and summed; one P operand per
+//                 V block, scaled by that block's v scale.
+#include <type_traits>
+
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -46,6 +56,39 @@ struct Mfma16<BF16> {
     static __device__ __forceinline__ float back(uint16_t x) { return bf16_to_f32(x); }
 };
 
+// KV storage formats: Raw = one lane's 8-element chunk as loaded from HBM,
+// to16() = the same 8 elements as 16-bit MFMA operands.
+template <typename DT>
+struct Kv16 {
+    using M = Mfma16<DT>;
+    using Raw = uint4;
+    static constexpr bool kQ8 = false, kBlock = false;
+    static __device__ __forceinline__ uint4 to16(const uint4& r) { return r; }
+};
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// int8 -> f16, exact: with u = c + 128 (flip the sign bit), the f16 with
+// exponent byte 0x64 and low byte u is 1024 + u, and (1024 + u) - 1152 = c.
+__device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t two_bytes_spread) {
+    const half2_t h = __builtin_bit_cast(half2_t, two_bytes_spread | 0x64006400u) - half2_t{1152.0f16, 1152.0f16};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+template <bool BLOCK>
+struct KvQ8 {
+    using M = Mfma16<F16>;
+    using Raw = uint2;
+    static constexpr bool kQ8 = true, kBlock = BLOCK;
+    static __device__ __forceinline__ uint4 to16(const uint2& r) {
+        const uint32_t a = r.x ^ 0x80808080u, b = r.y ^ 0x80808080u;
+        return make_uint4(i8x2_to_f16x2((a & 0xffu) | ((a & 0xff00u) << 8)),
+                          i8x2_to_f16x2(((a >> 16) & 0xffu) | ((a >> 8) & 0xff0000u)),
+                          i8x2_to_f16x2((b & 0xffu) | ((b & 0xff00u) << 8)),
+                          i8x2_to_f16x2(((b >> 16) & 0xffu) | ((b >> 8) & 0xff0000u)));
+    }
+};
+
 constexpr int kMdThreads = 256;
 constexpr int kMdWaves = kMdThreads / 64;
 
@@ -56,10 +99,13 @@ constexpr float kMdLazyRescale = 8.0f;
 // NSUB groups of 32 keys per wave iteration.  1 is used: with 2, the d128
 // kernel needs 300 registers (one wave per SIMD) and measured slower than two
 // waves per SIMD streaming 32-key tiles.
-template <typename DT, int D, int NSUB>
+template <typename KV, int D, int NSUB>
 __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLaunch p) {
-    using M = Mfma16<DT>;
+    using M = typename KV::M;
+    using Raw = typename KV::Raw;
     constexpr bool kSplit = M::kSplit;
+    constexpr bool kQ8 = KV::kQ8, kBlock = KV::kBlock;
+    constexpr int NB = D / 32;                   // 32-element scale blocks per head (Q8 block mode)
     constexpr int TILE = 32 * NSUB;              // keys per wave iteration
     constexpr int NS16 = TILE / 16;              // 16-key score sub-tiles
     constexpr int DC = D / 8;                    // 16-byte chunks per row
@@ -70,8 +116,11 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
 
     // LDS: per-wave V^T tiles during the key loop, then (aliased) the wave merge.
     constexpr int kVtBytes = kMdWaves * D * VS * 2;
+    // Q8 block mode: per-wave scale tile [K|V][block][32 keys] after the V^T tiles
+    constexpr int kScBytes = kBlock ? kMdWaves * 2 * NB * TILE * 4 : 0;
+    constexpr int kLoopBytes = kVtBytes + kScBytes;
     constexpr int kMergeBytes = (kMdWaves * 16 * (D + 1) + 2 * kMdWaves * 16) * 4;
-    __shared__ __attribute__((aligned(16))) char smem[kVtBytes > kMergeBytes ? kVtBytes : kMergeBytes];
+    __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
     const int split = blockIdx.x;
     const int g = blockIdx.y;
@@ -86,14 +135,35 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
     uint16_t* vt = (uint16_t*)smem + wave * D * VS;
+    float* sct = (float*)(smem + kVtBytes) + wave * 2 * NB * TILE;  // block mode: [2][NB][TILE]
 
     // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
     // d = 32 ks + 8 g4 .. +7, pre-scaled to log2 units; queries >= kv_mul are 0.
+    // f16: each query row is also multiplied by a power of two 2^e that puts its
+    // largest element near 2^14, so that the lo halves of the hi/lo split stay
+    // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
     uint4 qf[KS], qfl[kSplit ? KS : 1];
+    float qback = 1.0f;
     {
         const bool qv = l16 < kv_mul;
         const float* qrow = p.q + ((size_t)s * p.n_heads + (size_t)g * kv_mul + (qv ? l16 : 0)) * D;
-        const float qscale = p.score_scale * kLog2e;
+        float qscale = p.score_scale * kLog2e;
+        if constexpr (std::is_same<M, Mfma16<F16>>::value) {
+            float qmax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, qv ? fabsf(qrow[32 * k + 8 * g4 + e] * qscale) : 0.0f);
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+            if (qmax > 0.0f && qmax < 3.0e38f) {
+                int ex;
+                (void)frexpf(qmax, &ex);               // qmax = m 2^ex, m in [0.5, 1)
+                const int e = min(max(14 - ex, -100), 100);
+                qscale *= ldexpf(1.0f, e);
+                qback = ldexpf(1.0f, -e);
+            }
+        }
 #pragma unroll
         for (int k = 0; k < KS; k++) {
             uint32_t hw[4], lw[4];
@@ -114,38 +184,77 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     }
 
     const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
-    const uint16_t* kc = (const uint16_t*)p.k_cache + slot * p.seq_stride + (size_t)g * D;
-    const uint16_t* vc = (const uint16_t*)p.v_cache + slot * p.seq_stride + (size_t)g * D;
+    // element pointers (one element = sizeof(Raw)/8 bytes)
+    typedef typename std::conditional<kQ8, int8_t, uint16_t>::type Elem;
+    const Elem* kc = (const Elem*)p.k_cache + slot * p.seq_stride + (size_t)g * D;
+    const Elem* vc = (const Elem*)p.v_cache + slot * p.seq_stride + (size_t)g * D;
     const int64_t rs = p.row_stride;
+    // Q8 scales: this lane's keys of S^T register j of sub-tile sb are
+    // t0 + 16 sb + 4 g4 + j; block mode adds the kv head's block offset.
+    const float* ksb = nullptr;
+    const float* vsb = nullptr;
+    int64_t srs = 0;
+    if constexpr (kQ8) {
+        const size_t so = slot * p.scale_seq_stride + (kBlock ? (size_t)g * NB : 0);
+        ksb = p.k_scale + so;
+        vsb = p.v_scale + so;
+        srs = p.scale_row_stride;
+    }
+    // Row mode: each lane prefetches the k / v scales of its 4 NS16 keys.  Block
+    // mode: the wave prefetches the tile's 32 x NB k and v block scales (NB/2 per
+    // lane, coalesced along a row) and stages them in LDS for the score and P passes.
+    constexpr int NRS = kQ8 && !kBlock ? 4 * NS16 : 1;
+    constexpr int NBS = kBlock ? TILE * NB / 64 : 1;
+    float ksc[NRS], vsc[NRS];
+    float kbs[NBS], vbs[NBS];
 
-    uint4 kr[NS16][KS];
-    uint4 vr[VTASK][4];
+    Raw kr[NS16][KS];
+    Raw vr[VTASK][4];
+    auto load_scales = [&](int t0) {
+        if constexpr (kBlock) {
+#pragma unroll
+            for (int u = 0; u < NBS; u++) {
+                const int e = lane + 64 * u;
+                const int key = min(t0 + e / NB, t_stop - 1);
+                kbs[u] = ksb[(int64_t)key * srs + e % NB];
+                vbs[u] = vsb[(int64_t)key * srs + e % NB];
+            }
+        } else if constexpr (kQ8) {
+#pragma unroll
+            for (int e = 0; e < NRS; e++) {
+                const int key = min(t0 + 16 * (e >> 2) + 4 * g4 + (e & 3), t_stop - 1);
+                ksc[e] = ksb[(int64_t)key * srs];
+                vsc[e] = vsb[(int64_t)key * srs];
+            }
+        }
+    };
     auto load_tile = [&](int t0) {
+        load_scales(t0);
         if (t0 + TILE <= t_stop) {  // whole tile inside the split: plain strided rows
-            const uint16_t* kt = kc + (int64_t)t0 * rs + 8 * g4;
-            const uint16_t* vtp = vc + (int64_t)t0 * rs;
+            const Elem* kt = kc + (int64_t)t0 * rs + 8 * g4;
+            const Elem* vtp = vc + (int64_t)t0 * rs;
 #pragma unroll
             for (int sb = 0; sb < NS16; sb++) {
-                const uint16_t* row = kt + (int64_t)(16 * sb + l16) * rs;
+                const Elem* row = kt + (int64_t)(16 * sb + l16) * rs;
 #pragma unroll
-                for (int k = 0; k < KS; k++) kr[sb][k] = *(const uint4*)(row + 32 * k);
+                for (int k = 0; k < KS; k++) kr[sb][k] = *(const Raw*)(row + 32 * k);
             }
 #pragma unroll
             for (int u = 0; u < VTASK; u++) {
                 const int task = lane + 64 * u;
                 const int dc = task % DC, kg = task / DC;
-                const uint16_t* v0 = vtp + (int64_t)(4 * kg) * rs + 8 * dc;
+                const Elem* v0 = vtp + (int64_t)(4 * kg) * rs + 8 * dc;
 #pragma unroll
-                for (int r = 0; r < 4; r++) vr[u][r] = *(const uint4*)(v0 + r * rs);
+                for (int r = 0; r < 4; r++) vr[u][r] = *(const Raw*)(v0 + r * rs);
             }
             return;
         }
 #pragma unroll
         for (int sb = 0; sb < NS16; sb++) {
             const int key = min(t0 + 16 * sb + l16, t_stop - 1);
-            const uint16_t* row = kc + (int64_t)key * rs + 8 * g4;
+            const Elem* row = kc + (int64_t)key * rs + 8 * g4;
 #pragma unroll
-            for (int k = 0; k < KS; k++) kr[sb][k] = *(const uint4*)(row + 32 * k);
+            for (int k = 0; k < KS; k++) kr[sb][k] = *(const Raw*)(row + 32 * k);
         }
 #pragma unroll
         for (int u = 0; u < VTASK; u++) {
@@ -154,7 +263,7 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int key = min(t0 + 4 * kg + r, t_stop - 1);
-                vr[u][r] = *(const uint4*)(vc + (int64_t)key * rs + 8 * dc);
+                vr[u][r] = *(const Raw*)(vc + (int64_t)key * rs + 8 * dc);
             }
         }
     };
@@ -163,6 +272,15 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
 #pragma unroll
     for (int dt = 0; dt < D / 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrow = -1e30f, lrow = 0.0f;
+    // Q8: P * v_scale is carried as P * v_scale * pw[pb] with a power of two pw
+    // that keeps the tile's largest v_scale * pw in [2^6, 2^7): the f16 hi/lo
+    // pair then stays clear of the subnormal range (whose 6e-8 floor, times int8
+    // codes up to 127, would show in the output) and P * v_scale * pw <= 2^15.
+    // O rows of block pb accumulate pw[pb] times the true value; pw only
+    // decreases (O rescaled) and is divided out after the loop.
+    constexpr int NPB = kBlock ? NB : 1;   // P operands (one per V scale block)
+    float pw[kQ8 ? NPB : 1];
+    bool pw_set = false;
 
     const int n_tiles = (t_stop - t_begin + TILE - 1) / TILE;
     int it = wave;
@@ -174,10 +292,11 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         for (int u = 0; u < VTASK; u++) {
             const int task = lane + 64 * u;
             const int dc = task % DC, kg = task / DC;
-            const uint32_t w[4][4] = {{vr[u][0].x, vr[u][0].y, vr[u][0].z, vr[u][0].w},
-                                      {vr[u][1].x, vr[u][1].y, vr[u][1].z, vr[u][1].w},
-                                      {vr[u][2].x, vr[u][2].y, vr[u][2].z, vr[u][2].w},
-                                      {vr[u][3].x, vr[u][3].y, vr[u][3].z, vr[u][3].w}};
+            const uint4 v16[4] = {KV::to16(vr[u][0]), KV::to16(vr[u][1]), KV::to16(vr[u][2]), KV::to16(vr[u][3])};
+            const uint32_t w[4][4] = {{v16[0].x, v16[0].y, v16[0].z, v16[0].w},
+                                      {v16[1].x, v16[1].y, v16[1].z, v16[1].w},
+                                      {v16[2].x, v16[2].y, v16[2].z, v16[2].w},
+                                      {v16[3].x, v16[3].y, v16[3].z, v16[3].w}};
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
                 const int wi = dd >> 1;
@@ -192,6 +311,22 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
                 *(uint2*)(vt + (8 * dc + dd) * VS + 4 * kg) = make_uint2(lo, hi);
             }
         }
+        float vbmax[kBlock ? NB : 1];  // block mode: the tile's largest v scale per block (wave-uniform)
+        if constexpr (kBlock) {
+            float vl = 0.0f;
+#pragma unroll
+            for (int u = 0; u < NBS; u++) {
+                const int e = lane + 64 * u;  // block e % NB == lane % NB for every u
+                sct[(e % NB) * TILE + e / NB] = kbs[u];
+                sct[(NB + e % NB) * TILE + e / NB] = vbs[u];
+                vl = fmaxf(vl, vbs[u]);
+            }
+#pragma unroll
+            for (int m = NB; m < 64; m <<= 1) vl = fmaxf(vl, __shfl_xor(vl, m, 64));
+#pragma unroll
+            for (int b = 0; b < NB; b++) vbmax[b] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vl), b));
+            __builtin_amdgcn_wave_barrier();
+        }
         // scores for the 16-key sub-tiles
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
         f32x4 sacc[NS16];
@@ -199,10 +334,33 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         for (int sb = 0; sb < NS16; sb++) {
 #pragma unroll
             for (int k = 0; k < KS; k++) {
-                sacc[sb] = M::mma(kr[sb][k], qf[k], k == 0 ? zero : sacc[sb]);
-                if constexpr (kSplit) sacc[sb] = M::mma(kr[sb][k], qfl[k], sacc[sb]);
+                const uint4 ka = KV::to16(kr[sb][k]);
+                if constexpr (kBlock) {
+                    // k-step k is scale block k: its own product, then scaled
+                    f32x4 part = M::mma(ka, qf[k], zero);
+                    if constexpr (kSplit) part = M::mma(ka, qfl[k], part);
+                    const float4 k4 = *(const float4*)(sct + k * TILE + 16 * sb + 4 * g4);
+                    const float kb[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        sacc[sb][j] = k == 0 ? part[j] * kb[j] : fmaf(part[j], kb[j], sacc[sb][j]);
+                } else {
+                    sacc[sb] = M::mma(ka, qf[k], k == 0 ? zero : sacc[sb]);
+                    if constexpr (kSplit) sacc[sb] = M::mma(ka, qfl[k], sacc[sb]);
+                }
+            }
+            if constexpr (kQ8 && !kBlock) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) sacc[sb][j] *= ksc[4 * sb + j] * qback;
+            } else if constexpr (std::is_same<M, Mfma16<F16>>::value) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) sacc[sb][j] *= qback;
             }
         }
+        // row-mode V scales of this tile (the prefetch below overwrites vsc)
+        float vcur[NRS];
+#pragma unroll
+        for (int e = 0; e < NRS; e++) vcur[e] = vsc[e];
         // prefetch the wave's next tile while this one is finished
         if (it + kMdWaves < n_tiles) load_tile(t_begin + (it + kMdWaves) * TILE);
 
@@ -237,40 +395,104 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
             psum += pv[e];
         }
         lrow += psum;
-        // B operand P^T per 32-key k-step kk: k-slot r <-> key 32 kk + 16 (r/4) + 4 g4 + r%4
-        uint4 pf[NSUB], pfl[kSplit ? NSUB : 1];
-#pragma unroll
-        for (int kk = 0; kk < NSUB; kk++) {
-            uint32_t ph[4], pl[4];
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float a0 = pv[8 * kk + 2 * w], a1 = pv[8 * kk + 2 * w + 1];
-                const uint16_t h0 = M::cvt(a0), h1 = M::cvt(a1);
-                ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                if constexpr (kSplit)
-                    pl[w] = (uint32_t)M::cvt(a0 - M::back(h0)) | ((uint32_t)M::cvt(a1 - M::back(h1)) << 16);
+        // B operand P^T per 32-key k-step kk: k-slot r <-> key 32 kk + 16 (r/4) + 4 g4 + r%4,
+        // i.e. pv[8 kk + r]; for Q8, P is multiplied by the v scale of its key (and,
+        // in block mode, of the V block `vb` that the output tiles of this pass cover).
+        // v scale of this lane's P slot r = 2 w + h of k-step kk, block vb
+        auto vscale_of = [&](int vb, int kk, int r) -> float {
+            if constexpr (kBlock) {
+                // pv[8 kk + r] is key 32 kk + 16 (r/4) + 4 g4 + r%4
+                return sct[(NB + vb) * TILE + 32 * kk + 16 * (r >> 2) + 4 * g4 + (r & 3)];
+            } else {
+                return vcur[kQ8 ? 8 * kk + r : 0];
             }
-            pf[kk] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-            if constexpr (kSplit) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        };
+        if constexpr (kQ8) {
+#pragma unroll
+            for (int pb = 0; pb < NPB; pb++) {
+                float vloc = 0.0f;
+                if constexpr (kBlock) {
+                    vloc = vbmax[pb];
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < NSUB; kk++)
+#pragma unroll
+                        for (int r = 0; r < 8; r++) vloc = fmaxf(vloc, vscale_of(pb, kk, r));
+                }
+                const bool grow = kBlock ? vloc * pw[pb] >= 128.0f : __any(vloc * pw[pb] >= 128.0f);
+                if (!pw_set || grow) {
+                    const float vmax = kBlock ? vloc : wave_max<64>(vloc);
+                    int ex;
+                    (void)frexpf(vmax, &ex);  // vmax = m 2^ex, m in [0.5, 1)
+                    const float npw = __int_as_float(__builtin_amdgcn_readfirstlane(
+                        __float_as_int(vmax > 0.0f ? ldexpf(1.0f, min(max(7 - ex, -120), 120)) : 1.0f)));
+                    if (pw_set && npw < pw[pb]) {
+                        const float f = npw / pw[pb];
+#pragma unroll
+                        for (int dd = 0; dd < (D / 16) / NPB; dd++) o[pb * ((D / 16) / NPB) + dd] *= f;
+                        pw[pb] = npw;
+                    } else if (!pw_set) {
+                        pw[pb] = npw;
+                    }
+                }
+            }
+            pw_set = true;
         }
+        auto make_p = [&](int vb, uint4* pf, uint4* pfl) {
+#pragma unroll
+            for (int kk = 0; kk < NSUB; kk++) {
+                uint32_t ph[4], pl[4];
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    float a0 = pv[8 * kk + 2 * w], a1 = pv[8 * kk + 2 * w + 1];
+                    if constexpr (kQ8) {
+                        a0 *= vscale_of(vb, kk, 2 * w) * pw[vb];
+                        a1 *= vscale_of(vb, kk, 2 * w + 1) * pw[vb];
+                    }
+                    const uint16_t h0 = M::cvt(a0), h1 = M::cvt(a1);
+                    ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    if constexpr (kSplit)
+                        pl[w] = (uint32_t)M::cvt(a0 - M::back(h0)) | ((uint32_t)M::cvt(a1 - M::back(h1)) << 16);
+                }
+                pf[kk] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+                if constexpr (kSplit) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+            }
+        };
         // LDS operations of one wave complete in issue order, so the V^T reads
         // below see this wave's stores; the barrier only pins the compiler's order.
         __builtin_amdgcn_wave_barrier();
+        constexpr int DTB = (D / 16) / NPB;    // 16-row output tiles per P operand
 #pragma unroll
-        for (int dt = 0; dt < D / 16; dt++) {
-            const uint16_t* vrow = vt + (16 * dt + l16) * VS + 4 * g4;
+        for (int pb = 0; pb < NPB; pb++) {
+            uint4 pf[NSUB], pfl[kSplit ? NSUB : 1];
+            make_p(pb, pf, pfl);
 #pragma unroll
-            for (int kk = 0; kk < NSUB; kk++) {
-                const uint2 lo = *(const uint2*)(vrow + 32 * kk);
-                const uint2 hi = *(const uint2*)(vrow + 32 * kk + 16);
-                const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                o[dt] = M::mma(a, pf[kk], o[dt]);
-                if constexpr (kSplit) o[dt] = M::mma(a, pfl[kk], o[dt]);
+            for (int dd = 0; dd < DTB; dd++) {
+                const int dt = pb * DTB + dd;
+                const uint16_t* vrow = vt + (16 * dt + l16) * VS + 4 * g4;
+#pragma unroll
+                for (int kk = 0; kk < NSUB; kk++) {
+                    const uint2 lo = *(const uint2*)(vrow + 32 * kk);
+                    const uint2 hi = *(const uint2*)(vrow + 32 * kk + 16);
+                    const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    o[dt] = M::mma(a, pf[kk], o[dt]);
+                    if constexpr (kSplit) o[dt] = M::mma(a, pfl[kk], o[dt]);
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();  // V^T reads done before the next tile overwrites it
     }
 
+    if constexpr (kQ8) {
+        if (pw_set) {
+#pragma unroll
+            for (int pb = 0; pb < NPB; pb++) {
+                const float inv = 1.0f / pw[pb];  // exact: pw is a power of two
+#pragma unroll
+                for (int dd = 0; dd < (D / 16) / NPB; dd++) o[pb * ((D / 16) / NPB) + dd] *= inv;
+            }
+        }
+    }
     // lane sums -> row sums (4 lanes share a query column)
     lrow += __shfl_xor(lrow, 16, 64);
     lrow += __shfl_xor(lrow, 32, 64);
@@ -310,12 +532,12 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     }
 }
 
-template <typename DT>
-static hipError_t launch_mfma_dt(const DecodeLaunch& p, hipStream_t st) {
+template <typename KV>
+static hipError_t launch_mfma_kv(const DecodeLaunch& p, hipStream_t st) {
     dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
     switch (p.head_dim) {
-        case 128: decode_mfma_kernel<DT, 128, 1><<<grid, kMdThreads, 0, st>>>(p); break;
-        case 256: decode_mfma_kernel<DT, 256, 1><<<grid, kMdThreads, 0, st>>>(p); break;
+        case 128: decode_mfma_kernel<KV, 128, 1><<<grid, kMdThreads, 0, st>>>(p); break;
+        case 256: decode_mfma_kernel<KV, 256, 1><<<grid, kMdThreads, 0, st>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -323,12 +545,17 @@ static hipError_t launch_mfma_dt(const DecodeLaunch& p, hipStream_t st) {
 
 bool decode_mfma_supported(const DecodeLaunch& p) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
-    return (p.kv_dtype == GR_DTYPE_F16 || p.kv_dtype == GR_DTYPE_BF16) && kv_mul <= 16 &&
-           (p.head_dim == 128 || p.head_dim == 256);
+    return (p.kv_dtype == GR_DTYPE_F16 || p.kv_dtype == GR_DTYPE_BF16 || p.kv_dtype == GR_DTYPE_Q8) &&
+           kv_mul <= 16 && (p.head_dim == 128 || p.head_dim == 256);
 }
 
 hipError_t launch_decode_mfma_split(const DecodeLaunch& p, hipStream_t st) {
-    return p.kv_dtype == GR_DTYPE_F16 ? launch_mfma_dt<F16>(p, st) : launch_mfma_dt<BF16>(p, st);
+    switch (p.kv_dtype) {
+        case GR_DTYPE_F16: return launch_mfma_kv<Kv16<F16>>(p, st);
+        case GR_DTYPE_BF16: return launch_mfma_kv<Kv16<BF16>>(p, st);
+        case GR_DTYPE_Q8: return p.q8_block ? launch_mfma_kv<KvQ8<true>>(p, st) : launch_mfma_kv<KvQ8<false>>(p, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace gr

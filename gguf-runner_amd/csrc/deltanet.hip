@@ -288,8 +288,10 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(cons
     __shared__ __attribute__((aligned(16))) float Ss[D][NC];
     __shared__ __attribute__((aligned(16))) float Dl[C][NC];
     const int tid = threadIdx.x;
-    const int h = blockIdx.y;
-    const int c0 = blockIdx.x * NC;
+    // blockIdx.x = head so that the column blocks of one head (linear ids
+    // h + H*cb) land on the same XCD and share its L2 copy of the workspace.
+    const int h = blockIdx.x;
+    const int c0 = blockIdx.y * NC;
     const int H = p.n_heads;
     float* Sh = p.state + (size_t)h * D * D;
     for (int e = tid; e < D * NC; e += kChunkThreads) Ss[e / NC][e % NC] = Sh[(size_t)(e / NC) * D + c0 + e % NC];
@@ -405,7 +407,7 @@ hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     deltanet_chunk_prep_kernel<D><<<dim3(n_chunks, p.n_heads), kChunkThreads, lds, st>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    deltanet_chunk_scan_kernel<D><<<dim3(D / kScanCols, p.n_heads), kChunkThreads, 0, st>>>(p);
+    deltanet_chunk_scan_kernel<D><<<dim3(p.n_heads, D / kScanCols), kChunkThreads, 0, st>>>(p);
     return hipGetLastError();
 }
 

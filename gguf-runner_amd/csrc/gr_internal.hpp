@@ -22,7 +22,13 @@ struct DecodeLaunch {
     float* out;
     float* ws_o;
     float* ws_ml;
-    int use_mfma;  // 16-bit caches: MFMA split kernel (decode_mfma.hip) instead of VALU
+    int use_mfma;  // 16-bit / Q8 caches: MFMA split kernel (decode_mfma.hip) instead of VALU
+    // Q8 cache: scale of (seq slot, row t, kv head g, element i) at
+    // slot*scale_seq_stride + t*scale_row_stride + (q8_block ? (g*head_dim + i)/32 : 0).
+    const float* k_scale;
+    const float* v_scale;
+    int64_t scale_seq_stride, scale_row_stride;
+    int q8_block;
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);
@@ -60,9 +66,32 @@ struct QkvPrepLaunch {
     int64_t cache_seq_stride;   // elements, used with cache_seq
     const int32_t* cache_seq;   // [n_tokens] sequence slot per token, or nullptr -> 0
     int64_t cache_row_stride;
+    int cache_by_index;         // 1: token i's K/V go to row i of the cache (staging), slot 0
 };
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);
+
+// Q8 KV write (kv_write_token's Q8 branch, inference.rs:1886-1917): n_rows f32
+// rows of kv_dim elements (k_rows / v_rows, row stride kv_dim) are quantised
+// into int8 cache rows with one scale per row or per 32-element block.
+// Destination row i: sequence slot (cache_seq ? cache_seq[i] : 0) and position
+// (cache_row ? cache_row[i] : row0 + i).
+struct Q8WriteLaunch {
+    int n_rows, kv_dim, block;
+    const float* k_rows;
+    const float* v_rows;
+    int8_t* k_cache;
+    int8_t* v_cache;
+    float* k_scale;
+    float* v_scale;
+    int64_t cache_seq_stride, cache_row_stride;  // elements
+    int64_t scale_seq_stride, scale_row_stride;  // floats
+    const int32_t* cache_row;
+    const int32_t* cache_seq;
+    int64_t row0;
+};
+
+hipError_t launch_q8_write(const Q8WriteLaunch& p, hipStream_t st);
 
 // Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
 // [m][n_heads][d] already multiplied by score_scale*log2(e); for bf16, q_lo

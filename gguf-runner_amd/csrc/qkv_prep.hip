@@ -72,8 +72,8 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
     }
     __syncthreads();
     float* rb = row_buf[wave][rsub];
-    const int64_t row = p.cache_row ? (int64_t)p.cache_row[i] : pos;
-    const int64_t sq = p.cache_seq ? (int64_t)p.cache_seq[i] : 0;
+    const int64_t row = p.cache_by_index ? (int64_t)i : (p.cache_row ? (int64_t)p.cache_row[i] : pos);
+    const int64_t sq = p.cache_by_index ? 0 : (p.cache_seq ? (int64_t)p.cache_seq[i] : 0);
 
     for (int hr0 = wave * RPW; hr0 < rows_per_token; hr0 += kPrepRowsPerBlock * RPW) {
         const int hr = hr0 + rsub;

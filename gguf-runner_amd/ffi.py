@@ -19,7 +19,7 @@ GR_ERR_HIP = -2
 GR_ERR_RANGE = -3
 GR_ERR_OOM = -4
 
-DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_Q8 = 0, 1, 2, 3
 ROPE_NONE, ROPE_ADJACENT, ROPE_NEOX = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -42,6 +42,8 @@ class DecodeArgs(ctypes.Structure):
         ("kv_dtype", _i32), ("split_keys", _i32), ("max_kv_len", _i32), ("score_scale", _f),
         ("q", _p), ("k_cache", _p), ("v_cache", _p), ("seq_stride", _i64), ("row_stride", _i64),
         ("kv_start", _p), ("kv_end", _p), ("out", _p), ("workspace", _p),
+        ("k_scale", _p), ("v_scale", _p), ("scale_seq_stride", _i64), ("scale_row_stride", _i64),
+        ("q8_block", _i32),
     ]
 
 
@@ -75,7 +77,7 @@ class AttnConfig(ctypes.Structure):
         ("rope_scale_global", _f), ("rope_scale_local", _f), ("layer_windows", _p),
         ("swa_pattern", _i32), ("is_gemma3", _i32), ("online_attn_fusion", _i32),
         ("rms_norm_eps", _f), ("q_norm", _p), ("k_norm", _p), ("qk_norm_present", _p),
-        ("ssm_n_heads", _i32), ("ssm_head_dim", _i32),
+        ("ssm_n_heads", _i32), ("ssm_head_dim", _i32), ("q8_block_scales", _i32),
     ]
 
 _lib = None
@@ -127,11 +129,13 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_qwen3next_state_step.argtypes = [_p, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_qwen3next_prefill.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_read_kv_rows.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
+    L.gr_read_kv_scales.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
     L.gr_read_ssm_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
     for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
               "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_decode_layer_batch",
               "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
+              "gr_read_kv_scales",
               "gr_read_ssm_state", "gr_write_ssm_state"):
         getattr(L, n).restype = ip
 

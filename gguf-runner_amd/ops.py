@@ -12,7 +12,8 @@ import torch
 
 from . import ffi
 
-_DT = {torch.float32: ffi.DTYPE_F32, torch.float16: ffi.DTYPE_F16, torch.bfloat16: ffi.DTYPE_BF16}
+_DT = {torch.float32: ffi.DTYPE_F32, torch.float16: ffi.DTYPE_F16, torch.bfloat16: ffi.DTYPE_BF16,
+       torch.int8: ffi.DTYPE_Q8}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -40,19 +41,21 @@ def _aligned(ws: torch.Tensor) -> int:
 class DecodeCall:
     """A prepared gr_decode_attention call (args + workspace), reusable for timing.
 
-    q [n_seq][Hq][d] f32; k_cache/v_cache [n_seq][seq_len][Hkv][d] (f32/f16/bf16);
+    q [n_seq][Hq][d] f32; k_cache/v_cache [n_seq][seq_len][Hkv][d] (f32/f16/bf16, or
+    int8 Q8 codes with f32 k_scale/v_scale [n_seq][seq_len] (one per row) or
+    [n_seq][seq_len][Hkv*d/32] (q8_block: one per 32 elements));
     kv_start/kv_end int32 [n_seq]; out [n_seq][Hq][d] f32.
     """
 
     def __init__(self, q, k_cache, v_cache, kv_start, kv_end, out, *, max_kv_len,
-                 score_scale=None, split_keys=0):
+                 score_scale=None, split_keys=0, k_scale=None, v_scale=None, q8_block=False):
         n_seq, n_heads, d = q.shape
         _, seq_len, n_kv, d2 = k_cache.shape
         assert d2 == d and v_cache.shape == k_cache.shape and out.shape == q.shape
         assert q.dtype == torch.float32 and out.dtype == torch.float32
         assert kv_start.dtype == torch.int32 and kv_end.dtype == torch.int32
         assert k_cache.is_contiguous() and v_cache.is_contiguous() and q.is_contiguous()
-        self._keep = (q, k_cache, v_cache, kv_start, kv_end, out)
+        self._keep = (q, k_cache, v_cache, kv_start, kv_end, out, k_scale, v_scale)
         a = ffi.DecodeArgs()
         a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim = n_seq, n_heads, n_kv, d
         a.kv_dtype = _DT[k_cache.dtype]
@@ -63,6 +66,15 @@ class DecodeCall:
         a.seq_stride = seq_len * n_kv * d
         a.row_stride = n_kv * d
         a.kv_start, a.kv_end, a.out = _ptr(kv_start), _ptr(kv_end), _ptr(out)
+        if k_cache.dtype == torch.int8:
+            per_row = n_kv * d // 32 if q8_block else 1
+            for t in (k_scale, v_scale):
+                assert t is not None and t.dtype == torch.float32 and t.is_contiguous()
+                assert t.numel() == n_seq * seq_len * per_row
+            a.k_scale, a.v_scale = _ptr(k_scale), _ptr(v_scale)
+            a.scale_seq_stride = seq_len * per_row
+            a.scale_row_stride = per_row
+            a.q8_block = int(bool(q8_block))
         L = ffi.lib()
         nbytes = L.gr_decode_workspace_size(ctypes.byref(a))
         self.ws = _workspace(nbytes, q.device)
@@ -74,13 +86,14 @@ class DecodeCall:
 
 
 def decode_attention(q, k_cache, v_cache, kv_start, kv_end, *, max_kv_len=None, score_scale=None,
-                     split_keys=0, out=None):
+                     split_keys=0, out=None, k_scale=None, v_scale=None, q8_block=False):
     if out is None:
         out = torch.empty_like(q)
     if max_kv_len is None:
         max_kv_len = int((kv_end - kv_start).max().item())
     DecodeCall(q, k_cache, v_cache, kv_start, kv_end, out, max_kv_len=max_kv_len,
-               score_scale=score_scale, split_keys=split_keys)()
+               score_scale=score_scale, split_keys=split_keys, k_scale=k_scale, v_scale=v_scale,
+               q8_block=q8_block)()
     return out
 
 

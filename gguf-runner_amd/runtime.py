@@ -34,7 +34,7 @@ class Config:
     head_dim: int
     seq_len: int
     n_seq: int = 1
-    kv_dtype: int = ffi.DTYPE_F32
+    kv_dtype: int = ffi.DTYPE_F32      # raw F32/F16/BF16, or DTYPE_Q8 (KvCacheFormat::Q8)
     rope_mode: int = ffi.ROPE_NEOX
     rope_dim: int = 0
     rope_theta: float = 10_000.0
@@ -51,6 +51,7 @@ class Config:
     qk_norm_present: list | None = None
     ssm_n_heads: int = 0
     ssm_head_dim: int = 128
+    q8_block_scales: bool = False       # GGUF_Q8_BLOCK_SCALES (inference.rs:1883)
     _keep: list = field(default_factory=list, repr=False)
 
     def to_c(self) -> ffi.AttnConfig:
@@ -64,6 +65,7 @@ class Config:
             setattr(c, name, float(getattr(self, name)))
         c.is_gemma3 = int(bool(self.is_gemma3))
         c.online_attn_fusion = int(bool(self.online_attn_fusion))
+        c.q8_block_scales = int(bool(self.q8_block_scales))
         self._keep = []
         if self.layer_windows is not None:
             w = np.ascontiguousarray([0 if x is None else int(x) for x in self.layer_windows],
@@ -180,11 +182,21 @@ def decode_layer_batch(p: Config, s: RunState, l: int, seqs, pos, q, k, v) -> np
 
 
 def read_kv_rows(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq: int = 0):
-    dt = np.float32 if p.kv_dtype == ffi.DTYPE_F32 else np.uint16
+    dt = {ffi.DTYPE_F32: np.float32, ffi.DTYPE_Q8: np.int8}.get(p.kv_dtype, np.uint16)
     k = np.zeros((n_rows, p.kv_dim), dt)
     v = np.zeros((n_rows, p.kv_dim), dt)
     ffi.check(ffi.lib().gr_read_kv_rows(s.handle, l, seq, row0, n_rows, _p(k), _p(v)))
     return k, v
+
+
+def read_kv_scales(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq: int = 0):
+    """key_cache_scale / value_cache_scale of a Q8 cache: [n_rows] (row mode) or
+    [n_rows][kv_dim/32] (block mode)."""
+    per = p.kv_dim // 32 if p.q8_block_scales else 1
+    ks = np.zeros((n_rows, per), np.float32)
+    vs = np.zeros((n_rows, per), np.float32)
+    ffi.check(ffi.lib().gr_read_kv_scales(s.handle, l, seq, row0, n_rows, _p(ks), _p(vs)))
+    return ks, vs
 
 
 def qwen3next_state_step(p: Config, s: RunState, l: int, q, k, v, g, beta) -> np.ndarray:

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define GR_ATTN_ABI_VERSION 1
+#define GR_ATTN_ABI_VERSION 2
 
 /* Status codes. */
 #define GR_OK 0
@@ -40,8 +40,11 @@ extern "C" {
 #define GR_ERR_RANGE (-3) /* position / range outside the context */
 #define GR_ERR_OOM (-4)   /* device allocation failed */
 
-/* Element types of activations and KV storage. */
-typedef enum gr_dtype { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2 } gr_dtype;
+/* Element types of activations and KV storage.  GR_DTYPE_Q8 is KV storage
+ * only: KvCacheFormat::Q8 (inference.rs:1886-1917), int8 rows plus f32 scales,
+ * one per kv_dim row or, in block mode (GGUF_Q8_BLOCK_SCALES), one per 32
+ * elements of the row. */
+typedef enum gr_dtype { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2, GR_DTYPE_Q8 = 3 } gr_dtype;
 
 /* RoPE pairing (apply_rope_qk, inference.rs:1817-1874). */
 typedef enum gr_rope_mode {
@@ -79,6 +82,15 @@ typedef struct gr_decode_args {
     const int32_t* kv_end;   /* [n_seq] device: one past the last visible key (pos + 1) */
     float* out;           /* [n_seq][n_heads][head_dim] f32 (s.xb rows) */
     void* workspace;      /* gr_decode_workspace_size() bytes, 256-byte aligned */
+    /* GR_DTYPE_Q8 only (NULL / 0 otherwise): key_cache_scale / value_cache_scale.
+     * The scale of (seq s, position t, kv head g, element i) is at
+     * s*scale_seq_stride + t*scale_row_stride + (q8_block ? (g*head_dim + i)/32 : 0)
+     * (inference.rs:1907-1916 row mode, 1888-1905 and 2021-2027 block mode). */
+    const float* k_scale;
+    const float* v_scale;
+    int64_t scale_seq_stride;
+    int64_t scale_row_stride;
+    int32_t q8_block;     /* 1: one scale per 32 elements (GGUF_Q8_BLOCK_SCALES) */
 } gr_decode_args;
 
 size_t gr_decode_workspace_size(const gr_decode_args* a);
@@ -188,7 +200,7 @@ typedef struct gr_attn_config {
     int32_t head_dim;
     int32_t seq_len;            /* cache rows per sequence (Config::seq_len) */
     int32_t n_seq;              /* sequence slots, one reference RunState each (>= 1) */
-    int32_t kv_dtype;           /* gr_dtype of the device KV cache (raw storage) */
+    int32_t kv_dtype;           /* gr_dtype of the device KV cache: raw F32/F16/BF16 or Q8 */
     int32_t rope_mode;          /* gr_rope_mode (NEOX for Gemma3/Qwen2/Qwen3*, ADJACENT for Llama) */
     int32_t rope_dim;           /* rotated dims, 0 -> head_dim (vendors/mod.rs:1015-1019) */
     float rope_theta;
@@ -206,6 +218,8 @@ typedef struct gr_attn_config {
     const uint8_t* qk_norm_present; /* host [n_layers] or NULL (= every layer when q_norm is set) */
     int32_t ssm_n_heads;        /* DeltaNet value heads, 0 = no SSM state */
     int32_t ssm_head_dim;       /* 128 */
+    int32_t q8_block_scales;    /* Q8 cache: 1 = one scale per 32 elements (GGUF_Q8_BLOCK_SCALES,
+                                 * inference.rs:1883), 0 = one scale per row */
 } gr_attn_config;
 
 /* malloc_run_state_with_kv_cache_format (inference.rs:1529-1748): validates
@@ -220,7 +234,9 @@ void gr_free_run_state(gr_run_state* s);
 int gr_qkv_norm(gr_run_state* s, int32_t layer, float* q, float* k);
 /* apply_rope_qk (inference.rs:1817-1874), in place on host q and k. */
 int gr_apply_rope_qk(gr_run_state* s, int32_t layer, int64_t pos, float* q, float* k);
-/* kv_write_token (inference.rs:1877-1965), raw storage: k, v -> cache row (layer, seq, pos). */
+/* kv_write_token (inference.rs:1877-1965): k, v -> cache row (layer, seq, pos),
+ * raw storage or, for a Q8 cache, quantize_row_q8 per row / 32-element block
+ * (inference.rs:166-268, 1886-1917). */
 int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* k,
                       const float* v);
 /* attention_token (inference.rs:1970-2530): q (post-RoPE) -> xb over the
@@ -259,6 +275,10 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
  * of a layer (f32 [ssm_n_heads][d][d]). */
 int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
                     void* k_out, void* v_out);
+/* Q8 cache only: the f32 scales of those rows (key_cache_scale / value_cache_scale),
+ * 1 per row, or kv_dim/32 per row in block mode. */
+int gr_read_kv_scales(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
+                      float* k_scale_out, float* v_scale_out);
 int gr_read_ssm_state(gr_run_state* s, int32_t layer, float* out);
 int gr_write_ssm_state(gr_run_state* s, int32_t layer, const float* in);
 

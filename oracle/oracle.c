@@ -35,7 +35,9 @@
 #define ORC_F32 0
 #define ORC_F16 1
 #define ORC_BF16 2
-#define ORC_Q8 3
+#define ORC_Q8 3  /* int8 rows, one f32 scale per kv_dim row */
+#define ORC_Q8B 4 /* int8 rows, one f32 scale per 32 elements (GGUF_Q8_BLOCK_SCALES) */
+#define ORC_Q8_BLOCK 32 /* Q4_BLOCK_SIZE */
 
 /* ---------------------------------------------------------------- dtypes */
 
@@ -80,7 +82,8 @@ static inline float load_kv(const void* base, size_t idx, int fmt) {
     switch (fmt) {
         case ORC_F16: return orc_f16_to_f32(((const uint16_t*)base)[idx]);
         case ORC_BF16: return orc_bf16_to_f32(((const uint16_t*)base)[idx]);
-        case ORC_Q8: return (float)((const int8_t*)base)[idx];
+        case ORC_Q8:
+        case ORC_Q8B: return (float)((const int8_t*)base)[idx];
         default: return ((const float*)base)[idx];
     }
 }
@@ -200,6 +203,21 @@ void orc_quantize_row_q8(const float* src, int n, int8_t* dst, float* scale_out)
     }
 }
 
+/* kv_write_token's Q8 branch, inference.rs:1886-1917, for one K or V row of
+ * kv_dim elements: block mode (GGUF_Q8_BLOCK_SCALES) quantises each 32-element
+ * block with quantize_row_q8 and writes kv_dim/32 scales; row mode quantises the
+ * whole row with one scale.  Pinned through orc_quantize_row_q8 and the
+ * per-block closed form in tests/test_oracle_rope_norm.py. */
+void orc_kv_quantize_row(const float* src, int kv_dim, int block, int8_t* dst, float* scales) {
+    if (block) {
+        for (int b = 0; b < kv_dim / ORC_Q8_BLOCK; b++)
+            orc_quantize_row_q8(src + b * ORC_Q8_BLOCK, ORC_Q8_BLOCK, dst + b * ORC_Q8_BLOCK,
+                                scales + b);
+    } else {
+        orc_quantize_row_q8(src, kv_dim, dst, scales);
+    }
+}
+
 /* ---------------------------------------------------------------- softmax */
 
 /* softmax, x86 branch, math.rs:263-280. */
@@ -245,6 +263,60 @@ static inline void row_axpy(float* dst, float a, const void* cache, size_t off, 
     }
 }
 
+/* dot_q8_row_blocks_ptr / axpy_q8_row_blocks_ptr, inference.rs:1368-1483:
+ * one dot_q8_row / axpy_q8_row per 32-element block with that block's scale,
+ * block dots added to the accumulator in block order (the 4-way unrolled loop
+ * keeps that order). */
+static inline float row_dot_blocks(const float* q, const int8_t* cache, size_t off, int n,
+                                   const float* scales) {
+    float acc = 0.0f;
+    for (int b = 0; b * ORC_Q8_BLOCK < n; b++) {
+        float part = 0.0f;
+        const int8_t* c = cache + off + (size_t)b * ORC_Q8_BLOCK;
+        const float* qb = q + b * ORC_Q8_BLOCK;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) part += qb[i] * ((float)c[i] * scales[b]);
+        acc += part;
+    }
+    return acc;
+}
+
+static inline void row_axpy_blocks(float* dst, float a, const int8_t* cache, size_t off, int n,
+                                   const float* scales) {
+    for (int b = 0; b * ORC_Q8_BLOCK < n; b++) {
+        float scaled = a * scales[b];
+        const int8_t* c = cache + off + (size_t)b * ORC_Q8_BLOCK;
+        float* d = dst + b * ORC_Q8_BLOCK;
+        for (int i = 0; i < ORC_Q8_BLOCK; i++) d[i] += scaled * (float)c[i];
+    }
+}
+
+/* Score and value update of key row t_row for one head, any storage format.
+ * Q8B scales of (row, kv head) start at t_row*kv_dim/32 + kv_head_offset/32
+ * (inference.rs:2021-2027 with sb = t_row*n_blocks_per_row). */
+static inline float key_dot(const float* q_head, const void* key_cache, size_t row_offset,
+                            int head_size, int fmt, const float* key_scale, size_t t_row,
+                            size_t kv_dim, size_t kv_head_offset) {
+    if (fmt == ORC_Q8B)
+        return row_dot_blocks(q_head, (const int8_t*)key_cache, row_offset, head_size,
+                              key_scale + t_row * (kv_dim / ORC_Q8_BLOCK) +
+                                  kv_head_offset / ORC_Q8_BLOCK);
+    return row_dot(q_head, key_cache, row_offset, head_size, fmt,
+                   fmt == ORC_Q8 ? key_scale[t_row] : 1.0f);
+}
+
+static inline void value_axpy(float* xb_head, float w, const void* value_cache, size_t row_offset,
+                              int head_size, int fmt, const float* value_scale, size_t t_row,
+                              size_t kv_dim, size_t kv_head_offset) {
+    if (fmt == ORC_Q8B) {
+        row_axpy_blocks(xb_head, w, (const int8_t*)value_cache, row_offset, head_size,
+                        value_scale + t_row * (kv_dim / ORC_Q8_BLOCK) +
+                            kv_head_offset / ORC_Q8_BLOCK);
+        return;
+    }
+    row_axpy(xb_head, w, value_cache, row_offset, head_size, fmt,
+             fmt == ORC_Q8 ? value_scale[t_row] : 1.0f);
+}
+
 /* One query head of attention_token, inference.rs:2008-2284 (the per-head
  * closure; the serial branch 2290-2528 computes the same thing).
  *   online == 0: two-pass: scores -> softmax (math.rs:263-280) -> axpy (2175-2283)
@@ -263,8 +335,8 @@ static void attention_head(const float* q_head, float* xb_head, float* att_head,
         for (size_t t = vis_start; t < vis_end; t++) {
             size_t t_row = layer_row_base + t;
             size_t row_offset = t_row * kv_dim + kv_head_offset;
-            float score = row_dot(q_head, key_cache, row_offset, head_size, fmt,
-                                  fmt == ORC_Q8 ? key_scale[t_row] : 1.0f);
+            float score = key_dot(q_head, key_cache, row_offset, head_size, fmt, key_scale, t_row,
+                                  kv_dim, kv_head_offset);
             if (apply_attn_scale) score *= attn_scale;
             if (score > max_score) {
                 if (score_sum > 0.0f) {
@@ -276,8 +348,8 @@ static void attention_head(const float* q_head, float* xb_head, float* att_head,
             }
             float weight = expf(score - max_score);
             score_sum += weight;
-            row_axpy(xb_head, weight, value_cache, row_offset, head_size, fmt,
-                     fmt == ORC_Q8 ? value_scale[t_row] : 1.0f);
+            value_axpy(xb_head, weight, value_cache, row_offset, head_size, fmt, value_scale, t_row,
+                       kv_dim, kv_head_offset);
         }
         if (score_sum > 0.0f) {
             float inv = 1.0f / score_sum;
@@ -288,8 +360,8 @@ static void attention_head(const float* q_head, float* xb_head, float* att_head,
         for (size_t t = vis_start; t < vis_end; t++) {
             size_t t_row = layer_row_base + t;
             size_t row_offset = t_row * kv_dim + kv_head_offset;
-            float score = row_dot(q_head, key_cache, row_offset, head_size, fmt,
-                                  fmt == ORC_Q8 ? key_scale[t_row] : 1.0f);
+            float score = key_dot(q_head, key_cache, row_offset, head_size, fmt, key_scale, t_row,
+                                  kv_dim, kv_head_offset);
             if (apply_attn_scale) score *= attn_scale;
             att_head[t - vis_start] = score;
         }
@@ -298,8 +370,8 @@ static void attention_head(const float* q_head, float* xb_head, float* att_head,
         for (size_t t = vis_start; t < vis_end; t++) {
             size_t t_row = layer_row_base + t;
             size_t row_offset = t_row * kv_dim + kv_head_offset;
-            row_axpy(xb_head, att_head[t - vis_start], value_cache, row_offset, head_size, fmt,
-                     fmt == ORC_Q8 ? value_scale[t_row] : 1.0f);
+            value_axpy(xb_head, att_head[t - vis_start], value_cache, row_offset, head_size, fmt,
+                       value_scale, t_row, kv_dim, kv_head_offset);
         }
     }
 }
@@ -390,9 +462,10 @@ static void store_kv(void* base, size_t idx, int fmt, float v) {
 }
 
 /* The serial prefill loop of transformer_prefill_batch, inference.rs:2981-3017,
- * for the attention part of one layer and one sequence, raw KV storage:
+ * for the attention part of one layer and one sequence:
  *   per token i (pos = base_pos + i):  qkv_bias_and_norm (QK-norm only, 2535-2572)
- *   -> apply_rope_qk (1817-1874) -> kv_write_token (1877-1965, raw storage)
+ *   -> apply_rope_qk (1817-1874) -> kv_write_token (1877-1965: raw storage, or Q8
+ *   rows + scales for fmt ORC_Q8 / ORC_Q8B into key_scale / value_scale)
  *   -> attention_token (1970-2530) -> xb row.
  * Inputs q [m][n_heads*d], k/v [m][n_kv_heads*d] are f32 (already upcast from the
  * test's f16/bf16 buffers).  key/value_cache are [seq_len][kv_dim] of `fmt`.
@@ -405,7 +478,7 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                        void* key_cache, void* value_cache, int fmt, int rope_dim, int neox,
                        const float* rope_freqs, float rope_scale, int is_gemma3, int online,
                        int64_t window, const float* q_norm, const float* k_norm, float eps,
-                       int n_threads) {
+                       float* key_scale, float* value_scale, int n_threads) {
     int q_dim = n_heads * head_size;
     int kv_dim = n_kv_heads * head_size;
     int half = rope_dim / 2;
@@ -431,14 +504,23 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
         } else if (is_gemma3) {
             for (int j = 0; j < q_dim; j++) q[j] *= attn_scale;
         }
-        for (int j = 0; j < kv_dim; j++) {
-            store_kv(key_cache, (size_t)pos * kv_dim + j, fmt, k[j]);
-            store_kv(value_cache, (size_t)pos * kv_dim + j, fmt, v_in[(size_t)i * kv_dim + j]);
+        if (fmt == ORC_Q8 || fmt == ORC_Q8B) {
+            const int blk = fmt == ORC_Q8B;
+            const size_t so = (size_t)pos * (blk ? (size_t)kv_dim / ORC_Q8_BLOCK : 1);
+            orc_kv_quantize_row(k, kv_dim, blk, (int8_t*)key_cache + (size_t)pos * kv_dim,
+                                key_scale + so);
+            orc_kv_quantize_row(v_in + (size_t)i * kv_dim, kv_dim, blk,
+                                (int8_t*)value_cache + (size_t)pos * kv_dim, value_scale + so);
+        } else {
+            for (int j = 0; j < kv_dim; j++) {
+                store_kv(key_cache, (size_t)pos * kv_dim + j, fmt, k[j]);
+                store_kv(value_cache, (size_t)pos * kv_dim + j, fmt, v_in[(size_t)i * kv_dim + j]);
+            }
         }
         int64_t s, e;
         orc_visible_keys(window, pos, &s, &e);
         orc_attention_token(q, xb_out + (size_t)i * q_dim, att, att_stride, n_heads, n_kv_heads,
-                            head_size, key_cache, value_cache, fmt, NULL, NULL, 0, (size_t)s,
+                            head_size, key_cache, value_cache, fmt, key_scale, value_scale, 0, (size_t)s,
                             (size_t)e, attn_scale, !is_gemma3, online, n_threads);
     }
     free(q);

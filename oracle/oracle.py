@@ -16,7 +16,8 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liboracle.so"
 
-F32, F16, BF16, Q8 = 0, 1, 2, 3
+F32, F16, BF16, Q8, Q8B = 0, 1, 2, 3, 4
+Q8_BLOCK = 32
 
 _lib = None
 
@@ -56,12 +57,13 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_apply_rope_qk.argtypes = [_p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _f]
     L.orc_rmsnorm_per_head.argtypes = [_p, _p, _i, _i, _f]
     L.orc_quantize_row_q8.argtypes = [_p, _i, _p, _p]
+    L.orc_kv_quantize_row.argtypes = [_p, _i, _i, _p, _p]
     L.orc_softmax.argtypes = [_p, _i]
     L.orc_attention_token.argtypes = [_p, _p, _p, _sz, _i, _i, _i, _p, _p, _i, _p, _p, _sz, _sz,
                                       _sz, _f, _i, _i, _i]
     L.orc_visible_keys.argtypes = [_i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
     L.orc_prefill_layer.argtypes = [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _i, _i, _i, _p,
-                                    _f, _i, _i, _i64, _p, _p, _f, _i]
+                                    _f, _i, _i, _i64, _p, _p, _f, _p, _p, _i]
     L.orc_deltanet_head_step.argtypes = [_p, _p, _p, _p, _p, _f, _f, _i]
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
@@ -126,6 +128,16 @@ def quantize_row_q8(src):
     return dst, float(scale[0])
 
 
+def kv_quantize_row(src, block: bool):
+    """kv_write_token's Q8 branch for one kv_dim row: (int8 row, scales) with one
+    scale (row mode) or kv_dim/32 scales (block mode)."""
+    src = _f32(src)
+    dst = np.zeros(src.size, np.int8)
+    scales = np.zeros(src.size // Q8_BLOCK if block else 1, np.float32)
+    lib().orc_kv_quantize_row(_ptr(src), src.size, int(block), _ptr(dst), _ptr(scales))
+    return dst, scales
+
+
 def softmax(x):
     x = _f32(x).copy()
     lib().orc_softmax(_ptr(x), x.size)
@@ -165,17 +177,27 @@ def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope
                   rope_freqs_tab, rope_scale, is_gemma3=False, online=False, window=0,
                   q_norm=None, k_norm=None, eps=1e-6, base_pos=0, key_cache=None,
                   value_cache=None, n_threads=1):
-    """Token-serial prefill of one layer (inference.rs:2981-3017), raw KV mode.
-    q [m][n_heads*d], k/v [m][n_kv_heads*d] f32.  Returns (xb [m][q_dim], kcache, vcache)."""
+    """Token-serial prefill of one layer (inference.rs:2981-3017), raw or Q8 KV.
+    q [m][n_heads*d], k/v [m][n_kv_heads*d] f32.  Returns (xb [m][q_dim], kcache, vcache);
+    for fmt Q8 / Q8B the caches are (int8 rows, scales) pairs."""
     q = _f32(q)
     k = _f32(k)
     v = _f32(v)
     m = q.shape[0]
     kv_dim = n_kv_heads * head_size
-    cdt = np.float32 if fmt == F32 else np.uint16
+    q8 = fmt in (Q8, Q8B)
+    cdt = np.float32 if fmt == F32 else (np.int8 if q8 else np.uint16)
+    ks = vs = None
+    if q8 and key_cache is not None:
+        key_cache, ks = key_cache
+        value_cache, vs = value_cache
     if key_cache is None:
         key_cache = np.zeros((seq_len, kv_dim), cdt)
         value_cache = np.zeros((seq_len, kv_dim), cdt)
+    if q8 and ks is None:
+        nsc = seq_len * (kv_dim // Q8_BLOCK if fmt == Q8B else 1)
+        ks = np.zeros(nsc, np.float32)
+        vs = np.zeros(nsc, np.float32)
     xb = np.zeros((m, n_heads * head_size), np.float32)
     freqs = _f32(rope_freqs_tab) if rope_freqs_tab is not None else None
     qn = _f32(q_norm) if q_norm is not None else None
@@ -183,7 +205,9 @@ def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope
     lib().orc_prefill_layer(_ptr(q), _ptr(k), _ptr(v), _ptr(xb), m, base_pos, n_heads, n_kv_heads,
                             head_size, _ptr(key_cache), _ptr(value_cache), fmt, rope_dim,
                             int(neox), _ptr(freqs), rope_scale, int(is_gemma3), int(online),
-                            window, _ptr(qn), _ptr(kn), eps, n_threads)
+                            window, _ptr(qn), _ptr(kn), eps, _ptr(ks), _ptr(vs), n_threads)
+    if q8:
+        return xb, (key_cache, ks), (value_cache, vs)
     return xb, key_cache, value_cache
 
 

@@ -114,3 +114,71 @@ def test_prefill_layer_closed_form_window_norm_rope(orc):
             exp = _np_attention(qq[h], Ks[s0:t + 1, g], Vs[s0:t + 1, g], 1.0)
             got = out[t, h * d:(h + 1) * d]
             assert np.all(np.abs(got - exp) <= 5e-5 * np.maximum(np.abs(exp), 1.0))
+
+
+@pytest.mark.parametrize("online", [False, True])
+@pytest.mark.parametrize("block", [False, True])
+def test_attention_token_q8_closed_form(orc, online, block):
+    """Q8 KV (inference.rs:1337-1483): scores and values use c * scale with the row's
+    scale (row mode) or the 32-element block's scale (GGUF_Q8_BLOCK_SCALES).  Blocks
+    and rows get very different magnitudes, so a wrong scale index fails."""
+    rng = np.random.default_rng(31 + int(block))
+    H, Hk, d, L = 8, 2, 128, 200
+    kv_dim = Hk * d
+    q = rng.standard_normal(H * d).astype(np.float32) * 0.2
+    kf = rng.standard_normal((L, kv_dim)).astype(np.float32)
+    vf = rng.standard_normal((L, kv_dim)).astype(np.float32)
+    mag = np.exp(rng.uniform(-2, 2, size=(L, kv_dim // 32))).astype(np.float32)
+    kf *= np.repeat(mag, 32, axis=1)
+    vf *= np.repeat(mag[:, ::-1], 32, axis=1)
+    rows = [orc.kv_quantize_row(kf[t], block) for t in range(L)]
+    kq = np.stack([r[0] for r in rows])
+    ks = np.concatenate([r[1] for r in rows])
+    rows = [orc.kv_quantize_row(vf[t], block) for t in range(L)]
+    vq = np.stack([r[0] for r in rows])
+    vs = np.concatenate([r[1] for r in rows])
+    per = kv_dim // 32 if block else 1
+    Kd = (kq.astype(np.float64) * np.repeat(ks.reshape(L, per), kv_dim // per, axis=1))
+    Vd = (vq.astype(np.float64) * np.repeat(vs.reshape(L, per), kv_dim // per, axis=1))
+    fmt = orc.Q8B if block else orc.Q8
+    s0, s1 = 5, 190
+    out = orc.attention_token(q, kq, vq, fmt, H, Hk, d, s0, s1, key_scale=ks, value_scale=vs,
+                              online=online, n_threads=4)
+    for h in range(H):
+        g = h // (H // Hk)
+        exp = _np_attention(q[h * d:(h + 1) * d], Kd[s0:s1, g * d:(g + 1) * d],
+                            Vd[s0:s1, g * d:(g + 1) * d], 1.0 / np.sqrt(d))
+        assert np.all(np.abs(out[h * d:(h + 1) * d] - exp) <= _tol(exp))
+
+
+@pytest.mark.parametrize("block", [False, True])
+def test_prefill_layer_q8_writes_quantised_rows(orc, block):
+    """Q8 prefill: every written row dequantises to within half a step of the post-RoPE
+    K (resp. V) row, and each token's output is the closed form over the dequantised
+    rows it can see."""
+    rng = np.random.default_rng(41)
+    H, Hk, d, m = 4, 2, 64, 24
+    kv_dim = Hk * d
+    q = rng.standard_normal((m, H * d)).astype(np.float32)
+    k = rng.standard_normal((m, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, kv_dim)).astype(np.float32)
+    fr = orc.rope_freqs(10000.0, d)
+    fmt = orc.Q8B if block else orc.Q8
+    xb, (kq, ks), (vq, vs) = orc.prefill_layer(q, k, v, n_heads=H, n_kv_heads=Hk, head_size=d,
+                                               seq_len=m, fmt=fmt, rope_dim=d, neox=True,
+                                               rope_freqs_tab=fr, rope_scale=1.0)
+    per = kv_dim // 32 if block else 1
+    Ks = np.repeat(ks.reshape(m, per), kv_dim // per, axis=1)
+    Vs = np.repeat(vs.reshape(m, per), kv_dim // per, axis=1)
+    Kd = kq.astype(np.float64) * Ks
+    Vd = vq.astype(np.float64) * Vs
+    assert np.all(np.abs(Vd - v) <= 0.5001 * Vs)
+    for i in range(m):
+        c, s = orc.rope_cache(fr, i, 1.0)
+        qi, ki = orc.apply_rope_qk(q[i], k[i], H, Hk, d, c, s, neox=True)
+        assert np.all(np.abs(Kd[i] - ki) <= 0.5001 * Ks[i])
+        for h in range(H):
+            g = h // (H // Hk)
+            exp = _np_attention(qi[h * d:(h + 1) * d], Kd[:i + 1, g * d:(g + 1) * d],
+                                Vd[:i + 1, g * d:(g + 1) * d], 1.0 / np.sqrt(d))
+            assert np.all(np.abs(xb[i, h * d:(h + 1) * d] - exp) <= _tol(exp))

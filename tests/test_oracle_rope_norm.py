@@ -156,3 +156,30 @@ def test_visible_keys_reference_cases(orc):
     assert orc.visible_keys(1024, 1023) == (0, 1024)
     assert orc.visible_keys(1024, 1024) == (1, 1025)
     assert orc.visible_keys(1, 77) == (77, 78)
+
+
+def test_kv_quantize_row_block_and_row_modes(orc):
+    """kv_write_token's Q8 branch (inference.rs:1886-1917): block mode quantises each
+    32-element block on its own (scale_b = amax_b/127), row mode uses one scale."""
+    rng = np.random.default_rng(12)
+    kv_dim = 256
+    x = rng.standard_normal(kv_dim).astype(np.float32)
+    x[32:64] *= 40.0   # one loud block
+    x[96:128] = 0.0    # one silent block: scale 1, zeros
+    qb, sb = orc.kv_quantize_row(x, True)
+    assert sb.shape == (kv_dim // 32,)
+    for b in range(kv_dim // 32):
+        blk = x[32 * b:32 * (b + 1)]
+        amax = np.float32(np.abs(blk).max())
+        if amax == 0:
+            assert sb[b] == 1.0 and not qb[32 * b:32 * (b + 1)].any()
+            continue
+        assert sb[b] == np.float32(amax / np.float32(127.0))
+        prod = (blk * (np.float32(127.0) / amax)).astype(np.float32)
+        exp = np.where(prod >= 0, np.floor(prod + 0.5), -np.floor(-prod + 0.5)).clip(-127, 127)
+        assert np.array_equal(qb[32 * b:32 * (b + 1)], exp.astype(np.int8))
+        # dequantised values sit within half a step of the input
+        assert np.all(np.abs(qb[32 * b:32 * (b + 1)] * sb[b] - blk) <= 0.5001 * sb[b])
+    qr, sr = orc.kv_quantize_row(x, False)
+    assert sr.shape == (1,) and sr[0] == np.float32(np.float32(np.abs(x).max()) / np.float32(127.0))
+    assert np.array_equal(qr, orc.quantize_row_q8(x)[0])
