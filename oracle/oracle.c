@@ -530,6 +530,282 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
     free(att);
 }
 
+/* ---------------------------------------------------------------- Turbo KV codec */
+
+/* KvCacheFormat::Turbo, inference.rs:346-1334 (x86 scalar branches).  Per KV
+ * head of a row: rotate (sign flips, normalised FWHT, sign flips), 2-bit
+ * Lloyd-Max code of rotated/sigma with sigma = |rotated|/sqrt(n), then a 1-bit
+ * sign sketch of the residual after a second rotation, with its norm gamma.
+ * Pinned by the reference's own tests (inference.rs:4534-4566: q2 packing,
+ * self-inverse transform), the SplitMix64 known answers, the Hadamard closed
+ * form and the fp64 attention closed form (tests/test_oracle_turbo.py). */
+static const float TQ_CENTROIDS[4] = {-1.510417f, -0.45278f, 0.45278f, 1.510417f}; /* 349 */
+#define TQ_THRESHOLD 0.9815985f                                                      /* 350-351 */
+static const uint64_t TQ_SALTS[4] = {0x9E3779B97F4A7C15ull, 0xC2B2AE3D27D4EB4Full,   /* 352-355 */
+                                     0x165667B19E3779F9ull, 0xD6E8FEB86659FD93ull};
+enum { TQ_ROT_PRE = 0, TQ_ROT_POST = 1, TQ_RES_PRE = 2, TQ_RES_POST = 3 };         /* 357-360 */
+
+/* splitmix64, inference.rs:674-679. */
+uint64_t orc_splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+/* turboquant_build_sign_table, inference.rs:370-395: layout
+ * [slot][layer][kv_head][ceil(head_size/8)], bit i set = multiply element i by -1. */
+void orc_turbo_sign_table(int n_layers, int n_kv_heads, int head_size, uint8_t* table) {
+    const size_t bytes = (size_t)(head_size + 7) / 8;
+    const size_t stride = (size_t)n_layers * n_kv_heads * bytes;
+    memset(table, 0, 4 * stride);
+    for (int slot = 0; slot < 4; slot++)
+        for (int l = 0; l < n_layers; l++)
+            for (int g = 0; g < n_kv_heads; g++) {
+                const uint64_t seed = orc_splitmix64(((uint64_t)l << 32) ^ (uint64_t)g ^ TQ_SALTS[slot]);
+                uint8_t* bits = table + slot * stride + ((size_t)l * n_kv_heads + g) * bytes;
+                for (int i = 0; i < head_size; i++)
+                    if (orc_splitmix64(seed ^ (uint64_t)i) & 1) bits[i / 8] |= (uint8_t)(1u << (i & 7));
+            }
+}
+
+static const uint8_t* tq_slot(const uint8_t* table, int slot, int layer, int kv_head, int n_layers,
+                              int n_kv_heads, int head_size) {
+    const size_t bytes = (size_t)(head_size + 7) / 8;
+    return table + (size_t)slot * n_layers * n_kv_heads * bytes + ((size_t)layer * n_kv_heads + kv_head) * bytes;
+}
+
+/* turboquant_apply_signs_bits (scalar tail), inference.rs:430-436. */
+static void tq_apply_signs(float* v, int n, const uint8_t* bits) {
+    for (int i = 0; i < n; i++)
+        if ((bits[i / 8] >> (i & 7)) & 1) v[i] = -v[i];
+}
+
+/* turboquant_fwht_inplace_scalar, inference.rs:681-701; no-op unless n is a power of two (799). */
+static void tq_fwht(float* v, int n) {
+    if (n <= 0 || (n & (n - 1))) return;
+    for (int width = 1; width < n; width *= 2)
+        for (int base = 0; base < n; base += 2 * width)
+            for (int i = 0; i < width; i++) {
+                const float a = v[base + i], b = v[base + i + width];
+                v[base + i] = a + b;
+                v[base + i + width] = a - b;
+            }
+    const float scale = 1.0f / sqrtf((float)n);
+    for (int i = 0; i < n; i++) v[i] *= scale;
+}
+
+/* turboquant_transform_with_bits, inference.rs:596-605 (x86 path). */
+void orc_turbo_transform(float* v, int n, const uint8_t* first_bits, const uint8_t* second_bits) {
+    tq_apply_signs(v, n, first_bits);
+    tq_fwht(v, n);
+    tq_apply_signs(v, n, second_bits);
+}
+
+/* l2_norm, math.rs:467-473. */
+static float tq_l2(const float* x, int n) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    return sqrtf(ss);
+}
+
+/* turboquant_quantize_code, inference.rs:805-816. */
+static int tq_code(float x) {
+    if (x < -TQ_THRESHOLD) return 0;
+    if (x < 0.0f) return 1;
+    if (x < TQ_THRESHOLD) return 2;
+    return 3;
+}
+
+/* quantize_turboquant_head, inference.rs:855-925, for one head of n elements
+ * starting at element `elem_offset` of the packed base (4 codes per byte, low
+ * bits first) and sign (8 bits per byte, bit set = residual >= 0) arrays. */
+void orc_turbo_quantize_head(const float* src, int n, const uint8_t* table, int layer, int kv_head,
+                             int n_layers, int n_kv_heads, uint8_t* base, uint8_t* sign,
+                             size_t elem_offset, float* scale_out, float* residual_norm_out) {
+    float* rot = (float*)malloc(sizeof(float) * (size_t)n);
+    float* res = (float*)malloc(sizeof(float) * (size_t)n);
+    memcpy(rot, src, sizeof(float) * (size_t)n);
+    orc_turbo_transform(rot, n, tq_slot(table, TQ_ROT_PRE, layer, kv_head, n_layers, n_kv_heads, n),
+                        tq_slot(table, TQ_ROT_POST, layer, kv_head, n_layers, n_kv_heads, n));
+    const float sigma = tq_l2(rot, n) / sqrtf((float)n);
+    *scale_out = sigma;
+    if (sigma == 0.0f) {
+        *residual_norm_out = 0.0f;
+        for (int i = 0; i < (n + 3) / 4; i++) base[elem_offset / 4 + i] = 0;
+        for (int i = 0; i < n; i++) sign[(elem_offset + i) / 8] |= (uint8_t)(1u << ((elem_offset + i) & 7));
+        free(rot);
+        free(res);
+        return;
+    }
+    const float inv_sigma = 1.0f / sigma;
+    for (int i = 0; i < n; i += 4) {
+        uint8_t packed = 0;
+        for (int k = 0; k < 4 && i + k < n; k++) {
+            const float value = rot[i + k];
+            const int code = tq_code(value * inv_sigma);
+            res[i + k] = value - TQ_CENTROIDS[code] * sigma;
+            packed |= (uint8_t)(code << (k * 2));
+        }
+        base[elem_offset / 4 + i / 4] = packed;
+    }
+    const float gamma = tq_l2(res, n);
+    *residual_norm_out = gamma;
+    if (gamma == 0.0f) {
+        for (int i = 0; i < n; i++) sign[(elem_offset + i) / 8] |= (uint8_t)(1u << ((elem_offset + i) & 7));
+        free(rot);
+        free(res);
+        return;
+    }
+    for (int i = 0; i < n; i++) res[i] /= gamma;
+    orc_turbo_transform(res, n, tq_slot(table, TQ_RES_PRE, layer, kv_head, n_layers, n_kv_heads, n),
+                        tq_slot(table, TQ_RES_POST, layer, kv_head, n_layers, n_kv_heads, n));
+    for (int i = 0; i < n; i++) {
+        const size_t e = elem_offset + (size_t)i;
+        if (res[i] >= 0.0f) sign[e / 8] |= (uint8_t)(1u << (e & 7));
+        else sign[e / 8] &= (uint8_t)~(1u << (e & 7));
+    }
+    free(rot);
+    free(res);
+}
+
+/* kv_write_token's Turbo branch, inference.rs:1918-1963: both rows of one token,
+ * aux index row_index*n_kv_heads + kv_head (turboquant_aux_index, 669-672). */
+void orc_kv_write_turbo(const float* k, const float* v, int n_kv_heads, int head_size,
+                        const uint8_t* table, int layer, int n_layers, size_t row_index,
+                        uint8_t* kbase, uint8_t* ksign, float* kscale, float* kres, uint8_t* vbase,
+                        uint8_t* vsign, float* vscale, float* vres) {
+    const size_t kv_dim = (size_t)n_kv_heads * head_size;
+    for (int g = 0; g < n_kv_heads; g++) {
+        const size_t off = row_index * kv_dim + (size_t)g * head_size;
+        const size_t aux = row_index * n_kv_heads + g;
+        orc_turbo_quantize_head(k + (size_t)g * head_size, head_size, table, layer, g, n_layers,
+                                n_kv_heads, kbase, ksign, off, kscale + aux, kres + aux);
+        orc_turbo_quantize_head(v + (size_t)g * head_size, head_size, table, layer, g, n_layers,
+                                n_kv_heads, vbase, vsign, off, vscale + aux, vres + aux);
+    }
+}
+
+/* turboquant_residual_scale, inference.rs:947-954. */
+static float tq_residual_scale(int n, float residual_norm) {
+    return residual_norm == 0.0f ? 0.0f : residual_norm * sqrtf(1.5707964f / (float)n);
+}
+
+/* dot_turboquant_head_scalar, inference.rs:1246-1272. */
+static float tq_dot(const float* q_rot, const float* q_proj, int n, const uint8_t* base,
+                    const uint8_t* sign, size_t off, float scale, float residual_norm) {
+    float acc = 0.0f;
+    if (scale != 0.0f)
+        for (int i = 0; i < n; i++) {
+            const int code = (base[(off + i) / 4] >> (((off + i) & 3) * 2)) & 3;
+            acc += q_rot[i] * (TQ_CENTROIDS[code] * scale);
+        }
+    const float rs = tq_residual_scale(n, residual_norm);
+    if (rs != 0.0f)
+        for (int i = 0; i < n; i++)
+            acc += ((sign[(off + i) / 8] >> ((off + i) & 7)) & 1) ? rs * q_proj[i] : -rs * q_proj[i];
+    return acc;
+}
+
+/* axpy_turboquant_head_scalar, inference.rs:1286-1310. */
+static void tq_axpy(float* base_acc, float* res_acc, float a, int n, const uint8_t* base,
+                    const uint8_t* sign, size_t off, float scale, float residual_norm) {
+    if (scale != 0.0f)
+        for (int i = 0; i < n; i++) {
+            const int code = (base[(off + i) / 4] >> (((off + i) & 3) * 2)) & 3;
+            base_acc[i] += a * TQ_CENTROIDS[code] * scale;
+        }
+    const float rs = a * tq_residual_scale(n, residual_norm);
+    if (rs != 0.0f)
+        for (int i = 0; i < n; i++)
+            res_acc[i] += ((sign[(off + i) / 8] >> ((off + i) & 7)) & 1) ? rs : -rs;
+}
+
+/* attention_token over a Turbo cache (inference.rs:2008-2290, Turbo arms) for one
+ * (layer, pos): turboquant_prepare_query (954-968) per head, scores with
+ * tq_dot, softmax (two-pass) or online accumulation with the residual
+ * accumulator rescaled alongside, then finalize_turboquant_value_head
+ * (1323-1334): inverse residual rotation, accum (= add), inverse rotation. */
+void orc_attention_token_turbo(const float* q, float* xb, float* att, size_t att_stride, int n_heads,
+                               int n_kv_heads, int head_size, const uint8_t* kbase,
+                               const uint8_t* ksign, const float* kscale, const float* kres,
+                               const uint8_t* vbase, const uint8_t* vsign, const float* vscale,
+                               const float* vres, const uint8_t* table, int layer, int n_layers,
+                               size_t layer_row_base, size_t vis_start, size_t vis_end,
+                               float attn_scale, int apply_attn_scale, int online, int n_threads) {
+    const int kv_mul = n_heads / n_kv_heads;
+    const size_t kv_dim = (size_t)n_kv_heads * head_size;
+    const int n = head_size;
+#pragma omp parallel for schedule(static) num_threads(n_threads > 0 ? n_threads : 1) if (n_threads > 1)
+    for (int h = 0; h < n_heads; h++) {
+        const int g = h / kv_mul;
+        float* qr = (float*)malloc(sizeof(float) * (size_t)n);
+        float* qp = (float*)malloc(sizeof(float) * (size_t)n);
+        float* racc = (float*)calloc((size_t)n, sizeof(float));
+        float* out = xb + (size_t)h * n;
+        float* ah = att + (size_t)h * att_stride;
+        const uint8_t* rot_pre = tq_slot(table, TQ_ROT_PRE, layer, g, n_layers, n_kv_heads, n);
+        const uint8_t* rot_post = tq_slot(table, TQ_ROT_POST, layer, g, n_layers, n_kv_heads, n);
+        const uint8_t* res_pre = tq_slot(table, TQ_RES_PRE, layer, g, n_layers, n_kv_heads, n);
+        const uint8_t* res_post = tq_slot(table, TQ_RES_POST, layer, g, n_layers, n_kv_heads, n);
+        memcpy(qr, q + (size_t)h * n, sizeof(float) * (size_t)n);
+        orc_turbo_transform(qr, n, rot_pre, rot_post);
+        memcpy(qp, qr, sizeof(float) * (size_t)n);
+        orc_turbo_transform(qp, n, res_pre, res_post);
+        for (int i = 0; i < n; i++) out[i] = 0.0f;
+        if (online) {
+            float max_score = -INFINITY, score_sum = 0.0f;
+            for (size_t t = vis_start; t < vis_end; t++) {
+                const size_t t_row = layer_row_base + t;
+                const size_t off = t_row * kv_dim + (size_t)g * n;
+                const size_t aux = t_row * n_kv_heads + g;
+                float score = tq_dot(qr, qp, n, kbase, ksign, off, kscale[aux], kres[aux]);
+                if (apply_attn_scale) score *= attn_scale;
+                if (score > max_score) {
+                    if (score_sum > 0.0f) {
+                        const float rescale = expf(max_score - score);
+                        for (int i = 0; i < n; i++) out[i] *= rescale;
+                        for (int i = 0; i < n; i++) racc[i] *= rescale;
+                        score_sum *= rescale;
+                    }
+                    max_score = score;
+                }
+                const float w = expf(score - max_score);
+                score_sum += w;
+                tq_axpy(out, racc, w, n, vbase, vsign, off, vscale[aux], vres[aux]);
+            }
+            if (score_sum > 0.0f) {
+                const float inv = 1.0f / score_sum;
+                for (int i = 0; i < n; i++) out[i] *= inv;
+                for (int i = 0; i < n; i++) racc[i] *= inv;
+            }
+        } else {
+            const size_t cnt = vis_end - vis_start;
+            for (size_t t = vis_start; t < vis_end; t++) {
+                const size_t t_row = layer_row_base + t;
+                const size_t off = t_row * kv_dim + (size_t)g * n;
+                const size_t aux = t_row * n_kv_heads + g;
+                float score = tq_dot(qr, qp, n, kbase, ksign, off, kscale[aux], kres[aux]);
+                if (apply_attn_scale) score *= attn_scale;
+                ah[t - vis_start] = score;
+            }
+            orc_softmax(ah, (int)cnt);
+            for (size_t t = vis_start; t < vis_end; t++) {
+                const size_t t_row = layer_row_base + t;
+                const size_t off = t_row * kv_dim + (size_t)g * n;
+                const size_t aux = t_row * n_kv_heads + g;
+                tq_axpy(out, racc, ah[t - vis_start], n, vbase, vsign, off, vscale[aux], vres[aux]);
+            }
+        }
+        orc_turbo_transform(racc, n, res_post, res_pre);
+        for (int i = 0; i < n; i++) out[i] += racc[i];
+        orc_turbo_transform(out, n, rot_post, rot_pre);
+        free(qr);
+        free(qp);
+        free(racc);
+    }
+}
+
 /* ---------------------------------------------------------------- gated DeltaNet */
 
 /* axpy_inplace on x86 with AVX2+FMA, quant.rs:1023-1047 + 1069-1080:

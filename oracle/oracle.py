@@ -68,6 +68,14 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
     L.orc_max_threads.restype = _i
+    L.orc_splitmix64.argtypes = [ctypes.c_uint64]
+    L.orc_splitmix64.restype = ctypes.c_uint64
+    L.orc_turbo_sign_table.argtypes = [_i, _i, _i, _p]
+    L.orc_turbo_transform.argtypes = [_p, _i, _p, _p]
+    L.orc_turbo_quantize_head.argtypes = [_p, _i, _p, _i, _i, _i, _i, _p, _p, _sz, _p, _p]
+    L.orc_kv_write_turbo.argtypes = [_p, _p, _i, _i, _p, _i, _i, _sz, _p, _p, _p, _p, _p, _p, _p, _p]
+    L.orc_attention_token_turbo.argtypes = [_p, _p, _p, _sz, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p,
+                                            _p, _p, _i, _i, _sz, _sz, _sz, _f, _i, _i, _i]
 
 
 def _ptr(a: np.ndarray | None):
@@ -233,6 +241,94 @@ def deltanet_scan(q, k, v, gate, beta, state, *, l2norm=True, eps=1e-6, n_thread
     lib().orc_deltanet_scan(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta), _ptr(state),
                             _ptr(out), T, H, d, int(l2norm), eps, n_threads)
     return out, state
+
+
+# ---- Turbo KV codec ----------------------------------------------------------
+
+TQ_ROT_PRE, TQ_ROT_POST, TQ_RES_PRE, TQ_RES_POST = 0, 1, 2, 3
+
+
+def splitmix64(x: int) -> int:
+    return int(lib().orc_splitmix64(x & 0xFFFFFFFFFFFFFFFF))
+
+
+def turbo_sign_table(n_layers, n_kv_heads, head_size) -> np.ndarray:
+    """[4 slots][n_layers][n_kv_heads][ceil(head_size/8)] sign bits (bit set = negate)."""
+    nb = (head_size + 7) // 8
+    t = np.zeros((4, n_layers, n_kv_heads, nb), np.uint8)
+    lib().orc_turbo_sign_table(n_layers, n_kv_heads, head_size, _ptr(t))
+    return t
+
+
+def turbo_transform(v, first_bits, second_bits) -> np.ndarray:
+    v = _f32(v).copy()
+    a = np.ascontiguousarray(first_bits, np.uint8)
+    b = np.ascontiguousarray(second_bits, np.uint8)
+    lib().orc_turbo_transform(_ptr(v), v.size, _ptr(a), _ptr(b))
+    return v
+
+
+def turbo_quantize_head(src, table, layer, kv_head):
+    """quantize_turboquant_head for one head: (base bytes [n/4], sign bytes [n/8], sigma, gamma)."""
+    src = _f32(src)
+    n = src.size
+    _, n_layers, n_kv, _ = table.shape
+    base = np.zeros((n + 3) // 4, np.uint8)
+    sign = np.zeros((n + 7) // 8, np.uint8)
+    sc = np.zeros(1, np.float32)
+    gm = np.zeros(1, np.float32)
+    lib().orc_turbo_quantize_head(_ptr(src), n, _ptr(np.ascontiguousarray(table)), layer, kv_head,
+                                  n_layers, n_kv, _ptr(base), _ptr(sign), 0, _ptr(sc), _ptr(gm))
+    return base, sign, float(sc[0]), float(gm[0])
+
+
+class TurboCache:
+    """Host Turbo KV storage of `rows` rows (RunState's key/value_cache_turbo_base,
+    _sign, key/value_cache_scale and _residual_norm)."""
+
+    def __init__(self, rows, n_kv_heads, head_size):
+        kv_dim = n_kv_heads * head_size
+        self.n_kv_heads, self.head_size = n_kv_heads, head_size
+        self.kbase = np.zeros(rows * kv_dim // 4, np.uint8)
+        self.vbase = np.zeros(rows * kv_dim // 4, np.uint8)
+        self.ksign = np.zeros(rows * kv_dim // 8, np.uint8)
+        self.vsign = np.zeros(rows * kv_dim // 8, np.uint8)
+        self.kscale = np.zeros(rows * n_kv_heads, np.float32)
+        self.vscale = np.zeros(rows * n_kv_heads, np.float32)
+        self.kres = np.zeros(rows * n_kv_heads, np.float32)
+        self.vres = np.zeros(rows * n_kv_heads, np.float32)
+
+
+def kv_write_turbo(cache: TurboCache, row, k, v, table, layer):
+    k = _f32(k)
+    v = _f32(v)
+    n_layers = table.shape[1]
+    lib().orc_kv_write_turbo(_ptr(k), _ptr(v), cache.n_kv_heads, cache.head_size,
+                             _ptr(np.ascontiguousarray(table)), layer, n_layers, row,
+                             _ptr(cache.kbase), _ptr(cache.ksign), _ptr(cache.kscale),
+                             _ptr(cache.kres), _ptr(cache.vbase), _ptr(cache.vsign),
+                             _ptr(cache.vscale), _ptr(cache.vres))
+
+
+def attention_token_turbo(q, cache: TurboCache, table, layer, n_heads, vis_start, vis_end, *,
+                          layer_row_base=0, attn_scale=None, apply_attn_scale=True, online=False,
+                          n_threads=1):
+    q = _f32(q)
+    d = cache.head_size
+    xb = np.zeros(n_heads * d, np.float32)
+    att_stride = max(vis_end - vis_start, 1)
+    att = np.zeros(n_heads * att_stride, np.float32)
+    if attn_scale is None:
+        attn_scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    n_layers = table.shape[1]
+    c = cache
+    lib().orc_attention_token_turbo(_ptr(q), _ptr(xb), _ptr(att), att_stride, n_heads, c.n_kv_heads, d,
+                                    _ptr(c.kbase), _ptr(c.ksign), _ptr(c.kscale), _ptr(c.kres),
+                                    _ptr(c.vbase), _ptr(c.vsign), _ptr(c.vscale), _ptr(c.vres),
+                                    _ptr(np.ascontiguousarray(table)), layer, n_layers,
+                                    layer_row_base, vis_start, vis_end, attn_scale,
+                                    int(apply_attn_scale), int(online), n_threads)
+    return xb
 
 
 def f16_bits(x) -> np.ndarray:
