@@ -114,6 +114,31 @@ def decode_q8_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128, block=False):
     return call, nbytes, (q, kc, vc, ks, vs, st, en, out)
 
 
+def decode_turbo_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
+    """Config-3 shape over a Turbo cache: random code and sign bytes, sigma / gamma
+    ~U[0.5, 1.5] (the decode's cost does not depend on the values)."""
+    import torch
+    from gguf_runner_amd import ops
+    n_seq = len(lens)
+    L = int(max(lens))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    kv_dim = n_kv * d
+    rnd8 = lambda w: torch.randint(0, 256, (n_seq, L, w), generator=g, device=dev, dtype=torch.uint8)
+    aux = lambda: torch.rand((n_seq, L, n_kv), generator=g, device=dev) + 0.5
+    q = torch.randn((n_seq, n_heads, d), generator=g, device=dev)
+    kb, vb, ks_, vs_ = rnd8(kv_dim // 4), rnd8(kv_dim // 4), rnd8(kv_dim // 8), rnd8(kv_dim // 8)
+    sig_k, sig_v, gam_k, gam_v = aux(), aux(), aux(), aux()
+    table = torch.from_numpy(ops.turbo_sign_table(1, n_kv, d)).to(dev)
+    st = torch.zeros(n_seq, dtype=torch.int32, device=dev)
+    en = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    call = ops.TurboDecodeCall(q, kb, vb, ks_, vs_, sig_k, sig_v, gam_k, gam_v, table, 0, st, en, out,
+                               max_kv_len=L)
+    nbytes = int(sum(lens)) * n_kv * 2 * (d // 4 + d // 8 + 8)
+    return call, nbytes, (q, kb, vb, ks_, vs_, sig_k, sig_v, gam_k, gam_v, table, st, en, out)
+
+
 def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
     import torch
     from gguf_runner_amd import ffi, ops
@@ -194,6 +219,11 @@ def run_one(args, dev, stream, lens) -> int:
         call, nbytes, keep = decode_workload(dev, ls, 3)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+    elif args.only == "decode32k_turbo":
+        call, nbytes, keep = decode_turbo_workload(dev, [32768] * 16, 35)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes,
+                   f16_equiv_gbs=16 * 32768 * 4 * 128 * 4 / (ms * 1e-3) / 1e9)
     elif args.only in ("decode32k_q8", "decode32k_q8b"):
         call, nbytes, keep = decode_q8_workload(dev, [32768] * 16, 34,
                                                 block=args.only.endswith("b"))
@@ -229,7 +259,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b",
+                    choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "deltanet", "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()

@@ -34,6 +34,33 @@ void clear_error() { g_last_error.clear(); }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// ---------------------------------------------------------------- Turbo sign table
+
+// splitmix64, inference.rs:674-679.
+static uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// turboquant_build_sign_table, inference.rs:370-395 (salts 352-355).
+void turbo_sign_table_host(int n_layers, int n_kv_heads, int head_size, uint8_t* table) {
+    static const uint64_t salts[4] = {0x9E3779B97F4A7C15ull, 0xC2B2AE3D27D4EB4Full, 0x165667B19E3779F9ull,
+                                      0xD6E8FEB86659FD93ull};
+    const size_t bytes = (size_t)(head_size + 7) / 8;
+    const size_t stride = (size_t)n_layers * n_kv_heads * bytes;
+    memset(table, 0, 4 * stride);
+    for (int slot = 0; slot < 4; slot++)
+        for (int l = 0; l < n_layers; l++)
+            for (int g = 0; g < n_kv_heads; g++) {
+                const uint64_t seed = splitmix64(((uint64_t)l << 32) ^ (uint64_t)g ^ salts[slot]);
+                uint8_t* bits = table + slot * stride + ((size_t)l * n_kv_heads + g) * bytes;
+                for (int i = 0; i < head_size; i++)
+                    if (splitmix64(seed ^ (uint64_t)i) & 1) bits[i / 8] |= (uint8_t)(1u << (i & 7));
+            }
+}
+
 // ---------------------------------------------------------------- decode
 namespace {
 
@@ -42,6 +69,7 @@ struct DecodePlan {
     int n_splits;
     size_t ws_o_bytes;
     size_t ws_ml_bytes;
+    size_t ws_q_bytes;  // Turbo: rotated / projected queries
 };
 
 // Split size: aim for ~2048 (sequence, KV head, split) work units so the 256
@@ -61,8 +89,12 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     pl.split_keys = split;
     pl.n_splits = (max_len + split - 1) / split;
     const size_t parts = (size_t)a->n_seq * a->n_heads * pl.n_splits;
-    pl.ws_o_bytes = align_up(parts * a->head_dim * sizeof(float), 256);
+    const size_t per_part = a->kv_dtype == GR_DTYPE_TURBO ? 2 : 1;  // Turbo: base + residual
+    pl.ws_o_bytes = align_up(parts * per_part * a->head_dim * sizeof(float), 256);
     pl.ws_ml_bytes = align_up(parts * 2 * sizeof(float), 256);
+    pl.ws_q_bytes = a->kv_dtype == GR_DTYPE_TURBO
+                        ? align_up((size_t)a->n_seq * a->n_heads * 2 * a->head_dim * sizeof(float), 256)
+                        : 0;
     return pl;
 }
 
@@ -82,8 +114,21 @@ int check_decode(const gr_decode_args* a) {
     if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
         return fail(GR_ERR_ARG, "gr_decode_attention: head_dim %d unsupported (64,128,256)",
                     a->head_dim);
-    if (a->kv_dtype < GR_DTYPE_F32 || a->kv_dtype > GR_DTYPE_Q8)
+    if (a->kv_dtype < GR_DTYPE_F32 || a->kv_dtype > GR_DTYPE_TURBO)
         return fail(GR_ERR_ARG, "gr_decode_attention: bad kv_dtype %d", a->kv_dtype);
+    if (a->kv_dtype == GR_DTYPE_TURBO) {
+        if (a->head_dim != 128) return fail(GR_ERR_ARG, "gr_decode_attention: Turbo KV needs head_dim 128");
+        if (!a->k_sign || !a->v_sign || !a->k_scale || !a->v_scale || !a->k_rnorm || !a->v_rnorm ||
+            !a->turbo_signs)
+            return fail(GR_ERR_ARG, "gr_decode_attention: Turbo KV needs sign, scale, rnorm and sign-table arrays");
+        if (a->row_stride % 128 != 0 || a->seq_stride % 128 != 0 ||
+            ((uintptr_t)a->k_cache | (uintptr_t)a->v_cache | (uintptr_t)a->k_sign | (uintptr_t)a->v_sign) % 16 != 0)
+            return fail(GR_ERR_ARG,
+                        "gr_decode_attention: Turbo arrays must be 16-byte aligned with element strides "
+                        "that are multiples of 128");
+        if (a->scale_row_stride < a->n_kv_heads || a->scale_seq_stride < 0 || a->turbo_slot_stride <= 0)
+            return fail(GR_ERR_ARG, "gr_decode_attention: bad Turbo aux or sign-table strides");
+    }
     if (a->kv_dtype == GR_DTYPE_Q8) {
         if (a->head_dim != 128 && a->head_dim != 256)
             return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs head_dim 128 or 256");
@@ -106,9 +151,10 @@ int check_decode(const gr_decode_args* a) {
     if (a->row_stride < (int64_t)a->n_kv_heads * a->head_dim)
         return fail(GR_ERR_ARG, "gr_decode_attention: row_stride %lld < n_kv_heads*head_dim",
                     (long long)a->row_stride);
-    const int eb = a->kv_dtype == GR_DTYPE_F32 ? 4 : (a->kv_dtype == GR_DTYPE_Q8 ? 1 : 2);
-    if (((uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 != 0 ||
-        (a->row_stride * eb) % 16 != 0 || (a->seq_stride * eb) % 16 != 0)
+    const int eb = a->kv_dtype == GR_DTYPE_F32 ? 4 : (a->kv_dtype == GR_DTYPE_Q8 || a->kv_dtype == GR_DTYPE_TURBO ? 1 : 2);
+    if (a->kv_dtype != GR_DTYPE_TURBO &&
+        (((uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 != 0 || (a->row_stride * eb) % 16 != 0 ||
+         (a->seq_stride * eb) % 16 != 0))
         return fail(GR_ERR_ARG, "gr_decode_attention: caches and strides must be 16-byte aligned");
     if ((uintptr_t)a->workspace % 256 != 0)
         return fail(GR_ERR_ARG, "gr_decode_attention: workspace must be 256-byte aligned");
@@ -152,6 +198,19 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
         p.scale_row_stride = a->scale_row_stride;
         p.q8_block = a->q8_block ? 1 : 0;
     }
+    if (a->kv_dtype == GR_DTYPE_TURBO) {
+        p.k_scale = a->k_scale;
+        p.v_scale = a->v_scale;
+        p.scale_seq_stride = a->scale_seq_stride;
+        p.scale_row_stride = a->scale_row_stride;
+        p.k_sign = a->k_sign;
+        p.v_sign = a->v_sign;
+        p.k_rnorm = a->k_rnorm;
+        p.v_rnorm = a->v_rnorm;
+        p.turbo_signs = a->turbo_signs;
+        p.turbo_slot_stride = a->turbo_slot_stride;
+        p.ws_q = (float*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes);
+    }
     hipError_t e = launch_decode(p, st);
     if (e != hipSuccess) return hip_fail(e, "gr_decode_attention launch");
     return GR_OK;
@@ -160,7 +219,7 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
 size_t decode_ws_bytes(const gr_decode_args* a) {
     if (check_decode_shape_only(a)) return 0;
     const DecodePlan pl = plan_decode(a);
-    return pl.ws_o_bytes + pl.ws_ml_bytes;
+    return pl.ws_o_bytes + pl.ws_ml_bytes + pl.ws_q_bytes;
 }
 
 int check_decode_shape_only(const gr_decode_args* a) {
@@ -182,6 +241,14 @@ size_t gr_decode_workspace_size(const gr_decode_args* a) { return gr::decode_ws_
 int gr_decode_attention(const gr_decode_args* a, void* stream) {
     gr::clear_error();
     return gr::decode_enqueue(a, (hipStream_t)stream);
+}
+
+int gr_turbo_sign_table(int32_t n_layers, int32_t n_kv_heads, int32_t head_size, uint8_t* out) {
+    gr::clear_error();
+    if (n_layers <= 0 || n_kv_heads <= 0 || head_size <= 0 || !out)
+        return gr::fail(GR_ERR_ARG, "gr_turbo_sign_table: bad arguments");
+    gr::turbo_sign_table_host(n_layers, n_kv_heads, head_size, out);
+    return GR_OK;
 }
 
 }  // extern "C"

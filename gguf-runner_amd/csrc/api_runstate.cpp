@@ -31,6 +31,15 @@ struct gr_run_state {
     float* k_scale = nullptr;
     float* v_scale = nullptr;
     size_t sc_per_row = 0, sc_seq_stride = 0, sc_layer_stride = 0;
+    // Turbo cache: k_cache / v_cache hold the 2-bit codes (element e at byte e/4),
+    // k_sign / v_sign the residual sign bits (byte e/8), k_scale / v_scale sigma
+    // and k_rnorm / v_rnorm gamma with sc_per_row = n_kv_heads; the sign table
+    // (turboquant_build_sign_table) lives on the device.
+    uint8_t* k_sign = nullptr;
+    uint8_t* v_sign = nullptr;
+    float* k_rnorm = nullptr;
+    float* v_rnorm = nullptr;
+    uint8_t* turbo_table = nullptr;
     float* freqs = nullptr;
     float* freqs_swa = nullptr;
     float* qn = nullptr;
@@ -46,6 +55,13 @@ namespace gr {
 namespace {
 
 int elem_bytes(int dt) { return dt == GR_DTYPE_F32 ? 4 : (dt == GR_DTYPE_Q8 ? 1 : 2); }
+
+bool is_turbo(const gr_run_state* s) { return s->cfg.kv_dtype == GR_DTYPE_TURBO; }
+
+// Byte offset of cache element `e` in the K/V storage (Turbo codes: 4 per byte).
+size_t cache_bytes_at(const gr_run_state* s, size_t e) {
+    return is_turbo(s) ? e / 4 : e * elem_bytes(s->cfg.kv_dtype);
+}
 
 // RAII: make the state's device current for the duration of a call.
 struct DeviceScope {
@@ -133,13 +149,15 @@ int check_pos(const gr_run_state* s, int seq, int64_t pos, int64_t count) {
     return GR_OK;
 }
 
-void* layer_k(gr_run_state* s, int l) { return (char*)s->k_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
-void* layer_v(gr_run_state* s, int l) { return (char*)s->v_cache + (size_t)l * s->layer_stride * elem_bytes(s->cfg.kv_dtype); }
+void* layer_k(gr_run_state* s, int l) { return (char*)s->k_cache + cache_bytes_at(s, (size_t)l * s->layer_stride); }
+void* layer_v(gr_run_state* s, int l) { return (char*)s->v_cache + cache_bytes_at(s, (size_t)l * s->layer_stride); }
 
 bool is_q8(const gr_run_state* s) { return s->cfg.kv_dtype == GR_DTYPE_Q8; }
 
-// Extra staging bytes a K/V write of n rows needs (Q8: f32 rows before quantising).
-size_t q8_stage_bytes(const gr_run_state* s, size_t n) { return is_q8(s) ? 8 * n * s->kv_dim + 512 : 0; }
+// Extra staging bytes a K/V write of n rows needs (Q8 / Turbo: f32 rows before quantising).
+size_t q8_stage_bytes(const gr_run_state* s, size_t n) {
+    return is_q8(s) || is_turbo(s) ? 8 * n * s->kv_dim + 512 : 0;
+}
 
 // Run the prep kernel and store its K/V rows into layer `l`'s cache.  Raw
 // storage: the prep kernel writes the cache itself (p.k_cache / p.v_cache set by
@@ -148,19 +166,55 @@ size_t q8_stage_bytes(const gr_run_state* s, size_t n) { return is_q8(s) ? 8 * n
 // kernel quantises them into the cache rows (kv_write_token, inference.rs:1886-1917).
 int prep_and_store(gr_run_state* s, int l, int seq, QkvPrepLaunch p, Carve& cv) {
     hipError_t e;
-    if (!is_q8(s)) {
+    if (!is_q8(s) && !is_turbo(s)) {
         e = launch_qkv_prep(p, s->stream);
         return e == hipSuccess ? GR_OK : hip_fail(e, "prep launch");
     }
     float* kst = cv.take<float>((size_t)p.n_tokens * s->kv_dim);
     float* vst = cv.take<float>((size_t)p.n_tokens * s->kv_dim);
+    const size_t so = p.cache_seq ? 0 : (size_t)seq;
+    if (is_turbo(s)) {
+        TurboWriteLaunch w{};
+        w.n_rows = p.n_tokens;
+        w.n_kv_heads = s->cfg.n_kv_heads;
+        w.head_dim = s->d;
+        w.k_rows = kst;
+        w.v_rows = vst;
+        const size_t e0 = (size_t)l * s->layer_stride + so * s->seq_stride;
+        w.k_base = (uint8_t*)s->k_cache + e0 / 4;
+        w.v_base = (uint8_t*)s->v_cache + e0 / 4;
+        w.k_sign = s->k_sign + e0 / 8;
+        w.v_sign = s->v_sign + e0 / 8;
+        const size_t a0 = (size_t)l * s->sc_layer_stride + so * s->sc_seq_stride;
+        w.k_scale = s->k_scale + a0;
+        w.v_scale = s->v_scale + a0;
+        w.k_rnorm = s->k_rnorm + a0;
+        w.v_rnorm = s->v_rnorm + a0;
+        w.signs = s->turbo_table + (size_t)l * s->cfg.n_kv_heads * (s->d / 8);
+        w.slot_stride = (int64_t)s->cfg.n_layers * s->cfg.n_kv_heads * (s->d / 8);
+        w.cache_seq_stride = (int64_t)s->seq_stride;
+        w.cache_row_stride = s->kv_dim;
+        w.aux_seq_stride = (int64_t)s->sc_seq_stride;
+        w.aux_row_stride = (int64_t)s->sc_per_row;
+        w.cache_row = p.cache_row ? p.cache_row : p.pos;
+        w.cache_seq = p.cache_seq;
+        w.row0 = p.pos0;
+        p.k_cache = kst;
+        p.v_cache = vst;
+        p.cache_dtype = GR_DTYPE_F32;
+        p.cache_row_stride = s->kv_dim;
+        p.cache_by_index = 1;
+        e = launch_qkv_prep(p, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "prep launch");
+        e = launch_turbo_write(w, s->stream);
+        return e == hipSuccess ? GR_OK : hip_fail(e, "turbo kv write launch");
+    }
     Q8WriteLaunch w{};
     w.n_rows = p.n_tokens;
     w.kv_dim = s->kv_dim;
     w.block = s->cfg.q8_block_scales ? 1 : 0;
     w.k_rows = kst;
     w.v_rows = vst;
-    const size_t so = p.cache_seq ? 0 : (size_t)seq;
     w.k_cache = (int8_t*)layer_k(s, l) + so * s->seq_stride;
     w.v_cache = (int8_t*)layer_v(s, l) + so * s->seq_stride;
     w.k_scale = s->k_scale + (size_t)l * s->sc_layer_stride + so * s->sc_seq_stride;
@@ -229,7 +283,9 @@ int validate_config(const gr_attn_config* c) {
         return fail(GR_ERR_ARG, "n_heads %d is not a multiple of n_kv_heads %d", c->n_heads, c->n_kv_heads);
     if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "head_dim %d unsupported (64, 128, 256)", c->head_dim);
-    if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_Q8) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
+    if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_TURBO) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
+    if (c->kv_dtype == GR_DTYPE_TURBO && c->head_dim != 128)
+        return fail(GR_ERR_ARG, "Turbo KV cache needs head_dim 128");
     if (c->kv_dtype == GR_DTYPE_Q8 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "Q8 KV cache needs head_dim 128 or 256");
     if (c->rope_mode < GR_ROPE_NONE || c->rope_mode > GR_ROPE_NEOX) return fail(GR_ERR_ARG, "bad rope_mode %d", c->rope_mode);
@@ -290,11 +346,33 @@ int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out) {
     if (e != hipSuccess) return cleanup_fail(hip_fail(e, "stream create"));
     s->seq_stride = (size_t)cfg->seq_len * s->kv_dim;
     s->layer_stride = s->seq_stride * cfg->n_seq;
-    const size_t cache_bytes = s->layer_stride * cfg->n_layers * elem_bytes(cfg->kv_dtype);
+    const size_t cache_bytes = cache_bytes_at(s, s->layer_stride * cfg->n_layers);
     if (hipMalloc(&s->k_cache, cache_bytes) != hipSuccess || hipMalloc(&s->v_cache, cache_bytes) != hipSuccess)
         return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate KV cache (%zu bytes each); reduce --context-size", cache_bytes));
     (void)hipMemsetAsync(s->k_cache, 0, cache_bytes, s->stream);
     (void)hipMemsetAsync(s->v_cache, 0, cache_bytes, s->stream);
+    if (cfg->kv_dtype == GR_DTYPE_TURBO) {
+        const size_t total = s->layer_stride * cfg->n_layers;
+        if (hipMalloc(&s->k_sign, total / 8) != hipSuccess || hipMalloc(&s->v_sign, total / 8) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate Turbo sign caches (%zu bytes each)", total / 8));
+        (void)hipMemsetAsync(s->k_sign, 0, total / 8, s->stream);
+        (void)hipMemsetAsync(s->v_sign, 0, total / 8, s->stream);
+        s->sc_per_row = (size_t)cfg->n_kv_heads;
+        s->sc_seq_stride = (size_t)cfg->seq_len * s->sc_per_row;
+        s->sc_layer_stride = s->sc_seq_stride * cfg->n_seq;
+        const size_t sb = s->sc_layer_stride * cfg->n_layers * 4;
+        if (hipMalloc(&s->k_scale, sb) != hipSuccess || hipMalloc(&s->v_scale, sb) != hipSuccess ||
+            hipMalloc(&s->k_rnorm, sb) != hipSuccess || hipMalloc(&s->v_rnorm, sb) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate Turbo scale / norm buffers (%zu bytes each)", sb));
+        for (float* b : {s->k_scale, s->v_scale, s->k_rnorm, s->v_rnorm}) (void)hipMemsetAsync(b, 0, sb, s->stream);
+        const size_t tb = 4 * (size_t)cfg->n_layers * cfg->n_kv_heads * (s->d / 8);
+        std::vector<uint8_t> table(tb);
+        turbo_sign_table_host(cfg->n_layers, cfg->n_kv_heads, s->d, table.data());
+        if (hipMalloc(&s->turbo_table, tb) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate the Turbo sign table"));
+        e = hipMemcpy(s->turbo_table, table.data(), tb, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return cleanup_fail(hip_fail(e, "Turbo sign table upload"));
+    }
     if (cfg->kv_dtype == GR_DTYPE_Q8) {
         s->sc_per_row = cfg->q8_block_scales ? (size_t)s->kv_dim / 32 : 1;
         s->sc_seq_stride = (size_t)cfg->seq_len * s->sc_per_row;
@@ -343,7 +421,8 @@ void gr_free_run_state(gr_run_state* s) {
     if (!s) return;
     DeviceScope ds(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
-    for (void* p : {s->k_cache, s->v_cache, (void*)s->k_scale, (void*)s->v_scale, (void*)s->freqs,
+    for (void* p : {s->k_cache, s->v_cache, (void*)s->k_scale, (void*)s->v_scale, (void*)s->k_sign,
+                    (void*)s->v_sign, (void*)s->k_rnorm, (void*)s->v_rnorm, (void*)s->turbo_table, (void*)s->freqs,
                     (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn, (void*)s->ssm, s->stage})
         if (p) (void)hipFree(p);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -409,8 +488,8 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
     p.k = kin;
     p.v = vin;
     p.q_out = nullptr;
-    p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
-    p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    p.k_cache = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
+    p.v_cache = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
     hipError_t e = hipStreamSynchronize(s->stream);
     return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
@@ -442,14 +521,28 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
     a.max_kv_len = max_len;
     a.score_scale = score_scale(s);
     a.q = qdev;
-    const size_t eb = elem_bytes(s->cfg.kv_dtype);
-    a.k_cache = (char*)layer_k(s, layer) + (slots_dev ? 0 : (size_t)seq * s->seq_stride * eb);
-    a.v_cache = (char*)layer_v(s, layer) + (slots_dev ? 0 : (size_t)seq * s->seq_stride * eb);
+    const size_t seq_el = slots_dev ? 0 : (size_t)seq * s->seq_stride;
+    a.k_cache = (char*)layer_k(s, layer) + cache_bytes_at(s, seq_el);
+    a.v_cache = (char*)layer_v(s, layer) + cache_bytes_at(s, seq_el);
     a.seq_stride = slots_dev ? (int64_t)s->seq_stride : 0;
     a.row_stride = s->kv_dim;
     a.kv_start = se;
     a.kv_end = se + n;
     a.out = xb_dev;
+    if (is_turbo(s)) {
+        const size_t so = (size_t)layer * s->sc_layer_stride + (slots_dev ? 0 : (size_t)seq * s->sc_seq_stride);
+        const size_t e0 = (size_t)layer * s->layer_stride + seq_el;
+        a.k_sign = s->k_sign + e0 / 8;
+        a.v_sign = s->v_sign + e0 / 8;
+        a.k_scale = s->k_scale + so;
+        a.v_scale = s->v_scale + so;
+        a.k_rnorm = s->k_rnorm + so;
+        a.v_rnorm = s->v_rnorm + so;
+        a.scale_seq_stride = slots_dev ? (int64_t)s->sc_seq_stride : 0;
+        a.scale_row_stride = (int64_t)s->sc_per_row;
+        a.turbo_signs = s->turbo_table + (size_t)layer * s->cfg.n_kv_heads * (s->d / 8);
+        a.turbo_slot_stride = (int64_t)s->cfg.n_layers * s->cfg.n_kv_heads * (s->d / 8);
+    }
     if (is_q8(s)) {
         const size_t so = slots_dev ? 0 : (size_t)seq * s->sc_seq_stride;
         a.k_scale = s->k_scale + (size_t)layer * s->sc_layer_stride + so;
@@ -476,6 +569,7 @@ int gr_attention_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos,
     probe.n_heads = s->cfg.n_heads;
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
+    probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = en - st;
     if ((rc = ensure_stage(s, 8 * (size_t)s->q_dim + decode_ws_bytes(&probe) + 4096))) return rc;
     Carve cv(s->stage);
@@ -500,6 +594,7 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     probe.n_heads = s->cfg.n_heads;
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
+    probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = en - st;
     if ((rc = ensure_stage(s, 4 * (3 * (size_t)s->q_dim + 2 * (size_t)s->kv_dim) + decode_ws_bytes(&probe) +
                                   q8_stage_bytes(s, 1) + 8192)))
@@ -519,8 +614,8 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     p.k = kin;
     p.v = vin;
     p.q_out = qp;
-    p.k_cache = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
-    p.v_cache = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * elem_bytes(s->cfg.kv_dtype);
+    p.k_cache = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
+    p.v_cache = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
     if ((rc = run_decode(s, layer, 1, qp, nullptr, seq, {st}, {en}, xo, cv))) return rc;
     return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
@@ -549,6 +644,7 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
     probe.n_heads = s->cfg.n_heads;
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
+    probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = max_len;
     const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m);
     if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
@@ -627,6 +723,7 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     probe.n_heads = s->cfg.n_heads;
     probe.n_kv_heads = s->cfg.n_kv_heads;
     probe.head_dim = s->d;
+    probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = max_len;
     const size_t qb = 4 * (size_t)n * s->q_dim, kb = 4 * (size_t)n * s->kv_dim;
     if ((rc = ensure_stage(s, 3 * qb + 2 * kb + decode_ws_bytes(&probe) + 16 * (size_t)n + q8_stage_bytes(s, n) +
@@ -754,11 +851,30 @@ int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, i
     int rc = check_layer(s, layer);
     if (rc || (rc = check_pos(s, seq, row0, n_rows))) return rc;
     DeviceScope dsc(s->device);
-    const size_t eb = elem_bytes(s->cfg.kv_dtype);
-    const size_t off = ((size_t)seq * s->seq_stride + (size_t)row0 * s->kv_dim) * eb;
-    const size_t nb = (size_t)n_rows * s->kv_dim * eb;
+    const size_t off = cache_bytes_at(s, (size_t)seq * s->seq_stride + (size_t)row0 * s->kv_dim);
+    const size_t nb = cache_bytes_at(s, (size_t)n_rows * s->kv_dim);
     if (k_out && (rc = d2h_sync(s, k_out, (char*)layer_k(s, layer) + off, nb))) return rc;
     if (v_out && (rc = d2h_sync(s, v_out, (char*)layer_v(s, layer) + off, nb))) return rc;
+    return GR_OK;
+}
+
+int gr_read_turbo_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows, uint8_t* k_base,
+                       uint8_t* k_sign, float* k_rnorm, uint8_t* v_base, uint8_t* v_sign, float* v_rnorm) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, row0, n_rows))) return rc;
+    if (!is_turbo(s)) return fail(GR_ERR_ARG, "run state has no Turbo KV cache (kv_dtype %d)", s->cfg.kv_dtype);
+    DeviceScope dsc(s->device);
+    const size_t e0 = (size_t)layer * s->layer_stride + (size_t)seq * s->seq_stride + (size_t)row0 * s->kv_dim;
+    const size_t ne = (size_t)n_rows * s->kv_dim;
+    const size_t a0 = (size_t)layer * s->sc_layer_stride + (size_t)seq * s->sc_seq_stride + (size_t)row0 * s->sc_per_row;
+    const size_t na = (size_t)n_rows * s->sc_per_row * 4;
+    if (k_base && (rc = d2h_sync(s, k_base, (uint8_t*)s->k_cache + e0 / 4, ne / 4))) return rc;
+    if (v_base && (rc = d2h_sync(s, v_base, (uint8_t*)s->v_cache + e0 / 4, ne / 4))) return rc;
+    if (k_sign && (rc = d2h_sync(s, k_sign, s->k_sign + e0 / 8, ne / 8))) return rc;
+    if (v_sign && (rc = d2h_sync(s, v_sign, s->v_sign + e0 / 8, ne / 8))) return rc;
+    if (k_rnorm && (rc = d2h_sync(s, k_rnorm, s->k_rnorm + a0, na))) return rc;
+    if (v_rnorm && (rc = d2h_sync(s, v_rnorm, s->v_rnorm + a0, na))) return rc;
     return GR_OK;
 }
 
@@ -767,7 +883,8 @@ int gr_read_kv_scales(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0,
     clear_error();
     int rc = check_layer(s, layer);
     if (rc || (rc = check_pos(s, seq, row0, n_rows))) return rc;
-    if (!is_q8(s)) return fail(GR_ERR_ARG, "run state has no Q8 KV cache (kv_dtype %d)", s->cfg.kv_dtype);
+    if (!is_q8(s) && !is_turbo(s))
+        return fail(GR_ERR_ARG, "run state has no Q8 or Turbo KV cache (kv_dtype %d)", s->cfg.kv_dtype);
     DeviceScope dsc(s->device);
     const size_t off = (size_t)layer * s->sc_layer_stride + (size_t)seq * s->sc_seq_stride + (size_t)row0 * s->sc_per_row;
     const size_t nb = (size_t)n_rows * s->sc_per_row * 4;

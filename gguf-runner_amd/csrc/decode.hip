@@ -298,6 +298,7 @@ static hipError_t launch_combine(const DecodeLaunch& p, hipStream_t st) {
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
+    if (p.kv_dtype == GR_DTYPE_TURBO) return decode_turbo_supported(p) ? launch_decode_turbo(p, st) : hipErrorInvalidValue;
     if (p.use_mfma && decode_mfma_supported(p)) {
         hipError_t e = launch_decode_mfma_split(p, st);
         if (e != hipSuccess) return e;

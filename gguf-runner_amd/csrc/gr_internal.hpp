@@ -29,6 +29,19 @@ struct DecodeLaunch {
     const float* v_scale;
     int64_t scale_seq_stride, scale_row_stride;
     int q8_block;
+    // Turbo cache: k_cache / v_cache hold the 2-bit codes (element e at byte e/4),
+    // k_sign / v_sign the residual sign bits (byte e/8); k_scale / v_scale sigma and
+    // k_rnorm / v_rnorm gamma of (slot, row t, kv head g) at
+    // slot*scale_seq_stride + t*scale_row_stride + g; turbo_signs the layer's sign
+    // table rows (slot i at turbo_signs + i*turbo_slot_stride, kv head g at + g*d/8);
+    // ws_q the rotated / projected queries [n_seq][n_heads][2][d].
+    const void* k_sign;
+    const void* v_sign;
+    const float* k_rnorm;
+    const float* v_rnorm;
+    const uint8_t* turbo_signs;
+    int64_t turbo_slot_stride;
+    float* ws_q;
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);
@@ -92,6 +105,37 @@ struct Q8WriteLaunch {
 };
 
 hipError_t launch_q8_write(const Q8WriteLaunch& p, hipStream_t st);
+
+// Turbo KV write (kv_write_token's Turbo branch, inference.rs:1918-1963): n_rows
+// f32 rows of n_kv_heads*head_dim elements quantised per kv head into 2-bit
+// codes + residual sign bits + (sigma, gamma).  Destination row i: slot
+// (cache_seq ? cache_seq[i] : 0), position (cache_row ? cache_row[i] : row0 + i);
+// element strides for the code / sign arrays, float strides for the aux arrays
+// (aux index slot*aux_seq_stride + row*aux_row_stride + kv head).
+struct TurboWriteLaunch {
+    int n_rows, n_kv_heads, head_dim;
+    const float* k_rows;
+    const float* v_rows;
+    uint8_t* k_base;
+    uint8_t* v_base;
+    uint8_t* k_sign;
+    uint8_t* v_sign;
+    float* k_scale;
+    float* v_scale;
+    float* k_rnorm;
+    float* v_rnorm;
+    const uint8_t* signs;   // the layer's sign table rows (see DecodeLaunch::turbo_signs)
+    int64_t slot_stride;
+    int64_t cache_seq_stride, cache_row_stride;
+    int64_t aux_seq_stride, aux_row_stride;
+    const int32_t* cache_row;
+    const int32_t* cache_seq;
+    int64_t row0;
+};
+
+hipError_t launch_turbo_write(const TurboWriteLaunch& p, hipStream_t st);
+bool decode_turbo_supported(const DecodeLaunch& p);
+hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st);
 
 // Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
 // [m][n_heads][d] already multiplied by score_scale*log2(e); for bf16, q_lo

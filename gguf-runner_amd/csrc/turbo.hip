@@ -1,0 +1,661 @@
+// Turbo KV cache (KvCacheFormat::Turbo, reference inference.rs:346-1334) on the
+// device: the quantising KV write, the query rotation, the split-K decode over
+// the packed codes and the merge + value finalisation.
+//
+// Per KV head of a row the reference stores (x86 scalar paths):
+//   rotated  = S_post H S_pre x              (sign flips, FWHT / sqrt(n); 596-605)
+//   sigma    = |rotated| / sqrt(n);  code = 2-bit Lloyd-Max code of rotated/sigma
+//   residual = rotated - C[code] sigma;  gamma = |residual|
+//   sign bit = (S'_post H S'_pre residual/gamma >= 0)
+// and attention reads
+//   score = sigma (q_rot . C[code]) + gamma sqrt(pi/2/n) (q_proj . sgn)
+//   out   = R^-1 ( sum_t p_t sigma_t C[code_t] + R'^-1 sum_t p_t r_t sgn_t ) / l.
+//
+// Device layout per wave: a head of D (64, 128, 256) elements lives as
+// x[j] = element lane + 64 j.  The FWHT runs its widths in the reference's
+// order (1, 2, 4, ...: lanes via shuffles, then within the lane) and the norms
+// are sequential sums in element order, so the written codes, signs, sigma and
+// gamma are bit-exact with the reference for the same f32 row (no FMA
+// contraction in this file).
+//
+// The decode keeps every product exact in f16: C[code] = c0 s + (c1 - c0) s_big
+// with s, s_big, sgn in {-1, 0, +1}, so K and V enter the MFMAs as exact +-1/0
+// operands and the f32 factors (c0, c1 - c0, sigma, gamma) ride on the other
+// operand, carried as f16 hi + lo pairs (with power-of-two range scaling as in
+// the Q8 decode).
+#pragma clang fp contract(off)
+
+#include "gr_common.hpp"
+#include "gr_internal.hpp"
+
+namespace gr {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kTqC0 = 0.45278f;    // TURBOQUANT_CENTROIDS, inference.rs:349
+constexpr float kTqC1 = 1.510417f;
+constexpr float kTqTh = 0.9815985f;  // TURBOQUANT_THRESHOLD_HI, inference.rs:351
+constexpr float kFracPi2 = 1.5707964f;
+
+__device__ __forceinline__ float tq_centroid(int code) {
+    return code == 0 ? -kTqC1 : code == 1 ? -kTqC0 : code == 2 ? kTqC0 : kTqC1;
+}
+
+__device__ __forceinline__ int tq_code(float x) {
+    return x < -kTqTh ? 0 : (x < 0.0f ? 1 : (x < kTqTh ? 2 : 3));
+}
+
+// sign flips of a wave-held head: bit i of `bits` set -> negate element i
+template <int D>
+__device__ __forceinline__ void wave_signs(float (&x)[D / 64], const uint8_t* bits, int lane) {
+#pragma unroll
+    for (int j = 0; j < D / 64; j++) {
+        const int i = lane + 64 * j;
+        if ((bits[i >> 3] >> (i & 7)) & 1) x[j] = -x[j];
+    }
+}
+
+// turboquant_fwht_inplace_scalar (inference.rs:681-701) on a wave-held head
+template <int D>
+__device__ __forceinline__ void wave_fwht(float (&x)[D / 64], int lane) {
+#pragma unroll
+    for (int w = 1; w < 64; w <<= 1)
+#pragma unroll
+        for (int j = 0; j < D / 64; j++) {
+            const float p = __shfl_xor(x[j], w, 64);
+            x[j] = (lane & w) ? p - x[j] : x[j] + p;  // lower a+b, upper a-b
+        }
+#pragma unroll
+    for (int w = 1; w < D / 64; w <<= 1)
+#pragma unroll
+        for (int j = 0; j < D / 64; j++)
+            if (!(j & w)) {
+                const float a = x[j], b = x[j | w];
+                x[j] = a + b;
+                x[j | w] = a - b;
+            }
+    const float sc = 1.0f / sqrtf((float)D);
+#pragma unroll
+    for (int j = 0; j < D / 64; j++) x[j] *= sc;
+}
+
+template <int D>
+__device__ __forceinline__ void wave_transform(float (&x)[D / 64], const uint8_t* first, const uint8_t* second,
+                                               int lane) {
+    wave_signs<D>(x, first, lane);
+    wave_fwht<D>(x, lane);
+    wave_signs<D>(x, second, lane);
+}
+
+// l2_norm (math.rs:467-473): sequential sum in element order, every lane the same
+template <int D>
+__device__ __forceinline__ float wave_l2_sequential(const float (&x)[D / 64], float* buf, int lane) {
+#pragma unroll
+    for (int j = 0; j < D / 64; j++) buf[lane + 64 * j] = x[j];
+    __syncthreads();  // one-wave workgroup
+    float ss = 0.0f;
+    for (int e = 0; e < D; e++) {
+        const float v = buf[e];
+        ss = ss + v * v;
+    }
+    __syncthreads();  // buf is reused by the caller
+    return sqrtf(ss);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- KV write
+
+// quantize_turboquant_head (inference.rs:855-925) for one (row, kv head, K|V):
+// grid (n_rows, n_kv_heads, 2), one wave.
+template <int D>
+__global__ __launch_bounds__(64) void turbo_write_kernel(const TurboWriteLaunch p) {
+    constexpr int J = D / 64;
+    __shared__ float buf[D];
+    __shared__ uint8_t codes[D];
+    const int lane = threadIdx.x;
+    const int i = blockIdx.x, g = blockIdx.y;
+    const bool is_v = blockIdx.z != 0;
+    const int kv_dim = p.n_kv_heads * D;
+    const float* src = (is_v ? p.v_rows : p.k_rows) + (size_t)i * kv_dim + (size_t)g * D;
+    const int64_t row = p.cache_row ? (int64_t)p.cache_row[i] : p.row0 + i;
+    const int64_t sq = p.cache_seq ? (int64_t)p.cache_seq[i] : 0;
+    const int64_t elem = sq * p.cache_seq_stride + row * p.cache_row_stride + (int64_t)g * D;
+    uint8_t* base = (is_v ? p.v_base : p.k_base) + elem / 4;
+    uint8_t* sign = (is_v ? p.v_sign : p.k_sign) + elem / 8;
+    const int64_t aux = sq * p.aux_seq_stride + row * p.aux_row_stride + g;
+    float* scale_out = (is_v ? p.v_scale : p.k_scale) + aux;
+    float* rnorm_out = (is_v ? p.v_rnorm : p.k_rnorm) + aux;
+    const uint8_t* sg = p.signs + (size_t)g * (D / 8);
+    const int64_t ss = p.slot_stride;
+
+    float x[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) x[j] = src[lane + 64 * j];
+    wave_transform<D>(x, sg, sg + ss, lane);  // rot_pre, rot_post
+    const float sigma = wave_l2_sequential<D>(x, buf, lane) / sqrtf((float)D);
+    if (sigma == 0.0f) {
+        if (lane == 0) {
+            *scale_out = 0.0f;
+            *rnorm_out = 0.0f;
+        }
+        if (lane < D / 4) base[lane] = 0;
+        if (lane < D / 8) sign[lane] = 0xff;
+        return;
+    }
+    const float inv_sigma = 1.0f / sigma;
+    float r[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int c = tq_code(x[j] * inv_sigma);
+        r[j] = x[j] - tq_centroid(c) * sigma;
+        codes[lane + 64 * j] = (uint8_t)c;
+    }
+    const float gamma = wave_l2_sequential<D>(r, buf, lane);  // its barrier also publishes `codes`
+    if (lane < D / 4)
+        base[lane] = (uint8_t)(codes[4 * lane] | (codes[4 * lane + 1] << 2) | (codes[4 * lane + 2] << 4) |
+                               (codes[4 * lane + 3] << 6));
+    if (lane == 0) {
+        *scale_out = sigma;
+        *rnorm_out = gamma;
+    }
+    if (gamma == 0.0f) {
+        if (lane < D / 8) sign[lane] = 0xff;
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) r[j] = r[j] / gamma;
+    wave_transform<D>(r, sg + 2 * ss, sg + 3 * ss, lane);  // res_pre, res_post
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const uint64_t m = __ballot(r[j] >= 0.0f);  // bit l = element 64 j + l
+        if (lane == 0) *(uint64_t*)(sign + 8 * j) = m;
+    }
+}
+
+hipError_t launch_turbo_write(const TurboWriteLaunch& p, hipStream_t st) {
+    if (p.n_rows <= 0) return hipSuccess;
+    dim3 grid((unsigned)p.n_rows, (unsigned)p.n_kv_heads, 2);
+    switch (p.head_dim) {
+        case 64: turbo_write_kernel<64><<<grid, 64, 0, st>>>(p); break;
+        case 128: turbo_write_kernel<128><<<grid, 64, 0, st>>>(p); break;
+        case 256: turbo_write_kernel<256><<<grid, 64, 0, st>>>(p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- query rotation
+
+// turboquant_prepare_query (inference.rs:954-968): q_rot = R q, q_proj = R' q_rot,
+// written as ws_q[s][h][2][D].  grid (n_heads, n_seq), one wave.
+template <int D>
+__global__ __launch_bounds__(64) void turbo_query_kernel(const DecodeLaunch p) {
+    constexpr int J = D / 64;
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int g = h / (p.n_heads / p.n_kv_heads);
+    const uint8_t* sg = p.turbo_signs + (size_t)g * (D / 8);
+    const int64_t ss = p.turbo_slot_stride;
+    const float* q = p.q + ((size_t)s * p.n_heads + h) * D;
+    float* out = p.ws_q + ((size_t)s * p.n_heads + h) * 2 * D;
+    float x[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) x[j] = q[lane + 64 * j];
+    wave_transform<D>(x, sg, sg + ss, lane);
+#pragma unroll
+    for (int j = 0; j < J; j++) out[lane + 64 * j] = x[j];
+    wave_transform<D>(x, sg + 2 * ss, sg + 3 * ss, lane);
+#pragma unroll
+    for (int j = 0; j < J; j++) out[D + lane + 64 * j] = x[j];
+}
+
+// ---------------------------------------------------------------- split-K decode
+
+namespace {
+
+__device__ __forceinline__ f32x4 mma16(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
+                                                  c, 0, 0, 0);
+}
+
+// f16 hi/lo words of two floats
+__device__ __forceinline__ void split2(float a0, float a1, uint32_t& hi, uint32_t& lo) {
+    const uint16_t h0 = f32_to_f16(a0), h1 = f32_to_f16(a1);
+    hi = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    lo = (uint32_t)f32_to_f16(a0 - f16_to_f32(h0)) | ((uint32_t)f32_to_f16(a1 - f16_to_f32(h1)) << 16);
+}
+
+// +-1 / 0 operands of 8 elements: c16 = their 2-bit codes (element e at bits 2e),
+// s8 = their residual sign bits (element e at bit e).  f16 +1 = 0x3C00, -1 = 0xBC00.
+//   a_s   = sign of the centroid (code bit 1)
+//   a_sb  = a_s where the centroid is the outer one (codes 0 and 3), else 0
+//   a_g   = residual sign
+__device__ __forceinline__ void tq_operands(uint32_t c16, uint32_t s8, uint4& a_s, uint4& a_sb, uint4& a_g) {
+    uint32_t ws[4], wb[4], wg[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t c = c16 >> (4 * w);  // codes of elements 2w (bits 0-1), 2w+1 (bits 2-3)
+        const uint32_t pos = ((c >> 1) & 1u) | (((c >> 3) & 1u) << 16);      // code bit 1 per half
+        const uint32_t outer = ~((c ^ (c >> 1)) & 0x5u);                     // bit0 / bit2: code in {0,3}
+        const uint32_t om = ((outer & 1u) ? 0xffffu : 0u) | ((outer & 4u) ? 0xffff0000u : 0u);
+        ws[w] = 0xBC00BC00u ^ (pos << 15);
+        wb[w] = ws[w] & om;
+        const uint32_t sb = (s8 >> (2 * w)) & 3u;
+        wg[w] = 0xBC00BC00u ^ ((sb & 1u) << 15) ^ ((sb & 2u) << 30);
+    }
+    a_s = make_uint4(ws[0], ws[1], ws[2], ws[3]);
+    a_sb = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+    a_g = make_uint4(wg[0], wg[1], wg[2], wg[3]);
+}
+
+__device__ __forceinline__ float pow2_for(float vmax, int top) {
+    int ex;
+    (void)frexpf(vmax, &ex);  // vmax = m 2^ex, m in [0.5, 1)
+    return vmax > 0.0f ? ldexpf(1.0f, min(max(top - ex, -120), 120)) : 1.0f;
+}
+
+}  // namespace
+
+constexpr int kTdThreads = 256;
+constexpr int kTdWaves = kTdThreads / 64;
+
+// One workgroup per (split, kv head, sequence); each wave streams 32-key tiles.
+//   S^T[key][q] = sigma (A_s . B_c0 + A_sb . B_c1) + r (A_g . B_proj)
+//     A = +-1/0 operands of the key row (lane: key l16, its D/4 contiguous dims),
+//     B = the rotated / projected query, times c0 or c1 - c0, as f16 hi + lo;
+//   O_base^T += A_s^T . (c0 P sigma) + A_sb^T . ((c1 - c0) P sigma),
+//   O_res^T  += A_g^T . (P r)
+//     A^T operands from the tile's code / sign bytes staged byte-transposed in LDS.
+// Partials: ws_o [s][h][split][2][D] (base, residual), ws_ml as the other decodes.
+template <int D>
+__global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLaunch p) {
+    constexpr int TILE = 32;
+    constexpr int KS = D / 32;   // MFMA k-steps over d
+    constexpr int DQ = D / 4;    // dims per lane group in the score pass
+    constexpr int NBC = D / 4;   // code bytes per head row
+    constexpr int NSC = D / 8;   // sign bytes per head row
+    constexpr int DT = D / 16;   // output tiles
+    constexpr float kLazy = 8.0f;
+    // LDS per wave: codes [NBC][TILE] and signs [NSC][TILE] bytes (byte-transposed)
+    constexpr int kWaveBytes = (NBC + NSC) * TILE;
+    constexpr int kMergeBytes = (kTdWaves * 16 * (2 * D + 1) + 2 * kTdWaves * 16) * 4;
+    __shared__ __attribute__((aligned(16))) char smem[kTdWaves * kWaveBytes > kMergeBytes ? kTdWaves * kWaveBytes
+                                                                                          : kMergeBytes];
+    const int split = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+    const int t_begin = p.kv_start[s] + split * p.split_keys;
+    const int t_limit = p.kv_end[s];
+    if (t_begin >= t_limit) return;
+    const int t_stop = min(t_limit, t_begin + p.split_keys);
+    const int kv_mul = p.n_heads / p.n_kv_heads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, g4 = lane >> 4;
+    uint8_t* cT = (uint8_t*)smem + wave * kWaveBytes;  // [NBC][TILE]
+    uint8_t* sT = cT + NBC * TILE;                     // [NSC][TILE]
+
+    // B operands of the score pass: lane (query l16, group g4), k-step k holds dims
+    // DQ g4 + 8 k .. +7 (the same dims the A operand of the lane's key carries).
+    uint4 bc0[KS], bc0l[KS], bc1[KS], bc1l[KS], bpj[KS], bpjl[KS];
+    float qback_c = 1.0f, qback_r = 1.0f;
+    {
+        const bool qv = l16 < kv_mul;
+        const float* qr = p.ws_q + ((size_t)s * p.n_heads + (size_t)g * kv_mul + (qv ? l16 : 0)) * 2 * D;
+        const float qs = p.score_scale * kLog2e;
+        float mr = 0.0f, mp = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DQ; e++) {
+            mr = fmaxf(mr, qv ? fabsf(qr[DQ * g4 + e]) : 0.0f);
+            mp = fmaxf(mp, qv ? fabsf(qr[D + DQ * g4 + e]) : 0.0f);
+        }
+        mr = fmaxf(mr, __shfl_xor(mr, 16, 64));
+        mr = fmaxf(mr, __shfl_xor(mr, 32, 64));
+        mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
+        mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
+        // q * qs * 2^e with the row maximum near 2^12 (times c1 - c0 < 1.06 stays < 2^13)
+        const float pr = pow2_for(mr * qs, 12), pp = pow2_for(mp * qs, 12);
+        qback_c = 1.0f / pr;
+        qback_r = 1.0f / pp;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            uint32_t h0[4], l0[4], h1[4], l1[4], hp[4], lp[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const int d0 = DQ * g4 + 8 * k + 2 * w;
+                const float x0 = qv ? qr[d0] * qs * pr : 0.0f, x1 = qv ? qr[d0 + 1] * qs * pr : 0.0f;
+                const float y0 = qv ? qr[D + d0] * qs * pp : 0.0f, y1 = qv ? qr[D + d0 + 1] * qs * pp : 0.0f;
+                split2(kTqC0 * x0, kTqC0 * x1, h0[w], l0[w]);
+                split2((kTqC1 - kTqC0) * x0, (kTqC1 - kTqC0) * x1, h1[w], l1[w]);
+                split2(y0, y1, hp[w], lp[w]);
+            }
+            bc0[k] = make_uint4(h0[0], h0[1], h0[2], h0[3]);
+            bc0l[k] = make_uint4(l0[0], l0[1], l0[2], l0[3]);
+            bc1[k] = make_uint4(h1[0], h1[1], h1[2], h1[3]);
+            bc1l[k] = make_uint4(l1[0], l1[1], l1[2], l1[3]);
+            bpj[k] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+            bpjl[k] = make_uint4(lp[0], lp[1], lp[2], lp[3]);
+        }
+    }
+
+    const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
+    const int64_t e0 = (int64_t)slot * p.seq_stride + (int64_t)g * D;  // element index of (t=0, head g)
+    const uint8_t* kb = (const uint8_t*)p.k_cache;
+    const uint8_t* vb = (const uint8_t*)p.v_cache;
+    const uint8_t* ksg = (const uint8_t*)p.k_sign;
+    const uint8_t* vsg = (const uint8_t*)p.v_sign;
+    const int64_t rs = p.row_stride;
+    const int64_t a0 = (int64_t)slot * p.scale_seq_stride + g;
+    const int64_t ars = p.scale_row_stride;
+    const float rfac = sqrtf(kFracPi2 / (float)D);
+
+    // per-tile registers: K codes/signs of the lane's key for both 16-key sub-tiles,
+    // V code/sign bytes for the staging (lane: key lane/2, half lane%2 of the row),
+    // and sigma / gamma of the lane's score keys (t0 + 16 sb + 4 g4 + j).
+    constexpr int KCW = DQ / 16;  // u32 words of codes per lane (D/4 dims x 2 bits)
+    uint32_t kc[2][KCW], ks_[2];
+    uint32_t vcw[NBC / 8], vsw[NSC / 8];  // half a row each: NBC/2 and NSC/2 bytes
+    float ksig[8], kgam[8], vsig[8], vgam[8];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+            const int key = min(t0 + 16 * sb + l16, t_stop - 1);
+            const int64_t el = e0 + (int64_t)key * rs + DQ * g4;
+#pragma unroll
+            for (int w = 0; w < KCW; w++) kc[sb][w] = *(const uint32_t*)(kb + el / 4 + 4 * w);
+            ks_[sb] = *(const uint32_t*)(ksg + el / 8);
+        }
+        {
+            const int key = min(t0 + (lane >> 1), t_stop - 1);
+            const int64_t el = e0 + (int64_t)key * rs;
+            const int half = lane & 1;
+#pragma unroll
+            for (int w = 0; w < NBC / 8; w++) vcw[w] = *(const uint32_t*)(vb + el / 4 + half * (NBC / 2) + 4 * w);
+#pragma unroll
+            for (int w = 0; w < NSC / 8; w++) vsw[w] = *(const uint32_t*)(vsg + el / 8 + half * (NSC / 2) + 4 * w);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int key = min(t0 + 16 * (e >> 2) + 4 * g4 + (e & 3), t_stop - 1);
+            const int64_t a = a0 + (int64_t)key * ars;
+            ksig[e] = p.k_scale[a];
+            kgam[e] = p.k_rnorm[a];
+            vsig[e] = p.v_scale[a];
+            vgam[e] = p.v_rnorm[a];
+        }
+    };
+    static_assert(D == 128, "decode_turbo_kernel: the K sign word is sized for D/4 = 32 dims per lane group");
+
+    f32x4 ob[DT], orr[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) ob[dt] = orr[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mrow = -1e30f, lrow = 0.0f;
+    float pwb = 1.0f, pwr = 1.0f;  // power-of-two range factors of the two P operands
+    bool pw_set = false;
+
+    const int n_tiles = (t_stop - t_begin + TILE - 1) / TILE;
+    int it = wave;
+    if (it < n_tiles) load_tile(t_begin + it * TILE);
+    for (; it < n_tiles; it += kTdWaves) {
+        const int t0 = t_begin + it * TILE;
+        // V bytes -> LDS, transposed to [byte column][key]
+        {
+            const int key = lane >> 1, half = lane & 1;
+#pragma unroll
+            for (int w = 0; w < NBC / 8; w++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) cT[(half * (NBC / 2) + 4 * w + b) * TILE + key] = (uint8_t)(vcw[w] >> (8 * b));
+#pragma unroll
+            for (int w = 0; w < NSC / 8; w++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) sT[(half * (NSC / 2) + 4 * w + b) * TILE + key] = (uint8_t)(vsw[w] >> (8 * b));
+        }
+        // scores
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 sc[2], sr[2];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++) {
+#pragma unroll
+            for (int k = 0; k < KS; k++) {
+                uint4 as, asb, ag;
+                tq_operands((kc[sb][k >> 1] >> (16 * (k & 1))) & 0xffffu, (ks_[sb] >> (8 * k)) & 0xffu, as, asb, ag);
+                sc[sb] = mma16(as, bc0[k], k == 0 ? zero : sc[sb]);
+                sc[sb] = mma16(as, bc0l[k], sc[sb]);
+                sc[sb] = mma16(asb, bc1[k], sc[sb]);
+                sc[sb] = mma16(asb, bc1l[k], sc[sb]);
+                sr[sb] = mma16(ag, bpj[k], k == 0 ? zero : sr[sb]);
+                sr[sb] = mma16(ag, bpjl[k], sr[sb]);
+            }
+        }
+        float sv[8], vs_cur[8], vr_cur[8];
+        const bool tail = t0 + TILE > t_stop;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = 4 * sb + j;
+                const int key = t0 + 16 * sb + 4 * g4 + j;
+                const float v = ksig[e] * (sc[sb][j] * qback_c) + (kgam[e] * rfac) * (sr[sb][j] * qback_r);
+                sv[e] = (!tail || key < t_stop) ? v : -INFINITY;
+                vs_cur[e] = vsig[e];
+                vr_cur[e] = vgam[e] * rfac;
+            }
+        if (it + kTdWaves < n_tiles) load_tile(t_begin + (it + kTdWaves) * TILE);
+
+        float mx = sv[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) mx = fmaxf(mx, sv[e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (__any(mx > mrow + kLazy)) {
+            const float mnew = fmaxf(mrow, mx);
+            const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+            mrow = mnew;
+            lrow *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                ob[dt] *= alpha;
+                orr[dt] *= alpha;
+            }
+        }
+        float pv[8], psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            pv[e] = __builtin_amdgcn_exp2f(sv[e] - mrow);
+            psum += pv[e];
+        }
+        lrow += psum;
+        // range factors: the tile's largest sigma / r scaled into [2^5, 2^6)
+        {
+            float lb = 0.0f, lr = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                lb = fmaxf(lb, vs_cur[e]);
+                lr = fmaxf(lr, vr_cur[e]);
+            }
+            if (!pw_set || __any(lb * pwb >= 64.0f || lr * pwr >= 64.0f)) {
+                const float nb = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pow2_for(wave_max<64>(lb), 6))));
+                const float nr = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pow2_for(wave_max<64>(lr), 6))));
+                if (!pw_set) {
+                    pwb = nb;
+                    pwr = nr;
+                } else {
+                    if (nb < pwb) {
+                        const float f = nb / pwb;
+#pragma unroll
+                        for (int dt = 0; dt < DT; dt++) ob[dt] *= f;
+                        pwb = nb;
+                    }
+                    if (nr < pwr) {
+                        const float f = nr / pwr;
+#pragma unroll
+                        for (int dt = 0; dt < DT; dt++) orr[dt] *= f;
+                        pwr = nr;
+                    }
+                }
+                pw_set = true;
+            }
+        }
+        // P operands: k-slot r <-> key 16 (r/4) + 4 g4 + r%4, i.e. pv[r]
+        uint4 pc0, pc0l, pc1, pc1l, pr, prl;
+        {
+            uint32_t h0[4], l0[4], h1[4], l1[4], hr[4], lr[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float b0 = pv[2 * w] * vs_cur[2 * w] * pwb, b1 = pv[2 * w + 1] * vs_cur[2 * w + 1] * pwb;
+                split2(kTqC0 * b0, kTqC0 * b1, h0[w], l0[w]);
+                split2((kTqC1 - kTqC0) * b0, (kTqC1 - kTqC0) * b1, h1[w], l1[w]);
+                split2(pv[2 * w] * vr_cur[2 * w] * pwr, pv[2 * w + 1] * vr_cur[2 * w + 1] * pwr, hr[w], lr[w]);
+            }
+            pc0 = make_uint4(h0[0], h0[1], h0[2], h0[3]);
+            pc0l = make_uint4(l0[0], l0[1], l0[2], l0[3]);
+            pc1 = make_uint4(h1[0], h1[1], h1[2], h1[3]);
+            pc1l = make_uint4(l1[0], l1[1], l1[2], l1[3]);
+            pr = make_uint4(hr[0], hr[1], hr[2], hr[3]);
+            prl = make_uint4(lr[0], lr[1], lr[2], lr[3]);
+        }
+        __builtin_amdgcn_wave_barrier();  // LDS stores of this wave precede its reads (in-order LDS)
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            const int d = 16 * dt + l16;
+            // codes / sign bits of dim d for keys 4 g4 + j and 16 + 4 g4 + j
+            const uint32_t c_lo = *(const uint32_t*)(cT + (d >> 2) * TILE + 4 * g4);
+            const uint32_t c_hi = *(const uint32_t*)(cT + (d >> 2) * TILE + 16 + 4 * g4);
+            const uint32_t s_lo = *(const uint32_t*)(sT + (d >> 3) * TILE + 4 * g4);
+            const uint32_t s_hi = *(const uint32_t*)(sT + (d >> 3) * TILE + 16 + 4 * g4);
+            const int cs = 2 * (d & 3), bs = d & 7;
+            uint32_t c16 = 0, s8 = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                c16 |= ((c_lo >> (8 * j + cs)) & 3u) << (2 * j);
+                c16 |= ((c_hi >> (8 * j + cs)) & 3u) << (2 * j + 8);
+                s8 |= ((s_lo >> (8 * j + bs)) & 1u) << j;
+                s8 |= ((s_hi >> (8 * j + bs)) & 1u) << (j + 4);
+            }
+            uint4 as, asb, ag;
+            tq_operands(c16, s8, as, asb, ag);
+            ob[dt] = mma16(as, pc0, ob[dt]);
+            ob[dt] = mma16(as, pc0l, ob[dt]);
+            ob[dt] = mma16(asb, pc1, ob[dt]);
+            ob[dt] = mma16(asb, pc1l, ob[dt]);
+            orr[dt] = mma16(ag, pr, orr[dt]);
+            orr[dt] = mma16(ag, prl, orr[dt]);
+        }
+        __builtin_amdgcn_wave_barrier();  // reads done before the next tile's stores
+    }
+    if (pw_set) {
+        const float ib = 1.0f / pwb, ir = 1.0f / pwr;  // exact: powers of two
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            ob[dt] *= ib;
+            orr[dt] *= ir;
+        }
+    }
+
+    lrow += __shfl_xor(lrow, 16, 64);
+    lrow += __shfl_xor(lrow, 32, 64);
+    __syncthreads();
+    float (*sh_o)[16][2 * D + 1] = (float (*)[16][2 * D + 1])smem;
+    float (*sh_m)[16] = (float (*)[16])((float*)smem + kTdWaves * 16 * (2 * D + 1));
+    float (*sh_l)[16] = sh_m + kTdWaves;
+    if (g4 == 0) {
+        sh_m[wave][l16] = mrow;
+        sh_l[wave][l16] = lrow;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            sh_o[wave][l16][16 * dt + 4 * g4 + j] = ob[dt][j];
+            sh_o[wave][l16][D + 16 * dt + 4 * g4 + j] = orr[dt][j];
+        }
+    __syncthreads();
+    const int n_splits = p.n_splits;
+    for (int idx = tid; idx < kv_mul * 2 * D; idx += kTdThreads) {
+        const int q = idx / (2 * D), i = idx % (2 * D);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kTdWaves; w++) mx = fmaxf(mx, sh_m[w][q]);
+        float lt = 0.0f, ot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kTdWaves; w++) {
+            const float a = exp2f(sh_m[w][q] - mx);
+            lt += sh_l[w][q] * a;
+            ot += sh_o[w][q][i] * a;
+        }
+        const size_t part = ((size_t)s * p.n_heads + (size_t)g * kv_mul + q) * n_splits + split;
+        p.ws_o[part * 2 * D + i] = ot;
+        if (i == 0) {
+            p.ws_ml[part * 2 + 0] = mx;
+            p.ws_ml[part * 2 + 1] = lt;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- merge + finalize
+
+// One wave per (head, sequence): merge the split partials of the base and residual
+// accumulators (log2-domain weights), divide by the softmax sum, then
+// finalize_turboquant_value_head (inference.rs:1323-1334): residual <- R'^-1
+// residual, base += residual, out = R^-1 base.
+template <int D>
+__global__ __launch_bounds__(64) void turbo_combine_kernel(const DecodeLaunch p) {
+    constexpr int J = D / 64;
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int g = h / (p.n_heads / p.n_kv_heads);
+    const int t_len = p.kv_end[s] - p.kv_start[s];
+    const int n_used = t_len > 0 ? (t_len + p.split_keys - 1) / p.split_keys : 0;
+    const size_t part0 = ((size_t)s * p.n_heads + h) * p.n_splits;
+    float mx = -INFINITY;
+    for (int sp = lane; sp < n_used; sp += 64) mx = fmaxf(mx, p.ws_ml[(part0 + sp) * 2]);
+    mx = wave_max<64>(mx);
+    float lt = 0.0f;
+    for (int sp = lane; sp < n_used; sp += 64) lt += p.ws_ml[(part0 + sp) * 2 + 1] * exp2f(p.ws_ml[(part0 + sp) * 2] - mx);
+    lt = wave_sum<64>(lt);
+    float b[J], r[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) b[j] = r[j] = 0.0f;
+    for (int sp = 0; sp < n_used; sp++) {
+        const float w = exp2f(p.ws_ml[(part0 + sp) * 2] - mx);
+        const float* o = p.ws_o + (part0 + sp) * 2 * D;
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            b[j] += o[lane + 64 * j] * w;
+            r[j] += o[D + lane + 64 * j] * w;
+        }
+    }
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        b[j] *= inv;
+        r[j] *= inv;
+    }
+    const uint8_t* sg = p.turbo_signs + (size_t)g * (D / 8);
+    const int64_t ss = p.turbo_slot_stride;
+    wave_transform<D>(r, sg + 3 * ss, sg + 2 * ss, lane);  // res_post, res_pre: inverse
+#pragma unroll
+    for (int j = 0; j < J; j++) b[j] += r[j];
+    wave_transform<D>(b, sg + ss, sg, lane);  // rot_post, rot_pre: inverse
+    float* out = p.out + ((size_t)s * p.n_heads + h) * D;
+#pragma unroll
+    for (int j = 0; j < J; j++) out[lane + 64 * j] = b[j];
+}
+
+bool decode_turbo_supported(const DecodeLaunch& p) {
+    return p.head_dim == 128 && p.n_heads / p.n_kv_heads <= 16;
+}
+
+hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st) {
+    if (p.head_dim != 128) return hipErrorInvalidValue;
+    turbo_query_kernel<128><<<dim3(p.n_heads, p.n_seq), 64, 0, st>>>(p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    decode_turbo_kernel<128><<<dim3(p.n_splits, p.n_kv_heads, p.n_seq), kTdThreads, 0, st>>>(p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    turbo_combine_kernel<128><<<dim3(p.n_heads, p.n_seq), 64, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace gr

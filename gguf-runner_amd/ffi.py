@@ -19,7 +19,7 @@ GR_ERR_HIP = -2
 GR_ERR_RANGE = -3
 GR_ERR_OOM = -4
 
-DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_Q8 = 0, 1, 2, 3
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_Q8, DTYPE_TURBO = 0, 1, 2, 3, 4
 ROPE_NONE, ROPE_ADJACENT, ROPE_NEOX = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -43,7 +43,8 @@ class DecodeArgs(ctypes.Structure):
         ("q", _p), ("k_cache", _p), ("v_cache", _p), ("seq_stride", _i64), ("row_stride", _i64),
         ("kv_start", _p), ("kv_end", _p), ("out", _p), ("workspace", _p),
         ("k_scale", _p), ("v_scale", _p), ("scale_seq_stride", _i64), ("scale_row_stride", _i64),
-        ("q8_block", _i32),
+        ("q8_block", _i32), ("k_sign", _p), ("v_sign", _p), ("k_rnorm", _p), ("v_rnorm", _p),
+        ("turbo_signs", _p), ("turbo_slot_stride", _i64),
     ]
 
 
@@ -110,6 +111,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_prefill_attention.restype = ctypes.c_int
     L.gr_rope_freqs.argtypes = [_f, _i32, _p]
     L.gr_rope_freqs.restype = ctypes.c_int
+    L.gr_turbo_sign_table.argtypes = [_i32, _i32, _i32, _p]
+    L.gr_turbo_sign_table.restype = ctypes.c_int
     L.gr_deltanet_workspace_size.argtypes = [ctypes.POINTER(DeltaNetArgs)]
     L.gr_deltanet_workspace_size.restype = ctypes.c_size_t
     L.gr_deltanet_attention.argtypes = [ctypes.POINTER(DeltaNetArgs), _p]
@@ -130,12 +133,13 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_qwen3next_prefill.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_read_kv_rows.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
     L.gr_read_kv_scales.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
+    L.gr_read_turbo_rows.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p, _p, _p, _p, _p]
     L.gr_read_ssm_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
     for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
               "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_decode_layer_batch",
               "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
-              "gr_read_kv_scales",
+              "gr_read_kv_scales", "gr_read_turbo_rows",
               "gr_read_ssm_state", "gr_write_ssm_state"):
         getattr(L, n).restype = ip
 

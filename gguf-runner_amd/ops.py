@@ -85,6 +85,58 @@ class DecodeCall:
         ffi.check(ffi.lib().gr_decode_attention(ctypes.byref(self.args), _stream(stream)))
 
 
+def turbo_sign_table(n_layers: int, n_kv_heads: int, head_size: int):
+    """gr_turbo_sign_table: host uint8 [4][n_layers][n_kv_heads][ceil(head_size/8)]."""
+    import numpy as np
+    t = np.zeros((4, n_layers, n_kv_heads, (head_size + 7) // 8), np.uint8)
+    ffi.check(ffi.lib().gr_turbo_sign_table(n_layers, n_kv_heads, head_size, t.ctypes.data))
+    return t
+
+
+class TurboDecodeCall:
+    """gr_decode_attention over a Turbo cache (device tensors):
+    codes k_base/v_base uint8 [n_seq][seq_len][Hkv*d/4], signs k_sign/v_sign uint8
+    [n_seq][seq_len][Hkv*d/8], sigma k_scale/v_scale and gamma k_rnorm/v_rnorm f32
+    [n_seq][seq_len][Hkv], signs_dev uint8 [4][n_layers][Hkv][d/8] (the whole table)
+    and the layer index; q / out as DecodeCall."""
+
+    def __init__(self, q, k_base, v_base, k_sign, v_sign, k_scale, v_scale, k_rnorm, v_rnorm,
+                 signs_dev, layer, kv_start, kv_end, out, *, max_kv_len, score_scale=None,
+                 split_keys=0):
+        n_seq, n_heads, d = q.shape
+        _, seq_len, nb = k_base.shape
+        n_kv = nb * 4 // d
+        _, n_layers, n_kv2, sb = signs_dev.shape
+        assert n_kv2 == n_kv and sb == d // 8 and k_sign.shape == (n_seq, seq_len, n_kv * d // 8)
+        for t in (k_scale, v_scale, k_rnorm, v_rnorm):
+            assert t.shape == (n_seq, seq_len, n_kv) and t.dtype == torch.float32 and t.is_contiguous()
+        self._keep = (q, k_base, v_base, k_sign, v_sign, k_scale, v_scale, k_rnorm, v_rnorm, signs_dev,
+                      kv_start, kv_end, out)
+        a = ffi.DecodeArgs()
+        a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim = n_seq, n_heads, n_kv, d
+        a.kv_dtype = ffi.DTYPE_TURBO
+        a.split_keys = split_keys
+        a.max_kv_len = int(max_kv_len)
+        a.score_scale = 1.0 / math.sqrt(d) if score_scale is None else float(score_scale)
+        a.q, a.k_cache, a.v_cache = _ptr(q), _ptr(k_base), _ptr(v_base)
+        a.seq_stride = seq_len * n_kv * d
+        a.row_stride = n_kv * d
+        a.kv_start, a.kv_end, a.out = _ptr(kv_start), _ptr(kv_end), _ptr(out)
+        a.k_scale, a.v_scale, a.k_rnorm, a.v_rnorm = _ptr(k_scale), _ptr(v_scale), _ptr(k_rnorm), _ptr(v_rnorm)
+        a.k_sign, a.v_sign = _ptr(k_sign), _ptr(v_sign)
+        a.scale_seq_stride = seq_len * n_kv
+        a.scale_row_stride = n_kv
+        a.turbo_signs = signs_dev.data_ptr() + layer * n_kv * sb
+        a.turbo_slot_stride = n_layers * n_kv * sb
+        L = ffi.lib()
+        self.ws = _workspace(L.gr_decode_workspace_size(ctypes.byref(a)), q.device)
+        a.workspace = _aligned(self.ws)
+        self.args = a
+
+    def __call__(self, stream=None) -> None:
+        ffi.check(ffi.lib().gr_decode_attention(ctypes.byref(self.args), _stream(stream)))
+
+
 def decode_attention(q, k_cache, v_cache, kv_start, kv_end, *, max_kv_len=None, score_scale=None,
                      split_keys=0, out=None, k_scale=None, v_scale=None, q8_block=False):
     if out is None:

@@ -182,21 +182,42 @@ def decode_layer_batch(p: Config, s: RunState, l: int, seqs, pos, q, k, v) -> np
 
 
 def read_kv_rows(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq: int = 0):
-    dt = {ffi.DTYPE_F32: np.float32, ffi.DTYPE_Q8: np.int8}.get(p.kv_dtype, np.uint16)
-    k = np.zeros((n_rows, p.kv_dim), dt)
-    v = np.zeros((n_rows, p.kv_dim), dt)
+    dt = {ffi.DTYPE_F32: np.float32, ffi.DTYPE_Q8: np.int8, ffi.DTYPE_TURBO: np.uint8}.get(p.kv_dtype,
+                                                                                           np.uint16)
+    width = p.kv_dim // 4 if p.kv_dtype == ffi.DTYPE_TURBO else p.kv_dim
+    k = np.zeros((n_rows, width), dt)
+    v = np.zeros((n_rows, width), dt)
     ffi.check(ffi.lib().gr_read_kv_rows(s.handle, l, seq, row0, n_rows, _p(k), _p(v)))
     return k, v
 
 
 def read_kv_scales(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq: int = 0):
     """key_cache_scale / value_cache_scale of a Q8 cache: [n_rows] (row mode) or
-    [n_rows][kv_dim/32] (block mode)."""
-    per = p.kv_dim // 32 if p.q8_block_scales else 1
+    [n_rows][kv_dim/32] (block mode); Turbo: sigma [n_rows][n_kv_heads]."""
+    per = (p.n_kv_heads if p.kv_dtype == ffi.DTYPE_TURBO else
+           (p.kv_dim // 32 if p.q8_block_scales else 1))
     ks = np.zeros((n_rows, per), np.float32)
     vs = np.zeros((n_rows, per), np.float32)
     ffi.check(ffi.lib().gr_read_kv_scales(s.handle, l, seq, row0, n_rows, _p(ks), _p(vs)))
     return ks, vs
+
+
+def read_turbo_rows(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq: int = 0):
+    """Turbo cache rows: dict of k/v codes [n_rows][kv_dim/4], signs [n_rows][kv_dim/8],
+    sigma and gamma [n_rows][n_kv_heads]."""
+    out = {}
+    for side in ("k", "v"):
+        out[side + "_base"] = np.zeros((n_rows, p.kv_dim // 4), np.uint8)
+        out[side + "_sign"] = np.zeros((n_rows, p.kv_dim // 8), np.uint8)
+        out[side + "_rnorm"] = np.zeros((n_rows, p.n_kv_heads), np.float32)
+    ffi.check(ffi.lib().gr_read_turbo_rows(s.handle, l, seq, row0, n_rows, _p(out["k_base"]),
+                                           _p(out["k_sign"]), _p(out["k_rnorm"]), _p(out["v_base"]),
+                                           _p(out["v_sign"]), _p(out["v_rnorm"])))
+    ks = np.zeros((n_rows, p.n_kv_heads), np.float32)
+    vs = np.zeros((n_rows, p.n_kv_heads), np.float32)
+    ffi.check(ffi.lib().gr_read_kv_scales(s.handle, l, seq, row0, n_rows, _p(ks), _p(vs)))
+    out["k_scale"], out["v_scale"] = ks, vs
+    return out
 
 
 def qwen3next_state_step(p: Config, s: RunState, l: int, q, k, v, g, beta) -> np.ndarray:

@@ -44,7 +44,15 @@ extern "C" {
  * only: KvCacheFormat::Q8 (inference.rs:1886-1917), int8 rows plus f32 scales,
  * one per kv_dim row or, in block mode (GGUF_Q8_BLOCK_SCALES), one per 32
  * elements of the row. */
-typedef enum gr_dtype { GR_DTYPE_F32 = 0, GR_DTYPE_F16 = 1, GR_DTYPE_BF16 = 2, GR_DTYPE_Q8 = 3 } gr_dtype;
+typedef enum gr_dtype {
+    GR_DTYPE_F32 = 0,
+    GR_DTYPE_F16 = 1,
+    GR_DTYPE_BF16 = 2,
+    GR_DTYPE_Q8 = 3,
+    GR_DTYPE_TURBO = 4 /* KvCacheFormat::Turbo (inference.rs:346-1334, the reference's
+                        * default): per kv head 2-bit codes + residual sign bits + sigma,
+                        * gamma; head_dim 128 */
+} gr_dtype;
 
 /* RoPE pairing (apply_rope_qk, inference.rs:1817-1874). */
 typedef enum gr_rope_mode {
@@ -91,6 +99,20 @@ typedef struct gr_decode_args {
     int64_t scale_seq_stride;
     int64_t scale_row_stride;
     int32_t q8_block;     /* 1: one scale per 32 elements (GGUF_Q8_BLOCK_SCALES) */
+    /* GR_DTYPE_TURBO only: k_cache / v_cache are key/value_cache_turbo_base (2-bit
+     * codes, element e at byte e/4, bits 2(e%4)), k_sign / v_sign the
+     * _turbo_sign arrays (bit e%8 of byte e/8), k_scale / v_scale sigma and
+     * k_rnorm / v_rnorm gamma of (seq s, position t, kv head g) at
+     * s*scale_seq_stride + t*scale_row_stride + g (turboquant_aux_index,
+     * inference.rs:669-672).  turbo_signs points at the layer's rows of the
+     * sign table (gr_turbo_sign_table): slot i of kv head g at
+     * turbo_signs + i*turbo_slot_stride + g*head_dim/8. */
+    const void* k_sign;
+    const void* v_sign;
+    const float* k_rnorm;
+    const float* v_rnorm;
+    const uint8_t* turbo_signs;
+    int64_t turbo_slot_stride;
 } gr_decode_args;
 
 size_t gr_decode_workspace_size(const gr_decode_args* a);
@@ -137,6 +159,12 @@ typedef struct gr_prefill_args {
 
 size_t gr_prefill_workspace_size(const gr_prefill_args* a);
 int gr_prefill_attention(const gr_prefill_args* a, void* stream);
+
+/* turboquant_build_sign_table (inference.rs:370-395), host memory:
+ * [4 slots: rot_pre, rot_post, res_pre, res_post][n_layers][n_kv_heads][ceil(head_size/8)],
+ * bit i set = negate element i; bits from splitmix64 of the per-(slot, layer,
+ * kv head) seed.  Copy it to the device for gr_decode_attention. */
+int gr_turbo_sign_table(int32_t n_layers, int32_t n_kv_heads, int32_t head_size, uint8_t* out);
 
 /* RoPE frequency table freq_i = 1 / theta^(2i / rope_dim), i < rope_dim/2, in
  * f32 with the host libm powf, exactly as malloc_run_state builds rope_freqs
@@ -200,7 +228,7 @@ typedef struct gr_attn_config {
     int32_t head_dim;
     int32_t seq_len;            /* cache rows per sequence (Config::seq_len) */
     int32_t n_seq;              /* sequence slots, one reference RunState each (>= 1) */
-    int32_t kv_dtype;           /* gr_dtype of the device KV cache: raw F32/F16/BF16 or Q8 */
+    int32_t kv_dtype;           /* gr_dtype of the device KV cache: raw F32/F16/BF16, Q8 or TURBO */
     int32_t rope_mode;          /* gr_rope_mode (NEOX for Gemma3/Qwen2/Qwen3*, ADJACENT for Llama) */
     int32_t rope_dim;           /* rotated dims, 0 -> head_dim (vendors/mod.rs:1015-1019) */
     float rope_theta;
@@ -275,10 +303,16 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
  * of a layer (f32 [ssm_n_heads][d][d]). */
 int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
                     void* k_out, void* v_out);
-/* Q8 cache only: the f32 scales of those rows (key_cache_scale / value_cache_scale),
- * 1 per row, or kv_dim/32 per row in block mode. */
+/* Q8 cache: the f32 scales of those rows (key_cache_scale / value_cache_scale),
+ * 1 per row, or kv_dim/32 per row in block mode.  Turbo cache: sigma, n_kv_heads
+ * per row. */
 int gr_read_kv_scales(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
                       float* k_scale_out, float* v_scale_out);
+/* Turbo cache only: code bytes (kv_dim/4 per row), sign bytes (kv_dim/8 per row)
+ * and gamma (n_kv_heads per row) of those rows; any pointer may be NULL. */
+int gr_read_turbo_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows,
+                       uint8_t* k_base, uint8_t* k_sign, float* k_rnorm, uint8_t* v_base,
+                       uint8_t* v_sign, float* v_rnorm);
 int gr_read_ssm_state(gr_run_state* s, int32_t layer, float* out);
 int gr_write_ssm_state(gr_run_state* s, int32_t layer, const float* in);
 

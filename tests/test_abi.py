@@ -93,3 +93,11 @@ def test_rope_freqs_match_oracle_bitwise(pkg, orc):
     for theta, dim in ((5e5, 128), (1e4, 256), (1e6, 64)):
         a = np.array(ops.rope_freqs(theta, dim), np.float32)
         assert np.array_equal(a, orc.rope_freqs(theta, dim))
+
+
+def test_turbo_sign_table_matches_oracle_bitwise(pkg, orc):
+    """gr_turbo_sign_table (host) == the oracle's turboquant_build_sign_table restatement."""
+    import numpy as np
+    from gguf_runner_amd import ops
+    for L, G, d in ((2, 8, 128), (3, 4, 64), (1, 1, 40)):
+        assert np.array_equal(ops.turbo_sign_table(L, G, d), orc.turbo_sign_table(L, G, d))

@@ -1,0 +1,191 @@
+"""Turbo KV cache on the device (KvCacheFormat::Turbo, the reference's default
+format, inference.rs:346-1334): the quantising write and attention over the
+packed codes, against the CPU oracle.
+
+Tolerances (fixed before measuring):
+  codes, sign bits, sigma and gamma the device writes from a given f32 row:
+      bit-exact with the oracle's quantize_turboquant_head;
+  attention over a Turbo cache (f32 semantics): max |gpu - ref| <= 1e-5 against
+      the oracle's attention_token on the same packed rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _oracle_cache(orc, rows_k, rows_v, table, layer, n_kv, d):
+    c = orc.TurboCache(rows_k.shape[0], n_kv, d)
+    for r in range(rows_k.shape[0]):
+        orc.kv_write_turbo(c, r, rows_k[r], rows_v[r], table, layer)
+    return c
+
+
+def _decode_case(orc, dev, *, n_heads, n_kv, d, starts, ends, seq_len, seed, online=False, layer=1,
+                 n_layers=2):
+    from gguf_runner_amd import ops
+    rng = np.random.default_rng(seed)
+    n_seq = len(ends)
+    kv_dim = n_kv * d
+    table = orc.turbo_sign_table(n_layers, n_kv, d)
+    q = rng.standard_normal((n_seq, n_heads, d), dtype=np.float32)
+    caches = []
+    for s in range(n_seq):
+        kk = rng.standard_normal((seq_len, kv_dim), dtype=np.float32)
+        vv = rng.standard_normal((seq_len, kv_dim), dtype=np.float32)
+        caches.append(_oracle_cache(orc, kk, vv, table, layer, n_kv, d))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    stack = lambda name, w: T(np.stack([getattr(c, name).reshape(seq_len, w) for c in caches]))
+    out = torch.empty((n_seq, n_heads, d), device=dev)
+    call = ops.TurboDecodeCall(T(q), stack("kbase", kv_dim // 4), stack("vbase", kv_dim // 4),
+                               stack("ksign", kv_dim // 8), stack("vsign", kv_dim // 8),
+                               stack("kscale", n_kv), stack("vscale", n_kv), stack("kres", n_kv),
+                               stack("vres", n_kv), T(table), layer,
+                               torch.tensor(starts, dtype=torch.int32, device=dev),
+                               torch.tensor(ends, dtype=torch.int32, device=dev), out,
+                               max_kv_len=max(e - s for s, e in zip(starts, ends)))
+    call()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = np.stack([orc.attention_token_turbo(q[s].reshape(-1), caches[s], table, layer, n_heads,
+                                              starts[s], ends[s], online=online,
+                                              n_threads=orc.env_threads()).reshape(n_heads, d)
+                    for s in range(n_seq)])
+    return got, ref
+
+
+@pytest.mark.parametrize("online", [False, True])
+def test_config1_turbo_decode(orc, dev, online):
+    """Config 1 over the reference's default KV format: 16 Q / 8 KV heads, d128, 1024 keys."""
+    got, ref = _decode_case(orc, dev, n_heads=16, n_kv=8, d=128, starts=[0], ends=[1024], seq_len=1024,
+                            seed=1201, online=online)
+    assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
+
+
+def test_turbo_decode_ragged_gqa8_tails_and_windows(orc, dev):
+    """Config-3 shape (32 Q / 4 KV heads) with lengths ending inside a 32-key tile and
+    sliding-window starts."""
+    ends = [1, 31, 33, 1000, 3000]
+    starts = [0, 0, 5, 0, 3000 - 1024]
+    got, ref = _decode_case(orc, dev, n_heads=32, n_kv=4, d=128, starts=starts, ends=ends, seq_len=3000,
+                            seed=1203)
+    assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
+
+
+def _turbo_state(rt, ffi, *, rope=False, n_seq=1, seq_len=256, n_heads=16, n_kv=8, d=128):
+    rng = np.random.default_rng(78)
+    if rope:
+        kw = dict(rope_mode=ffi.ROPE_NEOX, rope_theta=1e6, rms_norm_eps=1e-6,
+                  q_norm=(1 + 0.1 * rng.standard_normal((2, d))).astype(np.float32),
+                  k_norm=(1 + 0.1 * rng.standard_normal((2, d))).astype(np.float32))
+    else:
+        kw = dict(rope_mode=ffi.ROPE_NONE)
+    p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=seq_len, n_seq=n_seq,
+                  kv_dtype=ffi.DTYPE_TURBO, **kw)
+    return p, rt.malloc_run_state(p)
+
+
+def _assert_rows_equal(dev_rows, c, row0, n, n_kv, d):
+    kv_dim = n_kv * d
+    for side, base, sign, sc, rn in (("k", c.kbase, c.ksign, c.kscale, c.kres),
+                                     ("v", c.vbase, c.vsign, c.vscale, c.vres)):
+        assert np.array_equal(dev_rows[side + "_base"], base.reshape(-1, kv_dim // 4)[row0:row0 + n]), side
+        assert np.array_equal(dev_rows[side + "_sign"], sign.reshape(-1, kv_dim // 8)[row0:row0 + n]), side
+        assert np.array_equal(dev_rows[side + "_scale"], sc.reshape(-1, n_kv)[row0:row0 + n]), side
+        assert np.array_equal(dev_rows[side + "_rnorm"], rn.reshape(-1, n_kv)[row0:row0 + n]), side
+
+
+def test_turbo_kv_write_token_bit_exact(orc, dev):
+    """gr_kv_write_token into a Turbo cache writes the oracle's codes, sign bits, sigma
+    and gamma bit for bit: random rows of several magnitudes, an all-zero row (sigma 0),
+    a row with one silent head, and a row whose rotation is one centroid exactly."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p, s = _turbo_state(rt, ffi, seq_len=128)
+    rng = np.random.default_rng(9)
+    n, layer, d = 24, 1, 128
+    k = (rng.standard_normal((n, p.kv_dim)) * rng.uniform(0.01, 30, size=(n, 1))).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    k[2] = 0.0
+    v[5, :d] = 0.0
+    for t in range(n):
+        s.k[:], s.v[:] = k[t], v[t]
+        rt.kv_write_token(p, s, layer, 60 + t)
+    table = orc.turbo_sign_table(2, p.n_kv_heads, d)
+    c = orc.TurboCache(60 + n, p.n_kv_heads, d)
+    for t in range(n):
+        orc.kv_write_turbo(c, 60 + t, k[t], v[t], table, layer)
+    _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 60, n), c, 60, n, p.n_kv_heads, d)
+
+
+def test_turbo_layer_token_loop_and_chunked_prefill(orc, dev):
+    """Qwen3-0.6B-shaped layer (QK-norm, NeoX theta 1e6) over a Turbo cache: the
+    token-serial gr_attention_layer_token loop and 64-token prefill chunks write the
+    same rows, those rows are the oracle's encoding of the device's normed and RoPE'd
+    k (and of v), bit for bit, and each output equals the oracle's attention over
+    them with the device's q (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p, s_tok = _turbo_state(rt, ffi, rope=True)
+    _, s_chk = _turbo_state(rt, ffi, rope=True)
+    _, s_aux = _turbo_state(rt, ffi, rope=True)
+    rng = np.random.default_rng(10)
+    m, layer, d = 130, 1, 128
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    tok = np.zeros((m, p.q_dim), np.float32)
+    for t in range(m):
+        s_tok.q[:], s_tok.k[:], s_tok.v[:] = q[t], k[t], v[t]
+        rt.attention_layer_token(p, s_tok, layer, t)
+        tok[t] = s_tok.xb
+    chk = np.concatenate([rt.prefill_attention_chunk(p, s_chk, layer, b, q[b:b + 64], k[b:b + 64],
+                                                     v[b:b + 64]) for b in range(0, m, 64)])
+    r1 = rt.read_turbo_rows(p, s_tok, layer, 0, m)
+    r2 = rt.read_turbo_rows(p, s_chk, layer, 0, m)
+    for key in r1:
+        assert np.array_equal(r1[key], r2[key]), key
+    assert float(np.abs(tok - chk).max()) <= TOL
+    table = orc.turbo_sign_table(2, p.n_kv_heads, d)
+    c = orc.TurboCache(m, p.n_kv_heads, d)
+    qs = []
+    for t in range(m):
+        s_aux.q[:], s_aux.k[:] = q[t], k[t]
+        rt.qkv_bias_and_norm(p, s_aux, layer)
+        rt.apply_rope_qk(p, s_aux, layer, t)
+        orc.kv_write_turbo(c, t, s_aux.k, v[t], table, layer)
+        qs.append(s_aux.q.copy())
+    _assert_rows_equal(r1, c, 0, m, p.n_kv_heads, d)
+    for t in range(m):
+        ref = orc.attention_token_turbo(qs[t], c, table, layer, 16, 0, t + 1)
+        assert float(np.abs(tok[t] - ref).max()) <= TOL, (t, float(np.abs(tok[t] - ref).max()))
+
+
+def test_turbo_decode_layer_batch_slots(orc, dev):
+    """gr_decode_layer_batch over three sequence slots of a Turbo cache."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p, s = _turbo_state(rt, ffi, n_seq=3, seq_len=300, n_heads=32, n_kv=4)
+    rng = np.random.default_rng(11)
+    lens = [5, 170, 299]
+    table = orc.turbo_sign_table(2, 4, 128)
+    caches = []
+    for sq, L in enumerate(lens):
+        kk = rng.standard_normal((L + 1, p.kv_dim)).astype(np.float32)
+        vv = rng.standard_normal((L + 1, p.kv_dim)).astype(np.float32)
+        for t in range(L):
+            s.k[:], s.v[:] = kk[t], vv[t]
+            rt.kv_write_token(p, s, 0, t, seq=sq)
+        caches.append((kk, vv))
+    q = rng.standard_normal((3, p.q_dim)).astype(np.float32)
+    order = [2, 0, 1]
+    got = rt.decode_layer_batch(p, s, 0, order, [lens[i] for i in order], q[order],
+                                np.stack([caches[i][0][lens[i]] for i in order]),
+                                np.stack([caches[i][1][lens[i]] for i in order]))
+    for b, sq in enumerate(order):
+        c = _oracle_cache(orc, caches[sq][0], caches[sq][1], table, 0, 4, 128)
+        ref = orc.attention_token_turbo(q[sq], c, table, 0, 32, 0, lens[sq] + 1)
+        assert float(np.abs(got[b] - ref).max()) <= TOL, (sq, float(np.abs(got[b] - ref).max()))
