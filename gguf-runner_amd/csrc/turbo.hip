@@ -229,27 +229,49 @@ __device__ __forceinline__ void split2(float a0, float a1, uint32_t& hi, uint32_
     lo = (uint32_t)f32_to_f16(a0 - f16_to_f32(h0)) | ((uint32_t)f32_to_f16(a1 - f16_to_f32(h1)) << 16);
 }
 
-// +-1 / 0 operands of 8 elements: c16 = their 2-bit codes (element e at bits 2e),
-// s8 = their residual sign bits (element e at bit e).  f16 +1 = 0x3C00, -1 = 0xBC00.
-//   a_s   = sign of the centroid (code bit 1)
-//   a_sb  = a_s where the centroid is the outer one (codes 0 and 3), else 0
-//   a_g   = residual sign
-__device__ __forceinline__ void tq_operands(uint32_t c16, uint32_t s8, uint4& a_s, uint4& a_sb, uint4& a_g) {
-    uint32_t ws[4], wb[4], wg[4];
+// Lookup tables of the +-1 / 0 MFMA operands (f16 +1 = 0x3C00, -1 = 0xBC00):
+//   lut_c[byte of 4 codes] = {a_s of elements 0-1, 2-3, a_sb of elements 0-1, 2-3}
+//     a_s  = sign of the centroid (code bit 1), a_sb = a_s for the outer
+//     centroids (codes 0, 3) and 0 for the inner ones: C = c0 a_s + (c1 - c0) a_sb;
+//   lut_g[byte of 8 residual sign bits] = a_g of elements 0-7 (bit set = +1).
+__device__ __forceinline__ void build_luts(uint4* lut_c, uint4* lut_g, int tid) {
+    if (tid < 256) {
+        uint32_t hs[4], hb[4];
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const uint32_t c = c16 >> (4 * w);  // codes of elements 2w (bits 0-1), 2w+1 (bits 2-3)
-        const uint32_t pos = ((c >> 1) & 1u) | (((c >> 3) & 1u) << 16);      // code bit 1 per half
-        const uint32_t outer = ~((c ^ (c >> 1)) & 0x5u);                     // bit0 / bit2: code in {0,3}
-        const uint32_t om = ((outer & 1u) ? 0xffffu : 0u) | ((outer & 4u) ? 0xffff0000u : 0u);
-        ws[w] = 0xBC00BC00u ^ (pos << 15);
-        wb[w] = ws[w] & om;
-        const uint32_t sb = (s8 >> (2 * w)) & 3u;
-        wg[w] = 0xBC00BC00u ^ ((sb & 1u) << 15) ^ ((sb & 2u) << 30);
+        for (int e = 0; e < 4; e++) {
+            const int c = (tid >> (2 * e)) & 3;
+            hs[e] = c >= 2 ? 0x3C00u : 0xBC00u;
+            hb[e] = (c == 0 || c == 3) ? hs[e] : 0u;
+        }
+        lut_c[tid] = make_uint4(hs[0] | (hs[1] << 16), hs[2] | (hs[3] << 16), hb[0] | (hb[1] << 16),
+                                hb[2] | (hb[3] << 16));
+        uint32_t g[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            g[w] = (((tid >> (2 * w)) & 1) ? 0x3C00u : 0xBC00u) | ((((tid >> (2 * w + 1)) & 1) ? 0x3C00u : 0xBC00u) << 16);
+        lut_g[tid] = make_uint4(g[0], g[1], g[2], g[3]);
     }
-    a_s = make_uint4(ws[0], ws[1], ws[2], ws[3]);
-    a_sb = make_uint4(wb[0], wb[1], wb[2], wb[3]);
-    a_g = make_uint4(wg[0], wg[1], wg[2], wg[3]);
+}
+
+// 2-bit fields at bits 0-1 of each byte of v -> one byte (byte i at bits 2i)
+__device__ __forceinline__ uint32_t gather2(uint32_t v) {
+    v &= 0x03030303u;
+    v |= v >> 6;
+    v |= v >> 12;
+    return v & 0xffu;
+}
+// bit 0 of each byte of v -> one nibble (byte i at bit i)
+__device__ __forceinline__ uint32_t gather1(uint32_t v) {
+    v &= 0x01010101u;
+    v |= v >> 7;
+    v |= v >> 14;
+    return v & 0xfu;
+}
+
+// Raw buffer access: a wave-uniform base in a scalar descriptor plus a 32-bit
+// byte offset per lane (gfx9-family descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)0xffffffff, 0x00020000);
 }
 
 __device__ __forceinline__ float pow2_for(float vmax, int top) {
@@ -264,15 +286,18 @@ constexpr int kTdThreads = 256;
 constexpr int kTdWaves = kTdThreads / 64;
 
 // One workgroup per (split, kv head, sequence); each wave streams 32-key tiles.
-//   S^T[key][q] = sigma (A_s . B_c0 + A_sb . B_c1) + r (A_g . B_proj)
-//     A = +-1/0 operands of the key row (lane: key l16, its D/4 contiguous dims),
-//     B = the rotated / projected query, times c0 or c1 - c0, as f16 hi + lo;
+//   S^T[key][q] = sigma (c0 (A_s . B_rot) + (c1 - c0) (A_sb . B_rot)) + r (A_g . B_proj)
+//     A = +-1/0 operands of the key row from the lookup tables (lane: key l16,
+//     its D/4 contiguous dims), B = the rotated / projected query as f16 hi + lo;
 //   O_base^T += A_s^T . (c0 P sigma) + A_sb^T . ((c1 - c0) P sigma),
 //   O_res^T  += A_g^T . (P r)
-//     A^T operands from the tile's code / sign bytes staged byte-transposed in LDS.
-// Partials: ws_o [s][h][split][2][D] (base, residual), ws_ml as the other decodes.
+//     A^T operands from the tile's code / sign bytes, staged byte-transposed in LDS.
+// sigma and r = gamma sqrt(pi/2/D) of the tile's keys go through LDS as well
+// (one coalesced load per lane).  Partials: ws_o [s][h][split][2][D] (base,
+// residual), ws_ml as the other decodes.
 template <int D>
-__global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLaunch p) {
+__global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const DecodeLaunch p) {
+    static_assert(D == 128, "decode_turbo_kernel: lane layouts are sized for head_dim 128");
     constexpr int TILE = 32;
     constexpr int KS = D / 32;   // MFMA k-steps over d
     constexpr int DQ = D / 4;    // dims per lane group in the score pass
@@ -280,11 +305,13 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
     constexpr int NSC = D / 8;   // sign bytes per head row
     constexpr int DT = D / 16;   // output tiles
     constexpr float kLazy = 8.0f;
-    // LDS per wave: codes [NBC][TILE] and signs [NSC][TILE] bytes (byte-transposed)
-    constexpr int kWaveBytes = (NBC + NSC) * TILE;
+    // LDS: lookup tables | per wave: codes [NBC][TILE] and signs [NSC][TILE] bytes
+    // (byte-transposed), aux [4][TILE] floats (sigma_k, r_k, sigma_v, r_v)
+    constexpr int kLutBytes = 2 * 256 * 16;
+    constexpr int kWaveBytes = (NBC + NSC) * TILE + 4 * TILE * 4;
+    constexpr int kLoopBytes = kLutBytes + kTdWaves * kWaveBytes;
     constexpr int kMergeBytes = (kTdWaves * 16 * (2 * D + 1) + 2 * kTdWaves * 16) * 4;
-    __shared__ __attribute__((aligned(16))) char smem[kTdWaves * kWaveBytes > kMergeBytes ? kTdWaves * kWaveBytes
-                                                                                          : kMergeBytes];
+    __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
     const int split = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
     const int t_begin = p.kv_start[s] + split * p.split_keys;
     const int t_limit = p.kv_end[s];
@@ -293,12 +320,18 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
     const int kv_mul = p.n_heads / p.n_kv_heads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
-    uint8_t* cT = (uint8_t*)smem + wave * kWaveBytes;  // [NBC][TILE]
-    uint8_t* sT = cT + NBC * TILE;                     // [NSC][TILE]
+    uint4* lut_c = (uint4*)smem;
+    uint4* lut_g = lut_c + 256;
+    uint8_t* cT = (uint8_t*)smem + kLutBytes + wave * kWaveBytes;  // [NBC][TILE]
+    uint8_t* sT = cT + NBC * TILE;                                 // [NSC][TILE]
+    float* auxT = (float*)(sT + NSC * TILE);                       // [4][TILE]
+    build_luts(lut_c, lut_g, tid);
+    __syncthreads();
 
     // B operands of the score pass: lane (query l16, group g4), k-step k holds dims
-    // DQ g4 + 8 k .. +7 (the same dims the A operand of the lane's key carries).
-    uint4 bc0[KS], bc0l[KS], bc1[KS], bc1l[KS], bpj[KS], bpjl[KS];
+    // DQ g4 + 8 k .. +7 (the same dims the A operand of the lane's key carries),
+    // scaled by a power of two that puts the row maximum near 2^14.
+    uint4 bq[KS], bql[KS], bp[KS], bpl[KS];
     float qback_c = 1.0f, qback_r = 1.0f;
     {
         const bool qv = l16 < kv_mul;
@@ -314,78 +347,75 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
         mr = fmaxf(mr, __shfl_xor(mr, 32, 64));
         mp = fmaxf(mp, __shfl_xor(mp, 16, 64));
         mp = fmaxf(mp, __shfl_xor(mp, 32, 64));
-        // q * qs * 2^e with the row maximum near 2^12 (times c1 - c0 < 1.06 stays < 2^13)
-        const float pr = pow2_for(mr * qs, 12), pp = pow2_for(mp * qs, 12);
+        const float pr = pow2_for(mr * qs, 14), pp = pow2_for(mp * qs, 14);
         qback_c = 1.0f / pr;
         qback_r = 1.0f / pp;
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            uint32_t h0[4], l0[4], h1[4], l1[4], hp[4], lp[4];
+            uint32_t hr[4], lr[4], hp[4], lp[4];
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 const int d0 = DQ * g4 + 8 * k + 2 * w;
-                const float x0 = qv ? qr[d0] * qs * pr : 0.0f, x1 = qv ? qr[d0 + 1] * qs * pr : 0.0f;
-                const float y0 = qv ? qr[D + d0] * qs * pp : 0.0f, y1 = qv ? qr[D + d0 + 1] * qs * pp : 0.0f;
-                split2(kTqC0 * x0, kTqC0 * x1, h0[w], l0[w]);
-                split2((kTqC1 - kTqC0) * x0, (kTqC1 - kTqC0) * x1, h1[w], l1[w]);
-                split2(y0, y1, hp[w], lp[w]);
+                split2(qv ? qr[d0] * qs * pr : 0.0f, qv ? qr[d0 + 1] * qs * pr : 0.0f, hr[w], lr[w]);
+                split2(qv ? qr[D + d0] * qs * pp : 0.0f, qv ? qr[D + d0 + 1] * qs * pp : 0.0f, hp[w], lp[w]);
             }
-            bc0[k] = make_uint4(h0[0], h0[1], h0[2], h0[3]);
-            bc0l[k] = make_uint4(l0[0], l0[1], l0[2], l0[3]);
-            bc1[k] = make_uint4(h1[0], h1[1], h1[2], h1[3]);
-            bc1l[k] = make_uint4(l1[0], l1[1], l1[2], l1[3]);
-            bpj[k] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
-            bpjl[k] = make_uint4(lp[0], lp[1], lp[2], lp[3]);
+            bq[k] = make_uint4(hr[0], hr[1], hr[2], hr[3]);
+            bql[k] = make_uint4(lr[0], lr[1], lr[2], lr[3]);
+            bp[k] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+            bpl[k] = make_uint4(lp[0], lp[1], lp[2], lp[3]);
         }
     }
 
+    // wave-uniform bases of (slot, kv head); per-key offsets in 32 bits
     const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
-    const int64_t e0 = (int64_t)slot * p.seq_stride + (int64_t)g * D;  // element index of (t=0, head g)
-    const uint8_t* kb = (const uint8_t*)p.k_cache;
-    const uint8_t* vb = (const uint8_t*)p.v_cache;
-    const uint8_t* ksg = (const uint8_t*)p.k_sign;
-    const uint8_t* vsg = (const uint8_t*)p.v_sign;
-    const int64_t rs = p.row_stride;
+    const int64_t e0 = (int64_t)slot * p.seq_stride + (int64_t)g * D;
+    const __amdgpu_buffer_rsrc_t kbh = buf_rsrc((const uint8_t*)p.k_cache + e0 / 4);
+    const __amdgpu_buffer_rsrc_t vbh = buf_rsrc((const uint8_t*)p.v_cache + e0 / 4);
+    const __amdgpu_buffer_rsrc_t ksh = buf_rsrc((const uint8_t*)p.k_sign + e0 / 8);
+    const __amdgpu_buffer_rsrc_t vsh = buf_rsrc((const uint8_t*)p.v_sign + e0 / 8);
     const int64_t a0 = (int64_t)slot * p.scale_seq_stride + g;
-    const int64_t ars = p.scale_row_stride;
+    const __amdgpu_buffer_rsrc_t ksig = buf_rsrc(p.k_scale + a0);
+    const __amdgpu_buffer_rsrc_t kgam = buf_rsrc(p.k_rnorm + a0);
+    const __amdgpu_buffer_rsrc_t vsig = buf_rsrc(p.v_scale + a0);
+    const __amdgpu_buffer_rsrc_t vgam = buf_rsrc(p.v_rnorm + a0);
+    const uint32_t rsc = (uint32_t)(p.row_stride / 4), rss = (uint32_t)(p.row_stride / 8);
+    const uint32_t ars = (uint32_t)p.scale_row_stride;
     const float rfac = sqrtf(kFracPi2 / (float)D);
 
-    // per-tile registers: K codes/signs of the lane's key for both 16-key sub-tiles,
-    // V code/sign bytes for the staging (lane: key lane/2, half lane%2 of the row),
-    // and sigma / gamma of the lane's score keys (t0 + 16 sb + 4 g4 + j).
-    constexpr int KCW = DQ / 16;  // u32 words of codes per lane (D/4 dims x 2 bits)
-    uint32_t kc[2][KCW], ks_[2];
-    uint32_t vcw[NBC / 8], vsw[NSC / 8];  // half a row each: NBC/2 and NSC/2 bytes
-    float ksig[8], kgam[8], vsig[8], vgam[8];
+    // per-tile registers: K codes / signs of the lane's key in both 16-key sub-tiles,
+    // V code / sign bytes for the staging (lane: key lane/2, half lane%2 of the row),
+    // the lane's aux pair (key lane%32; K for lanes < 32, V above)
+    uint2 kc[2];
+    uint32_t ksb[2];
+    uint4 vcw;
+    uint2 vsw;
+    float xs, xg;
     auto load_tile = [&](int t0) {
 #pragma unroll
         for (int sb = 0; sb < 2; sb++) {
-            const int key = min(t0 + 16 * sb + l16, t_stop - 1);
-            const int64_t el = e0 + (int64_t)key * rs + DQ * g4;
-#pragma unroll
-            for (int w = 0; w < KCW; w++) kc[sb][w] = *(const uint32_t*)(kb + el / 4 + 4 * w);
-            ks_[sb] = *(const uint32_t*)(ksg + el / 8);
+            const uint32_t key = (uint32_t)min(t0 + 16 * sb + l16, t_stop - 1);
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(kbh, (int)(key * rsc + 8 * g4), 0, 0);
+            kc[sb] = make_uint2(v2[0], v2[1]);
+            ksb[sb] = __builtin_amdgcn_raw_buffer_load_b32(ksh, (int)(key * rss + 4 * g4), 0, 0);
         }
         {
-            const int key = min(t0 + (lane >> 1), t_stop - 1);
-            const int64_t el = e0 + (int64_t)key * rs;
-            const int half = lane & 1;
-#pragma unroll
-            for (int w = 0; w < NBC / 8; w++) vcw[w] = *(const uint32_t*)(vb + el / 4 + half * (NBC / 2) + 4 * w);
-#pragma unroll
-            for (int w = 0; w < NSC / 8; w++) vsw[w] = *(const uint32_t*)(vsg + el / 8 + half * (NSC / 2) + 4 * w);
+            const uint32_t key = (uint32_t)min(t0 + (lane >> 1), t_stop - 1);
+            const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(vbh, (int)(key * rsc + 16 * (lane & 1)), 0, 0);
+            vcw = make_uint4(v4[0], v4[1], v4[2], v4[3]);
+            const auto v2 = __builtin_amdgcn_raw_buffer_load_b64(vsh, (int)(key * rss + 8 * (lane & 1)), 0, 0);
+            vsw = make_uint2(v2[0], v2[1]);
         }
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int key = min(t0 + 16 * (e >> 2) + 4 * g4 + (e & 3), t_stop - 1);
-            const int64_t a = a0 + (int64_t)key * ars;
-            ksig[e] = p.k_scale[a];
-            kgam[e] = p.k_rnorm[a];
-            vsig[e] = p.v_scale[a];
-            vgam[e] = p.v_rnorm[a];
+        {
+            const int off = (int)((uint32_t)min(t0 + (lane & 31), t_stop - 1) * ars * 4);
+            if (lane < 32) {
+                xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ksig, off, 0, 0));
+                xg = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(kgam, off, 0, 0));
+            } else {
+                xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vsig, off, 0, 0));
+                xg = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vgam, off, 0, 0));
+            }
         }
     };
-    static_assert(D == 128, "decode_turbo_kernel: the K sign word is sized for D/4 = 32 dims per lane group");
 
     f32x4 ob[DT], orr[DT];
 #pragma unroll
@@ -399,48 +429,61 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
     if (it < n_tiles) load_tile(t_begin + it * TILE);
     for (; it < n_tiles; it += kTdWaves) {
         const int t0 = t_begin + it * TILE;
-        // V bytes -> LDS, transposed to [byte column][key]
+        // stage: V bytes transposed to [byte column][key]; aux as [4][key]
         {
-            const int key = lane >> 1, half = lane & 1;
+            const int key = lane >> 1, col_c = (lane & 1) * (NBC / 2), col_s = (lane & 1) * (NSC / 2);
+            const uint32_t wc[4] = {vcw.x, vcw.y, vcw.z, vcw.w};
+            const uint32_t ws[2] = {vsw.x, vsw.y};
 #pragma unroll
-            for (int w = 0; w < NBC / 8; w++)
+            for (int b = 0; b < 16; b++) cT[(col_c + b) * TILE + key] = (uint8_t)(wc[b >> 2] >> (8 * (b & 3)));
 #pragma unroll
-                for (int b = 0; b < 4; b++) cT[(half * (NBC / 2) + 4 * w + b) * TILE + key] = (uint8_t)(vcw[w] >> (8 * b));
-#pragma unroll
-            for (int w = 0; w < NSC / 8; w++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) sT[(half * (NSC / 2) + 4 * w + b) * TILE + key] = (uint8_t)(vsw[w] >> (8 * b));
+            for (int b = 0; b < 8; b++) sT[(col_s + b) * TILE + key] = (uint8_t)(ws[b >> 2] >> (8 * (b & 3)));
+            const int a = 2 * (lane >> 5);
+            auxT[a * TILE + (lane & 31)] = xs;
+            auxT[(a + 1) * TILE + (lane & 31)] = xg * rfac;
         }
         // scores
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        f32x4 sc[2], sr[2];
+        f32x4 s1[2], s2[2], sr[2];
 #pragma unroll
         for (int sb = 0; sb < 2; sb++) {
 #pragma unroll
             for (int k = 0; k < KS; k++) {
-                uint4 as, asb, ag;
-                tq_operands((kc[sb][k >> 1] >> (16 * (k & 1))) & 0xffffu, (ks_[sb] >> (8 * k)) & 0xffu, as, asb, ag);
-                sc[sb] = mma16(as, bc0[k], k == 0 ? zero : sc[sb]);
-                sc[sb] = mma16(as, bc0l[k], sc[sb]);
-                sc[sb] = mma16(asb, bc1[k], sc[sb]);
-                sc[sb] = mma16(asb, bc1l[k], sc[sb]);
-                sr[sb] = mma16(ag, bpj[k], k == 0 ? zero : sr[sb]);
-                sr[sb] = mma16(ag, bpjl[k], sr[sb]);
+                const uint32_t c16 = (k < 2 ? kc[sb].x : kc[sb].y) >> (16 * (k & 1));
+                const uint4 e0l = lut_c[c16 & 0xffu], e1l = lut_c[(c16 >> 8) & 0xffu];
+                const uint4 ag = lut_g[(ksb[sb] >> (8 * k)) & 0xffu];
+                const uint4 as = make_uint4(e0l.x, e0l.y, e1l.x, e1l.y);
+                const uint4 asb = make_uint4(e0l.z, e0l.w, e1l.z, e1l.w);
+                s1[sb] = mma16(as, bq[k], k == 0 ? zero : s1[sb]);
+                s1[sb] = mma16(as, bql[k], s1[sb]);
+                s2[sb] = mma16(asb, bq[k], k == 0 ? zero : s2[sb]);
+                s2[sb] = mma16(asb, bql[k], s2[sb]);
+                sr[sb] = mma16(ag, bp[k], k == 0 ? zero : sr[sb]);
+                sr[sb] = mma16(ag, bpl[k], sr[sb]);
             }
         }
-        float sv[8], vs_cur[8], vr_cur[8];
+        __builtin_amdgcn_wave_barrier();  // aux stores precede the reads below (in-order LDS)
+        float sv[8], vsg[8], vrr[8];
         const bool tail = t0 + TILE > t_stop;
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++)
+        for (int sb = 0; sb < 2; sb++) {
+            const float4 ks4 = *(const float4*)(auxT + 0 * TILE + 16 * sb + 4 * g4);
+            const float4 kr4 = *(const float4*)(auxT + 1 * TILE + 16 * sb + 4 * g4);
+            const float4 vs4 = *(const float4*)(auxT + 2 * TILE + 16 * sb + 4 * g4);
+            const float4 vr4 = *(const float4*)(auxT + 3 * TILE + 16 * sb + 4 * g4);
+            const float ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w}, krv[4] = {kr4.x, kr4.y, kr4.z, kr4.w};
+            const float vsv[4] = {vs4.x, vs4.y, vs4.z, vs4.w}, vrv[4] = {vr4.x, vr4.y, vr4.z, vr4.w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int e = 4 * sb + j;
                 const int key = t0 + 16 * sb + 4 * g4 + j;
-                const float v = ksig[e] * (sc[sb][j] * qback_c) + (kgam[e] * rfac) * (sr[sb][j] * qback_r);
+                const float base = (kTqC0 * s1[sb][j] + (kTqC1 - kTqC0) * s2[sb][j]) * qback_c;
+                const float v = ksv[j] * base + krv[j] * (sr[sb][j] * qback_r);
                 sv[e] = (!tail || key < t_stop) ? v : -INFINITY;
-                vs_cur[e] = vsig[e];
-                vr_cur[e] = vgam[e] * rfac;
+                vsg[e] = vsv[j];
+                vrr[e] = vrv[j];
             }
+        }
         if (it + kTdWaves < n_tiles) load_tile(t_begin + (it + kTdWaves) * TILE);
 
         float mx = sv[0];
@@ -471,8 +514,8 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
             float lb = 0.0f, lr = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                lb = fmaxf(lb, vs_cur[e]);
-                lr = fmaxf(lr, vr_cur[e]);
+                lb = fmaxf(lb, vsg[e]);
+                lr = fmaxf(lr, vrr[e]);
             }
             if (!pw_set || __any(lb * pwb >= 64.0f || lr * pwr >= 64.0f)) {
                 const float nb = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(pow2_for(wave_max<64>(lb), 6))));
@@ -503,10 +546,10 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
             uint32_t h0[4], l0[4], h1[4], l1[4], hr[4], lr[4];
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                const float b0 = pv[2 * w] * vs_cur[2 * w] * pwb, b1 = pv[2 * w + 1] * vs_cur[2 * w + 1] * pwb;
+                const float b0 = pv[2 * w] * vsg[2 * w] * pwb, b1 = pv[2 * w + 1] * vsg[2 * w + 1] * pwb;
                 split2(kTqC0 * b0, kTqC0 * b1, h0[w], l0[w]);
                 split2((kTqC1 - kTqC0) * b0, (kTqC1 - kTqC0) * b1, h1[w], l1[w]);
-                split2(pv[2 * w] * vr_cur[2 * w] * pwr, pv[2 * w + 1] * vr_cur[2 * w + 1] * pwr, hr[w], lr[w]);
+                split2(pv[2 * w] * vrr[2 * w] * pwr, pv[2 * w + 1] * vrr[2 * w + 1] * pwr, hr[w], lr[w]);
             }
             pc0 = make_uint4(h0[0], h0[1], h0[2], h0[3]);
             pc0l = make_uint4(l0[0], l0[1], l0[2], l0[3]);
@@ -515,7 +558,6 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
             pr = make_uint4(hr[0], hr[1], hr[2], hr[3]);
             prl = make_uint4(lr[0], lr[1], lr[2], lr[3]);
         }
-        __builtin_amdgcn_wave_barrier();  // LDS stores of this wave precede its reads (in-order LDS)
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
             const int d = 16 * dt + l16;
@@ -525,16 +567,10 @@ __global__ __launch_bounds__(kTdThreads) void decode_turbo_kernel(const DecodeLa
             const uint32_t s_lo = *(const uint32_t*)(sT + (d >> 3) * TILE + 4 * g4);
             const uint32_t s_hi = *(const uint32_t*)(sT + (d >> 3) * TILE + 16 + 4 * g4);
             const int cs = 2 * (d & 3), bs = d & 7;
-            uint32_t c16 = 0, s8 = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                c16 |= ((c_lo >> (8 * j + cs)) & 3u) << (2 * j);
-                c16 |= ((c_hi >> (8 * j + cs)) & 3u) << (2 * j + 8);
-                s8 |= ((s_lo >> (8 * j + bs)) & 1u) << j;
-                s8 |= ((s_hi >> (8 * j + bs)) & 1u) << (j + 4);
-            }
-            uint4 as, asb, ag;
-            tq_operands(c16, s8, as, asb, ag);
+            const uint4 e0l = lut_c[gather2(c_lo >> cs)], e1l = lut_c[gather2(c_hi >> cs)];
+            const uint4 ag = lut_g[gather1(s_lo >> bs) | (gather1(s_hi >> bs) << 4)];
+            const uint4 as = make_uint4(e0l.x, e0l.y, e1l.x, e1l.y);
+            const uint4 asb = make_uint4(e0l.z, e0l.w, e1l.z, e1l.w);
             ob[dt] = mma16(as, pc0, ob[dt]);
             ob[dt] = mma16(as, pc0l, ob[dt]);
             ob[dt] = mma16(asb, pc1, ob[dt]);
