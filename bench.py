@@ -10,6 +10,9 @@ call (split kernel + combine kernel) over the whole batch.
 Also reported in the same line:
   decode_32k   -- the decode target run (all 16 sequences at 32768 keys)
   decode_32k_q8 -- the same over a Q8 cache (int8 rows + one f32 scale per row)
+  decode_32k_turbo -- the same over a Turbo cache (2-bit codes + residual signs + 2
+                  f32 per kv head and row; compute-bound, so also given as the f16
+                  cache bytes per second it replaces)
   prefill      -- config 2 (Llama-3-8B-shaped causal prefill, 2048 tokens, f16,
                   RoPE fused) and the 8k target run, in TFLOP/s with
                   flops = 4 * Hq * d * sum_q visible(q)
@@ -300,6 +303,12 @@ def main() -> int:
     q_gbs = qbytes / (q_ms * 1e-3) / 1e9
     del _keep_q, qcall
 
+    # and over a Turbo cache (the reference's default KV format)
+    ucall, ubytes, _keep_u = decode_turbo_workload(dev, [32768] * 16, 35)
+    u_ms, _ = _timed(ucall, args.steps, args.warmup, stream)
+    u_gbs = ubytes / (u_ms * 1e-3) / 1e9
+    del _keep_u, ucall
+
     pre = {}
     for S, seed in ((2048, 2), (8192, 8)):
         pcall, flops, _keep_p = prefill_workload(dev, S, seed)
@@ -334,6 +343,8 @@ def main() -> int:
                        "frac_of_hbm": round(t_gbs / HBM_PEAK_GBS, 4), "bytes": tbytes},
         "decode_32k_q8": {"gbs": round(q_gbs, 2), "ms": round(q_ms, 5),
                           "frac_of_hbm": round(q_gbs / HBM_PEAK_GBS, 4), "bytes": qbytes},
+        "decode_32k_turbo": {"gbs": round(u_gbs, 2), "ms": round(u_ms, 5), "bytes": ubytes,
+                             "f16_equivalent_gbs": round(tbytes / (u_ms * 1e-3) / 1e9, 2)},
         "prefill": pre,
         "wall_ms_per_step": round(dec_wall, 5),
     }
