@@ -46,6 +46,13 @@ struct gr_run_state {
     float* kn = nullptr;
     float* ssm = nullptr;
     size_t ssm_layer = 0;  // floats per layer
+    // Qwen3.5 SSM layer weights and conv history (ssm_conv_state)
+    int ssm_conv_dim = 0;
+    float* ssm_conv_w = nullptr;  // [n_layers][conv_dim][K]
+    float* ssm_a = nullptr;       // [n_layers][n_v]
+    float* ssm_dt = nullptr;      // [n_layers][n_v]
+    float* ssm_nw = nullptr;      // [n_layers][head_dim]
+    float* ssm_hist = nullptr;    // [n_layers][K-1][conv_dim]
     void* stage = nullptr;
     size_t stage_bytes = 0;
 };
@@ -299,6 +306,14 @@ int validate_config(const gr_attn_config* c) {
         return fail(GR_ERR_ARG, "q_norm and k_norm must be both set or both NULL");
     if (c->ssm_n_heads < 0 || (c->ssm_n_heads > 0 && c->ssm_head_dim != 128))
         return fail(GR_ERR_ARG, "DeltaNet state needs ssm_head_dim 128");
+    if (c->ssm_conv1d) {
+        if (c->ssm_n_heads <= 0 || c->ssm_n_k_heads <= 0 || c->ssm_conv_kernel < 1 || c->ssm_conv_kernel > 9)
+            return fail(GR_ERR_ARG, "invalid qwen3next SSM config");
+        if (c->ssm_n_heads % c->ssm_n_k_heads)
+            return fail(GR_ERR_ARG, "unsupported qwen3next SSM shape: n_v_heads %d not divisible by n_k_heads %d",
+                        c->ssm_n_heads, c->ssm_n_k_heads);
+        if (!c->ssm_a || !c->ssm_dt_bias || !c->ssm_norm) return fail(GR_ERR_ARG, "missing qwen3next SSM tensors");
+    }
     return GR_OK;
 }
 
@@ -325,6 +340,7 @@ int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out) {
     s->cfg = *cfg;
     s->cfg.layer_windows = nullptr;
     s->cfg.q_norm = s->cfg.k_norm = nullptr;
+    s->cfg.ssm_conv1d = s->cfg.ssm_a = s->cfg.ssm_dt_bias = s->cfg.ssm_norm = nullptr;  // copied to the device below
     s->cfg.qk_norm_present = nullptr;
     if (cfg->layer_windows) s->windows.assign(cfg->layer_windows, cfg->layer_windows + cfg->n_layers);
     s->d = cfg->head_dim;
@@ -411,6 +427,22 @@ int gr_malloc_run_state(const gr_attn_config* cfg, gr_run_state** out) {
         if (hipMalloc(&s->ssm, nb) != hipSuccess) return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate SSM state"));
         (void)hipMemsetAsync(s->ssm, 0, nb, s->stream);
     }
+    if (cfg->ssm_conv1d) {
+        const int d = cfg->ssm_head_dim, nv = cfg->ssm_n_heads, K = cfg->ssm_conv_kernel;
+        s->ssm_conv_dim = (nv + 2 * cfg->ssm_n_k_heads) * d;
+        const size_t L = (size_t)cfg->n_layers;
+        const size_t wb = L * s->ssm_conv_dim * K * 4, vb = L * nv * 4, nb = L * d * 4;
+        const size_t hb = std::max<size_t>(L * (K - 1) * s->ssm_conv_dim * 4, 4);
+        if (hipMalloc(&s->ssm_conv_w, wb) != hipSuccess || hipMalloc(&s->ssm_a, vb) != hipSuccess ||
+            hipMalloc(&s->ssm_dt, vb) != hipSuccess || hipMalloc(&s->ssm_nw, nb) != hipSuccess ||
+            hipMalloc(&s->ssm_hist, hb) != hipSuccess)
+            return cleanup_fail(fail(GR_ERR_OOM, "unable to allocate qwen3next SSM weights / conv state"));
+        (void)hipMemcpyAsync(s->ssm_conv_w, cfg->ssm_conv1d, wb, hipMemcpyHostToDevice, s->stream);
+        (void)hipMemcpyAsync(s->ssm_a, cfg->ssm_a, vb, hipMemcpyHostToDevice, s->stream);
+        (void)hipMemcpyAsync(s->ssm_dt, cfg->ssm_dt_bias, vb, hipMemcpyHostToDevice, s->stream);
+        (void)hipMemcpyAsync(s->ssm_nw, cfg->ssm_norm, nb, hipMemcpyHostToDevice, s->stream);
+        (void)hipMemsetAsync(s->ssm_hist, 0, hb, s->stream);
+    }
     e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return cleanup_fail(hip_fail(e, "run state initialisation"));
     *out = s;
@@ -422,7 +454,8 @@ void gr_free_run_state(gr_run_state* s) {
     DeviceScope ds(s->device);
     if (s->stream) (void)hipStreamSynchronize(s->stream);
     for (void* p : {s->k_cache, s->v_cache, (void*)s->k_scale, (void*)s->v_scale, (void*)s->k_sign,
-                    (void*)s->v_sign, (void*)s->k_rnorm, (void*)s->v_rnorm, (void*)s->turbo_table, (void*)s->freqs,
+                    (void*)s->v_sign, (void*)s->k_rnorm, (void*)s->v_rnorm, (void*)s->turbo_table, (void*)s->ssm_conv_w,
+                    (void*)s->ssm_a, (void*)s->ssm_dt, (void*)s->ssm_nw, (void*)s->ssm_hist, (void*)s->freqs,
                     (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn, (void*)s->ssm, s->stage})
         if (p) (void)hipFree(p);
     if (s->stream) (void)hipStreamDestroy(s->stream);
@@ -843,6 +876,109 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
     a.workspace = ws ? cv.take<char>(ws) : nullptr;
     if ((rc = deltanet_enqueue(&a, s->stream))) return rc;
     return d2h_sync(s, out, od, rb);
+}
+
+int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const float* qkv, const float* z,
+                           const float* gate_a, const float* gate_b, float* out) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!s->ssm_conv_w) return fail(GR_ERR_ARG, "missing qwen3next SSM tensors");
+    if (T < 0) return fail(GR_ERR_ARG, "T < 0");
+    if (T == 0) return GR_OK;
+    if (!qkv || !z || !gate_a || !out) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const int nv = s->cfg.ssm_n_heads, d = s->cfg.ssm_head_dim, K = s->cfg.ssm_conv_kernel;
+    const size_t cd = (size_t)s->ssm_conv_dim, di = (size_t)nv * d;
+    const size_t ga_rows = gate_b ? (size_t)nv : 2 * (size_t)nv;
+    gr_deltanet_args a{};
+    a.n_tokens = T;
+    a.n_heads = nv;
+    a.head_dim = d;
+    a.in_dtype = GR_DTYPE_F32;
+    a.l2norm = 1;
+    a.algo = GR_DELTANET_AUTO;
+    a.eps = s->eps;
+    const size_t ws = deltanet_ws(&a);
+    const size_t need = 4 * ((size_t)T * (cd + 6 * di + ga_rows + 3 * nv)) + ws + 16384;
+    if ((rc = ensure_stage(s, need))) return rc;
+    Carve cv(s->stage);
+    float* qkv_d = cv.take<float>((size_t)T * cd);
+    float* z_d = cv.take<float>((size_t)T * di);
+    float* ga_d = cv.take<float>((size_t)T * ga_rows);
+    float* gb_d = gate_b ? cv.take<float>((size_t)T * nv) : nullptr;
+    float* q_d = cv.take<float>((size_t)T * di);
+    float* k_d = cv.take<float>((size_t)T * di);
+    float* v_d = cv.take<float>((size_t)T * di);
+    float* beta_d = cv.take<float>((size_t)T * nv);
+    float* gate_d = cv.take<float>((size_t)T * nv);
+    float* o_d = cv.take<float>((size_t)T * di);
+    float* out_d = cv.take<float>((size_t)T * di);
+    if ((rc = h2d(s, qkv_d, qkv, 4 * (size_t)T * cd)) || (rc = h2d(s, z_d, z, 4 * (size_t)T * di)) ||
+        (rc = h2d(s, ga_d, gate_a, 4 * (size_t)T * ga_rows)) ||
+        (gate_b && (rc = h2d(s, gb_d, gate_b, 4 * (size_t)T * nv))))
+        return rc;
+    SsmLaunch p{};
+    p.n_tokens = T;
+    p.n_k_heads = s->cfg.ssm_n_k_heads;
+    p.n_v_heads = nv;
+    p.head_dim = d;
+    p.conv_kernel = K;
+    p.eps = s->eps;
+    p.qkv = qkv_d;
+    p.z = z_d;
+    p.gate_a = ga_d;
+    p.gate_b = gb_d;
+    p.conv_w = s->ssm_conv_w + (size_t)layer * cd * K;
+    p.dt_bias = s->ssm_dt + (size_t)layer * nv;
+    p.ssm_a = s->ssm_a + (size_t)layer * nv;
+    p.ssm_norm = s->ssm_nw + (size_t)layer * d;
+    p.conv_hist = s->ssm_hist + (size_t)layer * (K - 1) * cd;
+    p.q_out = q_d;
+    p.k_out = k_d;
+    p.v_out = v_d;
+    p.beta_out = beta_d;
+    p.gate_out = gate_d;
+    p.o = o_d;
+    p.out = out_d;
+    hipError_t e = launch_ssm_pre(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "ssm pre launch");
+    a.q = q_d;
+    a.k = k_d;
+    a.v = v_d;
+    a.gate = gate_d;
+    a.beta = beta_d;
+    a.state = s->ssm + (size_t)layer * s->ssm_layer;
+    a.out = o_d;
+    a.workspace = ws ? cv.take<char>(ws) : nullptr;
+    if ((rc = deltanet_enqueue(&a, s->stream))) return rc;
+    e = launch_ssm_post(p, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "ssm post launch");
+    return d2h_sync(s, out, out_d, 4 * (size_t)T * di);
+}
+
+int gr_read_ssm_conv_state(gr_run_state* s, int32_t layer, float* out) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!s->ssm_conv_w) return fail(GR_ERR_ARG, "missing qwen3next SSM tensors");
+    if (!out) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const size_t n = (size_t)(s->cfg.ssm_conv_kernel - 1) * s->ssm_conv_dim;
+    return d2h_sync(s, out, s->ssm_hist + (size_t)layer * n, 4 * n);
+}
+
+int gr_write_ssm_conv_state(gr_run_state* s, int32_t layer, const float* in) {
+    clear_error();
+    int rc = check_ssm(s, layer);
+    if (rc) return rc;
+    if (!s->ssm_conv_w) return fail(GR_ERR_ARG, "missing qwen3next SSM tensors");
+    if (!in) return fail(GR_ERR_ARG, "null buffer");
+    DeviceScope dsc(s->device);
+    const size_t n = (size_t)(s->cfg.ssm_conv_kernel - 1) * s->ssm_conv_dim;
+    if ((rc = h2d(s, s->ssm_hist + (size_t)layer * n, in, 4 * n))) return rc;
+    hipError_t e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
 }
 
 int gr_read_kv_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0, int64_t n_rows, void* k_out,

@@ -142,8 +142,11 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     float* ks = qs + C * DS;            // [C][DS] normalised k
     constexpr int AS = C + 4;           // A row stride (16-byte aligned rows)
     float* As = ks + C * DS;            // [C][AS] strictly lower-triangular A
-    float* lg = As + C * AS;            // [C] in-chunk cumulative log decay
-    float* bt = lg + C;                 // [C] beta
+    // [C] in-chunk cumulative log decay, in double: with strong decays the prefix
+    // sums reach ~-100 within a chunk, and a decay exp(lg[t] - lg[s]) taken from two
+    // f32 prefix sums would carry ~100 ulp of absolute error in its exponent
+    double* lg = (double*)(As + C * AS);
+    float* bt = (float*)(lg + C);       // [C] beta
     float* gm = bt + C;                 // [C] gamma_t = exp(lg[t])
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -182,15 +185,15 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     // in-chunk cumulative log decay (inclusive) and beta; padded tokens: gate 0, beta 0
     if (wave == 0) {
         const bool valid = lane < Cn;
-        float gl = valid ? p.gate[(size_t)(t0 + lane) * H + h] : 0.0f;
+        double gl = valid ? (double)p.gate[(size_t)(t0 + lane) * H + h] : 0.0;
         // inclusive prefix sum over the 64 lanes
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(gl, off, 64);
+            const double o = __shfl_up(gl, off, 64);
             if (lane >= off) gl += o;
         }
         lg[lane] = gl;
-        gm[lane] = expf(gl);
+        gm[lane] = expf((float)gl);
         bt[lane] = valid ? finite_or_zero(p.beta[(size_t)(t0 + lane) * H + h]) : 0.0f;
     }
     __syncthreads();
@@ -212,12 +215,12 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
                 aqk[u] = fmaf(qt.x, kk.x, fmaf(qt.y, kk.y, fmaf(qt.z, kk.z, fmaf(qt.w, kk.w, aqk[u]))));
             }
         }
-        const float lt = lg[t];
+        const double lt = lg[t];
         const float bet = bt[t];
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const int s = sb + u;
-            const float decay = s <= t ? expf(lt - lg[s]) : 0.0f;
+            const float decay = s <= t ? expf((float)(lt - lg[s])) : 0.0f;
             As[t * AS + s] = s < t ? bet * decay * akk[u] : 0.0f;
             ws[ChunkWs<D>::P + t * C + s] = s <= t ? decay * aqk[u] : 0.0f;
         }
@@ -225,14 +228,14 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     __syncthreads();
 
     // 3. Qg = gamma_t q_t and Kd^T[j][s] = (gamma_last / gamma_s) k_s[j]
-    const float lglast = lg[C - 1];
+    const double lglast = lg[C - 1];
     for (int e = tid; e < C * D; e += kChunkThreads) {
         const int t = e / D, j = e % D;
         ws[ChunkWs<D>::QG + e] = gm[t] * qs[t * DS + j];
     }
     for (int e = tid; e < D * C; e += kChunkThreads) {
         const int j = e / C, s2 = e % C;
-        ws[ChunkWs<D>::KDT + e] = expf(lglast - lg[s2]) * ks[s2 * DS + j];
+        ws[ChunkWs<D>::KDT + e] = expf((float)(lglast - lg[s2])) * ks[s2 * DS + j];
     }
 
     // 4. [U | W] = (I + A)^-1 [beta V | beta gamma K] by blocked forward
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
             for (int tt = 0; tt < RB; tt++) dst[(b * RB + tt) * D + cc] = x[tt];
         }
     }
-    if (tid == 0) ws[ChunkWs<D>::GL] = expf(lglast);
+    if (tid == 0) ws[ChunkWs<D>::GL] = expf((float)lglast);
 }
 
 constexpr int kScanCols = 16;
@@ -399,7 +402,7 @@ hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     if (p.head_dim != 128) return hipErrorInvalidValue;
     constexpr int D = 128;
-    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 3 * kChunk) * sizeof(float);
+    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 4 * kChunk) * sizeof(float);
     hipError_t ea = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ea != hipSuccess) return ea;

@@ -134,6 +134,37 @@ struct TurboWriteLaunch {
 };
 
 hipError_t launch_turbo_write(const TurboWriteLaunch& p, hipStream_t st);
+
+// Qwen3.5 SSM layer pre/post around the DeltaNet recurrence for a chunk of
+// n_tokens tokens.  qkv [T][conv_dim] (conv_dim = (n_v + 2 n_k) head_dim),
+// z [T][n_v head_dim], gate_a [T][2 n_v] fused (gate_b == nullptr) or [T][n_v]
+// with gate_b [T][n_v]; conv_w [conv_dim][conv_kernel]; conv_hist
+// [(conv_kernel - 1)][conv_dim] read by the pre pass and advanced past the chunk.
+// Outputs of the pre pass: q/k/v [T][n_v][head_dim] (q, k before their L2 norms),
+// beta and log-decay gate [T][n_v].  The post pass maps o [T][n_v][head_dim] to out.
+struct SsmLaunch {
+    int n_tokens, n_k_heads, n_v_heads, head_dim, conv_kernel;
+    float eps;
+    const float* qkv;
+    const float* z;
+    const float* gate_a;
+    const float* gate_b;
+    const float* conv_w;
+    const float* dt_bias;
+    const float* ssm_a;
+    const float* ssm_norm;
+    float* conv_hist;
+    float* q_out;
+    float* k_out;
+    float* v_out;
+    float* beta_out;
+    float* gate_out;
+    const float* o;
+    float* out;
+};
+
+hipError_t launch_ssm_pre(const SsmLaunch& p, hipStream_t st);
+hipError_t launch_ssm_post(const SsmLaunch& p, hipStream_t st);
 bool decode_turbo_supported(const DecodeLaunch& p);
 hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st);
 

@@ -79,6 +79,8 @@ class AttnConfig(ctypes.Structure):
         ("swa_pattern", _i32), ("is_gemma3", _i32), ("online_attn_fusion", _i32),
         ("rms_norm_eps", _f), ("q_norm", _p), ("k_norm", _p), ("qk_norm_present", _p),
         ("ssm_n_heads", _i32), ("ssm_head_dim", _i32), ("q8_block_scales", _i32),
+        ("ssm_n_k_heads", _i32), ("ssm_conv_kernel", _i32), ("ssm_conv1d", _p), ("ssm_a", _p),
+        ("ssm_dt_bias", _p), ("ssm_norm", _p),
     ]
 
 _lib = None
@@ -135,12 +137,16 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_read_kv_scales.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p]
     L.gr_read_turbo_rows.argtypes = [_p, _i32, _i32, _i64, _i64, _p, _p, _p, _p, _p, _p]
     L.gr_read_ssm_state.argtypes = [_p, _i32, _p]
+    L.gr_qwen3next_ssm_layer.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p]
+    L.gr_read_ssm_conv_state.argtypes = [_p, _i32, _p]
+    L.gr_write_ssm_conv_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
     for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
               "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_decode_layer_batch",
               "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
               "gr_read_kv_scales", "gr_read_turbo_rows",
-              "gr_read_ssm_state", "gr_write_ssm_state"):
+              "gr_read_ssm_state", "gr_write_ssm_state", "gr_qwen3next_ssm_layer",
+              "gr_read_ssm_conv_state", "gr_write_ssm_conv_state"):
         getattr(L, n).restype = ip
 
 

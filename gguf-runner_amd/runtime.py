@@ -52,13 +52,20 @@ class Config:
     ssm_n_heads: int = 0
     ssm_head_dim: int = 128
     q8_block_scales: bool = False       # GGUF_Q8_BLOCK_SCALES (inference.rs:1883)
+    # Qwen3.5 SSM layer (Qwen3NextLinearAttentionShape, math.rs:549-620)
+    ssm_n_k_heads: int = 0              # ssm_group_count
+    ssm_conv_kernel: int = 0
+    ssm_conv1d: np.ndarray | None = None  # [n_layers][conv_dim][K]
+    ssm_a: np.ndarray | None = None       # [n_layers][n_v]
+    ssm_dt_bias: np.ndarray | None = None  # [n_layers][n_v]
+    ssm_norm: np.ndarray | None = None    # [n_layers][ssm_head_dim]
     _keep: list = field(default_factory=list, repr=False)
 
     def to_c(self) -> ffi.AttnConfig:
         c = ffi.AttnConfig()
         for name in ("n_layers", "n_heads", "n_kv_heads", "head_dim", "seq_len", "n_seq",
                      "kv_dtype", "rope_mode", "rope_dim", "swa_pattern", "ssm_n_heads",
-                     "ssm_head_dim"):
+                     "ssm_head_dim", "ssm_n_k_heads", "ssm_conv_kernel"):
             setattr(c, name, int(getattr(self, name)))
         for name in ("rope_theta", "rope_theta_swa", "rope_scale_global", "rope_scale_local",
                      "rms_norm_eps"):
@@ -72,7 +79,7 @@ class Config:
                                      dtype=np.int32)
             self._keep.append(w)
             c.layer_windows = w.ctypes.data
-        for name in ("q_norm", "k_norm"):
+        for name in ("q_norm", "k_norm", "ssm_conv1d", "ssm_a", "ssm_dt_bias", "ssm_norm"):
             arr = getattr(self, name)
             if arr is not None:
                 a = np.ascontiguousarray(arr, dtype=np.float32)
@@ -217,6 +224,29 @@ def read_turbo_rows(p: Config, s: RunState, l: int, row0: int, n_rows: int, seq:
     vs = np.zeros((n_rows, p.n_kv_heads), np.float32)
     ffi.check(ffi.lib().gr_read_kv_scales(s.handle, l, seq, row0, n_rows, _p(ks), _p(vs)))
     out["k_scale"], out["v_scale"] = ks, vs
+    return out
+
+
+def qwen3next_ssm_layer(p: Config, s: RunState, l: int, qkv, z, gate_a, gate_b=None) -> np.ndarray:
+    """qwen3next_linear_attention_step_from_projections (math.rs:715-953) for T
+    consecutive tokens: qkv [T][conv_dim], z [T][d_inner], gate_a the fused [T][2 n_v]
+    (gate_b None) or alpha [T][n_v] with gate_b = beta [T][n_v].  Returns ssm_proj
+    [T][d_inner]."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    z = np.ascontiguousarray(z, np.float32)
+    ga = np.ascontiguousarray(gate_a, np.float32)
+    gb = np.ascontiguousarray(gate_b, np.float32) if gate_b is not None else None
+    T = qkv.shape[0]
+    out = np.zeros((T, p.ssm_n_heads * p.ssm_head_dim), np.float32)
+    ffi.check(ffi.lib().gr_qwen3next_ssm_layer(s.handle, l, T, _p(qkv), _p(z), _p(ga),
+                                               _p(gb) if gb is not None else None, _p(out)))
+    return out
+
+
+def read_ssm_conv_state(p: Config, s: RunState, l: int) -> np.ndarray:
+    conv_dim = (p.ssm_n_heads + 2 * p.ssm_n_k_heads) * p.ssm_head_dim
+    out = np.zeros((max(p.ssm_conv_kernel - 1, 0), conv_dim), np.float32)
+    ffi.check(ffi.lib().gr_read_ssm_conv_state(s.handle, l, _p(out)))
     return out
 
 

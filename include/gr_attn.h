@@ -248,6 +248,16 @@ typedef struct gr_attn_config {
     int32_t ssm_head_dim;       /* 128 */
     int32_t q8_block_scales;    /* Q8 cache: 1 = one scale per 32 elements (GGUF_Q8_BLOCK_SCALES,
                                  * inference.rs:1883), 0 = one scale per row */
+    /* Qwen3.5 SSM layer weights for gr_qwen3next_ssm_layer (NULL when unused),
+     * host memory copied at allocation (Qwen3NextLinearAttentionShape,
+     * math.rs:549-620: n_v = ssm_n_heads = ssm_time_step_rank, n_k =
+     * ssm_group_count, conv_dim = (n_v + 2 n_k) * ssm_head_dim). */
+    int32_t ssm_n_k_heads;      /* ssm_group_count; ssm_n_heads % ssm_n_k_heads == 0 */
+    int32_t ssm_conv_kernel;    /* ssm_conv_kernel, 1..9 */
+    const float* ssm_conv1d;    /* [n_layers][conv_dim][ssm_conv_kernel] (blk.l.ssm_conv1d.weight) */
+    const float* ssm_a;         /* [n_layers][ssm_n_heads] (ssm_a) */
+    const float* ssm_dt_bias;   /* [n_layers][ssm_n_heads] (ssm_dt_bias) */
+    const float* ssm_norm;      /* [n_layers][ssm_head_dim] (ssm_norm) */
 } gr_attn_config;
 
 /* malloc_run_state_with_kv_cache_format (inference.rs:1529-1748): validates
@@ -298,6 +308,20 @@ int gr_qwen3next_state_step(gr_run_state* s, int32_t layer, const float* q, cons
 int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float* q,
                          const float* k, const float* v, const float* gate, const float* beta,
                          float* out);
+/* qwen3next_linear_attention_step_from_projections (math.rs:715-953) for T
+ * consecutive tokens of layer `layer`, the serial loop of inference.rs:2866-2885
+ * as one device pass: conv1d + SiLU over the layer's conv history, K -> V head
+ * tiling, L2 norms, beta / decay gates, the gated delta rule on the layer's
+ * state, gated RMSNorm with SiLU(z).  Host rows: qkv [T][conv_dim],
+ * z [T][ssm_n_heads*ssm_head_dim], gate_a [T][2*ssm_n_heads] (fused ssm_ba,
+ * gate_b NULL) or gate_a = alpha [T][ssm_n_heads] with gate_b = beta
+ * [T][ssm_n_heads]; out [T][ssm_n_heads*ssm_head_dim] (ssm_proj). */
+int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const float* qkv, const float* z,
+                           const float* gate_a, const float* gate_b, float* out);
+/* The conv history of a layer ([ssm_conv_kernel - 1][conv_dim] f32, oldest row first). */
+int gr_read_ssm_conv_state(gr_run_state* s, int32_t layer, float* out);
+int gr_write_ssm_conv_state(gr_run_state* s, int32_t layer, const float* in);
+
 /* Host copies of device state (for checks and snapshots): `n_rows` cache rows
  * of (layer, seq) starting at row0 as raw kv_dtype elements, and the SSM state
  * of a layer (f32 [ssm_n_heads][d][d]). */

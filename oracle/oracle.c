@@ -871,6 +871,103 @@ void orc_deltanet_l2norm(float* q, float* k, int d, float eps) {
     }
 }
 
+/* sigmoidf / siluf / softplusf, math.rs:406-424. */
+static float orc_sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+static float orc_siluf(float x) { return x * orc_sigmoidf(x); }
+static float orc_softplusf(float x) {
+    if (x > 20.0f) return x;
+    if (x < -20.0f) return expf(x);
+    return logf(1.0f + expf(x));
+}
+
+/* qwen3next_linear_attention_projected_state, math.rs:766-953, for one token
+ * of one layer (what qwen3next_linear_attention_step_from_projections,
+ * math.rs:715-764, runs per token in the serial prefill loop,
+ * inference.rs:2866-2885):
+ *   causal depthwise conv1d over [history (K-1 rows), qkv] with SiLU (800-817),
+ *   history shift (819-825), per value head h the q/k of key head h % n_k
+ *   (periodic tiling, 826) L2-normalised (q also / sqrt(d)) and v (827-846),
+ *   beta = sigmoid(b), g = exp(softplus(a + dt_bias) A) from the fused [b | a]
+ *   projection (group-major, 853-864) or the split ones (866-870),
+ *   the gated delta rule per head (492-546), then the gated RMSNorm with
+ *   SiLU(z) (478-488).
+ * gate_b == NULL selects the fused layout: gate_a holds 2*n_v values.
+ * conv_w is [conv_dim][K]; conv_hist [(K-1)][conv_dim] and state [n_v][d][d]
+ * are updated in place; out is [n_v*d] (ssm_proj).  Pinned by the float64
+ * stage-by-stage closed form in tests/test_oracle_deltanet.py. */
+void orc_qwen3next_ssm_token(const float* qkv, const float* z, const float* gate_a, const float* gate_b,
+                             int n_k_heads, int n_v_heads, int head_dim, int conv_kernel,
+                             const float* conv_w, const float* dt_bias, const float* ssm_a,
+                             const float* ssm_norm, float eps, float* conv_hist, float* state,
+                             float* out) {
+    const int d = head_dim;
+    const int d_inner = n_v_heads * d;
+    const int conv_dim = d_inner + 2 * n_k_heads * d;
+    const int hist = conv_kernel - 1;
+    float* conv = (float*)malloc(sizeof(float) * (size_t)conv_dim);
+    float* q = (float*)malloc(sizeof(float) * (size_t)d_inner);
+    float* k = (float*)malloc(sizeof(float) * (size_t)d_inner);
+    float* v = (float*)malloc(sizeof(float) * (size_t)d_inner);
+    for (int c = 0; c < conv_dim; c++) {
+        float acc = qkv[c] * conv_w[c * conv_kernel + hist];
+        for (int t = 0; t < hist; t++) acc += conv_hist[t * conv_dim + c] * conv_w[c * conv_kernel + t];
+        if (!isfinite(acc)) acc = 0.0f;
+        conv[c] = orc_siluf(acc);
+    }
+    if (hist > 0) {
+        if (hist > 1) memmove(conv_hist, conv_hist + conv_dim, sizeof(float) * (size_t)(hist - 1) * conv_dim);
+        memcpy(conv_hist + (size_t)(hist - 1) * conv_dim, qkv, sizeof(float) * (size_t)conv_dim);
+    }
+    const int k_off = n_k_heads * d, v_off = 2 * n_k_heads * d;
+    const float inv_scale_q = 1.0f / sqrtf((float)d);
+    for (int h = 0; h < n_v_heads; h++) {
+        const int src_h = h % n_k_heads;
+        const float* qs = conv + src_h * d;
+        const float* ks = conv + k_off + src_h * d;
+        const float* vs = conv + v_off + h * d;
+        float q_ss = 0.0f, k_ss = 0.0f;
+        for (int i = 0; i < d; i++) {
+            q_ss += qs[i] * qs[i];
+            k_ss += ks[i] * ks[i];
+        }
+        const float q_inv = 1.0f / sqrtf(q_ss + eps), k_inv = 1.0f / sqrtf(k_ss + eps);
+        for (int i = 0; i < d; i++) {
+            q[h * d + i] = finite_or_zero(qs[i] * q_inv * inv_scale_q);
+            k[h * d + i] = finite_or_zero(ks[i] * k_inv);
+            v[h * d + i] = finite_or_zero(vs[i]);
+        }
+    }
+    const int hpg = n_v_heads / n_k_heads;
+    for (int h = 0; h < n_v_heads; h++) {
+        float beta, alpha;
+        if (!gate_b) {
+            const int group = h / hpg, idx = h % hpg, base = group * 2 * hpg;
+            beta = orc_sigmoidf(gate_a[base + idx]);
+            alpha = gate_a[base + hpg + idx] + dt_bias[h];
+        } else {
+            beta = orc_sigmoidf(gate_b[h]);
+            alpha = gate_a[h] + dt_bias[h];
+        }
+        float gate = orc_softplusf(alpha) * ssm_a[h];
+        if (!isfinite(gate)) gate = 0.0f;
+        const float g = finite_or_zero(expf(gate));
+        orc_deltanet_head_step(state + (size_t)h * d * d, out + h * d, q + h * d, k + h * d, v + h * d, g,
+                               finite_or_zero(beta), d);
+    }
+    for (int h = 0; h < n_v_heads; h++) {
+        float* o = out + h * d;
+        const float* zh = z + h * d;
+        float ss = 0.0f;
+        for (int i = 0; i < d; i++) ss += o[i] * o[i];
+        const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+        for (int i = 0; i < d; i++) o[i] = finite_or_zero(ssm_norm[i] * (o[i] * inv) * orc_siluf(zh[i]));
+    }
+    free(conv);
+    free(q);
+    free(k);
+    free(v);
+}
+
 /* Token-serial recurrence over T tokens for n_heads heads, as the reference's
  * prefill runs it (inference.rs:2866-2885 -> math.rs:890-934 per token).
  * q,k,v are [T][H][d] f32 (raw, pre-normalisation when l2norm != 0),

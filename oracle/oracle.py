@@ -68,6 +68,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
     L.orc_max_threads.restype = _i
+    L.orc_qwen3next_ssm_token.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p, _p, _p]
     L.orc_splitmix64.argtypes = [ctypes.c_uint64]
     L.orc_splitmix64.restype = ctypes.c_uint64
     L.orc_turbo_sign_table.argtypes = [_i, _i, _i, _p]
@@ -329,6 +330,30 @@ def attention_token_turbo(q, cache: TurboCache, table, layer, n_heads, vis_start
                                     layer_row_base, vis_start, vis_end, attn_scale,
                                     int(apply_attn_scale), int(online), n_threads)
     return xb
+
+
+def qwen3next_ssm_tokens(qkv, z, gate_a, gate_b, *, n_k_heads, n_v_heads, head_dim, conv_kernel,
+                         conv_w, dt_bias, ssm_a, ssm_norm, eps, conv_hist=None, state=None):
+    """The per-token SSM layer (math.rs:766-953) over T tokens in order (the serial
+    prefill loop, inference.rs:2866-2885).  gate_b None = fused [b | a] gates.
+    Returns (out [T][n_v*d], conv_hist [(K-1)][conv_dim], state [n_v][d][d])."""
+    qkv = _f32(qkv)
+    z = _f32(z)
+    ga = _f32(gate_a)
+    gb = _f32(gate_b) if gate_b is not None else None
+    T = qkv.shape[0]
+    d_inner = n_v_heads * head_dim
+    conv_dim = d_inner + 2 * n_k_heads * head_dim
+    hist = np.zeros((max(conv_kernel - 1, 0), conv_dim), np.float32) if conv_hist is None else _f32(conv_hist).copy()
+    st = np.zeros((n_v_heads, head_dim, head_dim), np.float32) if state is None else _f32(state).copy()
+    out = np.zeros((T, d_inner), np.float32)
+    cw, db, sa, sn = _f32(conv_w), _f32(dt_bias), _f32(ssm_a), _f32(ssm_norm)
+    for t in range(T):
+        lib().orc_qwen3next_ssm_token(_ptr(qkv[t]), _ptr(z[t]), _ptr(ga[t]),
+                                      _ptr(gb[t]) if gb is not None else None, n_k_heads, n_v_heads,
+                                      head_dim, conv_kernel, _ptr(cw), _ptr(db), _ptr(sa), _ptr(sn), eps,
+                                      _ptr(hist), _ptr(st), _ptr(out[t]))
+    return out, hist, st
 
 
 def f16_bits(x) -> np.ndarray:

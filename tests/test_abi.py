@@ -101,3 +101,27 @@ def test_turbo_sign_table_matches_oracle_bitwise(pkg, orc):
     from gguf_runner_amd import ops
     for L, G, d in ((2, 8, 128), (3, 4, 64), (1, 1, 40)):
         assert np.array_equal(ops.turbo_sign_table(L, G, d), orc.turbo_sign_table(L, G, d))
+
+
+def test_ssm_config_validation(pkg):
+    """Qwen3NextLinearAttentionShape checks (math.rs:571-584) at allocation, before any
+    device work: n_v % n_k, missing tensors."""
+    import numpy as np
+    from gguf_runner_amd import ffi, runtime as rt
+    base = dict(n_layers=1, n_heads=2, n_kv_heads=1, head_dim=128, seq_len=8, ssm_n_heads=6,
+                ssm_head_dim=128, ssm_n_k_heads=4, ssm_conv_kernel=4,
+                ssm_conv1d=np.zeros((1, 14 * 128, 4), np.float32), ssm_a=np.zeros((1, 6), np.float32),
+                ssm_dt_bias=np.zeros((1, 6), np.float32), ssm_norm=np.ones((1, 128), np.float32))
+    try:
+        rt.malloc_run_state(rt.Config(**base))
+    except ffi.GrError as e:
+        assert "not divisible by n_k_heads" in str(e)
+    else:
+        raise AssertionError("accepted n_v % n_k != 0")
+    base.update(ssm_n_k_heads=3, ssm_a=None)
+    try:
+        rt.malloc_run_state(rt.Config(**base))
+    except ffi.GrError as e:
+        assert "missing qwen3next SSM tensors" in str(e)
+    else:
+        raise AssertionError("accepted missing ssm_a")

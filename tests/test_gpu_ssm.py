@@ -1,0 +1,78 @@
+"""The Qwen3.5 SSM layer around the DeltaNet recurrence (conv1d + SiLU, K -> V
+head tiling, L2 norms, beta / decay gates, gated RMSNorm with SiLU(z); reference
+math.rs:766-953) through gr_qwen3next_ssm_layer, against the oracle's token-serial
+restatement (the loop of inference.rs:2866-2885).
+
+Tolerances (fp32 path):
+  recurrent state: max |gpu - ref| <= 1e-5 (the DeltaNet bar);
+  layer output: |gpu - ref| <= 1e-5 * max(1, |ref|) elementwise.  The gated RMSNorm
+      rescales o to unit RMS and multiplies it by SiLU(z) * w, so outputs reach ~20,
+      where a few ulps of any fp32 evaluation order exceed 1e-5 absolute: on the
+      first case below the oracle's own token loop sits 6.1e-6 from a float64
+      evaluation and the device 2e-5 from the oracle (1e-6 relative);
+  conv history: bit-exact (a copy of the last K - 1 raw inputs).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _weights(rng, n_layers, nk, nv, d, K):
+    conv_dim = (nv + 2 * nk) * d
+    return dict(
+        ssm_conv1d=(0.3 * rng.standard_normal((n_layers, conv_dim, K))).astype(np.float32),
+        ssm_a=-rng.uniform(0.2, 1.2, (n_layers, nv)).astype(np.float32),
+        ssm_dt_bias=(0.1 * rng.standard_normal((n_layers, nv))).astype(np.float32),
+        ssm_norm=(1 + 0.1 * rng.standard_normal((n_layers, d))).astype(np.float32))
+
+
+@pytest.mark.parametrize("nk,fused,chunks", [(8, True, (300, 37)), (16, False, (37, 130))])
+def test_qwen3next_ssm_layer_matches_token_loop(orc, dev, nk, fused, chunks):
+    """Config-5 shape (16 value heads, d128, conv kernel 4): two consecutive calls
+    (chunked and recurrent DeltaNet paths) carry the conv history and the state."""
+    from gguf_runner_amd import runtime as rt
+    rng = np.random.default_rng(500 + nk)
+    nv, d, K, layer, eps = 16, 128, 4, 1, 1e-6
+    W = _weights(rng, 2, nk, nv, d, K)
+    p = rt.Config(n_layers=2, n_heads=2, n_kv_heads=1, head_dim=128, seq_len=16, ssm_n_heads=nv,
+                  ssm_head_dim=d, ssm_n_k_heads=nk, ssm_conv_kernel=K, rms_norm_eps=eps, **W)
+    s = rt.malloc_run_state(p)
+    conv_dim = (nv + 2 * nk) * d
+    hist = None
+    state = None
+    for T in chunks:
+        qkv = rng.standard_normal((T, conv_dim)).astype(np.float32)
+        z = rng.standard_normal((T, nv * d)).astype(np.float32)
+        ga = rng.standard_normal((T, 2 * nv if fused else nv)).astype(np.float32)
+        gb = None if fused else rng.standard_normal((T, nv)).astype(np.float32)
+        got = rt.qwen3next_ssm_layer(p, s, layer, qkv, z, ga, gb)
+        ref, hist, state = orc.qwen3next_ssm_tokens(
+            qkv, z, ga, gb, n_k_heads=nk, n_v_heads=nv, head_dim=d, conv_kernel=K,
+            conv_w=W["ssm_conv1d"][layer], dt_bias=W["ssm_dt_bias"][layer], ssm_a=W["ssm_a"][layer],
+            ssm_norm=W["ssm_norm"][layer], eps=eps, conv_hist=hist, state=state)
+        rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)
+        assert float(rel.max()) <= TOL, (T, float(rel.max()), float(np.abs(got - ref).max()))
+        assert np.array_equal(rt.read_ssm_conv_state(p, s, layer), hist)
+        dev_state = np.zeros((nv, d, d), np.float32)
+        from gguf_runner_amd import ffi
+        ffi.check(ffi.lib().gr_read_ssm_state(s.handle, layer, dev_state.ctypes.data))
+        assert float(np.abs(dev_state - state).max()) <= TOL
+    # layer 0 untouched
+    assert not rt.read_ssm_conv_state(p, s, 0).any()
+
+
+def test_qwen3next_ssm_layer_errors(dev):
+    from gguf_runner_amd import ffi, runtime as rt
+    p = rt.Config(n_layers=1, n_heads=2, n_kv_heads=1, head_dim=128, seq_len=16, ssm_n_heads=4,
+                  ssm_head_dim=128)
+    s = rt.malloc_run_state(p)
+    with pytest.raises(ffi.GrError, match="missing qwen3next SSM tensors"):
+        rt.qwen3next_ssm_layer(p, s, 0, np.zeros((1, 4 * 128 * 3), np.float32),
+                               np.zeros((1, 512), np.float32), np.zeros((1, 8), np.float32))

@@ -3,6 +3,7 @@ against the delta-rule invariants and a float64 brute-force recurrence (CPU only
 from __future__ import annotations
 
 import numpy as np
+import pytest
 
 
 def _unit(rng, d):
@@ -93,3 +94,92 @@ def test_scan_thread_invariant(orc):
     a = orc.deltanet_scan(*args, gate, beta, S0, n_threads=1)
     b = orc.deltanet_scan(*args, gate, beta, S0, n_threads=8)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+# ---- the SSM layer around the recurrence (math.rs:766-953) ---------------------
+
+def _ssm_f64(qkv, z, ga, gb, nk, nv, d, K, cw, db, sa, sn, eps):
+    """Float64 statement of the layer, stage by stage, from the reference's formulas."""
+    T = qkv.shape[0]
+    d_inner = nv * d
+    conv_dim = d_inner + 2 * nk * d
+    x = np.concatenate([np.zeros((K - 1, conv_dim)), qkv.astype(np.float64)])
+    cw = cw.reshape(conv_dim, K).astype(np.float64)
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+    softplus = lambda v: v if v > 20 else (np.exp(v) if v < -20 else np.log1p(np.exp(v)))
+    S = np.zeros((nv, d, d))
+    out = np.zeros((T, d_inner))
+    hpg = nv // nk
+    for t in range(T):
+        win = x[t:t + K]                                  # K rows, oldest first
+        acc = (win * cw.T).sum(axis=0)                    # depthwise causal conv
+        conv = acc * sig(acc)
+        for h in range(nv):
+            sh = h % nk                                   # periodic K -> V tiling
+            q = conv[sh * d:(sh + 1) * d]
+            k = conv[nk * d + sh * d:nk * d + (sh + 1) * d]
+            v = conv[2 * nk * d + h * d:2 * nk * d + (h + 1) * d]
+            q = q / np.sqrt((q * q).sum() + eps) / np.sqrt(d)
+            k = k / np.sqrt((k * k).sum() + eps)
+            if gb is None:
+                grp, idx = h // hpg, h % hpg
+                beta = sig(ga[t, grp * 2 * hpg + idx])
+                alpha = ga[t, grp * 2 * hpg + hpg + idx] + db[h]
+            else:
+                beta = sig(gb[t, h])
+                alpha = ga[t, h] + db[h]
+            g = np.exp(softplus(float(alpha)) * sa[h])
+            S[h] *= g
+            delta = beta * (v - S[h].T @ k)
+            S[h] += np.outer(k, delta)
+            o = S[h].T @ q
+            inv = 1.0 / np.sqrt((o * o).mean() + eps)
+            out[t, h * d:(h + 1) * d] = sn * (o * inv) * (z[t, h * d:(h + 1) * d] * sig(z[t, h * d:(h + 1) * d]))
+    return out, x[T:T + K - 1], S
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_qwen3next_ssm_token_loop_closed_form(orc, fused):
+    rng = np.random.default_rng(60 + int(fused))
+    nk, nv, d, K, T, eps = 2, 4, 16, 4, 7, 1e-6
+    conv_dim = nv * d + 2 * nk * d
+    qkv = rng.standard_normal((T, conv_dim)).astype(np.float32)
+    z = rng.standard_normal((T, nv * d)).astype(np.float32)
+    ga = rng.standard_normal((T, 2 * nv if fused else nv)).astype(np.float32)
+    gb = None if fused else rng.standard_normal((T, nv)).astype(np.float32)
+    ga[2, 0] = 25.0                                       # softplus branches x > 20 / x < -20
+    ga[3, 1] = -30.0
+    cw = (0.3 * rng.standard_normal(conv_dim * K)).astype(np.float32)
+    db = (0.1 * rng.standard_normal(nv)).astype(np.float32)
+    sa = -rng.uniform(0.2, 1.0, nv).astype(np.float32)
+    sn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    out, hist, st = orc.qwen3next_ssm_tokens(qkv, z, ga, gb, n_k_heads=nk, n_v_heads=nv, head_dim=d,
+                                            conv_kernel=K, conv_w=cw, dt_bias=db, ssm_a=sa, ssm_norm=sn,
+                                            eps=eps)
+    e_out, e_hist, e_st = _ssm_f64(qkv, z, ga, gb, nk, nv, d, K, cw, db, sa, sn, eps)
+    assert np.allclose(out, e_out, rtol=2e-5, atol=2e-5)
+    assert np.array_equal(hist, qkv[T - (K - 1):])        # history = the last K-1 raw inputs
+    assert np.allclose(st, e_st, rtol=2e-5, atol=2e-5)
+
+
+def test_qwen3next_ssm_tiling_is_periodic(orc):
+    """K -> V head tiling repeats the key heads periodically ([h0..h(nk-1), h0..],
+    math.rs:824-826): with distinct key heads and identical gates / values, value
+    heads h and h + nk see the same q and k, so their outputs coincide."""
+    rng = np.random.default_rng(70)
+    nk, nv, d, K = 2, 4, 8, 2
+    conv_dim = nv * d + 2 * nk * d
+    qkv = rng.standard_normal((3, conv_dim)).astype(np.float32)
+    v_part = qkv[:, 2 * nk * d:].reshape(3, nv, d)
+    v_part[:, 2:] = v_part[:, :2]                         # v of heads 2,3 = heads 0,1
+    qkv[:, 2 * nk * d:] = v_part.reshape(3, -1)
+    z = np.ones((3, nv * d), np.float32)
+    ga = np.zeros((3, nv), np.float32)
+    gb = np.zeros((3, nv), np.float32)
+    cw = np.tile(np.array([0.2, 0.9], np.float32), conv_dim)
+    out, _, _ = orc.qwen3next_ssm_tokens(qkv, z, ga, gb, n_k_heads=nk, n_v_heads=nv, head_dim=d,
+                                        conv_kernel=K, conv_w=cw, dt_bias=np.zeros(nv, np.float32),
+                                        ssm_a=-np.ones(nv, np.float32), ssm_norm=np.ones(d, np.float32),
+                                        eps=1e-6)
+    o = out.reshape(3, nv, d)
+    assert np.array_equal(o[:, 2:], o[:, :2]) and not np.allclose(o[:, 0], o[:, 1])
