@@ -18,6 +18,8 @@
 namespace gr {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -29,8 +31,9 @@ struct Mfma32<F16> {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
                                                       __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
     }
+    // one v_cvt_pk_f16_f32 (round to nearest even)
     static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-        return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2_t{lo, hi}, half2_t));
     }
     static constexpr bool kSplit = false;
 };
@@ -48,6 +51,16 @@ struct Mfma32<BF16> {
         return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
     }
 };
+
+// Raw buffer access: wave-uniform base in a scalar descriptor, 32-bit byte
+// offsets per lane (gfx9-family descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pf_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)0xffffffff, 0x00020000);
+}
+__device__ __forceinline__ uint4 pf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 constexpr int kPfThreads = 256;
 constexpr int kPfBM = 128;  // query rows per query block (32 per wave)
@@ -129,10 +142,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
 
         uint4 kreg[KCH];
         uint4 vreg[VT][4];
-        // Tiles that end inside the cache take the plain strided addresses; only the
-        // last tile clamps its rows to kend - 1.
+        // Tiles that end inside the cache load through a descriptor at the tile's
+        // first row plus per-thread byte offsets fixed for the whole loop; only
+        // the last tile clamps its rows to kend - 1.
         auto load_tile = [&](int t0) {
-            if (t0 + BN <= kend) {
+            if (!kSplit && t0 + BN <= kend) {
+                const __amdgpu_buffer_rsrc_t kr = pf_rsrc(kc + (int64_t)t0 * rs);
+                const __amdgpu_buffer_rsrc_t vr = pf_rsrc(vc + (int64_t)t0 * rs);
+                const int rsb = (int)rs * 2;
+                // chunk c = tid + 256 u: row c / DC = tid / DC + u (256 / DC), column c % DC = tid % DC
+                const int koff = (tid / DC) * rsb + (tid % DC) * 16;
+                const int voff = 4 * (tid / DC) * rsb + (tid % DC) * 16;
+#pragma unroll
+                for (int u = 0; u < KCH; u++) kreg[u] = pf_load16(kr, koff, u * (kPfThreads / DC) * rsb);
+#pragma unroll
+                for (int u = 0; u < VT; u++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) vreg[u][r] = pf_load16(vr, voff, (4 * u * (kPfThreads / DC) + r) * rsb);
+                return;
+            }
+            if (kSplit && t0 + BN <= kend) {  // bf16: plain strided addresses (fewer registers live)
                 const uint16_t* kt = kc + (int64_t)t0 * rs;
                 const uint16_t* vtp = vc + (int64_t)t0 * rs;
 #pragma unroll
@@ -246,13 +275,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
                 for (int dt = 0; dt < D / 32; dt++) o[dt] *= alpha;
             }
             float pv[16];
-            float psum = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) {
-                pv[e] = __builtin_amdgcn_exp2f(sacc[e] - mrow);
-                psum += pv[e];
+            for (int e = 0; e < 16; e++) pv[e] = __builtin_amdgcn_exp2f(sacc[e] - mrow);
+            if constexpr (kSplit) {
+                float psum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) psum += pv[e];
+                lrow += psum;
             }
-            lrow += psum;
             // B operand P^T, k-step t: k-slot r <-> key t0 + 16 t + 8 (r/4) + 4 lg + r%4
             uint4 pf[2];
             uint4 pfl[kSplit ? 2 : 1];
@@ -272,6 +302,17 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
                         lw[w] = M::pack2(r0, r1);
                     }
                     pfl[t] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+                }
+            }
+            if constexpr (!kSplit) {
+                // row sum of the f16 P that enters the product (v_dot2c_f32_f16 with 1.0)
+                const half2_t one2 = {1.0f16, 1.0f16};
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].x), one2, lrow, false);
+                    lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].y), one2, lrow, false);
+                    lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].z), one2, lrow, false);
+                    lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].w), one2, lrow, false);
                 }
             }
 #pragma unroll
