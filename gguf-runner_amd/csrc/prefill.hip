@@ -5,10 +5,13 @@
 // cache, start = 0 for global layers and pos + 1 - W for window W
 // (LanguageAttentionPolicy::visible_keys, attention.rs:74-96).
 //
-// Block = 4 waves = 128 query rows of one query head; KV tiles of 64 keys are
-// staged in LDS (K row-major, V transposed).  Each wave computes
-//   S^T = K . Q^T   (v_mfma_f32_32x32x16: A = K rows from LDS, B = Q from VGPRs)
-//   O^T += V^T . P^T (A = V^T from LDS, B = P straight from the S^T accumulators)
+// Block = 4 waves = 128 query rows of one query head.  K and V tiles of BN keys
+// go from the cache straight into LDS (buffer_load ... lds, no register
+// staging), both row-major with their 16-byte chunks XOR-swizzled per row so
+// that every LDS read below is free of bank conflicts.  Each wave computes
+//   S^T = K . Q^T    (v_mfma_f32_32x32x16: A = K rows (ds_read_b128), B = Q in VGPRs)
+//   O^T += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from the row-major V tile,
+//                     B = P straight from the S^T accumulators)
 // so both accumulators hold one query per lane column and the online-softmax
 // statistics of a row live in the two lanes (l, l^32) that own it.
 // Q arrives prepared: RoPE'd / normed and multiplied by softmax_scale*log2(e).
@@ -22,6 +25,8 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define GR_LDS __attribute__((address_space(3)))
 
 template <typename DT>
 struct Mfma32;
@@ -57,55 +62,126 @@ struct Mfma32<BF16> {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t pf_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)0xffffffff, 0x00020000);
 }
-__device__ __forceinline__ uint4 pf_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    return make_uint4(v[0], v[1], v[2], v[3]);
+
+// 16 bytes per lane from the buffer at byte offset voff into LDS at
+// lds + 16 * lane (lds wave-uniform).  The builtin exists for the device pass
+// only; the host pass of the kernel templates must not see it.
+__device__ __forceinline__ void pf_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (GR_LDS void*)lds, 16, voff, 0, 0, 0);
+#endif
 }
+
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
+__device__ __forceinline__ void pf_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Position of 16-byte chunk c of tile row r: c ^ pf_swz(r & 15).  With it the
+// K reads (16 consecutive rows, one chunk each) and the V transpose reads (4
+// consecutive rows x 4 chunks per 32 lanes) each touch distinct banks.
+__device__ __forceinline__ int pf_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
 
 constexpr int kPfThreads = 256;
 constexpr int kPfBM = 128;  // query rows per query block (32 per wave)
-constexpr int kPfBN = 64;   // keys per LDS tile
+
+template <int D>
+struct PfTile;
+template <>
+struct PfTile<128> {
+    static constexpr int BN = 64;   // keys per LDS tile
+    static constexpr int kOcc = 2;  // workgroups per CU (8 waves, <= 256 VGPRs each)
+};
+template <>
+struct PfTile<256> {
+    static constexpr int BN = 32;
+    static constexpr int kOcc = 1;
+};
 
 // Softmax reference maxima are only raised when a row's tile maximum exceeds
 // them by more than this (log2 units): until then P = 2^(s - m_ref) <= 2^8 and
 // the accumulators need no rescale.  The final O / l is exact either way.
 constexpr float kLazyRescale = 8.0f;
 
+__device__ __forceinline__ float pf_xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pf_xsum32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename DT, int D>
-// Two workgroups per CU (8 waves): keeps each wave within 256 registers, so the
-// MFMA accumulators stay in VGPRs next to the softmax.
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLaunch p) {
-    constexpr int BM = kPfBM, BN = kPfBN;
-    constexpr int KS = D + 8;   // K tile row stride (elements)
-    constexpr int VS = BN + 8;  // V^T tile row stride (elements)
-    constexpr int DC = D / 8;   // 16-byte chunks per row
-    constexpr int KCH = BN * DC / kPfThreads;        // K chunks per thread
-    constexpr int VT = (BN / 4) * DC / kPfThreads;   // V 4-key tasks per thread
-    static_assert(KCH >= 1 && VT >= 1, "tile too small for the block");
+__global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(const PrefillLaunch p) {
+    constexpr int BM = kPfBM, BN = PfTile<D>::BN;
+    constexpr int CPR = D / 8;                   // 16-byte chunks per cache row
+    constexpr int LD = BN * CPR / kPfThreads;    // DMA chunks per thread per K (or V) tile
+    constexpr int RPU = kPfThreads / CPR;        // tile rows filled by one DMA round
+    static_assert(LD >= 1 && BN % 32 == 0 && kPfThreads % CPR == 0, "tile shape");
     using M = Mfma32<DT>;
     constexpr bool kSplit = M::kSplit;
 
-    // double-buffered K (row-major) and V^T tiles
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KS];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * VS];
+    // Double-buffered K and V tiles; four distinct arrays so that the compiler
+    // sees the DMA into one buffer never aliases the reads of the other.
+    __shared__ __attribute__((aligned(16))) uint16_t Ks0[BN * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Ks1[BN * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs0[BN * D];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs1[BN * D];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int ln = lane & 31, lg = lane >> 5;
-    const int h = blockIdx.x;
-    const int kv_mul = p.n_heads / p.n_kv_heads;
-    const int g = h / kv_mul;
     const int m = p.n_tokens;
     const int P0 = (int)p.base_pos;
     const int W = p.window;
     const int n_qb = (m + BM - 1) / BM;
+    const int n_pairs = (n_qb + 1) / 2;
+
+    // Work item = (query head, pair of query blocks), head-major.  Workgroup b
+    // runs on XCD b % 8; giving each XCD a contiguous run of items keeps the
+    // query heads of one GQA group (same K/V) in one XCD's L2.
+    const int n_items = p.n_heads * n_pairs;
+    const int per_xcd = (n_items + 7) / 8;
+    const int item = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    if (item >= n_items) return;
+    const int h = item / n_pairs;
+    const int j = item - h * n_pairs;
+    const int kv_mul = p.n_heads / p.n_kv_heads;
+    const int g = h / kv_mul;
     const uint16_t* kc = (const uint16_t*)p.k_cache + (size_t)g * D;
     const uint16_t* vc = (const uint16_t*)p.v_cache + (size_t)g * D;
     const int64_t rs = p.cache_row_stride;
+    const int rsb = (int)rs * 2;
 
-    // Each workgroup takes query blocks n_qb-1-j and j: causal work per workgroup
-    // is then nearly constant.
-    const int j = blockIdx.y;
+    // DMA: thread tid fills chunk position tid + 256 u of the tile: row
+    // tid / CPR + u * RPU, position tid % CPR, which holds chunk
+    // (tid % CPR) ^ swz(row) of that cache row.
+    int dma_off[LD];  // byte offsets from the tile's first row (full tiles)
+    int dma_row[LD];
+    int dma_col[LD];  // byte offset of the source chunk within its row
+#pragma unroll
+    for (int u = 0; u < LD; u++) {
+        const int r = tid / CPR + u * RPU;
+        dma_row[u] = r;
+        dma_col[u] = ((tid % CPR) ^ pf_swz(r & 15)) * 16;
+        dma_off[u] = r * rsb + dma_col[u];
+    }
+    // K fragment reads: row 32 sb + ln (row & 15 == ln & 15), chunk 2 s + lg.
+    const int swz_k = pf_swz(ln & 15);
+    // V^T transpose reads (ds_read_b64_tr_b16): lane i of 16-lane group G
+    // supplies row k0 + i/4, columns d0 + 4 (i%4) .. +3, with
+    // k0 = 32 sb + 16 t + 8 b + 4 lg and d0 = 32 dt + 16 (G & 1); it receives
+    // V[k0 + 0..3][d0 + i], i.e. A-operand slots 4b .. 4b+3 of row d0 + i.
+    const int gi = lane & 15;
+    const int v_chunk = 2 * ((lane >> 4) & 1) + ((gi & 3) >> 1);
+    int v_base[2], v_swz[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const int r = 8 * b + 4 * lg + (gi >> 2);
+        v_base[b] = r * D + (gi & 1) * 4;
+        v_swz[b] = pf_swz(r & 15);
+    }
+
     for (int pass = 0; pass < 2; pass++) {
         const int qblk = pass == 0 ? n_qb - 1 - j : j;
         if (pass == 1 && qblk >= n_qb - 1 - j) break;
@@ -140,91 +216,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
         const int t_first = kbeg / BN * BN;
         const int n_tiles = (kend - t_first + BN - 1) / BN;
 
-        uint4 kreg[KCH];
-        uint4 vreg[VT][4];
-        // Tiles that end inside the cache load through a descriptor at the tile's
-        // first row plus per-thread byte offsets fixed for the whole loop; only
-        // the last tile clamps its rows to kend - 1.
-        auto load_tile = [&](int t0) {
-            if (!kSplit && t0 + BN <= kend) {
-                const __amdgpu_buffer_rsrc_t kr = pf_rsrc(kc + (int64_t)t0 * rs);
-                const __amdgpu_buffer_rsrc_t vr = pf_rsrc(vc + (int64_t)t0 * rs);
-                const int rsb = (int)rs * 2;
-                // chunk c = tid + 256 u: row c / DC = tid / DC + u (256 / DC), column c % DC = tid % DC
-                const int koff = (tid / DC) * rsb + (tid % DC) * 16;
-                const int voff = 4 * (tid / DC) * rsb + (tid % DC) * 16;
+        // Issue the DMA of the tile starting at key t0.  Rows past kend - 1 are
+        // clamped to it (they are masked; the clamp keeps P.V free of stale data).
+        auto dma_tile = [&](int t0, uint16_t* kdst, uint16_t* vdst) {
+            const __amdgpu_buffer_rsrc_t kr = pf_rsrc(kc + (int64_t)t0 * rs);
+            const __amdgpu_buffer_rsrc_t vr = pf_rsrc(vc + (int64_t)t0 * rs);
+            if (t0 + BN <= kend) {
 #pragma unroll
-                for (int u = 0; u < KCH; u++) kreg[u] = pf_load16(kr, koff, u * (kPfThreads / DC) * rsb);
-#pragma unroll
-                for (int u = 0; u < VT; u++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) vreg[u][r] = pf_load16(vr, voff, (4 * u * (kPfThreads / DC) + r) * rsb);
-                return;
-            }
-            if (kSplit && t0 + BN <= kend) {  // bf16: plain strided addresses (fewer registers live)
-                const uint16_t* kt = kc + (int64_t)t0 * rs;
-                const uint16_t* vtp = vc + (int64_t)t0 * rs;
-#pragma unroll
-                for (int u = 0; u < KCH; u++) {
-                    const int c = tid + kPfThreads * u;
-                    kreg[u] = *(const uint4*)(kt + (c / DC) * rs + (c % DC) * 8);
+                for (int u = 0; u < LD; u++) {
+                    const int dst = (wave * 64 + u * kPfThreads) * 8;
+                    pf_dma16(kr, kdst + dst, dma_off[u]);
+                    pf_dma16(vr, vdst + dst, dma_off[u]);
                 }
+            } else {
+                const int last = kend - 1 - t0;
 #pragma unroll
-                for (int u = 0; u < VT; u++) {
-                    const int c = tid + kPfThreads * u;
-                    const int kg = c / DC, dc = c % DC;
-                    const uint16_t* vr0 = vtp + (4 * kg) * rs + dc * 8;
-#pragma unroll
-                    for (int r = 0; r < 4; r++) vreg[u][r] = *(const uint4*)(vr0 + r * rs);
-                }
-                return;
-            }
-#pragma unroll
-            for (int u = 0; u < KCH; u++) {
-                const int c = tid + kPfThreads * u;
-                const int key = min(t0 + c / DC, kend - 1);
-                kreg[u] = *(const uint4*)(kc + (int64_t)key * rs + (c % DC) * 8);
-            }
-#pragma unroll
-            for (int u = 0; u < VT; u++) {
-                const int c = tid + kPfThreads * u;
-                const int kg = c / DC, dc = c % DC;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int key = min(t0 + 4 * kg + r, kend - 1);
-                    vreg[u][r] = *(const uint4*)(vc + (int64_t)key * rs + dc * 8);
+                for (int u = 0; u < LD; u++) {
+                    const int off = min(dma_row[u], last) * rsb + dma_col[u];
+                    const int dst = (wave * 64 + u * kPfThreads) * 8;
+                    pf_dma16(kr, kdst + dst, off);
+                    pf_dma16(vr, vdst + dst, off);
                 }
             }
         };
-        auto store_tile = [&](int buf) {
-#pragma unroll
-            for (int u = 0; u < KCH; u++) {
-                const int c = tid + kPfThreads * u;
-                *(uint4*)(&Ks[buf][(c / DC) * KS + (c % DC) * 8]) = kreg[u];
-            }
-#pragma unroll
-            for (int u = 0; u < VT; u++) {
-                const int c = tid + kPfThreads * u;
-                const int kg = c / DC, dc = c % DC;
-                const uint32_t w[4][4] = {{vreg[u][0].x, vreg[u][0].y, vreg[u][0].z, vreg[u][0].w},
-                                          {vreg[u][1].x, vreg[u][1].y, vreg[u][1].z, vreg[u][1].w},
-                                          {vreg[u][2].x, vreg[u][2].y, vreg[u][2].z, vreg[u][2].w},
-                                          {vreg[u][3].x, vreg[u][3].y, vreg[u][3].z, vreg[u][3].w}};
-#pragma unroll
-                for (int dd = 0; dd < 8; dd++) {
-                    const int wi = dd >> 1;
-                    uint32_t lo, hi;
-                    if ((dd & 1) == 0) {
-                        lo = (w[0][wi] & 0xffffu) | (w[1][wi] << 16);
-                        hi = (w[2][wi] & 0xffffu) | (w[3][wi] << 16);
-                    } else {
-                        lo = (w[0][wi] >> 16) | (w[1][wi] & 0xffff0000u);
-                        hi = (w[2][wi] >> 16) | (w[3][wi] & 0xffff0000u);
-                    }
-                    *(uint2*)(&Vt[buf][(dc * 8 + dd) * VS + 4 * kg]) = make_uint2(lo, hi);
-                }
-            }
-        };
+
         f32x16 o[D / 32];
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
@@ -233,39 +248,61 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
         float mrow = -1e30f;  // reference maximum of this lane's row (finite start)
         float lrow = 0.0f;    // this lane's share of the row sum
 
-        // S^T for the 32-key sub-tile sb of buffer buf
-        auto qk = [&](int buf, int sb, f32x16& sacc) {
+        // One 32-key sub-tile: rows 32 sb .. 32 sb + 31 of the tile in (kb, vb),
+        // first key ts.
+        auto subtile = [&](const uint16_t* kb, const uint16_t* vb, int sb, int ts) {
             const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                  0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            const uint16_t* krow = &Ks[buf][(32 * sb + ln) * KS + 8 * lg];
+            // S^T = K Q^T
+            f32x16 sacc;
+            const uint16_t* krow = kb + (32 * sb + ln) * D;
 #pragma unroll
             for (int s = 0; s < D / 16; s++) {
-                const uint4 a = *(const uint4*)(krow + 16 * s);
+                const int c = (2 * s + lg) ^ swz_k;
+                const uint4 a = *(const uint4*)(krow + c * 8);
                 sacc = M::mma(a, qf[s], s == 0 ? zero : sacc);
                 if constexpr (kSplit) sacc = M::mma(a, qfl[s], sacc);
             }
-        };
+            // V^T fragment (dt, t) of this sub-tile: two transpose reads
+            auto load_va = [&](int dt, int t) {
+                i16x4 part[2];
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    const int off = (32 * sb + 16 * t) * D + v_base[b] + (((4 * dt + v_chunk) ^ v_swz[b]) << 3);
+                    part[b] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((GR_LDS i16x4*)(vb + off));
+                }
+                const uint2 lo = __builtin_bit_cast(uint2, part[0]);
+                const uint2 hi = __builtin_bit_cast(uint2, part[1]);
+                return make_uint4(lo.x, lo.y, hi.x, hi.y);
+            };
+            // d = 128: all V^T fragments are read before the softmax (they do not
+            // depend on it); d = 256 reads them next to their MFMAs (registers).
+            constexpr bool kPreV = D == 128;
+            uint4 va[kPreV ? D / 32 : 1][2];
+            if constexpr (kPreV) {
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                    for (int t = 0; t < 2; t++) va[dt][t] = load_va(dt, t);
+            }
 
-        // softmax of the 32-key sub-tile starting at key t0 (sub-tile sb of
-        // buffer buf) and O += V^T P^T over those keys
-        auto softmax_pv = [&](int t0, int buf, int sb, f32x16& sacc) {
-            const bool need_mask = (t0 + 31 > wpos_min) || (W > 0 && t0 < wpos_max + 1 - W);
-            // element e of the accumulator is key t0 + 8 (e/4) + 4 lg + e%4
+            // element e of the accumulator is key ts + 8 (e/4) + 4 lg + e%4
+            const bool need_mask = (ts + 31 > wpos_min) || (W > 0 && ts < wpos_max + 1 - W);
             if (need_mask) {
                 // visible iff lo <= key <= my_pos: one unsigned compare per element
                 const int lo = W > 0 ? my_pos + 1 - W : 0;
                 const unsigned range = (unsigned)(my_pos - lo);
-                const int kb = t0 + 4 * lg - lo;
+                const int kb0 = ts + 4 * lg - lo;
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int off = 8 * (e >> 2) + (e & 3);
-                    sacc[e] = (unsigned)(kb + off) <= range ? sacc[e] : -INFINITY;
+                    sacc[e] = (unsigned)(kb0 + off) <= range ? sacc[e] : -INFINITY;
                 }
             }
             float mx = fmaxf(sacc[0], sacc[1]);
 #pragma unroll
             for (int e = 2; e < 16; e++) mx = fmaxf(mx, sacc[e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = pf_xmax32(mx);
             if (__any(mx > mrow + kLazyRescale)) {
                 const float mnew = fmaxf(mrow, mx);
                 const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
@@ -283,7 +320,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
                 for (int e = 0; e < 16; e++) psum += pv[e];
                 lrow += psum;
             }
-            // B operand P^T, k-step t: k-slot r <-> key t0 + 16 t + 8 (r/4) + 4 lg + r%4
+            // B operand P^T, k-step t: k-slot r <-> key ts + 16 t + 8 (r/4) + 4 lg + r%4
             uint4 pf[2];
             uint4 pfl[kSplit ? 2 : 1];
 #pragma unroll
@@ -315,39 +352,42 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
                     lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].w), one2, lrow, false);
                 }
             }
+            // O^T += V^T P^T; the V^T slot order matches P^T's: slots 0..3 are keys
+            // 16 t + 4 lg + 0..3, slots 4..7 keys 16 t + 8 + 4 lg + 0..3.
 #pragma unroll
-            for (int dt = 0; dt < D / 32; dt++) {
-                const uint16_t* vrow = &Vt[buf][(32 * dt + ln) * VS + 32 * sb + 4 * lg];
+            for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
                 for (int t = 0; t < 2; t++) {
-                    const uint2 lo = *(const uint2*)(vrow + 16 * t);
-                    const uint2 hi = *(const uint2*)(vrow + 16 * t + 8);
-                    const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    const uint4 a = kPreV ? va[kPreV ? dt : 0][t] : load_va(dt, t);
                     o[dt] = M::mma(a, pf[t], o[dt]);
                     if constexpr (kSplit) o[dt] = M::mma(a, pfl[t], o[dt]);
                 }
-            }
         };
-
-        __syncthreads();  // the previous pass is done with both LDS buffers
-        load_tile(t_first);
-        for (int it = 0; it < n_tiles; it++) {
-            const int t0 = t_first + it * BN;
-            const int cur = it & 1;
-            store_tile(cur);  // buffer cur was last read two tiles ago
-            __syncthreads();
-            if (it + 1 < n_tiles) load_tile(t0 + BN);
+        auto compute_tile = [&](const uint16_t* kb, const uint16_t* vb, int t0) {
 #pragma unroll
             for (int sb = 0; sb < BN / 32; sb++) {
                 const int ts = t0 + 32 * sb;
                 if (!(wave_active && ts <= wpos_max && (W <= 0 || ts + 31 >= wpos_min + 1 - W))) continue;
-                f32x16 sacc;
-                qk(cur, sb, sacc);
-                softmax_pv(ts, cur, sb, sacc);
+                subtile(kb, vb, sb, ts);
             }
+        };
+
+        __syncthreads();  // the previous pass is done with every LDS buffer
+        dma_tile(t_first, Ks0, Vs0);
+        for (int it = 0; it < n_tiles; it += 2) {
+            const int t0 = t_first + it * BN;
+            pf_wait_vmem();   // this thread's part of tile it is in LDS
+            __syncthreads();  // ... everyone's, and tile it-1's buffers are free
+            if (it + 1 < n_tiles) dma_tile(t0 + BN, Ks1, Vs1);
+            compute_tile(Ks0, Vs0, t0);
+            if (it + 1 >= n_tiles) break;
+            pf_wait_vmem();
+            __syncthreads();
+            if (it + 2 < n_tiles) dma_tile(t0 + 2 * BN, Ks0, Vs0);
+            compute_tile(Ks1, Vs1, t0 + BN);
         }
 
-        const float lsum = lrow + __shfl_xor(lrow, 32, 64);
+        const float lsum = pf_xsum32(lrow);
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         if (row_ok) {
             float* orow = p.out + ((size_t)my_row * p.n_heads + h) * D;
@@ -370,7 +410,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(const PrefillLau
 template <typename DT>
 static hipError_t launch_prefill_dt(const PrefillLaunch& p, hipStream_t st) {
     const int n_qb = (p.n_tokens + kPfBM - 1) / kPfBM;
-    dim3 grid(p.n_heads, (n_qb + 1) / 2);  // query blocks paired heavy + light
+    const int n_items = p.n_heads * ((n_qb + 1) / 2);  // query blocks paired heavy + light
+    dim3 grid(8 * ((n_items + 7) / 8));
     switch (p.head_dim) {
         case 128: prefill_kernel<DT, 128><<<grid, kPfThreads, 0, st>>>(p); break;
         case 256: prefill_kernel<DT, 256><<<grid, kPfThreads, 0, st>>>(p); break;
