@@ -5,10 +5,11 @@
 // cache, start = 0 for global layers and pos + 1 - W for window W
 // (LanguageAttentionPolicy::visible_keys, attention.rs:74-96).
 //
-// Block = 4 waves = 128 query rows of one query head.  K and V tiles of BN keys
-// go from the cache straight into LDS (buffer_load ... lds, no register
-// staging), both row-major with their 16-byte chunks XOR-swizzled per row so
-// that every LDS read below is free of bank conflicts.  Each wave computes
+// Workgroup = NW waves x 32 query rows of one query head (NW = 8 for large
+// launches, 4 for small ones).  K and V tiles of BN keys go from the cache
+// straight into LDS (buffer_load ... lds, no register staging), both row-major
+// with their 16-byte chunks XOR-swizzled per row so that every LDS read below
+// is free of bank conflicts.  Each wave computes
 //   S^T = K . Q^T    (v_mfma_f32_32x32x16: A = K rows (ds_read_b128), B = Q in VGPRs)
 //   O^T += V^T . P^T (A = V^T via ds_read_b64_tr_b16 from the row-major V tile,
 //                     B = P straight from the S^T accumulators)
@@ -80,18 +81,24 @@ __device__ __forceinline__ void pf_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F
 // consecutive rows x 4 chunks per 32 lanes) each touch distinct banks.
 __device__ __forceinline__ int pf_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
 
-constexpr int kPfThreads = 256;
-constexpr int kPfBM = 128;  // query rows per query block (32 per wave)
 
-template <int D>
+// Workgroup = NW waves of 32 query rows each.  Large launches use 8 waves
+// (256 query rows share every K / V tile, one workgroup per CU), small ones 4
+// waves (twice the workgroups, so short prompts still fill the GPU).
+template <int D, int NW>
 struct PfTile;
 template <>
-struct PfTile<128> {
-    static constexpr int BN = 64;   // keys per LDS tile
-    static constexpr int kOcc = 2;  // workgroups per CU (8 waves, <= 256 VGPRs each)
+struct PfTile<128, 8> {
+    static constexpr int BN = 128;  // keys per LDS tile
+    static constexpr int kOcc = 1;  // workgroups per CU (2 waves per SIMD, <= 256 VGPRs each)
 };
 template <>
-struct PfTile<256> {
+struct PfTile<128, 4> {
+    static constexpr int BN = 64;
+    static constexpr int kOcc = 2;
+};
+template <>
+struct PfTile<256, 4> {
     static constexpr int BN = 32;
     static constexpr int kOcc = 1;
 };
@@ -110,15 +117,20 @@ __device__ __forceinline__ float pf_xsum32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <typename DT, int D>
-__global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(const PrefillLaunch p) {
-    constexpr int BM = kPfBM, BN = PfTile<D>::BN;
+template <typename DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel(const PrefillLaunch p) {
+    constexpr int kPfThreads = NW * 64;
+    constexpr int BM = NW * 32, BN = PfTile<D, NW>::BN;
     constexpr int CPR = D / 8;                   // 16-byte chunks per cache row
     constexpr int LD = BN * CPR / kPfThreads;    // DMA chunks per thread per K (or V) tile
     constexpr int RPU = kPfThreads / CPR;        // tile rows filled by one DMA round
     static_assert(LD >= 1 && BN % 32 == 0 && kPfThreads % CPR == 0, "tile shape");
     using M = Mfma32<DT>;
     constexpr bool kSplit = M::kSplit;
+    // f16, d = 128: the S^T accumulators start from -m_off (a 16-register
+    // broadcast), so the MFMAs deliver s - m_off and the exponent needs no
+    // subtraction; the variants with more live registers subtract instead.
+    constexpr bool kFold = D == 128 && !kSplit;
 
     // Double-buffered K and V tiles; four distinct arrays so that the compiler
     // sees the DMA into one buffer never aliases the reads of the other.
@@ -245,8 +257,17 @@ __global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(co
         for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
             for (int e = 0; e < 16; e++) o[dt][e] = 0.0f;
-        float mrow = -1e30f;  // reference maximum of this lane's row (finite start)
-        float lrow = 0.0f;    // this lane's share of the row sum
+        // Online-softmax state of this lane's row: mrow is the reference maximum
+        // (finite start); with kFold, S^T arrives as s - m_off where m_off =
+        // mrow once the row has seen a key and 0 before, and a rescale is due
+        // when max(s - m_off) > thr = mrow + kLazyRescale - m_off.
+        float mrow = -1e30f;
+        float lrow = 0.0f;  // this lane's share of the row sum
+        float m_off = 0.0f;
+        float thr = -1e30f + kLazyRescale;
+        f32x16 negm;
+#pragma unroll
+        for (int e = 0; e < 16; e++) negm[e] = 0.0f;
 
         // One 32-key sub-tile: rows 32 sb .. 32 sb + 31 of the tile in (kb, vb),
         // first key ts.
@@ -260,7 +281,7 @@ __global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(co
             for (int s = 0; s < D / 16; s++) {
                 const int c = (2 * s + lg) ^ swz_k;
                 const uint4 a = *(const uint4*)(krow + c * 8);
-                sacc = M::mma(a, qf[s], s == 0 ? zero : sacc);
+                sacc = M::mma(a, qf[s], s == 0 ? (kFold ? negm : zero) : sacc);
                 if constexpr (kSplit) sacc = M::mma(a, qfl[s], sacc);
             }
             // V^T fragment (dt, t) of this sub-tile: two transpose reads
@@ -303,7 +324,22 @@ __global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(co
 #pragma unroll
             for (int e = 2; e < 16; e++) mx = fmaxf(mx, sacc[e]);
             mx = pf_xmax32(mx);
-            if (__any(mx > mrow + kLazyRescale)) {
+            if constexpr (kFold) {
+                if (__any(mx > thr)) {
+                    const float mnew = fmaxf(mrow, mx + m_off);
+                    const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+                    mrow = mnew;
+                    lrow *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < D / 32; dt++) o[dt] *= alpha;
+                    const float off_new = mnew > -1e29f ? mnew : 0.0f;
+                    sacc += m_off - off_new;
+                    m_off = off_new;
+                    thr = mrow + kLazyRescale - m_off;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) negm[e] = -m_off;
+                }
+            } else if (__any(mx > mrow + kLazyRescale)) {
                 const float mnew = fmaxf(mrow, mx);
                 const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
                 mrow = mnew;
@@ -313,7 +349,7 @@ __global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(co
             }
             float pv[16];
 #pragma unroll
-            for (int e = 0; e < 16; e++) pv[e] = __builtin_amdgcn_exp2f(sacc[e] - mrow);
+            for (int e = 0; e < 16; e++) pv[e] = __builtin_amdgcn_exp2f(kFold ? sacc[e] : sacc[e] - mrow);
             if constexpr (kSplit) {
                 float psum = 0.0f;
 #pragma unroll
@@ -407,17 +443,29 @@ __global__ __launch_bounds__(kPfThreads, PfTile<D>::kOcc) void prefill_kernel(co
     }
 }
 
-template <typename DT>
-static hipError_t launch_prefill_dt(const PrefillLaunch& p, hipStream_t st) {
-    const int n_qb = (p.n_tokens + kPfBM - 1) / kPfBM;
+template <typename DT, int D, int NW>
+static hipError_t launch_prefill_d(const PrefillLaunch& p, hipStream_t st) {
+    const int n_qb = (p.n_tokens + NW * 32 - 1) / (NW * 32);
     const int n_items = p.n_heads * ((n_qb + 1) / 2);  // query blocks paired heavy + light
     dim3 grid(8 * ((n_items + 7) / 8));
+    prefill_kernel<DT, D, NW><<<grid, NW * 64, 0, st>>>(p);
+    return hipGetLastError();
+}
+
+// Eight-wave workgroups once they alone fill every CU (256 on MI355X), else four.
+static int prefill_pick_waves(const PrefillLaunch& p) {
+    const int n_qb8 = (p.n_tokens + 255) / 256;
+    return p.head_dim == 128 && p.n_heads * ((n_qb8 + 1) / 2) >= 256 ? 8 : 4;
+}
+
+template <typename DT>
+static hipError_t launch_prefill_dt(const PrefillLaunch& p, hipStream_t st) {
     switch (p.head_dim) {
-        case 128: prefill_kernel<DT, 128><<<grid, kPfThreads, 0, st>>>(p); break;
-        case 256: prefill_kernel<DT, 256><<<grid, kPfThreads, 0, st>>>(p); break;
+        case 128:
+            return prefill_pick_waves(p) == 8 ? launch_prefill_d<DT, 128, 8>(p, st) : launch_prefill_d<DT, 128, 4>(p, st);
+        case 256: return launch_prefill_d<DT, 256, 4>(p, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st) {

@@ -7,10 +7,11 @@ library has not been built.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
 PKG_DIR = pathlib.Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "_build" / "libgr_attn.so"
+LIB_PATH = pathlib.Path(os.environ.get("GR_ATTN_LIB") or PKG_DIR / "_build" / "libgr_attn.so")
 HEADER = PKG_DIR.parent / "include" / "gr_attn.h"
 
 GR_OK = 0

@@ -145,3 +145,24 @@ def test_prefill_window_one_returns_v(orc, dev):
     v = orc.upcast(vc[0], orc.F16).reshape(130, 2, 128)
     exp = np.repeat(v, 2, axis=1).reshape(130, -1)
     assert np.array_equal(got, exp)
+
+
+def test_prefill_eight_wave_blocks_f16(orc, dev):
+    """Launches with >= 256 (query head, block pair) items take 256-row workgroups of
+    8 waves: 64 Q / 8 KV heads over 2048 tokens (64 x 4 pairs) selects them."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=64, n_kv=8, d=128, fmt=orc.F16,
+                             seed=2048, rope_mode=ffi.ROPE_ADJACENT, theta=5e5)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)
+
+
+def test_prefill_eight_wave_blocks_window_chunked_bf16(orc, dev):
+    """8-wave workgroups with a sliding window and a continuation chunk (base_pos 700,
+    1348 tokens, 96 heads: 96 x 3 pairs), bf16 hi/lo path, ragged last block."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=96, n_kv=8, d=128, fmt=orc.BF16,
+                             seed=96, rope_mode=ffi.ROPE_NEOX, theta=1e4, window=300,
+                             base_chunks=[700, 1348])
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.BF16, orc)
