@@ -67,10 +67,17 @@ namespace {
 struct DecodePlan {
     int split_keys;
     int n_splits;
+    bool stream;  // stream schedule (see DecodeLaunch::stream_sched)
     size_t ws_o_bytes;
     size_t ws_ml_bytes;
-    size_t ws_q_bytes;  // Turbo: rotated / projected queries
+    size_t ws_q_bytes;      // Turbo: rotated / projected queries
+    size_t ws_sched_bytes;  // stream: pair offsets per sequence + range size
 };
+
+// Keys per workgroup range on the stream schedule never drop below this, which
+// bounds the partial slots per (sequence, head) by ceil(max_kv_len / 256) + 1.
+constexpr int kStreamMinKeys = 256;
+constexpr int kStreamMaxSeq = 1024;
 
 // Split size: aim for ~2048 (sequence, KV head, split) work units so the 256
 // CUs stay fed even when sequences are ragged; never below 64 keys.
@@ -78,6 +85,23 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     DecodePlan pl{};
     const int max_len = a->max_kv_len > 0 ? a->max_kv_len : 1;
     int split = a->split_keys;
+    // Automatic splitting on the MFMA path (16-bit and Q8 caches) uses the stream
+    // schedule: one workgroup per resident slot, equal key ranges, so ragged
+    // batches leave no tail.  Explicit split_keys keeps the fixed split grid.
+    const int kv_mul = a->n_kv_heads > 0 ? a->n_heads / a->n_kv_heads : 0;
+    pl.stream = split <= 0 &&
+                (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16 || a->kv_dtype == GR_DTYPE_Q8) &&
+                kv_mul >= 1 && kv_mul <= 16 && (a->head_dim == 128 || a->head_dim == 256) &&
+                a->n_seq <= kStreamMaxSeq && (int64_t)a->n_seq * max_len * a->n_kv_heads < (int64_t)1 << 30;
+    if (pl.stream) {
+        pl.split_keys = kStreamMinKeys;
+        pl.n_splits = (max_len + kStreamMinKeys - 1) / kStreamMinKeys + 1;
+        const size_t parts = (size_t)a->n_seq * a->n_heads * pl.n_splits;
+        pl.ws_o_bytes = align_up(parts * a->head_dim * sizeof(float), 256);
+        pl.ws_ml_bytes = align_up(parts * 2 * sizeof(float), 256);
+        pl.ws_sched_bytes = align_up((size_t)(a->n_seq + 1) * sizeof(int32_t), 256);
+        return pl;
+    }
     if (split <= 0) {
         const long pairs = (long)a->n_seq * a->n_kv_heads;
         long want = (2048 + pairs - 1) / pairs;
@@ -191,6 +215,10 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
     p.use_mfma = 1;
+    if (pl.stream) {
+        p.stream_sched = (int*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes);
+        p.stream_min_keys = kStreamMinKeys;
+    }
     if (a->kv_dtype == GR_DTYPE_Q8) {
         p.k_scale = a->k_scale;
         p.v_scale = a->v_scale;
@@ -219,7 +247,7 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
 size_t decode_ws_bytes(const gr_decode_args* a) {
     if (check_decode_shape_only(a)) return 0;
     const DecodePlan pl = plan_decode(a);
-    return pl.ws_o_bytes + pl.ws_ml_bytes + pl.ws_q_bytes;
+    return pl.ws_o_bytes + pl.ws_ml_bytes + pl.ws_q_bytes + pl.ws_sched_bytes;
 }
 
 int check_decode_shape_only(const gr_decode_args* a) {

@@ -213,7 +213,14 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     const int s = blockIdx.y;
     if (h >= p.n_heads) return;
     const int len = p.kv_end[s] - p.kv_start[s];
-    const int nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
+    int nv;
+    if (p.stream_sched) {  // ranges of stream_sched[n_seq] keys that meet pair (s, h / kv_mul)
+        const int q = p.stream_sched[p.n_seq];
+        const int off = p.stream_sched[s] + (h / (p.n_heads / p.n_kv_heads)) * len;
+        nv = len > 0 ? min(p.n_splits, (off + len - 1) / q - off / q + 1) : 0;
+    } else {
+        nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
+    }
     const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
     float* out = p.out + ((size_t)s * p.n_heads + h) * D;
     // pass 1: global max and denominator, lanes over splits

@@ -22,6 +22,7 @@
 //   block scales  one QK MFMA chain per 32-element block (an MFMA k-step is
 //                 exactly one block), scaled and summed; one P operand per
 //                 V block, scaled by that block's v scale.
+#include <algorithm>
 #include <type_traits>
 
 #include "gr_common.hpp"
@@ -91,6 +92,7 @@ struct KvQ8 {
 
 constexpr int kMdThreads = 256;
 constexpr int kMdWaves = kMdThreads / 64;
+constexpr int kStreamMaxSeq = 1024;  // sequences per launch on the stream schedule
 
 // Raise a row's reference maximum only when a tile exceeds it by more than
 // this (log2 units); P = 2^(s - m_ref) <= 2^8 meanwhile and O needs no rescale.
@@ -122,18 +124,95 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     constexpr int kMergeBytes = (kMdWaves * 16 * (D + 1) + 2 * kMdWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
-    const int split = blockIdx.x;
-    const int g = blockIdx.y;
-    const int s = blockIdx.z;
-    const int t_begin = p.kv_start[s] + split * p.split_keys;
-    const int t_limit = p.kv_end[s];
-    if (t_begin >= t_limit) return;
-    const int t_stop = min(t_limit, t_begin + p.split_keys);
     const int kv_mul = p.n_heads / p.n_kv_heads;
-
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
+
+    // Segment = keys [t_begin, t_stop) of sequence s, KV head g; its partial
+    // goes to slot `split` of the (s, head) partial rows.
+    int s, g, t_begin, t_stop, split;
+    // stream schedule state (DecodeLaunch::stream_sched)
+    __shared__ int st_len[kStreamMaxSeq];
+    __shared__ int st_off[kStreamMaxSeq];
+    __shared__ int st_first;
+    int st_q = 0, st_pos = 0, st_hi = 0;
+    if (!p.stream_sched) {
+        split = blockIdx.x;
+        g = blockIdx.y;
+        s = blockIdx.z;
+        t_begin = p.kv_start[s] + split * p.split_keys;
+        const int t_limit = p.kv_end[s];
+        if (t_begin >= t_limit) return;
+        t_stop = min(t_limit, t_begin + p.split_keys);
+    } else {
+        // Flattened key space: pair (s, g) occupies [off_s + g L_s, off_s + (g+1) L_s)
+        // with off_s = n_kv * sum_{s' < s} L_s'.  Workgroup b takes keys
+        // [b Q, (b+1) Q), Q = max(stream_min_keys, ceil(total / #workgroups))
+        // rounded up to 32.  Consecutive sequences per thread, block-wide scan.
+        const int n = p.n_seq;
+        constexpr int C = kStreamMaxSeq / kMdThreads;
+        int loc[C];
+        int tsum = 0;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const int q = tid * C + c;
+            const int len = q < n ? max(0, p.kv_end[q] - p.kv_start[q]) : 0;
+            loc[c] = tsum;
+            tsum += len * p.n_kv_heads;
+            if (q < n) st_len[q] = len;
+        }
+        // inclusive scan of tsum over the workgroup
+        int incl = tsum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        __shared__ int wsum[kMdWaves];
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int base = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < kMdWaves; w++) {
+            base += w < wave ? wsum[w] : 0;
+            total += wsum[w];
+        }
+        const int excl = base + incl - tsum;
+        st_q = max(p.stream_min_keys, (total + (int)gridDim.x - 1) / (int)gridDim.x);
+        st_q = (st_q + 31) / 32 * 32;
+        const int lo = (int)blockIdx.x * st_q;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            const int q = tid * C + c;
+            if (q < n) {
+                const int off = excl + loc[c];
+                st_off[q] = off;
+                if (blockIdx.x == 0) p.stream_sched[q] = off;
+                if (lo >= off && lo < off + st_len[q] * p.n_kv_heads) st_first = q;
+            }
+        }
+        if (blockIdx.x == 0 && tid == 0) p.stream_sched[n] = st_q;
+        if (lo >= total) return;
+        __syncthreads();
+        st_pos = lo;
+        st_hi = min(total, lo + st_q);
+        s = st_first;
+        g = (lo - st_off[s]) / st_len[s];
+        t_begin = t_stop = split = 0;  // set per segment below
+    }
+
+    for (;;) {
+    if (p.stream_sched) {
+        const int len = st_len[s];
+        const int off = st_off[s] + g * len;
+        const int seg_end = min(st_hi, off + len);
+        split = (int)blockIdx.x - off / st_q;
+        t_begin = p.kv_start[s] + (st_pos - off);
+        t_stop = p.kv_start[s] + (seg_end - off);
+        st_pos = seg_end;
+        __syncthreads();  // the previous segment is done with the LDS
+    }
     uint16_t* vt = (uint16_t*)smem + wave * D * VS;
     float* sct = (float*)(smem + kVtBytes) + wave * 2 * NB * TILE;  // block mode: [2][NB][TILE]
 
@@ -523,6 +602,7 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
             lt += sh_l[w][q] * a;
             ot += sh_o[w][q][i] * a;
         }
+        if (split >= n_splits) break;  // a sequence longer than max_kv_len: slots end here
         const size_t part = ((size_t)s * p.n_heads + (size_t)g * kv_mul + q) * n_splits + split;
         p.ws_o[part * D + i] = ot;
         if (i == 0) {
@@ -530,17 +610,46 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
             p.ws_ml[part * 2 + 1] = lt;
         }
     }
+    if (!p.stream_sched || st_pos >= st_hi) break;
+    if (++g == p.n_kv_heads) {  // next pair: skip empty sequences
+        g = 0;
+        do {
+            s++;
+        } while (st_len[s] == 0);
+    }
+    }
+}
+
+// Workgroups of kernel k that fit on the device at once (CUs x occupancy).
+template <typename KV, int D>
+static int resident_wgs() {
+    static int cached = 0;  // per template instance; same value for every device of a node
+    if (cached == 0) {
+        int dev = 0, n_cu = 0, occ = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_mfma_kernel<KV, D, 1>, kMdThreads, 0) !=
+                hipSuccess)
+            return 256;
+        cached = std::max(1, n_cu * std::max(1, occ));
+    }
+    return cached;
+}
+
+template <typename KV, int D>
+static hipError_t launch_mfma_kv_d(const DecodeLaunch& p, hipStream_t st) {
+    const dim3 grid = p.stream_sched ? dim3(resident_wgs<KV, D>()) : dim3(p.n_splits, p.n_kv_heads, p.n_seq);
+    decode_mfma_kernel<KV, D, 1><<<grid, kMdThreads, 0, st>>>(p);
+    return hipGetLastError();
 }
 
 template <typename KV>
 static hipError_t launch_mfma_kv(const DecodeLaunch& p, hipStream_t st) {
-    dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
     switch (p.head_dim) {
-        case 128: decode_mfma_kernel<KV, 128, 1><<<grid, kMdThreads, 0, st>>>(p); break;
-        case 256: decode_mfma_kernel<KV, 256, 1><<<grid, kMdThreads, 0, st>>>(p); break;
+        case 128: return launch_mfma_kv_d<KV, 128>(p, st);
+        case 256: return launch_mfma_kv_d<KV, 256>(p, st);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 bool decode_mfma_supported(const DecodeLaunch& p) {

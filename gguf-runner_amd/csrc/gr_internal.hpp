@@ -23,6 +23,15 @@ struct DecodeLaunch {
     float* ws_o;
     float* ws_ml;
     int use_mfma;  // 16-bit / Q8 caches: MFMA split kernel (decode_mfma.hip) instead of VALU
+    // Stream schedule (MFMA split kernel only): when set, the grid is one row of
+    // workgroups that cut the flattened (sequence, KV head, key) space into
+    // equal ranges of at least stream_min_keys keys; partial slot j of (s, head)
+    // comes from the j-th range that meets pair (s, head / kv_mul), n_splits
+    // bounds the slots.  stream_sched[0 .. n_seq) receives the pair offsets
+    // off_s of every sequence and stream_sched[n_seq] the range size, for the
+    // combine kernel.
+    int* stream_sched;
+    int stream_min_keys;
     // Q8 cache: scale of (seq slot, row t, kv head g, element i) at
     // slot*scale_seq_stride + t*scale_row_stride + (q8_block ? (g*head_dim + i)/32 : 0).
     const float* k_scale;

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
     const int64_t rs = p.cache_row_stride;
     const int rsb = (int)rs * 2;
 
-    // DMA: thread tid fills chunk position tid + 256 u of the tile: row
+    // DMA: thread tid fills chunk position tid + NW * 64 * u of the tile: row
     // tid / CPR + u * RPU, position tid % CPR, which holds chunk
     // (tid % CPR) ^ swz(row) of that cache row.
     int dma_off[LD];  // byte offsets from the tile's first row (full tiles)
