@@ -478,7 +478,8 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                        void* key_cache, void* value_cache, int fmt, int rope_dim, int neox,
                        const float* rope_freqs, float rope_scale, int is_gemma3, int online,
                        int64_t window, const float* q_norm, const float* k_norm, float eps,
-                       float* key_scale, float* value_scale, int n_threads) {
+                       float* key_scale, float* value_scale, int n_threads,
+                       const uint8_t* attend) {
     int q_dim = n_heads * head_size;
     int kv_dim = n_kv_heads * head_size;
     int half = rope_dim / 2;
@@ -517,6 +518,10 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                 store_kv(value_cache, (size_t)pos * kv_dim + j, fmt, v_in[(size_t)i * kv_dim + j]);
             }
         }
+        /* attend == NULL: every row; else only rows i with attend[i] != 0 (each
+         * row's attention reads the cache rows written so far and nothing else,
+         * so skipping one changes no other row) */
+        if (attend && !attend[i]) continue;
         int64_t s, e;
         orc_visible_keys(window, pos, &s, &e);
         orc_attention_token(q, xb_out + (size_t)i * q_dim, att, att_stride, n_heads, n_kv_heads,

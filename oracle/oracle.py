@@ -63,7 +63,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                       _sz, _f, _i, _i, _i]
     L.orc_visible_keys.argtypes = [_i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
     L.orc_prefill_layer.argtypes = [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _i, _i, _i, _p,
-                                    _f, _i, _i, _i64, _p, _p, _f, _p, _p, _i]
+                                    _f, _i, _i, _i64, _p, _p, _f, _p, _p, _i, _p]
     L.orc_deltanet_head_step.argtypes = [_p, _p, _p, _p, _p, _f, _f, _i]
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
@@ -185,10 +185,12 @@ def attention_token(q, key_cache, value_cache, fmt, n_heads, n_kv_heads, head_si
 def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope_dim, neox,
                   rope_freqs_tab, rope_scale, is_gemma3=False, online=False, window=0,
                   q_norm=None, k_norm=None, eps=1e-6, base_pos=0, key_cache=None,
-                  value_cache=None, n_threads=1):
+                  value_cache=None, n_threads=1, attend_rows=None):
     """Token-serial prefill of one layer (inference.rs:2981-3017), raw or Q8 KV.
     q [m][n_heads*d], k/v [m][n_kv_heads*d] f32.  Returns (xb [m][q_dim], kcache, vcache);
-    for fmt Q8 / Q8B the caches are (int8 rows, scales) pairs."""
+    for fmt Q8 / Q8B the caches are (int8 rows, scales) pairs.  attend_rows (indices into
+    the m rows) limits the attention to those rows; every row is still normed, rotated and
+    written to the cache in order, and the other xb rows stay 0."""
     q = _f32(q)
     k = _f32(k)
     v = _f32(v)
@@ -211,10 +213,15 @@ def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope
     freqs = _f32(rope_freqs_tab) if rope_freqs_tab is not None else None
     qn = _f32(q_norm) if q_norm is not None else None
     kn = _f32(k_norm) if k_norm is not None else None
+    att = None
+    if attend_rows is not None:
+        att = np.zeros(m, np.uint8)
+        att[np.asarray(attend_rows, dtype=np.int64)] = 1
     lib().orc_prefill_layer(_ptr(q), _ptr(k), _ptr(v), _ptr(xb), m, base_pos, n_heads, n_kv_heads,
                             head_size, _ptr(key_cache), _ptr(value_cache), fmt, rope_dim,
                             int(neox), _ptr(freqs), rope_scale, int(is_gemma3), int(online),
-                            window, _ptr(qn), _ptr(kn), eps, _ptr(ks), _ptr(vs), n_threads)
+                            window, _ptr(qn), _ptr(kn), eps, _ptr(ks), _ptr(vs), n_threads,
+                            _ptr(att))
     if q8:
         return xb, (key_cache, ks), (value_cache, vs)
     return xb, key_cache, value_cache

@@ -182,3 +182,23 @@ def test_prefill_layer_q8_writes_quantised_rows(orc, block):
             exp = _np_attention(qi[h * d:(h + 1) * d], Kd[:i + 1, g * d:(g + 1) * d],
                                 Vd[:i + 1, g * d:(g + 1) * d], 1.0 / np.sqrt(d))
             assert np.all(np.abs(xb[i, h * d:(h + 1) * d] - exp) <= _tol(exp))
+
+
+def test_prefill_attend_rows_matches_full_run(orc):
+    """attend_rows only skips the attention of the other rows: the sampled rows and the
+    caches are bit-identical to the full token-serial run, the rest of xb stays 0."""
+    rng = np.random.default_rng(7)
+    m, h, kvh, d = 40, 4, 2, 16
+    q = rng.standard_normal((m, h * d)).astype(np.float32)
+    k = rng.standard_normal((m, kvh * d)).astype(np.float32)
+    v = rng.standard_normal((m, kvh * d)).astype(np.float32)
+    kw = dict(n_heads=h, n_kv_heads=kvh, head_size=d, seq_len=m, fmt=orc.BF16, rope_dim=d,
+              neox=True, rope_freqs_tab=orc.rope_freqs(1e4, d), rope_scale=1.0, window=9,
+              q_norm=np.full(d, 1.1, np.float32), k_norm=np.full(d, 0.9, np.float32))
+    full, kc, vc = orc.prefill_layer(q, k, v, **kw)
+    rows = [0, 5, 8, 9, 39]
+    part, kc2, vc2 = orc.prefill_layer(q, k, v, attend_rows=rows, **kw)
+    assert np.array_equal(part[rows], full[rows])
+    assert np.array_equal(kc2, kc) and np.array_equal(vc2, vc)
+    others = np.setdiff1d(np.arange(m), rows)
+    assert not part[others].any()
