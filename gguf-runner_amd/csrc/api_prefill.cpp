@@ -112,6 +112,7 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pf.dtype = a->dtype;
     pf.base_pos = a->base_pos;
     pf.window = a->window;
+    pf.bidirectional = a->bidirectional ? 1 : 0;
     pf.q = pp.q_out;
     pf.q_lo = pp.q_out_lo;
     pf.k_cache = a->k_cache;

@@ -654,13 +654,14 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
 }
 
-int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
-                               const float* q, const float* k, const float* v, float* xb) {
-    clear_error();
-    int rc = check_layer(s, layer);
-    if (rc || (rc = check_pos(s, seq, base_pos, m))) return rc;
+// The rows base_pos..base_pos+m-1 of one layer: QK-norm, RoPE and KV write of
+// every row, then attention of every row over its visible keys; block = the rows
+// are one bidirectional image block (attention.rs:87-94), else causal.
+static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
+                        const float* q, const float* k, const float* v, float* xb, bool block) {
     if (m == 0) return GR_OK;
     if (!q || !k || !v || !xb) return fail(GR_ERR_ARG, "null buffer");
+    int rc = GR_OK;
     DeviceScope dsc(s->device);
     const size_t qb = 4 * (size_t)m * s->q_dim, kb = 4 * (size_t)m * s->kv_dim;
     const bool mfma = (s->cfg.kv_dtype == GR_DTYPE_F16 || s->cfg.kv_dtype == GR_DTYPE_BF16) &&
@@ -670,6 +671,10 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
     int max_len = 1;
     for (int i = 0; i < m; i++) {
         visible(s, layer, base_pos + i, &starts[i], &ends[i]);
+        if (block) {
+            starts[i] = std::min(starts[i], (int32_t)base_pos);
+            ends[i] = (int32_t)(base_pos + m);
+        }
         max_len = std::max(max_len, ends[i] - starts[i]);
     }
     gr_decode_args probe{};
@@ -718,6 +723,7 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
         a.cache_row_stride = s->kv_dim;
         a.out = xo;
         a.workspace = cv.take<char>(2 * qb);
+        a.bidirectional = block ? 1 : 0;
         if ((rc = prefill_enqueue_ex(&a, GR_DTYPE_F32, s->stream))) return rc;
     } else {
         float* qp = cv.take<float>((size_t)m * s->q_dim);
@@ -733,6 +739,25 @@ int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int6
         if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) return rc;
     }
     return d2h_sync(s, xb, xo, qb);
+}
+
+int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
+                               const float* q, const float* k, const float* v, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc || (rc = check_pos(s, seq, base_pos, m))) return rc;
+    return prefill_rows(s, seq, layer, base_pos, m, q, k, v, xb, false);
+}
+
+int gr_prefill_image_block(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
+                           const float* q, const float* k, const float* v, float* xb) {
+    clear_error();
+    int rc = check_layer(s, layer);
+    if (rc) return rc;
+    if (m <= 0 || base_pos < 0 || base_pos + m > s->cfg.seq_len)
+        return fail(GR_ERR_RANGE, "image-block prefill must evaluate one complete supported block within context");
+    if ((rc = check_pos(s, seq, base_pos, m))) return rc;
+    return prefill_rows(s, seq, layer, base_pos, m, q, k, v, xb, true);
 }
 
 int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32_t* seqs, const int64_t* pos,

@@ -184,6 +184,7 @@ struct PrefillLaunch {
     int n_tokens, n_heads, n_kv_heads, head_dim, dtype;
     int64_t base_pos;
     int window;
+    int bidirectional;  // the n_tokens rows form one image block (see gr_prefill_args)
     const void* q;
     const void* q_lo;
     const void* k_cache;

@@ -207,6 +207,18 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
         const bool wave_active = wr0 < m;
         const int wpos_min = P0 + (wave_active ? wr0 : m - 1);
         const int wpos_max = P0 + min(wr0 + 31, m - 1);
+        // Keys visible to the row at position pos: [row_lo(pos), row_hi(pos)].
+        // Causal: [pos + 1 - W (or 0), pos].  Bidirectional image block (the m
+        // rows are one block, LanguageAttentionPolicy::visible_keys,
+        // attention.rs:87-94): [min(pos + 1 - W (or 0), P0), P0 + m - 1].
+        // Both ends are non-decreasing in pos.
+        auto row_lo = [&](int pos) {
+            const int wl = W > 0 ? pos + 1 - W : 0;
+            return p.bidirectional ? min(wl, P0) : wl;
+        };
+        auto row_hi = [&](int pos) { return p.bidirectional ? P0 + m - 1 : pos; };
+        const int lo_min = row_lo(wpos_min), lo_max = row_lo(wpos_max);
+        const int hi_min = row_hi(wpos_min), hi_max = row_hi(wpos_max);
 
         // Q fragments (B operand): lane (query ln, group lg) holds d = 16 s + 8 lg .. +7.
         uint4 qf[D / 16];
@@ -223,8 +235,9 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
             }
         }
 
-        const int kend = P0 + min(q0 + BM, m);  // keys [0, kend) exist in the cache
-        const int kbeg = W > 0 ? max(0, P0 + q0 + 1 - W) : 0;
+        // keys [kbeg, kend) of the cache are visible to some row of this block
+        const int kend = p.bidirectional ? P0 + m : P0 + min(q0 + BM, m);
+        const int kbeg = max(0, row_lo(P0 + q0));
         const int t_first = kbeg / BN * BN;
         const int n_tiles = (kend - t_first + BN - 1) / BN;
 
@@ -308,11 +321,11 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
             }
 
             // element e of the accumulator is key ts + 8 (e/4) + 4 lg + e%4
-            const bool need_mask = (ts + 31 > wpos_min) || (W > 0 && ts < wpos_max + 1 - W);
+            const bool need_mask = (ts + 31 > hi_min) || (ts < lo_max);
             if (need_mask) {
-                // visible iff lo <= key <= my_pos: one unsigned compare per element
-                const int lo = W > 0 ? my_pos + 1 - W : 0;
-                const unsigned range = (unsigned)(my_pos - lo);
+                // visible iff lo <= key <= hi: one unsigned compare per element
+                const int lo = row_lo(my_pos);
+                const unsigned range = (unsigned)(row_hi(my_pos) - lo);
                 const int kb0 = ts + 4 * lg - lo;
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
 #pragma unroll
             for (int sb = 0; sb < BN / 32; sb++) {
                 const int ts = t0 + 32 * sb;
-                if (!(wave_active && ts <= wpos_max && (W <= 0 || ts + 31 >= wpos_min + 1 - W))) continue;
+                if (!(wave_active && ts <= hi_max && ts + 31 >= lo_min)) continue;
                 subtile(kb, vb, sb, ts);
             }
         };

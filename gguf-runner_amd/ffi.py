@@ -56,7 +56,7 @@ class PrefillArgs(ctypes.Structure):
         ("rope_dim", _i32), ("rope_scale", _f), ("rope_freqs", _p), ("q_norm", _p),
         ("k_norm", _p), ("norm_eps", _f), ("is_gemma3", _i32), ("q", _p), ("k", _p), ("v", _p),
         ("k_cache", _p), ("v_cache", _p), ("cache_row_stride", _i64), ("out", _p),
-        ("workspace", _p),
+        ("workspace", _p), ("bidirectional", _i32),
     ]
 
 
@@ -131,6 +131,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_attention_token.argtypes = [_p, _i32, _i32, _i64, _p, _p]
     L.gr_attention_layer_token.argtypes = [_p, _i32, _i32, _i64, _p, _p, _p, _p]
     L.gr_prefill_attention_chunk.argtypes = [_p, _i32, _i32, _i64, _i32, _p, _p, _p, _p]
+    L.gr_prefill_image_block.argtypes = [_p, _i32, _i32, _i64, _i32, _p, _p, _p, _p]
     L.gr_decode_layer_batch.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_qwen3next_state_step.argtypes = [_p, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_qwen3next_prefill.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
@@ -143,7 +144,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_write_ssm_conv_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
     for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
-              "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_decode_layer_batch",
+              "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_prefill_image_block",
+              "gr_decode_layer_batch",
               "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
               "gr_read_kv_scales", "gr_read_turbo_rows",
               "gr_read_ssm_state", "gr_write_ssm_state", "gr_qwen3next_ssm_layer",

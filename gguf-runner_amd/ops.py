@@ -166,7 +166,7 @@ class PrefillCall:
 
     def __init__(self, q, k, v, k_cache, v_cache, out, *, base_pos=0, window=0,
                  rope_mode=ffi.ROPE_NONE, rope_dim=0, rope_scale=1.0, rope_freqs=None,
-                 q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False):
+                 q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False, bidirectional=False):
         m, n_heads, d = q.shape
         _, n_kv, d2 = k.shape
         assert d2 == d and v.shape == k.shape and out.shape == (m, n_heads, d)
@@ -184,6 +184,7 @@ class PrefillCall:
         a.q_norm, a.k_norm = _ptr(q_norm), _ptr(k_norm)
         a.norm_eps = float(norm_eps)
         a.is_gemma3 = int(bool(is_gemma3))
+        a.bidirectional = int(bool(bidirectional))
         a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
         a.k_cache, a.v_cache = _ptr(k_cache), _ptr(v_cache)
         a.cache_row_stride = n_kv * d

@@ -175,6 +175,20 @@ def prefill_attention_chunk(p: Config, s: RunState, l: int, base_pos: int, q, k,
     return xb
 
 
+def prefill_image_block(p: Config, s: RunState, l: int, base_pos: int, q, k, v,
+                        seq: int = 0) -> np.ndarray:
+    """The attention of transformer_prefill_image_block (media_prefill.rs:15-124) for
+    one complete bidirectional image block at base_pos..base_pos+m-1; returns xb rows."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    m = q.shape[0]
+    xb = np.zeros((m, p.q_dim), np.float32)
+    ffi.check(ffi.lib().gr_prefill_image_block(s.handle, seq, l, base_pos, m, _p(q), _p(k),
+                                               _p(v), _p(xb)))
+    return xb
+
+
 def decode_layer_batch(p: Config, s: RunState, l: int, seqs, pos, q, k, v) -> np.ndarray:
     seqs = np.ascontiguousarray(seqs, np.int32)
     pos = np.ascontiguousarray(pos, np.int64)

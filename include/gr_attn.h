@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define GR_ATTN_ABI_VERSION 2
+#define GR_ATTN_ABI_VERSION 3
 
 /* Status codes. */
 #define GR_OK 0
@@ -155,6 +155,13 @@ typedef struct gr_prefill_args {
     int64_t cache_row_stride; /* elements between cache rows (>= n_kv_heads*head_dim) */
     float* out;           /* [m][n_heads][head_dim] f32 (s.xb rows) */
     void* workspace;      /* gr_prefill_workspace_size() bytes, 256-byte aligned */
+    int32_t bidirectional; /* 0: causal rows (visible_keys start..pos+1).  1: the m rows
+                            * are one complete image block under
+                            * ImageAttentionMode::Bidirectional: row pos sees
+                            * [min(start(pos), base_pos), base_pos + m) with start(pos) =
+                            * pos + 1 - window (saturating) or 0, i.e. every key of the
+                            * block plus its causal / window history
+                            * (LanguageAttentionPolicy::visible_keys, attention.rs:74-96). */
 } gr_prefill_args;
 
 size_t gr_prefill_workspace_size(const gr_prefill_args* a);
@@ -291,6 +298,16 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
 int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos,
                                int32_t m, const float* q, const float* k, const float* v,
                                float* xb);
+/* The attention of transformer_prefill_image_block (media_prefill.rs:15-124) for
+ * one complete image block under ImageAttentionMode::Bidirectional: the m rows
+ * at base_pos..base_pos+m-1 are normed, rotated and written to the cache first,
+ * then row pos attends to [min(start(pos), base_pos), base_pos + m) (every key of
+ * the block plus its causal / window history, attention.rs:87-94).  Same row
+ * layout as gr_prefill_attention_chunk.  Fails with "image-block prefill must
+ * evaluate one complete supported block within context" when the block does
+ * not fit the context (media_prefill.rs:31-39). */
+int gr_prefill_image_block(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
+                           const float* q, const float* k, const float* v, float* xb);
 /* One decode step for n sequences at once (one token each, sequence slot
  * seqs[b] at position pos[b]): the per-sequence calls of
  * layer_attention_token_staged batched into one launch. */

@@ -479,7 +479,7 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                        const float* rope_freqs, float rope_scale, int is_gemma3, int online,
                        int64_t window, const float* q_norm, const float* k_norm, float eps,
                        float* key_scale, float* value_scale, int n_threads,
-                       const uint8_t* attend) {
+                       const uint8_t* attend, int block) {
     int q_dim = n_heads * head_size;
     int kv_dim = n_kv_heads * head_size;
     int half = rope_dim / 2;
@@ -490,6 +490,11 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
     float* sn = (float*)malloc(sizeof(float) * (size_t)(half > 0 ? half : 1));
     size_t att_stride = (size_t)(base_pos + m);
     float* att = (float*)malloc(sizeof(float) * (size_t)n_heads * att_stride);
+    /* block: the m rows are one bidirectional image block
+     * (transformer_prefill_image_block, media_prefill.rs:84-121): every row is
+     * staged (norm, RoPE, KV write) first, its q kept, then each row attends to
+     * [min(start, base_pos), base_pos + m) (attention.rs:87-94) */
+    float* q_rows = block ? (float*)malloc(sizeof(float) * (size_t)m * q_dim) : NULL;
     for (int i = 0; i < m; i++) {
         int64_t pos = base_pos + i;
         memcpy(q, q_in + (size_t)i * q_dim, sizeof(float) * (size_t)q_dim);
@@ -518,6 +523,10 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                 store_kv(value_cache, (size_t)pos * kv_dim + j, fmt, v_in[(size_t)i * kv_dim + j]);
             }
         }
+        if (block) {
+            memcpy(q_rows + (size_t)i * q_dim, q, sizeof(float) * (size_t)q_dim);
+            continue;
+        }
         /* attend == NULL: every row; else only rows i with attend[i] != 0 (each
          * row's attention reads the cache rows written so far and nothing else,
          * so skipping one changes no other row) */
@@ -528,6 +537,17 @@ void orc_prefill_layer(const float* q_in, const float* k_in, const float* v_in, 
                             head_size, key_cache, value_cache, fmt, key_scale, value_scale, 0, (size_t)s,
                             (size_t)e, attn_scale, !is_gemma3, online, n_threads);
     }
+    for (int i = 0; block && i < m; i++) {
+        if (attend && !attend[i]) continue;
+        int64_t s, e;
+        orc_visible_keys(window, base_pos + i, &s, &e);
+        if (s > base_pos) s = base_pos;
+        e = base_pos + m;
+        orc_attention_token(q_rows + (size_t)i * q_dim, xb_out + (size_t)i * q_dim, att, att_stride, n_heads,
+                            n_kv_heads, head_size, key_cache, value_cache, fmt, key_scale, value_scale, 0,
+                            (size_t)s, (size_t)e, attn_scale, !is_gemma3, online, n_threads);
+    }
+    free(q_rows);
     free(q);
     free(k);
     free(cs);

@@ -63,7 +63,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                       _sz, _f, _i, _i, _i]
     L.orc_visible_keys.argtypes = [_i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
     L.orc_prefill_layer.argtypes = [_p, _p, _p, _p, _i, _i64, _i, _i, _i, _p, _p, _i, _i, _i, _p,
-                                    _f, _i, _i, _i64, _p, _p, _f, _p, _p, _i, _p]
+                                    _f, _i, _i, _i64, _p, _p, _f, _p, _p, _i, _p, _i]
     L.orc_deltanet_head_step.argtypes = [_p, _p, _p, _p, _p, _f, _f, _i]
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
@@ -185,12 +185,15 @@ def attention_token(q, key_cache, value_cache, fmt, n_heads, n_kv_heads, head_si
 def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope_dim, neox,
                   rope_freqs_tab, rope_scale, is_gemma3=False, online=False, window=0,
                   q_norm=None, k_norm=None, eps=1e-6, base_pos=0, key_cache=None,
-                  value_cache=None, n_threads=1, attend_rows=None):
+                  value_cache=None, n_threads=1, attend_rows=None, image_block=False):
     """Token-serial prefill of one layer (inference.rs:2981-3017), raw or Q8 KV.
     q [m][n_heads*d], k/v [m][n_kv_heads*d] f32.  Returns (xb [m][q_dim], kcache, vcache);
     for fmt Q8 / Q8B the caches are (int8 rows, scales) pairs.  attend_rows (indices into
     the m rows) limits the attention to those rows; every row is still normed, rotated and
-    written to the cache in order, and the other xb rows stay 0."""
+    written to the cache in order, and the other xb rows stay 0.  image_block: the m rows
+    are one bidirectional image block (transformer_prefill_image_block, media_prefill.rs:
+    84-121): all rows are staged first, then row pos attends to [min(start, base_pos),
+    base_pos + m) (attention.rs:87-94)."""
     q = _f32(q)
     k = _f32(k)
     v = _f32(v)
@@ -221,7 +224,7 @@ def prefill_layer(q, k, v, *, n_heads, n_kv_heads, head_size, seq_len, fmt, rope
                             head_size, _ptr(key_cache), _ptr(value_cache), fmt, rope_dim,
                             int(neox), _ptr(freqs), rope_scale, int(is_gemma3), int(online),
                             window, _ptr(qn), _ptr(kn), eps, _ptr(ks), _ptr(vs), n_threads,
-                            _ptr(att))
+                            _ptr(att), int(bool(image_block)))
     if q8:
         return xb, (key_cache, ks), (value_cache, vs)
     return xb, key_cache, value_cache

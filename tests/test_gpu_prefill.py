@@ -166,3 +166,69 @@ def test_prefill_eight_wave_blocks_window_chunked_bf16(orc, dev):
                              base_chunks=[700, 1348])
     _assert_close(got, ref)
     _assert_cache(kc, vc, orc.BF16, orc)
+
+
+def _image_block_case(orc, dev, *, hist, blk, n_heads, n_kv, d, fmt, seed, window, rope_mode,
+                      theta, sample=None):
+    """`hist` causal rows, then one bidirectional image block of `blk` rows (the
+    attention of transformer_prefill_image_block, media_prefill.rs:84-121)."""
+    from gguf_runner_amd import ffi, ops
+    rng = np.random.default_rng(seed)
+    n = hist + blk
+    qb = _bits(rng.standard_normal((n, n_heads, d), dtype=np.float32), fmt, orc)
+    kb = _bits(rng.standard_normal((n, n_kv, d), dtype=np.float32), fmt, orc)
+    vb = _bits(rng.standard_normal((n, n_kv, d), dtype=np.float32), fmt, orc)
+    freqs = orc.rope_freqs(theta, d)
+    rope_dim = 0 if rope_mode == ffi.ROPE_NONE else d
+    kw = dict(n_heads=n_heads, n_kv_heads=n_kv, head_size=d, seq_len=n, fmt=fmt, rope_dim=rope_dim,
+              neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs, rope_scale=1.0, window=window,
+              n_threads=orc.env_threads())
+    up = lambda x: orc.upcast(x, fmt).reshape(x.shape[0], -1)
+    _, kc_ref, vc_ref = orc.prefill_layer(up(qb[:hist]), up(kb[:hist]), up(vb[:hist]), **kw)
+    rows = None if sample is None else sample
+    ref, kc_ref, vc_ref = orc.prefill_layer(up(qb[hist:]), up(kb[hist:]), up(vb[hist:]),
+                                            base_pos=hist, key_cache=kc_ref, value_cache=vc_ref,
+                                            image_block=True, attend_rows=rows, **kw)
+    q, k, v = (_t16(x, fmt, orc, dev) for x in (qb, kb, vb))
+    kc = torch.zeros((n, n_kv, d), dtype=q.dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    fr = torch.tensor(ops.rope_freqs(theta, d), dtype=torch.float32, device=dev)
+    common = dict(window=window, rope_mode=rope_mode, rope_dim=rope_dim, rope_freqs=fr)
+    h_out = torch.empty((hist, n_heads, d), dtype=torch.float32, device=dev)
+    ops.PrefillCall(q[:hist].contiguous(), k[:hist].contiguous(), v[:hist].contiguous(), kc, vc,
+                    h_out, base_pos=0, **common)()
+    out = torch.empty((blk, n_heads, d), dtype=torch.float32, device=dev)
+    ops.PrefillCall(q[hist:].contiguous(), k[hist:].contiguous(), v[hist:].contiguous(), kc, vc,
+                    out, base_pos=hist, bidirectional=True, **common)()
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(blk, -1)
+    if sample is not None:
+        return got[sample], ref[sample]
+    return got, ref
+
+
+@pytest.mark.parametrize("d,fmt_name,window", [(128, "F16", 0), (128, "BF16", 64),
+                                               (256, "BF16", 96), (256, "F16", 0)])
+def test_prefill_image_block_bidirectional(orc, dev, d, fmt_name, window):
+    """bidirectional = 1: 150 causal history rows, then a 200-row image block whose rows see
+    every block key (later ones included) plus their causal / window history
+    [min(start(pos), base_pos), base_pos + m) (attention.rs:87-94).  Window 64 / 96 < block
+    length: late rows see the whole block but no history."""
+    from gguf_runner_amd import ffi
+    fmt = getattr(orc, fmt_name)
+    got, ref = _image_block_case(orc, dev, hist=150, blk=200, n_heads=8, n_kv=2, d=d, fmt=fmt,
+                                 seed=d + window, window=window, rope_mode=ffi.ROPE_NEOX, theta=1e4)
+    _assert_close(got, ref)
+
+
+def test_prefill_image_block_eight_wave_sampled(orc, dev):
+    """A 2048-row block with 64 Q heads takes the 8-wave workgroups (64 x 4 pairs);
+    checked on 40 sampled rows of the oracle's block attention."""
+    from gguf_runner_amd import ffi
+    rng = np.random.default_rng(99)
+    sample = np.unique(np.concatenate([[0, 1, 255, 256, 1023, 1024, 2046, 2047],
+                                       rng.integers(0, 2048, 32)]))
+    got, ref = _image_block_case(orc, dev, hist=100, blk=2048, n_heads=64, n_kv=8, d=128,
+                                 fmt=orc.F16, seed=7, window=0, rope_mode=ffi.ROPE_ADJACENT,
+                                 theta=5e5, sample=sample)
+    _assert_close(got, ref)

@@ -206,3 +206,41 @@ def test_qwen3next_prefill_matches_oracle_scan(dev, orc):
                                   eps=1e-6, n_threads=orc.env_threads())
     assert float(np.abs(out - ref).max()) <= TOL_F32
     assert float(np.abs(rt.read_ssm_state(p, s, 1) - Sref).max()) <= TOL_F32
+
+
+@pytest.mark.parametrize("kv_dtype", [1, 3])
+def test_prefill_image_block_runstate(dev, orc, kv_dtype):
+    """gr_prefill_image_block (transformer_prefill_image_block's attention) after 40 causal
+    rows: f16 cache (MFMA prefill kernel, bidirectional) and Q8 cache (codec write, then the
+    batched decode kernels over the block ranges) against the oracle."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, kv_dtype)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(5)
+    hist, blk, layer = 40, 70, 1
+    n = hist + blk
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    rt.prefill_attention_chunk(p, s, layer, 0, q[:hist], k[:hist], v[:hist])
+    got = rt.prefill_image_block(p, s, layer, hist, q[hist:], k[hist:], v[hist:])
+    fmt = orc.F16 if kv_dtype == ffi.DTYPE_F16 else orc.Q8
+    kw = dict(n_heads=16, n_kv_heads=8, head_size=128, seq_len=n, fmt=fmt, rope_dim=128,
+              neox=True, rope_freqs_tab=orc.rope_freqs(1e6, 128), rope_scale=1.0,
+              q_norm=p.q_norm[layer], k_norm=p.k_norm[layer], eps=1e-6, n_threads=orc.env_threads())
+    _, kc, vc = orc.prefill_layer(q[:hist], k[:hist], v[:hist], **kw)
+    ref, _, _ = orc.prefill_layer(q[hist:], k[hist:], v[hist:], base_pos=hist, key_cache=kc,
+                                  value_cache=vc, image_block=True, **kw)
+    err = np.abs(got - ref)
+    assert not (err > ATOL_16 + RTOL_16 * np.abs(ref)).any(), err.max()
+
+
+def test_prefill_image_block_outside_context_is_rejected(dev):
+    """media_prefill.rs:31-39: a block that does not fit the context is an error."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = _qwen3_config(rt, ffi, ffi.DTYPE_F16, seq_len=64)
+    s = rt.malloc_run_state(p)
+    z = np.zeros((10, p.q_dim), np.float32)
+    zk = np.zeros((10, p.kv_dim), np.float32)
+    with pytest.raises(ffi.GrError, match="image-block prefill must evaluate one complete"):
+        rt.prefill_image_block(p, s, 0, 60, z, zk, zk)

@@ -202,3 +202,36 @@ def test_prefill_attend_rows_matches_full_run(orc):
     assert np.array_equal(kc2, kc) and np.array_equal(vc2, vc)
     others = np.setdiff1d(np.arange(m), rows)
     assert not part[others].any()
+
+
+@pytest.mark.parametrize("window", [0, 8, 3])
+def test_image_block_visibility_closed_form(orc, window):
+    """Bidirectional image block (attention.rs:87-94, media_prefill.rs:84-121): 6 causal
+    history rows, then a 5-row block at base_pos 6.  Row pos of the block attends to
+    [min(start(pos), 6), 11) with start(pos) = pos + 1 - W (saturating) or 0: window 8
+    reaches the history (row 6 sees 0..11, row 10 sees 3..11), window 3 does not (row 10
+    sees the block only, row 6 sees 4..11), and every row sees the later block rows.
+    Checked against float64 softmax(q K^T / sqrt(d)) V over exactly those keys."""
+    rng = np.random.default_rng(11 + window)
+    h, kvh, d, hist, blk = 4, 2, 16, 6, 5
+    n = hist + blk
+    q = rng.standard_normal((n, h * d)).astype(np.float32)
+    k = rng.standard_normal((n, kvh * d)).astype(np.float32)
+    v = rng.standard_normal((n, kvh * d)).astype(np.float32)
+    kw = dict(n_heads=h, n_kv_heads=kvh, head_size=d, seq_len=n, fmt=orc.F32, rope_dim=0,
+              neox=False, rope_freqs_tab=None, rope_scale=1.0, window=window)
+    _, kc, vc = orc.prefill_layer(q[:hist], k[:hist], v[:hist], **kw)
+    out, kc, vc = orc.prefill_layer(q[hist:], k[hist:], v[hist:], base_pos=hist, key_cache=kc,
+                                    value_cache=vc, image_block=True, **kw)
+    K = kc.astype(np.float64).reshape(n, kvh, d)
+    V = vc.astype(np.float64).reshape(n, kvh, d)
+    for i in range(blk):
+        pos = hist + i
+        start = max(0, pos + 1 - window) if window > 0 else 0
+        lo, hi = min(start, hist), n
+        for hh in range(h):
+            g = hh // (h // kvh)
+            s = K[lo:hi, g] @ q[pos, hh * d:(hh + 1) * d].astype(np.float64) / np.sqrt(d)
+            p = np.exp(s - s.max())
+            ref = (p / p.sum()) @ V[lo:hi, g]
+            np.testing.assert_allclose(out[i, hh * d:(hh + 1) * d], ref, rtol=0, atol=2e-5)
