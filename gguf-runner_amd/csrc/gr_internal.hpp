@@ -195,6 +195,17 @@ struct PrefillLaunch {
 
 hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st);
 
+// Encoder self-attention (encoder.hip): rows [n_seq * tokens][heads * head_dim] f32.
+struct EncoderLaunch {
+    int n_seq, tokens, heads, head_dim;
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+};
+
+hipError_t launch_encoder_attention(const EncoderLaunch& p, hipStream_t st);
+
 // Gated DeltaNet.
 struct DeltaNetLaunch {
     int n_tokens, n_heads, head_dim, in_dtype, l2norm;

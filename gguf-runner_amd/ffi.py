@@ -131,6 +131,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_attention_token.argtypes = [_p, _i32, _i32, _i64, _p, _p]
     L.gr_attention_layer_token.argtypes = [_p, _i32, _i32, _i64, _p, _p, _p, _p]
     L.gr_prefill_attention_chunk.argtypes = [_p, _i32, _i32, _i64, _i32, _p, _p, _p, _p]
+    L.gr_encoder_self_attention.argtypes = [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _p]
     L.gr_prefill_image_block.argtypes = [_p, _i32, _i32, _i64, _i32, _p, _p, _p, _p]
     L.gr_decode_layer_batch.argtypes = [_p, _i32, _i32, _p, _p, _p, _p, _p, _p]
     L.gr_qwen3next_state_step.argtypes = [_p, _i32, _p, _p, _p, _p, _p, _p]

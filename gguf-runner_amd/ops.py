@@ -204,6 +204,19 @@ def prefill_attention(q, k, v, k_cache, v_cache, **kw):
     return out
 
 
+def encoder_self_attention(q, k, v, *, n_seq, tokens, heads, head_dim, out=None, stream=None):
+    """gr_encoder_self_attention (encoder_self_attention, multimodal/mod.rs:145-256):
+    f32 device rows [n_seq*tokens][heads*head_dim]; returns out of the same shape."""
+    for t in (q, k, v):
+        assert t.dtype == torch.float32 and t.is_contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    ffi.check(ffi.lib().gr_encoder_self_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), int(n_seq),
+                                                  int(tokens), int(heads), int(head_dim),
+                                                  _stream(stream)))
+    return out
+
+
 class DeltaNetCall:
     """A prepared gr_deltanet_attention call.
 

@@ -180,6 +180,19 @@ int gr_turbo_sign_table(int32_t n_layers, int32_t n_kv_heads, int32_t head_size,
 int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out);
 
 /* ======================================================================
+ * Encoder self-attention: encoder_self_attention (src/engine/multimodal/
+ * mod.rs:145-256), the attention of the vision / audio encoders.  q, k, v, out
+ * are device f32 rows [n_seq * tokens][heads * head_dim]; each token attends to
+ * every token of its own sequence (no mask, no cache), scores scaled by
+ * 1/sqrt(head_dim).  head_dim <= 128.  Sizes of 0 are a no-op, like the
+ * reference's required == 0 case; negative sizes fail with its "encoder
+ * attention shape mismatch" message.  Enqueued on `stream`, allocates nothing.
+ * ====================================================================== */
+int gr_encoder_self_attention(float* out, const float* q, const float* k, const float* v,
+                              int32_t n_seq, int32_t tokens, int32_t heads, int32_t head_dim,
+                              void* stream);
+
+/* ======================================================================
  * Gated DeltaNet linear attention (Qwen3-Next / Qwen3.5 SSM layers).
  * Per value head h and token t, with state S[h] (f32 [d][d], S[j][i]):
  *   S *= exp(gate); kv = S^T k; delta = beta (v - kv); S += k delta^T; o = S^T q

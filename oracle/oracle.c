@@ -1019,6 +1019,69 @@ void orc_deltanet_scan(const float* q, const float* k, const float* v, const flo
     }
 }
 
+/* ---------------------------------------------------------------- encoder attention */
+
+/* dot_f32_simd on x86 with AVX2+FMA (quant.rs:741-763 dot_f32_avx2_ptr, via the
+ * dispatch at 955-958): two 8-lane FMA accumulators over 16-element blocks, the
+ * lanes of their sum added left to right, then a tail of separate multiply and
+ * add. */
+static float dot_f32_avx2(const float* a, const float* b, int n) {
+    float acc0[8] = {0}, acc1[8] = {0};
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 8; l++) {
+            acc0[l] = fmaf(a[i + l], b[i + l], acc0[l]);
+            acc1[l] = fmaf(a[i + 8 + l], b[i + 8 + l], acc1[l]);
+        }
+    float sum = 0.0f;
+    for (int l = 0; l < 8; l++) sum += acc0[l] + acc1[l];
+    for (; i < n; i++) sum += a[i] * b[i];
+    return sum;
+}
+
+/* encoder_self_attention_portable (multimodal/mod.rs:206-256): for each token of
+ * each sequence and each head, an online softmax over the tokens of its own
+ * sequence in order: score = dot * (1/sqrt(d)); on a new maximum the output is
+ * rescaled by exp(old - new) when the running sum is positive; the weight
+ * exp(score - max) is added to the sum and weight * v to the output (axpy); at
+ * the end the output is multiplied by 1/sum.  Rows [token][heads * d].  The
+ * reference parallelises over tokens (par_chunks_mut). */
+void orc_encoder_self_attention(float* out, const float* q, const float* k, const float* v, int n_seq,
+                                int tokens, int heads, int d, int n_threads) {
+    const int dim = heads * d;
+    const float inv_scale = 1.0f / sqrtf((float)d);
+    const long total = (long)n_seq * tokens;
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+    for (long t = 0; t < total; t++) {
+        const long seq_start = (t / tokens) * tokens;
+        for (int h = 0; h < heads; h++) {
+            float* dst = out + t * dim + (long)h * d;
+            const float* qv = q + t * dim + (long)h * d;
+            for (int i = 0; i < d; i++) dst[i] = 0.0f;
+            float maximum = -INFINITY, sum = 0.0f;
+            for (int j = 0; j < tokens; j++) {
+                const long src = (seq_start + j) * dim + (long)h * d;
+                const float score = dot_f32_avx2(qv, k + src, d) * inv_scale;
+                if (score > maximum) {
+                    if (sum > 0.0f) {
+                        const float rescale = expf(maximum - score);
+                        for (int i = 0; i < d; i++) dst[i] *= rescale;
+                        sum *= rescale;
+                    }
+                    maximum = score;
+                }
+                const float w = expf(score - maximum);
+                sum += w;
+                axpy_inplace(dst, w, v + src, d);
+            }
+            if (sum > 0.0f) {
+                const float inv = 1.0f / sum;
+                for (int i = 0; i < d; i++) dst[i] *= inv;
+            }
+        }
+    }
+}
+
 int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -68,6 +68,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_deltanet_l2norm.argtypes = [_p, _p, _i, _f]
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
     L.orc_max_threads.restype = _i
+    L.orc_encoder_self_attention.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _i]
     L.orc_qwen3next_ssm_token.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p, _p, _p]
     L.orc_splitmix64.argtypes = [ctypes.c_uint64]
     L.orc_splitmix64.restype = ctypes.c_uint64
@@ -257,6 +258,16 @@ def deltanet_scan(q, k, v, gate, beta, state, *, l2norm=True, eps=1e-6, n_thread
 # ---- Turbo KV codec ----------------------------------------------------------
 
 TQ_ROT_PRE, TQ_ROT_POST, TQ_RES_PRE, TQ_RES_POST = 0, 1, 2, 3
+
+
+def encoder_self_attention(q, k, v, *, n_seq, tokens, heads, head_dim, n_threads=1):
+    """encoder_self_attention (multimodal/mod.rs:145-256): rows [n_seq*tokens][heads*head_dim]
+    f32; every token attends to all tokens of its own sequence."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros((n_seq * tokens, heads * head_dim), np.float32)
+    lib().orc_encoder_self_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), n_seq, tokens, heads,
+                                     head_dim, n_threads)
+    return out
 
 
 def splitmix64(x: int) -> int:

@@ -1,0 +1,78 @@
+"""Encoder self-attention (gr_encoder_self_attention = encoder_self_attention,
+reference src/engine/multimodal/mod.rs:145-256) against the oracle's restatement of
+encoder_self_attention_portable on identical f32 inputs.
+
+Tolerance of this fp32 path: |gpu - ref| <= 1e-5 * max(|ref|, 1) elementwise, the
+1e-5 fp32 bar in the form of the reference's own bound (2e-5 * max(|x|, 1),
+multimodal/mod.rs:724).  For outputs of magnitude <= 1 this is max-abs 1e-5; the
+reference fixture's outputs reach ~100, where one float
+ulp is already 7.6e-6, so an absolute 1e-5 would demand sub-2-ulp agreement there.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _within(got, ref, tol=TOL):
+    return bool(np.all(np.abs(got - ref) <= tol * np.maximum(np.abs(ref), 1.0)))
+
+
+def _run(dev, q, k, v, **shape):
+    from gguf_runner_amd import ops
+    t = [torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev) for x in (q, k, v)]
+    out = ops.encoder_self_attention(*t, **shape)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_encoder_attention_reference_fixture(orc, dev):
+    """The inputs of encoder_attention_matches_reference_and_isolates_sequences
+    (multimodal/mod.rs:656-738): 2 sequences x 3 tokens, 2 heads of dim 2; sequence 0's
+    outputs stay below 10 and sequence 1's above 90 (no attention across sequences)."""
+    ns, tps, hc, hd = 2, 3, 2, 2
+    dim = hc * hd
+    idx = np.arange(ns * tps * dim)
+    q = ((((idx * 7) % 19).astype(np.float32) - 9.0) * np.float32(0.125)).reshape(-1, dim)
+    k = ((((idx * 11) % 23).astype(np.float32) - 11.0) * np.float32(0.1)).reshape(-1, dim)
+    v = ((idx // (tps * dim)).astype(np.float32) * 100.0
+         + (idx % (tps * dim)).astype(np.float32) * np.float32(0.25)).reshape(-1, dim)
+    shape = dict(n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
+    got = _run(dev, q, k, v, **shape)
+    ref = orc.encoder_self_attention(q, k, v, **shape)
+    assert _within(got, ref), f"max abs {np.abs(got - ref).max():.3e}"
+    assert np.all(got[:tps] < 10.0) and np.all(got[tps:] > 90.0)
+
+
+@pytest.mark.parametrize("ns,tps,hc,hd", [(1, 1, 2, 64), (2, 17, 4, 72), (3, 300, 16, 80),
+                                          (1, 1025, 16, 64), (2, 256, 8, 128), (1, 100, 3, 20),
+                                          (1, 50, 2, 100)])
+def test_encoder_attention_matches_oracle(orc, dev, ns, tps, hc, hd):
+    """Sequences of 1 to 1025 tokens; head dims of the vision encoders (64, 72, 80) and
+    dims that run zero-padded (20 -> 32, 100 -> 128)."""
+    rng = np.random.default_rng(ns * 1000 + tps + hd)
+    q, k, v = (rng.standard_normal((ns * tps, hc * hd)).astype(np.float32) for _ in range(3))
+    shape = dict(n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
+    got = _run(dev, q, k, v, **shape)
+    ref = orc.encoder_self_attention(q, k, v, n_threads=orc.env_threads(), **shape)
+    assert _within(got, ref), f"max abs {np.abs(got - ref).max():.3e}"
+
+
+def test_encoder_attention_sizes(dev):
+    """A zero size is a no-op (the reference returns Ok for required == 0); negative sizes
+    and head_dim > 128 are errors with a message."""
+    from gguf_runner_amd import ffi
+    L = ffi.lib()
+    assert L.gr_encoder_self_attention(None, None, None, None, 0, 5, 2, 64, None) == 0
+    assert L.gr_encoder_self_attention(None, None, None, None, -1, 5, 2, 64, None) < 0
+    assert b"encoder attention shape mismatch" in ffi.lib().gr_last_error()
+    x = torch.zeros((4, 2 * 160), device=dev)
+    assert L.gr_encoder_self_attention(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                                       1, 4, 2, 160, None) < 0
+    assert b"head_dim 160 unsupported" in ffi.lib().gr_last_error()

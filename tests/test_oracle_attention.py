@@ -235,3 +235,57 @@ def test_image_block_visibility_closed_form(orc, window):
             p = np.exp(s - s.max())
             ref = (p / p.sum()) @ V[lo:hi, g]
             np.testing.assert_allclose(out[i, hh * d:(hh + 1) * d], ref, rtol=0, atol=2e-5)
+
+
+def _encoder_fixture():
+    """The inputs of encoder_attention_matches_reference_and_isolates_sequences
+    (multimodal/mod.rs:656-676): 2 sequences x 3 tokens, 2 heads of dim 2."""
+    ns, tps, hc, hd = 2, 3, 2, 2
+    dim = hc * hd
+    total = ns * tps
+    idx = np.arange(total * dim)
+    q = (((idx * 7) % 19).astype(np.float32) - 9.0) * np.float32(0.125)
+    k = (((idx * 11) % 23).astype(np.float32) - 11.0) * np.float32(0.1)
+    seq = idx // (tps * dim)
+    v = seq.astype(np.float32) * 100.0 + (idx % (tps * dim)).astype(np.float32) * np.float32(0.25)
+    return ns, tps, hc, hd, q.reshape(total, dim), k.reshape(total, dim), v.reshape(total, dim)
+
+
+def test_encoder_attention_reference_fixture(orc):
+    """The reference's own test (multimodal/mod.rs:656-738): the scalar two-pass softmax of
+    each (sequence, token, head) within 2e-5 * max(|x|, 1); sequence 0's outputs stay below
+    10 and sequence 1's above 90 (no attention across sequences)."""
+    ns, tps, hc, hd, q, k, v = _encoder_fixture()
+    got = orc.encoder_self_attention(q, k, v, n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
+    inv = np.float32(1.0) / np.sqrt(np.float32(hd))
+    want = np.zeros_like(got)
+    for s in range(ns):
+        for t in range(tps):
+            for h in range(hc):
+                qt = q[s * tps + t, h * hd:(h + 1) * hd]
+                sc = np.array([np.float32(sum(qt[i] * k[s * tps + j, h * hd + i] for i in range(hd)))
+                               * inv for j in range(tps)], np.float32)
+                w = np.exp(sc - sc.max())
+                for j in range(tps):
+                    want[s * tps + t, h * hd:(h + 1) * hd] += w[j] / w.sum() * v[s * tps + j, h * hd:(h + 1) * hd]
+    assert np.all(np.abs(got - want) <= 2e-5 * np.maximum(np.abs(want), 1.0))
+    assert np.all(got[:tps] < 10.0) and np.all(got[tps:] > 90.0)
+
+
+@pytest.mark.parametrize("hd", [64, 72, 80])
+def test_encoder_attention_float64_closed_form(orc, hd):
+    """softmax(q K^T / sqrt(d)) V per sequence in float64, with head dims that exercise the
+    16-wide FMA blocks and the scalar tail of the reference's dot (72, 80 are not
+    multiples of 16)."""
+    rng = np.random.default_rng(hd)
+    ns, tps, hc = 3, 17, 2
+    q, k, v = (rng.standard_normal((ns * tps, hc * hd)).astype(np.float32) for _ in range(3))
+    got = orc.encoder_self_attention(q, k, v, n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
+    for s in range(ns):
+        rows = slice(s * tps, (s + 1) * tps)
+        for h in range(hc):
+            cols = slice(h * hd, (h + 1) * hd)
+            sc = q[rows, cols].astype(np.float64) @ k[rows, cols].astype(np.float64).T / np.sqrt(hd)
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            ref = (p / p.sum(axis=1, keepdims=True)) @ v[rows, cols].astype(np.float64)
+            np.testing.assert_allclose(got[rows, cols], ref, rtol=0, atol=2e-5)
