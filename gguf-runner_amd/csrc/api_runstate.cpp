@@ -12,76 +12,24 @@
 #include "gr_api_util.hpp"
 #include "gr_attn.h"
 #include "gr_internal.hpp"
-
-struct gr_run_state {
-    gr_attn_config cfg{};
-    std::vector<int32_t> windows;      // [n_layers], 0 = global
-    std::vector<uint8_t> norm_present;  // [n_layers]
-    bool has_norm = false;
-    int device = 0;
-    int d = 0, kv_dim = 0, q_dim = 0, rope_dim = 0;
-    float eps = 1e-5f;
-    hipStream_t stream = nullptr;
-    void* k_cache = nullptr;
-    void* v_cache = nullptr;
-    size_t seq_stride = 0;    // elements between sequence slots
-    size_t layer_stride = 0;  // elements between layers
-    // Q8 cache: key_cache_scale / value_cache_scale, sc_per_row scales per row
-    // (1, or kv_dim/32 in block mode), same [layer][slot][row] order as the cache.
-    float* k_scale = nullptr;
-    float* v_scale = nullptr;
-    size_t sc_per_row = 0, sc_seq_stride = 0, sc_layer_stride = 0;
-    // Turbo cache: k_cache / v_cache hold the 2-bit codes (element e at byte e/4),
-    // k_sign / v_sign the residual sign bits (byte e/8), k_scale / v_scale sigma
-    // and k_rnorm / v_rnorm gamma with sc_per_row = n_kv_heads; the sign table
-    // (turboquant_build_sign_table) lives on the device.
-    uint8_t* k_sign = nullptr;
-    uint8_t* v_sign = nullptr;
-    float* k_rnorm = nullptr;
-    float* v_rnorm = nullptr;
-    uint8_t* turbo_table = nullptr;
-    float* freqs = nullptr;
-    float* freqs_swa = nullptr;
-    float* qn = nullptr;
-    float* kn = nullptr;
-    float* ssm = nullptr;
-    size_t ssm_layer = 0;  // floats per layer
-    // Qwen3.5 SSM layer weights and conv history (ssm_conv_state)
-    int ssm_conv_dim = 0;
-    float* ssm_conv_w = nullptr;  // [n_layers][conv_dim][K]
-    float* ssm_a = nullptr;       // [n_layers][n_v]
-    float* ssm_dt = nullptr;      // [n_layers][n_v]
-    float* ssm_nw = nullptr;      // [n_layers][head_dim]
-    float* ssm_hist = nullptr;    // [n_layers][K-1][conv_dim]
-    void* stage = nullptr;
-    size_t stage_bytes = 0;
-};
+#include "gr_runstate.hpp"
 
 namespace gr {
 
-namespace {
-
-int elem_bytes(int dt) { return dt == GR_DTYPE_F32 ? 4 : (dt == GR_DTYPE_Q8 ? 1 : 2); }
-
-bool is_turbo(const gr_run_state* s) { return s->cfg.kv_dtype == GR_DTYPE_TURBO; }
-
-// Byte offset of cache element `e` in the K/V storage (Turbo codes: 4 per byte).
-size_t cache_bytes_at(const gr_run_state* s, size_t e) {
-    return is_turbo(s) ? e / 4 : e * elem_bytes(s->cfg.kv_dtype);
+int h2d(gr_run_state* s, void* dst, const void* src, size_t bytes) {
+    if (!bytes) return GR_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "host to device copy");
 }
 
-// RAII: make the state's device current for the duration of a call.
-struct DeviceScope {
-    int prev = -1;
-    explicit DeviceScope(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
-    }
-    ~DeviceScope() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
+int d2h_sync(gr_run_state* s, void* dst, const void* src, size_t bytes) {
+    hipError_t e = bytes ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "device to host copy");
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
+}
+
+namespace {
 
 // Staging arena: grows (never shrinks) and is carved per call.
 struct Carve {
@@ -108,19 +56,6 @@ int ensure_stage(gr_run_state* s, size_t bytes) {
     if (e != hipSuccess) return fail(GR_ERR_OOM, "unable to allocate %zu bytes of device staging", want);
     s->stage_bytes = want;
     return GR_OK;
-}
-
-int h2d(gr_run_state* s, void* dst, const void* src, size_t bytes) {
-    if (!bytes) return GR_OK;
-    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream);
-    return e == hipSuccess ? GR_OK : hip_fail(e, "host to device copy");
-}
-
-int d2h_sync(gr_run_state* s, void* dst, const void* src, size_t bytes) {
-    hipError_t e = bytes ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream) : hipSuccess;
-    if (e != hipSuccess) return hip_fail(e, "device to host copy");
-    e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
 }
 
 // is_swa_layer, inference.rs:1821-1825.
@@ -158,8 +93,6 @@ int check_pos(const gr_run_state* s, int seq, int64_t pos, int64_t count) {
 
 void* layer_k(gr_run_state* s, int l) { return (char*)s->k_cache + cache_bytes_at(s, (size_t)l * s->layer_stride); }
 void* layer_v(gr_run_state* s, int l) { return (char*)s->v_cache + cache_bytes_at(s, (size_t)l * s->layer_stride); }
-
-bool is_q8(const gr_run_state* s) { return s->cfg.kv_dtype == GR_DTYPE_Q8; }
 
 // Extra staging bytes a K/V write of n rows needs (Q8 / Turbo: f32 rows before quantising).
 size_t q8_stage_bytes(const gr_run_state* s, size_t n) {

@@ -26,6 +26,7 @@ ROPE_NONE, ROPE_ADJACENT, ROPE_NEOX = 0, 1, 2
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
 _f = ctypes.c_float
 
 
@@ -144,13 +145,15 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_read_ssm_conv_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_conv_state.argtypes = [_p, _i32, _p]
     L.gr_write_ssm_state.argtypes = [_p, _i32, _p]
+    L.gr_prefill_cache_snapshot.argtypes = [_p, _i32, _p, _i32, _u64, _u64, _p, _u64, _p]
+    L.gr_prefill_cache_inject.argtypes = [_p, _i32, _p, _u64, _p]
     for n in ("gr_qkv_norm", "gr_apply_rope_qk", "gr_kv_write_token", "gr_attention_token",
               "gr_attention_layer_token", "gr_prefill_attention_chunk", "gr_prefill_image_block",
               "gr_decode_layer_batch",
               "gr_qwen3next_state_step", "gr_qwen3next_prefill", "gr_read_kv_rows",
               "gr_read_kv_scales", "gr_read_turbo_rows",
               "gr_read_ssm_state", "gr_write_ssm_state", "gr_qwen3next_ssm_layer",
-              "gr_read_ssm_conv_state", "gr_write_ssm_conv_state"):
+              "gr_read_ssm_conv_state", "gr_prefill_cache_snapshot", "gr_prefill_cache_inject", "gr_write_ssm_conv_state"):
         getattr(L, n).restype = ip
 
 

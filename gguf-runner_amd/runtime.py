@@ -290,3 +290,34 @@ def read_ssm_state(p: Config, s: RunState, l: int) -> np.ndarray:
 def write_ssm_state(p: Config, s: RunState, l: int, state) -> None:
     st = np.ascontiguousarray(state, np.float32)
     ffi.check(ffi.lib().gr_write_ssm_state(s.handle, l, _p(st)))
+
+
+def write_ssm_conv_state(p: Config, s: RunState, l: int, hist) -> None:
+    h = np.ascontiguousarray(hist, np.float32)
+    ffi.check(ffi.lib().gr_write_ssm_conv_state(s.handle, l, _p(h)))
+
+
+def snapshot(p: Config, s: RunState, tokens, model_len: int, model_head_fnv: int,
+             seq: int = 0) -> bytes:
+    """snapshot (src/app/prefill_cache.rs:178-310): the GPFC v1 blob of the first
+    len(tokens) cache rows of every layer plus the SSM arrays, read from the device."""
+    tok = np.ascontiguousarray(tokens, np.int32)
+    L = ffi.lib()
+    size = ctypes.c_uint64()
+    tp = _p(tok) if tok.size else None
+    ffi.check(L.gr_prefill_cache_snapshot(s.handle, seq, tp, tok.size, model_len, model_head_fnv,
+                                          None, 0, ctypes.byref(size)))
+    buf = np.zeros(size.value, np.uint8)
+    ffi.check(L.gr_prefill_cache_snapshot(s.handle, seq, tp, tok.size, model_len, model_head_fnv,
+                                          _p(buf), buf.size, ctypes.byref(size)))
+    return buf.tobytes()
+
+
+def inject(p: Config, s: RunState, blob: bytes, seq: int = 0) -> int:
+    """PrefixCache::parse + inject (prefill_cache.rs:316-352, 380-507) into the
+    device state; returns the number of cached prompt tokens."""
+    b = np.frombuffer(blob, np.uint8)
+    k = ctypes.c_int32()
+    ffi.check(ffi.lib().gr_prefill_cache_inject(s.handle, seq, b.ctypes.data if b.size else None,
+                                                b.size, ctypes.byref(k)))
+    return k.value

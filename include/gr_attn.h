@@ -370,6 +370,30 @@ int gr_read_turbo_rows(gr_run_state* s, int32_t layer, int32_t seq, int64_t row0
 int gr_read_ssm_state(gr_run_state* s, int32_t layer, float* out);
 int gr_write_ssm_state(gr_run_state* s, int32_t layer, const float* in);
 
+/* Prefill cache (GPFC v1, src/app/prefill_cache.rs:1-19).  snapshot
+ * (prefill_cache.rs:178-310): the blob of the first k rows of sequence slot
+ * `seq` in every layer (Q8 or Turbo cache sections), the SSM conv history and
+ * state of every layer, the k prompt tokens and the caller's model fingerprint
+ * (model_fingerprint, prefill_cache.rs:65-68).  The q8_block byte is
+ * cfg.q8_block_scales (the reference writes GGUF_Q8_BLOCK_SCALES for either
+ * format).  out == NULL: only *size_out (the blob's byte size) is set; else
+ * cap must hold the blob.  Errors: "prefill cache requires kv_dim % 8 == 0",
+ * a raw (F32/F16/BF16) cache, k > seq_len. */
+int gr_prefill_cache_snapshot(gr_run_state* s, int32_t seq, const int32_t* tokens, int32_t k,
+                              uint64_t model_len, uint64_t model_head_fnv, uint8_t* out,
+                              uint64_t cap, uint64_t* size_out);
+/* PrefixCache::parse + inject (prefill_cache.rs:316-352, 380-507): copies the
+ * blob's k rows into rows 0..k-1 of slot `seq` (re-strided to this state's
+ * seq_len) and its SSM arrays into the state; *k_out = k.  Same messages as the
+ * reference ("prefill cache truncated", "...: bad magic", "...: unsupported
+ * version N", "...: bad kv format N", "...: model/config mismatch", "...: prefix
+ * longer than context", "...: section size mismatch", "...: bad f32 section
+ * length", "...: ssm state size mismatch"); every check runs before the first
+ * copy, so a rejected blob leaves the state unchanged.  The prompt-token match
+ * (match_len, prefill_cache.rs:366-377) stays with the caller. */
+int gr_prefill_cache_inject(gr_run_state* s, int32_t seq, const uint8_t* blob, uint64_t len,
+                            int32_t* k_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -408,3 +408,19 @@ def upcast(bits, fmt) -> np.ndarray:
 
 def env_threads() -> int:
     return int(os.environ.get("ORACLE_THREADS", "0")) or max_threads()
+
+
+def _load_gpfc():
+    """oracle/gpfc.py (the GPFC prefill-cache restatement) as `gpfc`."""
+    import importlib.util
+    import sys
+    name = "gr_oracle_gpfc"
+    if name not in sys.modules:
+        spec = importlib.util.spec_from_file_location(name, HERE / "gpfc.py")
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[name] = mod
+        spec.loader.exec_module(mod)
+    return sys.modules[name]
+
+
+gpfc = _load_gpfc()
