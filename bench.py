@@ -5,7 +5,9 @@ Headline (`value`): split-K decode attention
 32 Q / 4 KV heads, head_dim 128, f16 KV cache), in GB/s of algorithmic KV bytes
   bytes/step = sum_b L_b * Hkv * d * 2 (K and V) * 2 B
 with every input already resident in HBM.  A step is one gr_decode_attention
-call (split kernel + combine kernel) over the whole batch.
+call (split kernel + combine kernel) over the whole batch.  Consecutive steps
+read different copies of the workload (at least 768 MB of other inputs between
+two reads of one copy), so no step is served from the 256 MB Infinity Cache.
 
 Also reported in the same line:
   decode_32k   -- the decode target run (all 16 sequences at 32768 keys)
@@ -58,6 +60,31 @@ def _timed(fn, steps, warmup, stream):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return ev0.elapsed_time(ev1) / steps, wall * 1e3 / steps  # ms per step (events, wall)
+
+
+# MI355X has a 256 MB Infinity Cache (MALL) in front of HBM.  Calling one
+# single-layer decode over and over would let it serve part of the KV cache
+# from the previous call, which a real decode step never sees (every other
+# layer's KV is read before the same layer comes round again).  Decode
+# workloads therefore cycle through enough independent copies that at least
+# ROTATE_BYTES of other inputs are read between two calls on the same copy.
+ROTATE_BYTES = 768 << 20
+
+
+def rotating(build, seed):
+    """build(seed) -> (call, bytes, keep); returns a call that cycles through
+    1 + ceil(ROTATE_BYTES / bytes) copies, the bytes of one call, and the copies."""
+    first = build(seed)
+    n = 1 + -(-ROTATE_BYTES // first[1])
+    copies = [first] + [build(seed + 1000 * i) for i in range(1, n)]
+    state = {"i": 0}
+
+    def call():
+        copies[state["i"]][0]()
+        state["i"] = (state["i"] + 1) % n
+
+    call.copies = n
+    return call, first[1], copies
 
 
 def measured_traffic(name="decode_mfma_f16_d128_config3.md"):
@@ -219,17 +246,17 @@ def run_one(args, dev, stream, lens) -> int:
     res = {"only": args.only, "steps": args.steps}
     if args.only in ("decode3", "decode32k"):
         ls = lens if args.only == "decode3" else [32768] * 16
-        call, nbytes, keep = decode_workload(dev, ls, 3)
+        call, nbytes, keep = rotating(lambda sd: decode_workload(dev, ls, sd), 3)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
     elif args.only == "decode32k_turbo":
-        call, nbytes, keep = decode_turbo_workload(dev, [32768] * 16, 35)
+        call, nbytes, keep = rotating(lambda sd: decode_turbo_workload(dev, [32768] * 16, sd), 35)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes,
                    f16_equiv_gbs=16 * 32768 * 4 * 128 * 4 / (ms * 1e-3) / 1e9)
     elif args.only in ("decode32k_q8", "decode32k_q8b"):
-        call, nbytes, keep = decode_q8_workload(dev, [32768] * 16, 34,
-                                                block=args.only.endswith("b"))
+        blk = args.only.endswith("b")
+        call, nbytes, keep = rotating(lambda sd: decode_q8_workload(dev, [32768] * 16, sd, block=blk), 34)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
     elif args.only in ("prefill2k", "prefill8k"):
@@ -286,25 +313,25 @@ def main() -> int:
         return run_one(args, dev, stream, lens)
 
     # headline: config 3 decode (ragged)
-    dcall, dbytes, _keep_d = decode_workload(dev, lens, 3)
+    dcall, dbytes, _keep_d = rotating(lambda sd: decode_workload(dev, lens, sd), 3)
     dec_ms, dec_wall = _timed(dcall, args.steps, args.warmup, stream)
     dec_gbs = dbytes / (dec_ms * 1e-3) / 1e9
     del _keep_d, dcall
 
     # decode target run: all sequences at 32768 keys
-    tcall, tbytes, _keep_t = decode_workload(dev, [32768] * 16, 33)
+    tcall, tbytes, _keep_t = rotating(lambda sd: decode_workload(dev, [32768] * 16, sd), 33)
     t_ms, _ = _timed(tcall, args.steps, args.warmup, stream)
     t_gbs = tbytes / (t_ms * 1e-3) / 1e9
     del _keep_t, tcall
 
     # the same target run over a Q8 cache (row scales, the reference's Q8 format)
-    qcall, qbytes, _keep_q = decode_q8_workload(dev, [32768] * 16, 34)
+    qcall, qbytes, _keep_q = rotating(lambda sd: decode_q8_workload(dev, [32768] * 16, sd), 34)
     q_ms, _ = _timed(qcall, args.steps, args.warmup, stream)
     q_gbs = qbytes / (q_ms * 1e-3) / 1e9
     del _keep_q, qcall
 
     # and over a Turbo cache (the reference's default KV format)
-    ucall, ubytes, _keep_u = decode_turbo_workload(dev, [32768] * 16, 35)
+    ucall, ubytes, _keep_u = rotating(lambda sd: decode_turbo_workload(dev, [32768] * 16, sd), 35)
     u_ms, _ = _timed(ucall, args.steps, args.warmup, stream)
     u_gbs = ubytes / (u_ms * 1e-3) / 1e9
     del _keep_u, ucall

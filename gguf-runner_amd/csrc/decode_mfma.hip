@@ -4,16 +4,17 @@
 // (sequence, KV head, split); partials merged by decode_combine_kernel), but
 // the scores and the value accumulation run on v_mfma_f32_16x16x32 with the
 // kv_mul (<= 16) query heads of a GQA group on the N axis:
-//   S^T[key][q]  = K . Q^T        A = K rows straight from HBM (16 B per lane)
+//   S^T[key][q]  = K . Q^T        A = K rows (16-bit caches: from a per-wave
+//                                 LDS tile; Q8: straight from HBM)
 //   O^T[d][q]   += V^T . P^T      A = V^T from a per-wave LDS tile, B = P from
 //                                 the S^T accumulators (same lane <-> query map)
 // Each wave streams its own 32-key tiles (keys split between the 4 waves of
-// the workgroup, next tile prefetched into registers while the current one is
-// processed) and keeps its own online-softmax state; the waves merge in LDS.
-// Q and P are carried as hi + lo 16-bit pairs (two MFMAs per product; K and V
-// are exact 16-bit cache values), so the scores and weights keep ~fp32
-// precision even for large unscaled logits.  Decode is HBM-bound with the
-// matrix cores mostly idle, so the second MFMA costs no time.
+// the workgroup, the next tile prefetched into registers while the current one
+// is processed) and keeps its own online-softmax state; the waves merge in LDS.
+// Q is carried as a hi + lo 16-bit pair (two MFMAs per product; K and V are
+// exact 16-bit cache values), so the scores keep ~fp32 precision even for
+// large unscaled logits; P is one operand for f16 caches and a hi + lo pair
+// for bf16 and Q8.  Decode is HBM-bound with the matrix cores mostly idle.
 //
 // Q8 caches (KvCacheFormat::Q8, reference inference.rs:1337-1483): int8 codes
 // are exact in f16, so K and V tiles are widened to f16 in registers and the
@@ -118,13 +119,18 @@ constexpr float kMdLazyRescale = 8.0f;
 
 // NSUB groups of 32 keys per wave iteration.  1 is used: with 2, the d128
 // kernel needs 300 registers (one wave per SIMD) and measured slower than two
-// waves per SIMD streaming 32-key tiles.
+// waves per SIMD streaming 32-key tiles.  bf16 d128 needs the bound to stay
+// within 256 registers (two waves per SIMD).
 template <typename KV, int D, int NSUB>
-__global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLaunch p) {
+__global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16>>::value ? 2 : 1)) void decode_mfma_kernel(const DecodeLaunch p) {
     using M = typename KV::M;
     using Raw = typename KV::Raw;
     constexpr bool kSplit = M::kSplit;
     constexpr bool kQ8 = KV::kQ8, kBlock = KV::kBlock;
+    // P (<= 2^8 after the lazy rescale) as one f16 operand for f16 caches
+    // (relative rounding 2^-12, against a bar of 2e-3 + 1e-2 |ref|); bf16 (2^-9)
+    // and Q8 (fp32-level bar) keep the hi + lo pair.
+    constexpr bool kSplitP = kSplit && (kQ8 || !std::is_same<M, Mfma16<F16>>::value);
     constexpr int NB = D / 32;                   // 32-element scale blocks per head (Q8 block mode)
     constexpr int TILE = 32 * NSUB;              // keys per wave iteration
     constexpr int NS16 = TILE / 16;              // 16-key score sub-tiles
@@ -138,7 +144,12 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     constexpr int kVtBytes = kMdWaves * D * VS * 2;
     // Q8 block mode: per-wave scale tile [K|V][block][32 keys] after the V^T tiles
     constexpr int kScBytes = kBlock ? kMdWaves * 2 * NB * TILE * 4 : 0;
-    constexpr int kLoopBytes = kVtBytes + kScBytes;
+    // 16-bit caches: per-wave K tile [TILE rows][DC chunks], 16-byte chunk c of
+    // row r at chunk c ^ (r & 15) (conflict-free for the row-slice writes and the
+    // 16-row MFMA operand reads)
+    constexpr bool kKLds = !kQ8;
+    constexpr int kKBytes = kKLds ? kMdWaves * TILE * D * 2 : 0;
+    constexpr int kLoopBytes = kVtBytes + kScBytes + kKBytes;
     constexpr int kMergeBytes = (kMdWaves * 16 * (D + 1) + 2 * kMdWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
@@ -233,6 +244,7 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     }
     uint16_t* vt = (uint16_t*)smem + wave * D * VS;
     float* sct = (float*)(smem + kVtBytes) + wave * 2 * NB * TILE;  // block mode: [2][NB][TILE]
+    uint4* kst = (uint4*)(smem + kVtBytes + kScBytes) + wave * TILE * DC;  // 16-bit: K tile
 
     // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
     // d = 32 ks + 8 g4 .. +7, pre-scaled to log2 units; queries >= kv_mul are 0.
@@ -305,7 +317,8 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     float ksc[NRS], vsc[NRS];
     float kbs[NBS], vbs[NBS];
 
-    Raw kr[NS16][KS];
+    Raw kr[kKLds ? 1 : NS16][KS];   // Q8: K in the MFMA operand layout
+    Raw krs[kKLds ? VTASK : 1][4];  // 16-bit: K rows in the V row-slice layout
     Raw vr[VTASK][4];
     auto load_scales = [&](int t0) {
         if constexpr (kBlock) {
@@ -354,6 +367,20 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
     };
     auto load_k = [&](int t0) {
         load_scales(t0);
+        if constexpr (kKLds) {  // row slices, like V
+            const bool whole = t0 + TILE <= t_stop;
+#pragma unroll
+            for (int u = 0; u < VTASK; u++) {
+                const int task = lane + 64 * u;
+                const int dc = task % DC, kg = task / DC;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int key = whole ? t0 + 4 * kg + r : min(t0 + 4 * kg + r, t_stop - 1);
+                    ld_stream(&krs[u][r], kc + (int64_t)key * rs + 8 * dc);
+                }
+            }
+            return;
+        }
         if (t0 + TILE <= t_stop) {
             const Elem* kt = kc + (int64_t)t0 * rs + 8 * g4;
 #pragma unroll
@@ -435,8 +462,24 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
             for (int b = 0; b < NB; b++) vbmax[b] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vl), b));
             __builtin_amdgcn_wave_barrier();
         }
-        // the V rows of this tile are in LDS: fetch the wave's next V tile
-        if (it + kMdWaves < n_tiles) load_v(t_begin + (it + kMdWaves) * TILE);
+        if constexpr (kKLds) {
+#pragma unroll
+            for (int u = 0; u < VTASK; u++) {
+                const int task = lane + 64 * u;
+                const int dc = task % DC, kg = task / DC;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = 4 * kg + r;
+                    kst[row * DC + (dc ^ (row & 15))] = krs[u][r];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // this tile's rows are in LDS: fetch the wave's next V (and 16-bit K) tile
+        if (it + kMdWaves < n_tiles) {
+            load_v(t_begin + (it + kMdWaves) * TILE);
+            if constexpr (kKLds) load_k(t_begin + (it + kMdWaves) * TILE);
+        }
         // scores for the 16-key sub-tiles
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
         f32x4 sacc[NS16];
@@ -444,7 +487,13 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         for (int sb = 0; sb < NS16; sb++) {
 #pragma unroll
             for (int k = 0; k < KS; k++) {
-                const uint4 ka = KV::to16(kr[sb][k]);
+                uint4 ka;
+                if constexpr (kKLds) {
+                    const int row = 16 * sb + l16;
+                    ka = kst[row * DC + ((4 * k + g4) ^ (row & 15))];
+                } else {
+                    ka = KV::to16(kr[sb][k]);
+                }
                 if constexpr (kBlock) {
                     // k-step k is scale block k: its own product, then scaled
                     f32x4 part = M::mma(ka, qf[k], zero);
@@ -471,8 +520,9 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         float vcur[NRS];
 #pragma unroll
         for (int e = 0; e < NRS; e++) vcur[e] = vsc[e];
-        // prefetch the K rows (and scales) of the wave's next tile
-        if (it + kMdWaves < n_tiles) load_k(t_begin + (it + kMdWaves) * TILE);
+        // Q8: prefetch the K rows (and scales) of the wave's next tile
+        if constexpr (!kKLds)
+            if (it + kMdWaves < n_tiles) load_k(t_begin + (it + kMdWaves) * TILE);
 
         // S^T register j of sub-tile sb holds key t0 + 16 sb + 4 g4 + j (query l16).
         float sv[4 * NS16];
@@ -561,11 +611,11 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
                     }
                     const uint16_t h0 = M::cvt(a0), h1 = M::cvt(a1);
                     ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                    if constexpr (kSplit)
+                    if constexpr (kSplitP)
                         pl[w] = (uint32_t)M::cvt(a0 - M::back(h0)) | ((uint32_t)M::cvt(a1 - M::back(h1)) << 16);
                 }
                 pf[kk] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-                if constexpr (kSplit) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+                if constexpr (kSplitP) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
             }
         };
         // LDS operations of one wave complete in issue order, so the V^T reads
@@ -574,7 +624,7 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
         constexpr int DTB = (D / 16) / NPB;    // 16-row output tiles per P operand
 #pragma unroll
         for (int pb = 0; pb < NPB; pb++) {
-            uint4 pf[NSUB], pfl[kSplit ? NSUB : 1];
+            uint4 pf[NSUB], pfl[kSplitP ? NSUB : 1];
             make_p(pb, pf, pfl);
 #pragma unroll
             for (int dd = 0; dd < DTB; dd++) {
@@ -586,11 +636,11 @@ __global__ __launch_bounds__(kMdThreads) void decode_mfma_kernel(const DecodeLau
                     const uint2 hi = *(const uint2*)(vrow + 32 * kk + 16);
                     const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
                     o[dt] = M::mma(a, pf[kk], o[dt]);
-                    if constexpr (kSplit) o[dt] = M::mma(a, pfl[kk], o[dt]);
+                    if constexpr (kSplitP) o[dt] = M::mma(a, pfl[kk], o[dt]);
                 }
             }
         }
-        __builtin_amdgcn_wave_barrier();  // V^T reads done before the next tile overwrites it
+        __builtin_amdgcn_wave_barrier();  // V^T / K reads done before the next tile overwrites them
     }
 
     if constexpr (kQ8) {

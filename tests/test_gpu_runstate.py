@@ -124,7 +124,9 @@ def test_chunked_prefill_equals_sequential(dev, orc, kv_dtype):
 
 
 def test_decode_layer_batch_equals_per_sequence(dev):
-    """One batched decode launch over 3 sequence slots == per-slot layer tokens."""
+    """One batched decode launch over 3 sequence slots == per-slot layer tokens, to the
+    f16 path's bar: the two launches split the keys differently, and the f16 kernel
+    rounds P = 2^(s - m) relative to a running maximum m that depends on the split."""
     from gguf_runner_amd import ffi, runtime as rt
     p = _qwen3_config(rt, ffi, ffi.DTYPE_F16, n_seq=3, seq_len=300)
     s_a = rt.malloc_run_state(p)
@@ -145,7 +147,8 @@ def test_decode_layer_batch_equals_per_sequence(dev):
     for seq, L in enumerate(lens):
         s_b.q[:], s_b.k[:], s_b.v[:] = qn[seq], kn[seq], vn[seq]
         rt.attention_layer_token(p, s_b, layer, L, seq=seq)
-        assert np.allclose(batch[seq], s_b.xb, atol=1e-6)
+        err = np.abs(batch[seq] - s_b.xb)
+        assert not (err > ATOL_16 + RTOL_16 * np.abs(s_b.xb)).any(), float(err.max())
 
 
 def test_errors_follow_reference_messages(dev):
