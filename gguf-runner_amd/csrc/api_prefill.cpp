@@ -54,9 +54,24 @@ size_t prefill_q_bytes(const gr_prefill_args* a) {
     return align_up((size_t)a->n_tokens * a->n_heads * a->head_dim * 2, 256);
 }
 
-// bf16 carries Q as hi + lo residual pairs (two staging buffers).
+// The attention kernel prepares Q itself (norm, RoPE, scale) for head_dim 128
+// when every RoPE pair stays inside a lane's fragments; the prep pass then
+// writes only K / V and each token's (cos, sin) table.
+bool prefill_fused_q(const gr_prefill_args* a) {
+    if (a->head_dim != 128) return false;
+    if (a->rope_mode == GR_ROPE_NEOX) return a->rope_dim % 32 == 0;
+    return true;
+}
+
+size_t prefill_cs_bytes(const gr_prefill_args* a) {
+    return a->rope_mode == GR_ROPE_NONE ? 0 : align_up((size_t)a->n_tokens * a->rope_dim * 4, 256);
+}
+
+// Staging: the (cos, sin) table when Q is fused, else the prepared Q (bf16 as
+// hi + lo residual pairs, two buffers).  Both layouts fit the larger size.
 size_t prefill_ws_total(const gr_prefill_args* a) {
-    return prefill_q_bytes(a) * (a->dtype == GR_DTYPE_BF16 ? 2 : 1);
+    const size_t staged = prefill_q_bytes(a) * (a->dtype == GR_DTYPE_BF16 ? 2 : 1);
+    return staged > prefill_cs_bytes(a) ? staged : prefill_cs_bytes(a);
 }
 
 }  // namespace
@@ -90,8 +105,10 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pp.v = a->v;
     pp.q_row_stride = (int64_t)a->n_heads * a->head_dim;
     pp.kv_row_stride = (int64_t)a->n_kv_heads * a->head_dim;
-    pp.q_out = a->workspace;
-    pp.q_out_lo = a->dtype == GR_DTYPE_BF16 ? (char*)a->workspace + prefill_q_bytes(a) : nullptr;
+    const bool fused = prefill_fused_q(a);
+    pp.q_out = fused ? nullptr : a->workspace;
+    pp.q_out_lo = !fused && a->dtype == GR_DTYPE_BF16 ? (char*)a->workspace + prefill_q_bytes(a) : nullptr;
+    pp.rope_cs_out = fused && a->rope_mode != GR_ROPE_NONE ? (float*)a->workspace : nullptr;
     pp.q_out_dtype = a->dtype;
     pp.q_out_scale = score_scale * 1.4426950408889634f;
     pp.k_cache = a->k_cache;
@@ -115,6 +132,18 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pf.bidirectional = a->bidirectional ? 1 : 0;
     pf.q = pp.q_out;
     pf.q_lo = pp.q_out_lo;
+    if (fused) {
+        pf.q_raw = a->q;
+        pf.q_in_dtype = in_dtype;
+        pf.q_row_stride = (int64_t)a->n_heads * a->head_dim;
+        pf.q_norm = a->q_norm;
+        pf.norm_eps = a->norm_eps;
+        pf.rope_mode = a->rope_mode;
+        pf.rope_dim = a->rope_dim;
+        pf.rope_cs = pp.rope_cs_out;
+        pf.q_pre_scale = a->is_gemma3 ? 1.0f / std::sqrt((float)a->head_dim) : 1.0f;
+        pf.q_scale = pp.q_out_scale;
+    }
     pf.k_cache = a->k_cache;
     pf.v_cache = a->v_cache;
     pf.cache_row_stride = a->cache_row_stride;

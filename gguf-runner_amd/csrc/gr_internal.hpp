@@ -89,6 +89,7 @@ struct QkvPrepLaunch {
     const int32_t* cache_seq;   // [n_tokens] sequence slot per token, or nullptr -> 0
     int64_t cache_row_stride;
     int cache_by_index;         // 1: token i's K/V go to row i of the cache (staging), slot 0
+    float* rope_cs_out;         // [n_tokens][rope_dim / 2][2] (cos, sin) of each token, or nullptr
 };
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);
@@ -185,8 +186,21 @@ struct PrefillLaunch {
     int64_t base_pos;
     int window;
     int bidirectional;  // the n_tokens rows form one image block (see gr_prefill_args)
-    const void* q;
-    const void* q_lo;
+    const void* q;      // prepared Q: 16-bit rows [n_tokens][n_heads][head_dim] x q scale
+    const void* q_lo;   // bf16: the residuals of q
+    // Fused Q preparation (head_dim 128, q_raw set; q / q_lo unused): raw Q rows
+    // (q_in_dtype, row stride q_row_stride elements) are QK-normed with q_norm
+    // (nullable, eps norm_eps), rotated with the token's (cos, sin) pairs
+    // rope_cs[token][rope_dim / 2] (rope_mode; NeoX needs rope_dim % 32 == 0),
+    // multiplied by q_pre_scale (Gemma3 1/sqrt(d), else 1) and then q_scale.
+    const void* q_raw;
+    int q_in_dtype;
+    int64_t q_row_stride;
+    const float* q_norm;
+    float norm_eps;
+    int rope_mode, rope_dim;
+    const float* rope_cs;
+    float q_pre_scale, q_scale;
     const void* k_cache;
     const void* v_cache;
     int64_t cache_row_stride;

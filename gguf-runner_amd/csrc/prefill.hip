@@ -15,7 +15,9 @@
 //                     B = P straight from the S^T accumulators)
 // so both accumulators hold one query per lane column and the online-softmax
 // statistics of a row live in the two lanes (l, l^32) that own it.
-// Q arrives prepared: RoPE'd / normed and multiplied by softmax_scale*log2(e).
+// For head_dim 128 the kernel prepares Q itself from the raw rows (QK RMSNorm,
+// RoPE from a per-token (cos, sin) table, softmax_scale*log2(e)); otherwise Q
+// arrives prepared that way by the prep pass.
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -115,6 +117,107 @@ __device__ __forceinline__ float pf_xmax32(float x) {
 __device__ __forceinline__ float pf_xsum32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Fused Q preparation (head_dim 128).  Lane (query row, half lg) owns the
+// elements d = 16 c + 8 lg .. +7 of its row, c = 0 .. D/16 - 1, i.e. exactly the
+// B-operand fragments qf[c]; the QK RMSNorm sum pairs up with lane l ^ 32, and
+// every RoPE pair stays inside the lane (adjacent pairs sit in one chunk; NeoX
+// pairs (d, d + rope_dim / 2) are chunks c and c + rope_dim / 32).  The
+// arithmetic follows qkv_prep_kernel expression for expression.
+__device__ __forceinline__ void pf_load8(const void* base, size_t idx, int dt, float* v) {
+    if (dt == GR_DTYPE_F32) {
+        const float4 a = *(const float4*)((const float*)base + idx);
+        const float4 b = *(const float4*)((const float*)base + idx + 4);
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        return;
+    }
+    const uint4 u = *(const uint4*)((const uint16_t*)base + idx);
+    if (dt == GR_DTYPE_F16) unpack16<F16>(u, v);
+    else unpack16<BF16>(u, v);
+}
+
+template <int CS, int NC>
+__device__ __forceinline__ void pf_rope_neox(float (&x)[NC][8], const float* cs, int lg) {
+#pragma unroll
+    for (int c = 0; c < CS; c++) {
+        const float4* t = (const float4*)(cs + 2 * (16 * c + 8 * lg));
+        float cv[8], sv[8];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float4 w = t[u];
+            cv[2 * u] = w.x, sv[2 * u] = w.y, cv[2 * u + 1] = w.z, sv[2 * u + 1] = w.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v0 = x[c][e], v1 = x[c + CS][e];
+            x[c][e] = v0 * cv[e] - v1 * sv[e];
+            x[c + CS][e] = v0 * sv[e] + v1 * cv[e];
+        }
+    }
+}
+
+template <typename DT, int D>
+__device__ __forceinline__ void pf_prepare_q(const PrefillLaunch& p, int row, int h, int lg, uint4* qf, uint4* qfl) {
+    constexpr int NC = D / 16;
+    float x[NC][8];
+    const size_t base = (size_t)row * p.q_row_stride + (size_t)h * D + 8 * lg;
+#pragma unroll
+    for (int c = 0; c < NC; c++) pf_load8(p.q_raw, base + 16 * c, p.q_in_dtype, x[c]);
+    if (p.q_norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss += x[c][e] * x[c][e];
+        ss = pf_xsum32(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)D + p.norm_eps);
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[c][e] = p.q_norm[16 * c + 8 * lg + e] * (inv * x[c][e]);
+    }
+    if (p.rope_mode == GR_ROPE_ADJACENT) {
+        const float* cs = p.rope_cs + (size_t)row * (p.rope_dim / 2) * 2;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const float4* t = (const float4*)(cs + 2 * (8 * c + 4 * lg));  // pairs (16 c + 8 lg) / 2 ..
+            const float4 w0 = t[0], w1 = t[1];
+            const float cv[4] = {w0.x, w0.z, w1.x, w1.z}, sv[4] = {w0.y, w0.w, w1.y, w1.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float v0 = x[c][2 * u], v1 = x[c][2 * u + 1];
+                x[c][2 * u] = v0 * cv[u] - v1 * sv[u];
+                x[c][2 * u + 1] = v0 * sv[u] + v1 * cv[u];
+            }
+        }
+    } else if (p.rope_mode == GR_ROPE_NEOX) {
+        const float* cs = p.rope_cs + (size_t)row * (p.rope_dim / 2) * 2;
+        switch (p.rope_dim / 32) {
+            case 1: pf_rope_neox<1>(x, cs, lg); break;
+            case 2: pf_rope_neox<2>(x, cs, lg); break;
+            case 3: pf_rope_neox<3>(x, cs, lg); break;
+            default: pf_rope_neox<NC / 2>(x, cs, lg); break;
+        }
+    }
+    using M = Mfma32<DT>;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        float xs[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) xs[e] = (x[c][e] * p.q_pre_scale) * p.q_scale;
+        uint32_t hw[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) hw[w] = M::pack2(xs[2 * w], xs[2 * w + 1]);
+        qf[c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        if constexpr (M::kSplit) {
+            uint32_t lw[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+                lw[w] = M::pack2(xs[2 * w] - __uint_as_float(hw[w] << 16), xs[2 * w + 1] - __uint_as_float(hw[w] & 0xffff0000u));
+            qfl[c] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+    }
 }
 
 template <typename DT, int D, int NW>
@@ -223,7 +326,14 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
         // Q fragments (B operand): lane (query ln, group lg) holds d = 16 s + 8 lg .. +7.
         uint4 qf[D / 16];
         uint4 qfl[kSplit ? D / 16 : 1];
-        {
+        bool q_done = false;
+        if constexpr (D == 128) {
+            if (p.q_raw) {
+                pf_prepare_q<DT, D>(p, my_row_c, h, lg, qf, qfl);
+                q_done = true;
+            }
+        }
+        if (!q_done) {
             const size_t qoff = ((size_t)my_row_c * p.n_heads + h) * D + 8 * lg;
             const uint16_t* qrow = (const uint16_t*)p.q + qoff;
 #pragma unroll

@@ -4,7 +4,9 @@
 //   Gemma3 q *= 1/sqrt(head_dim)    (inference.rs:1871-1873)
 //   kv_write_token, raw storage     (inference.rs:1877-1965: the row goes to the cache)
 // Q rows are written to a staging buffer (f32 for decode, or 16-bit already
-// multiplied by the softmax scale * log2(e) for the MFMA prefill kernel).
+// multiplied by the softmax scale * log2(e) for the MFMA prefill kernel), or
+// skipped, with each token's RoPE (cos, sin) pairs written out instead for a
+// consumer that prepares Q itself.
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -68,6 +70,7 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
             sincosf(val, &sn, &cs);
             cs_t[f] = cs;
             sn_t[f] = sn;
+            if (p.rope_cs_out) *(float2*)(p.rope_cs_out + ((size_t)i * half + f) * 2) = make_float2(cs, sn);
         }
     }
     __syncthreads();
@@ -75,7 +78,10 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
     const int64_t row = p.cache_by_index ? (int64_t)i : (p.cache_row ? (int64_t)p.cache_row[i] : pos);
     const int64_t sq = p.cache_by_index ? 0 : (p.cache_seq ? (int64_t)p.cache_seq[i] : 0);
 
-    for (int hr0 = wave * RPW; hr0 < rows_per_token; hr0 += kPrepRowsPerBlock * RPW) {
+    // Without a Q staging buffer the Q rows are left to the consumer (the MFMA
+    // prefill kernel prepares them itself from rope_cs_out).
+    const int row0 = p.q_out ? 0 : p.n_heads;
+    for (int hr0 = row0 + wave * RPW; hr0 < rows_per_token; hr0 += kPrepRowsPerBlock * RPW) {
         const int hr = hr0 + rsub;
         const bool valid = hr < rows_per_token;
         const int hrc = valid ? hr : rows_per_token - 1;

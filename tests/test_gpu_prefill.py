@@ -30,7 +30,7 @@ def _bits(x, fmt, orc):
 
 
 def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_scale=1.0,
-          window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6):
+          window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6, rope_dim=None):
     from gguf_runner_amd import ffi, ops
     rng = np.random.default_rng(seed)
     qb = _bits(rng.standard_normal((m, n_heads, d), dtype=np.float32), fmt, orc)
@@ -40,19 +40,20 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
     if norm:
         qn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
         kn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
-    freqs = orc.rope_freqs(theta, d)
+    rope_dim = d if rope_dim is None else rope_dim
+    freqs = orc.rope_freqs(theta, rope_dim)
     # oracle (token-serial, raw cache of the same 16-bit format)
     ref, kc_ref, vc_ref = orc.prefill_layer(
         orc.upcast(qb, fmt).reshape(m, -1), orc.upcast(kb, fmt).reshape(m, -1),
         orc.upcast(vb, fmt).reshape(m, -1), n_heads=n_heads, n_kv_heads=n_kv, head_size=d,
-        seq_len=m, fmt=fmt, rope_dim=(0 if rope_mode == ffi.ROPE_NONE else d), neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs,
+        seq_len=m, fmt=fmt, rope_dim=(0 if rope_mode == ffi.ROPE_NONE else rope_dim), neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs,
         rope_scale=rope_scale, is_gemma3=is_gemma3, window=window, q_norm=qn, k_norm=kn, eps=eps,
         n_threads=orc.env_threads())
     # GPU
     q, k, v = (_t16(x, fmt, orc, dev) for x in (qb, kb, vb))
     kc = torch.zeros((m, n_kv, d), dtype=q.dtype, device=dev)
     vc = torch.zeros_like(kc)
-    fr = torch.tensor(ops.rope_freqs(theta, d), dtype=torch.float32, device=dev)
+    fr = torch.tensor(ops.rope_freqs(theta, rope_dim), dtype=torch.float32, device=dev)
     qnt = torch.from_numpy(qn).to(dev) if norm else None
     knt = torch.from_numpy(kn).to(dev) if norm else None
     chunks = base_chunks or [m]
@@ -62,7 +63,7 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
         ops.PrefillCall(q[b:b + c].contiguous(), k[b:b + c].contiguous(), v[b:b + c].contiguous(),
                         kc, vc, out_view := torch.empty((c, n_heads, d), dtype=torch.float32,
                                                         device=dev),
-                        base_pos=b, window=window, rope_mode=rope_mode, rope_dim=d,
+                        base_pos=b, window=window, rope_mode=rope_mode, rope_dim=rope_dim,
                         rope_scale=rope_scale, rope_freqs=fr, q_norm=qnt, k_norm=knt,
                         norm_eps=eps, is_gemma3=is_gemma3)()
         out[b:b + c] = out_view
@@ -89,6 +90,22 @@ def _assert_cache(kc, vc, fmt, orc):
     ulp = 2.0 ** (-10 if fmt == orc.F16 else -7)
     assert np.all(np.abs(a - b) <= 2 * ulp * np.maximum(np.abs(b), 2.0 ** -14)), \
         f"K cache max diff {np.abs(a - b).max():.3e}"
+
+
+@pytest.mark.parametrize("rope_dim", [32, 64, 96, 40])
+@pytest.mark.parametrize("fmt_name", ["F16", "BF16"])
+def test_prefill_partial_neox_rope_with_qk_norm(orc, dev, rope_dim, fmt_name):
+    """Partial NeoX RoPE (apply_rope_qk's rope_dim < head_dim tail, inference.rs:1817-1874)
+    with QK-norm on d128: widths whose rotation pairs (i, i + rope_dim/2) stay inside a
+    lane's Q fragments (32 / 64 / 96, prepared inside the attention kernel) and one whose
+    pairs do not (40, prepared by the staging pass)."""
+    from gguf_runner_amd import ffi
+    fmt = getattr(orc, fmt_name)
+    got, ref, kc, vc = _case(orc, dev, m=300, n_heads=8, n_kv=2, d=128, fmt=fmt, seed=rope_dim,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6, norm=True, rope_dim=rope_dim,
+                             base_chunks=[100, 200])
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, fmt, orc)
 
 
 def test_config2_llama3_8b_prefill_f16(orc, dev):
