@@ -8,9 +8,12 @@
 //                                 LDS tile; Q8: straight from HBM)
 //   O^T[d][q]   += V^T . P^T      A = V^T from a per-wave LDS tile, B = P from
 //                                 the S^T accumulators (same lane <-> query map)
-// Each wave streams its own 32-key tiles (keys split between the 4 waves of
-// the workgroup, the next tile prefetched into registers while the current one
-// is processed) and keeps its own online-softmax state; the waves merge in LDS.
+// Each wave streams its own 32-key tiles (8 waves per workgroup for d128
+// without block scales, else 4; wave w starts with tile w and then, with 8
+// waves, claims the next unclaimed tile of its segment from an LDS counter,
+// with 4 takes tile w + 4, w + 8, ...; the next tile is
+// prefetched into registers while the current one is processed) and keeps its
+// own online-softmax state; the waves merge in LDS.
 // Q is carried as a hi + lo 16-bit pair (two MFMAs per product; K and V are
 // exact 16-bit cache values), so the scores keep ~fp32 precision even for
 // large unscaled logits; P is one operand for f16 caches and a hi + lo pair
@@ -109,8 +112,12 @@ __device__ __forceinline__ void ld_stream(uint2* r, const void* p) { *r = *(cons
 template <typename R>
 __device__ __forceinline__ void ld_plain(R* r, const void* p) { *r = *(const R*)p; }
 
-constexpr int kMdThreads = 256;
-constexpr int kMdWaves = kMdThreads / 64;
+// Waves per workgroup: 8 (one workgroup per CU, two waves per SIMD) where the
+// registers (<= 256) and the per-wave LDS tiles allow it, else 4.
+template <typename KV, int D>
+struct MdWaves {
+    static constexpr int value = D <= 128 && !KV::kBlock ? 8 : 4;
+};
 constexpr int kStreamMaxSeq = 1024;  // sequences per launch on the stream schedule
 
 // Raise a row's reference maximum only when a tile exceeds it by more than
@@ -122,7 +129,10 @@ constexpr float kMdLazyRescale = 8.0f;
 // waves per SIMD streaming 32-key tiles.  bf16 d128 needs the bound to stay
 // within 256 registers (two waves per SIMD).
 template <typename KV, int D, int NSUB>
-__global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16>>::value ? 2 : 1)) void decode_mfma_kernel(const DecodeLaunch p) {
+__global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
+                             (D <= 128 && std::is_same<KV, Kv16<BF16>>::value ? 2 : 1)) void decode_mfma_kernel(const DecodeLaunch p) {
+    constexpr int kMdWaves = MdWaves<KV, D>::value;
+    constexpr int kMdThreads = kMdWaves * 64;
     using M = typename KV::M;
     using Raw = typename KV::Raw;
     constexpr bool kSplit = M::kSplit;
@@ -165,6 +175,10 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
     __shared__ int st_len[kStreamMaxSeq];
     __shared__ int st_off[kStreamMaxSeq];
     __shared__ int st_first;
+    // Tiles of the current segment: wave w starts with tile w, then claims the
+    // next unclaimed one from this counter, so waves that get more issue slots
+    // (the older wave of a SIMD) take more tiles and the waves finish together.
+    __shared__ int tile_next;
     int st_q = 0, st_pos = 0, st_hi = 0;
     if (!p.stream_sched) {
         split = blockIdx.x;
@@ -231,6 +245,8 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
         t_begin = t_stop = split = 0;  // set per segment below
     }
 
+    if (tid == 0) tile_next = kMdWaves;
+    __syncthreads();
     for (;;) {
     if (p.stream_sched) {
         const int len = st_len[s];
@@ -420,7 +436,7 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
         load_k(t_begin + it * TILE);
         load_v(t_begin + it * TILE);
     }
-    for (; it < n_tiles; it += kMdWaves) {
+    while (it < n_tiles) {
         const int t0 = t_begin + it * TILE;
         // V tile -> LDS, transposed: Vt[d][key]
 #pragma unroll
@@ -475,10 +491,17 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
             }
             __builtin_amdgcn_wave_barrier();
         }
-        // this tile's rows are in LDS: fetch the wave's next V (and 16-bit K) tile
-        if (it + kMdWaves < n_tiles) {
-            load_v(t_begin + (it + kMdWaves) * TILE);
-            if constexpr (kKLds) load_k(t_begin + (it + kMdWaves) * TILE);
+        // this tile's rows are in LDS: claim the wave's next tile, fetch its V (and 16-bit K).
+        // Four-wave workgroups (one wave per SIMD) keep the fixed order it + 4: the
+        // claim's LDS round trip measured slower there.
+        int nxt = it + kMdWaves;
+        if constexpr (kMdWaves == 8) {
+            if (lane == 0) nxt = atomicAdd(&tile_next, 1);
+            nxt = __builtin_amdgcn_readfirstlane(nxt);
+        }
+        if (nxt < n_tiles) {
+            load_v(t_begin + nxt * TILE);
+            if constexpr (kKLds) load_k(t_begin + nxt * TILE);
         }
         // scores for the 16-key sub-tiles
         const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -522,7 +545,7 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
         for (int e = 0; e < NRS; e++) vcur[e] = vsc[e];
         // Q8: prefetch the K rows (and scales) of the wave's next tile
         if constexpr (!kKLds)
-            if (it + kMdWaves < n_tiles) load_k(t_begin + (it + kMdWaves) * TILE);
+            if (nxt < n_tiles) load_k(t_begin + nxt * TILE);
 
         // S^T register j of sub-tile sb holds key t0 + 16 sb + 4 g4 + j (query l16).
         float sv[4 * NS16];
@@ -641,6 +664,7 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
             }
         }
         __builtin_amdgcn_wave_barrier();  // V^T / K reads done before the next tile overwrites them
+        it = nxt;
     }
 
     if constexpr (kQ8) {
@@ -692,6 +716,7 @@ __global__ __launch_bounds__(kMdThreads, (D <= 128 && std::is_same<KV, Kv16<BF16
         }
     }
     if (!p.stream_sched || st_pos >= st_hi) break;
+    if (tid == 0) tile_next = kMdWaves;  // ordered before the next segment's claims by its barrier
     if (++g == p.n_kv_heads) {  // next pair: skip empty sequences
         g = 0;
         do {
@@ -709,7 +734,7 @@ static int resident_wgs() {
         int dev = 0, n_cu = 0, occ = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_mfma_kernel<KV, D, 1>, kMdThreads, 0) !=
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_mfma_kernel<KV, D, 1>, MdWaves<KV, D>::value * 64, 0) !=
                 hipSuccess)
             return 256;
         cached = std::max(1, n_cu * std::max(1, occ));
@@ -720,7 +745,7 @@ static int resident_wgs() {
 template <typename KV, int D>
 static hipError_t launch_mfma_kv_d(const DecodeLaunch& p, hipStream_t st) {
     const dim3 grid = p.stream_sched ? dim3(resident_wgs<KV, D>()) : dim3(p.n_splits, p.n_kv_heads, p.n_seq);
-    decode_mfma_kernel<KV, D, 1><<<grid, kMdThreads, 0, st>>>(p);
+    decode_mfma_kernel<KV, D, 1><<<grid, MdWaves<KV, D>::value * 64, 0, st>>>(p);
     return hipGetLastError();
 }
 
