@@ -223,6 +223,42 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     }
     const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
     float* out = p.out + ((size_t)s * p.n_heads + h) * D;
+    constexpr int EPL = D / 64;
+    // Few partials (the usual case): every lane loads all (m, l) pairs and its
+    // own o values at once and reduces them itself, one round trip to memory.
+    constexpr int kFewSplits = 16;
+    if (nv <= kFewSplits) {
+        float mk[kFewSplits], lk[kFewSplits], ok[kFewSplits][EPL];
+#pragma unroll
+        for (int k = 0; k < kFewSplits; k++) {
+            mk[k] = -INFINITY, lk[k] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) ok[k][e] = 0.0f;
+            if (k < nv) {
+                const float2 ml = *(const float2*)(p.ws_ml + (base + k) * 2);
+                mk[k] = ml.x, lk[k] = ml.y;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) ok[k][e] = p.ws_o[(base + k) * D + lane + 64 * e];
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kFewSplits; k++) mx = fmaxf(mx, mk[k]);
+        float lt = 0.0f, acc[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; e++) acc[e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kFewSplits; k++) {
+            const float w = mk[k] == -INFINITY ? 0.0f : exp2f(mk[k] - mx);
+            lt += lk[k] * w;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[e] += ok[k][e] * w;
+        }
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) out[lane + 64 * e] = acc[e] * inv;
+        return;
+    }
     // pass 1: global max and denominator, lanes over splits
     float mx = -INFINITY;
     for (int k = lane; k < nv; k += 64) mx = fmaxf(mx, p.ws_ml[(base + k) * 2]);
@@ -235,7 +271,6 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     lt = wave_sum<64>(lt);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     // pass 2: weighted sum of o, lanes over dimensions; weights staged per 64 splits
-    constexpr int EPL = D / 64;
     float acc[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; e++) acc[e] = 0.0f;
