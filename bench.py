@@ -1,6 +1,6 @@
 """Benchmark of the attention hot path on one MI355X (prints ONE JSON line).
 
-Headline (`value`): split-K decode attention
+Headline (`value`): split-K decode attention, configuration 3 of the benchmark set
 (Qwen3-30B-A3B-shaped: 16 sequences with ragged cached lengths U[1024, 32768],
 32 Q / 4 KV heads, head_dim 128, f16 KV cache), in GB/s of algorithmic KV bytes
   bytes/step = sum_b L_b * Hkv * d * 2 (K and V) * 2 B
@@ -295,7 +295,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the attention path shards without communication (see DESIGN.md), "
+              "the attention path shards over heads and sequences without communication, "
               "so no multi-GPU figure is produced", file=sys.stderr)
         return 2
 
