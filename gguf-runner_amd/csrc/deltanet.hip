@@ -17,8 +17,7 @@
 //    parallel; deltanet_chunk_scan_kernel carries S across chunks with the
 //    state columns split over blocks of 4 (512 workgroups for 16 heads, two per
 //    CU: the chunk steps are sequential and latency-bound, so more, smaller
-//    blocks run faster even though each re-reads the chunk's W / Qg / P / Kd^T:
-//    4096 tokens x 16 heads, 16 columns per block 1.29 ms, 8 0.82 ms, 4 0.73 ms).
+//    blocks run faster even though each re-reads the chunk's W / Qg / P / Kd^T).
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -310,50 +309,57 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(cons
     const int ic = (tid & 1) * (NC / 2);
     for (int c = 0; c < n_chunks; c++) {
         const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
-        // A: Delta[t][i] = U[t][i] - sum_j W[t][j] S[j][i]
+        // phase C's row of Kd^T and gamma_last, requested now so that they arrive
+        // during phases A and B
+        float4 kd[C / 4];
+        {
+            const float* kr = ws + ChunkWs<D>::KDT + jc * C;
+#pragma unroll
+            for (int u = 0; u < C / 4; u++) kd[u] = *(const float4*)(kr + 4 * u);
+        }
+        const float gl = ws[ChunkWs<D>::GL];
+        // A: Delta[t][i] = U[t][i] - sum_j W[t][j] S[j][i], and the first part of
+        //    O[t][i], sum_j Qg[t][j] S[j][i], in the same pass over S
+        float acc_o = 0.0f;
         {
             float acc = ws[ChunkWs<D>::U + ta * D + c0 + ia];
             const float* wr = ws + ChunkWs<D>::W + ta * D;
+            const float* qr = ws + ChunkWs<D>::QG + ta * D;
             for (int j = 0; j < D; j += 4) {
                 const float4 w4 = *(const float4*)(wr + j);
-                acc = fmaf(-w4.x, Ss[j][ia], acc);
-                acc = fmaf(-w4.y, Ss[j + 1][ia], acc);
-                acc = fmaf(-w4.z, Ss[j + 2][ia], acc);
-                acc = fmaf(-w4.w, Ss[j + 3][ia], acc);
+                const float4 q4 = *(const float4*)(qr + j);
+                const float s0 = Ss[j][ia], s1 = Ss[j + 1][ia], s2 = Ss[j + 2][ia], s3 = Ss[j + 3][ia];
+                acc = fmaf(-w4.x, s0, acc);
+                acc = fmaf(-w4.y, s1, acc);
+                acc = fmaf(-w4.z, s2, acc);
+                acc = fmaf(-w4.w, s3, acc);
+                acc_o = fmaf(q4.x, s0, acc_o);
+                acc_o = fmaf(q4.y, s1, acc_o);
+                acc_o = fmaf(q4.z, s2, acc_o);
+                acc_o = fmaf(q4.w, s3, acc_o);
             }
             Dl[ta][ia] = acc;
         }
         __syncthreads();
-        // B: O[t][i] = sum_j Qg[t][j] S[j][i] + sum_{s<=t} P[t][s] Delta[s][i]
+        // B: O[t][i] += sum_{s<=t} P[t][s] Delta[s][i]
         {
-            float acc = 0.0f;
-            const float* qr = ws + ChunkWs<D>::QG + ta * D;
-            for (int j = 0; j < D; j += 4) {
-                const float4 q4 = *(const float4*)(qr + j);
-                acc = fmaf(q4.x, Ss[j][ia], acc);
-                acc = fmaf(q4.y, Ss[j + 1][ia], acc);
-                acc = fmaf(q4.z, Ss[j + 2][ia], acc);
-                acc = fmaf(q4.w, Ss[j + 3][ia], acc);
-            }
             const float* pr = ws + ChunkWs<D>::P + ta * C;
-            for (int s = 0; s <= ta; s++) acc = fmaf(pr[s], Dl[s][ia], acc);
+            for (int s = 0; s <= ta; s++) acc_o = fmaf(pr[s], Dl[s][ia], acc_o);
             const int t = c * C + ta;
-            if (t < p.n_tokens) p.out[((size_t)t * H + h) * D + c0 + ia] = finite_or_zero(acc);
+            if (t < p.n_tokens) p.out[((size_t)t * H + h) * D + c0 + ia] = finite_or_zero(acc_o);
         }
         // C: S'[j][i] = gamma_last S[j][i] + sum_s KdT[j][s] Delta[s][i]
         float nv[NC / 2];
         {
-            const float gl = ws[ChunkWs<D>::GL];
 #pragma unroll
             for (int u = 0; u < NC / 2; u++) nv[u] = gl * Ss[jc][ic + u];
-            const float* kr = ws + ChunkWs<D>::KDT + jc * C;
-            for (int s = 0; s < C; s += 4) {
-                const float4 k4 = *(const float4*)(kr + s);
-                const float kv[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+            for (int q = 0; q < C / 4; q++) {
+                const float kv[4] = {kd[q].x, kd[q].y, kd[q].z, kd[q].w};
 #pragma unroll
                 for (int w = 0; w < 4; w++)
 #pragma unroll
-                    for (int u = 0; u < NC / 2; u++) nv[u] = fmaf(kv[w], Dl[s + w][ic + u], nv[u]);
+                    for (int u = 0; u < NC / 2; u++) nv[u] = fmaf(kv[w], Dl[4 * q + w][ic + u], nv[u]);
             }
         }
         __syncthreads();  // every read of Ss / Dl for this chunk is done
