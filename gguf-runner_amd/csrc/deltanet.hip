@@ -150,6 +150,7 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     double* lg = (double*)(As + C * AS);
     float* bt = (float*)(lg + C);       // [C] beta
     float* gm = bt + C;                 // [C] gamma_t = exp(lg[t])
+    float* kf = gm + C;                 // [C] gamma_last / gamma_s = exp(lg[C-1] - lg[s])
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int c = blockIdx.x, h = blockIdx.y;
@@ -196,6 +197,8 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
         }
         lg[lane] = gl;
         gm[lane] = expf((float)gl);
+        const double gl_last = __shfl(gl, 63, 64);
+        kf[lane] = expf((float)(gl_last - gl));
         bt[lane] = valid ? finite_or_zero(p.beta[(size_t)(t0 + lane) * H + h]) : 0.0f;
     }
     __syncthreads();
@@ -237,49 +240,36 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
     }
     for (int e = tid; e < D * C; e += kChunkThreads) {
         const int j = e / C, s2 = e % C;
-        ws[ChunkWs<D>::KDT + e] = expf((float)(lglast - lg[s2])) * ks[s2 * DS + j];
+        ws[ChunkWs<D>::KDT + e] = kf[s2] * ks[s2 * DS + j];
     }
 
-    // 4. [U | W] = (I + A)^-1 [beta V | beta gamma K] by blocked forward
-    //    substitution, one right-hand-side column per thread: 4 blocks of 16 rows;
-    //    block b first subtracts A[b][b'] X[b'] for the earlier blocks (read back
-    //    from this thread's own column of the workspace), then solves its unit
-    //    lower-triangular 16x16 diagonal block in registers.
-    constexpr int RB = 16;
+    // 4. [U | W] = (I + A)^-1 [beta V | beta gamma K] by forward substitution,
+    //    one right-hand-side column per thread, the whole column in registers:
+    //    x[t] -= A[t][s] x[s] for s = 0 .. t-1 in order.
     for (int col = tid; col < 2 * D; col += kChunkThreads) {
         const bool isv = col < D;
         const int cc = isv ? col : col - D;
         float* dst = ws + (isv ? ChunkWs<D>::U : ChunkWs<D>::W);
+        float x[C];
 #pragma unroll
-        for (int b = 0; b < C / RB; b++) {
-            float x[RB];
+        for (int t = 0; t < C; t++)
+            x[t] = isv ? (t < Cn ? bt[t] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + t) * H + h) * D + cc, p.in_dtype))
+                                 : 0.0f)
+                       : bt[t] * gm[t] * ks[t * DS + cc];
 #pragma unroll
-            for (int tt = 0; tt < RB; tt++) {
-                const int t = b * RB + tt;
-                x[tt] = isv ? (t < Cn ? bt[t] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + t) * H + h) * D + cc, p.in_dtype))
-                                      : 0.0f)
-                            : bt[t] * gm[t] * ks[t * DS + cc];
+        for (int t = 1; t < C; t++) {
+            const float* arow = As + t * AS;
+#pragma unroll
+            for (int s4 = 0; s4 < t; s4 += 4) {
+                const float4 a4 = *(const float4*)(arow + s4);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (s4 + k < t) x[t] = fmaf(-av[k], x[s4 + k], x[t]);
             }
-            for (int bp = 0; bp < b; bp++) {
-                float xp[RB];
-#pragma unroll
-                for (int ss = 0; ss < RB; ss++) xp[ss] = dst[(bp * RB + ss) * D + cc];
-#pragma unroll
-                for (int tt = 0; tt < RB; tt++) {
-                    const float* arow = As + (b * RB + tt) * AS + bp * RB;
-#pragma unroll
-                    for (int ss = 0; ss < RB; ss++) x[tt] = fmaf(-arow[ss], xp[ss], x[tt]);
-                }
-            }
-#pragma unroll
-            for (int tt = 0; tt < RB; tt++) {
-                const float* arow = As + (b * RB + tt) * AS + b * RB;
-#pragma unroll
-                for (int ss = 0; ss < tt; ss++) x[tt] = fmaf(-arow[ss], x[ss], x[tt]);
-            }
-#pragma unroll
-            for (int tt = 0; tt < RB; tt++) dst[(b * RB + tt) * D + cc] = x[tt];
         }
+#pragma unroll
+        for (int t = 0; t < C; t++) dst[t * D + cc] = x[t];
     }
     if (tid == 0) ws[ChunkWs<D>::GL] = expf((float)lglast);
 }
@@ -388,7 +378,7 @@ hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     if (p.head_dim != 128) return hipErrorInvalidValue;
     constexpr int D = 128;
-    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 4 * kChunk) * sizeof(float);
+    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 5 * kChunk) * sizeof(float);
     hipError_t ea = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (ea != hipSuccess) return ea;
