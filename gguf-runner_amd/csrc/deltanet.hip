@@ -276,13 +276,38 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(cons
 
 constexpr int kScanCols = 4;
 
+// Raw buffer access (wave-uniform base in a scalar descriptor, 32-bit byte
+// offsets per lane) and 16 bytes per lane straight into LDS at lds + 16 * lane
+// (lds wave-uniform).  The builtin exists for the device pass only.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dn_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)0xffffffff, 0x00020000);
+}
+__device__ __forceinline__ void dn_dma16(__amdgpu_buffer_rsrc_t r, float* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+#endif
+}
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
+__device__ __forceinline__ void dn_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// The chunk steps are sequential, so every step's memory latency is exposed
+// unless it is requested early: W and Qg (read only by phase A) go by DMA into
+// LDS, the next chunk's as soon as phase A is done, and the P and Kd^T rows a
+// thread needs in phases B and C are loaded into registers when the step starts.
+// W / Qg tiles are [C][D] f32 rows of 32 16-byte chunks, chunk q of row r at
+// position q ^ (r & 15), so the 16 rows a wave reads at once hit distinct banks.
 template <int D>
 __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(const DeltaNetLaunch p) {
     constexpr int C = kChunk;
     constexpr int NC = kScanCols;
+    constexpr int RQ = D / 4;                 // 16-byte chunks per W / Qg row
+    static_assert(RQ == 32 && C * D * 4 == 4 * 8 * 1024, "tile DMA covers [C][D] in 4 waves x 8 KB");
     __shared__ __attribute__((aligned(16))) float Ss[D][NC];
     __shared__ __attribute__((aligned(16))) float Dl[C][NC];
+    __shared__ __attribute__((aligned(16))) float Wl[C * D];
+    __shared__ __attribute__((aligned(16))) float Ql[C * D];
     const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
     // blockIdx.x = head so that the column blocks of one head (linear ids
     // h + H*cb) land on the same XCD and share its L2 copy of the workspace.
     const int h = blockIdx.x;
@@ -290,51 +315,82 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(cons
     const int H = p.n_heads;
     float* Sh = p.state + (size_t)h * D * D;
     for (int e = tid; e < D * NC; e += kChunkThreads) Ss[e / NC][e % NC] = Sh[(size_t)(e / NC) * D + c0 + e % NC];
-    __syncthreads();
 
     const int n_chunks = (p.n_tokens + C - 1) / C;
-    const int ta = tid >> 2;          // phase A/B: row t
-    const int ia = tid & 3;           //            column
+    // DMA: instruction k of wave w fills LDS bytes [1 KB (8 w + k), +1 KB): lane l
+    // writes row 2 (8 w + k) + l / 32, position l % 32, which holds chunk
+    // (l % 32) ^ (row & 15) of that row.
+    int dma_off[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int r = 2 * (8 * wave + k) + (lane >> 5);
+        dma_off[k] = (r * RQ + ((lane & 31) ^ (r & 15))) * 16;
+    }
+    auto dma_wq = [&](int c) {
+        const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
+        const __amdgpu_buffer_rsrc_t rw = dn_rsrc(ws + ChunkWs<D>::W);
+        const __amdgpu_buffer_rsrc_t rq = dn_rsrc(ws + ChunkWs<D>::QG);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            dn_dma16(rw, Wl + (8 * wave + k) * 256, dma_off[k]);
+            dn_dma16(rq, Ql + (8 * wave + k) * 256, dma_off[k]);
+        }
+    };
+    if (n_chunks > 0) dma_wq(0);
+
+    const int ta = tid >> 2;          // phases A/B: row t
+    const int ia = tid & 3;           //             column
     const int jc = tid >> 1;          // phase C: state row j (D = 128 rows over 256 threads / 2)
     const int ic = (tid & 1) * (NC / 2);
+    const int swa = ta & 15;
     for (int c = 0; c < n_chunks; c++) {
         const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
-        // phase C's row of Kd^T and gamma_last, requested now so that they arrive
-        // during phases A and B
-        float4 kd[C / 4];
+        dn_wait_vmem();   // this thread's part of chunk c's W / Qg is in LDS
+        __syncthreads();  // ... everyone's (and the initial Ss)
+        // the P and Kd^T rows for phases B and C, U and gamma_last
+        float4 kd[C / 4], pr[C / 4];
         {
             const float* kr = ws + ChunkWs<D>::KDT + jc * C;
+            const float* prr = ws + ChunkWs<D>::P + ta * C;
 #pragma unroll
-            for (int u = 0; u < C / 4; u++) kd[u] = *(const float4*)(kr + 4 * u);
+            for (int u = 0; u < C / 4; u++) {
+                kd[u] = *(const float4*)(kr + 4 * u);
+                pr[u] = *(const float4*)(prr + 4 * u);
+            }
         }
         const float gl = ws[ChunkWs<D>::GL];
+        const float u0 = ws[ChunkWs<D>::U + ta * D + c0 + ia];
         // A: Delta[t][i] = U[t][i] - sum_j W[t][j] S[j][i], and the first part of
         //    O[t][i], sum_j Qg[t][j] S[j][i], in the same pass over S
-        float acc_o = 0.0f;
-        {
-            float acc = ws[ChunkWs<D>::U + ta * D + c0 + ia];
-            const float* wr = ws + ChunkWs<D>::W + ta * D;
-            const float* qr = ws + ChunkWs<D>::QG + ta * D;
-            for (int j = 0; j < D; j += 4) {
-                const float4 w4 = *(const float4*)(wr + j);
-                const float4 q4 = *(const float4*)(qr + j);
-                const float s0 = Ss[j][ia], s1 = Ss[j + 1][ia], s2 = Ss[j + 2][ia], s3 = Ss[j + 3][ia];
-                acc = fmaf(-w4.x, s0, acc);
-                acc = fmaf(-w4.y, s1, acc);
-                acc = fmaf(-w4.z, s2, acc);
-                acc = fmaf(-w4.w, s3, acc);
-                acc_o = fmaf(q4.x, s0, acc_o);
-                acc_o = fmaf(q4.y, s1, acc_o);
-                acc_o = fmaf(q4.z, s2, acc_o);
-                acc_o = fmaf(q4.w, s3, acc_o);
-            }
-            Dl[ta][ia] = acc;
+        float acc = 0.0f, acc_o = 0.0f;
+#pragma unroll 8
+        for (int q = 0; q < RQ; q++) {
+            const int pos = (ta * RQ + (q ^ swa)) * 4;
+            const float4 w4 = *(const float4*)(Wl + pos);
+            const float4 q4 = *(const float4*)(Ql + pos);
+            const int j = 4 * q;
+            const float s0 = Ss[j][ia], s1 = Ss[j + 1][ia], s2 = Ss[j + 2][ia], s3 = Ss[j + 3][ia];
+            acc = fmaf(-w4.x, s0, acc);
+            acc = fmaf(-w4.y, s1, acc);
+            acc = fmaf(-w4.z, s2, acc);
+            acc = fmaf(-w4.w, s3, acc);
+            acc_o = fmaf(q4.x, s0, acc_o);
+            acc_o = fmaf(q4.y, s1, acc_o);
+            acc_o = fmaf(q4.z, s2, acc_o);
+            acc_o = fmaf(q4.w, s3, acc_o);
         }
-        __syncthreads();
+        Dl[ta][ia] = u0 + acc;
+        __syncthreads();  // Delta is complete; W / Qg of chunk c are no longer read
+        if (c + 1 < n_chunks) dma_wq(c + 1);
         // B: O[t][i] += sum_{s<=t} P[t][s] Delta[s][i]
         {
-            const float* pr = ws + ChunkWs<D>::P + ta * C;
-            for (int s = 0; s <= ta; s++) acc_o = fmaf(pr[s], Dl[s][ia], acc_o);
+#pragma unroll
+            for (int u = 0; u < C / 4; u++) {
+                const float pv[4] = {pr[u].x, pr[u].y, pr[u].z, pr[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (4 * u + k <= ta) acc_o = fmaf(pv[k], Dl[4 * u + k][ia], acc_o);
+            }
             const int t = c * C + ta;
             if (t < p.n_tokens) p.out[((size_t)t * H + h) * D + c0 + ia] = finite_or_zero(acc_o);
         }
@@ -355,8 +411,8 @@ __global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(cons
         __syncthreads();  // every read of Ss / Dl for this chunk is done
 #pragma unroll
         for (int u = 0; u < NC / 2; u++) Ss[jc][ic + u] = nv[u];
-        __syncthreads();
     }
+    __syncthreads();
     for (int e = tid; e < D * NC; e += kChunkThreads) Sh[(size_t)(e / NC) * D + c0 + e % NC] = Ss[e / NC][e % NC];
 }
 
