@@ -669,7 +669,32 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         p.k_cache = kc;
         p.v_cache = vc;
         if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
-        if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) return rc;
+        if (is_q8(s)) {
+            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile)
+            PrefillQ8Launch pq{};
+            pq.n_tokens = m;
+            pq.n_heads = s->cfg.n_heads;
+            pq.n_kv_heads = s->cfg.n_kv_heads;
+            pq.head_dim = s->d;
+            pq.base_pos = base_pos;
+            pq.window = (int)w;
+            pq.bidirectional = block ? 1 : 0;
+            pq.block = s->cfg.q8_block_scales ? 1 : 0;
+            pq.score_scale = score_scale(s);
+            pq.q = qp;
+            pq.k_codes = (const int8_t*)kc;
+            pq.v_codes = (const int8_t*)vc;
+            pq.row_stride = s->kv_dim;
+            const size_t so = (size_t)layer * s->sc_layer_stride + (size_t)seq * s->sc_seq_stride;
+            pq.k_scale = s->k_scale + so;
+            pq.v_scale = s->v_scale + so;
+            pq.scale_row_stride = (int64_t)s->sc_per_row;
+            pq.out = xo;
+            const hipError_t e = launch_prefill_q8(pq, s->stream);
+            if (e != hipSuccess) return hip_fail(e, "q8 prefill launch");
+        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) {
+            return rc;
+        }
     }
     return d2h_sync(s, xb, xo, qb);
 }

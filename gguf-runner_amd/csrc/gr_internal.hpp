@@ -209,6 +209,29 @@ struct PrefillLaunch {
 
 hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st);
 
+// Prefill over a Q8 KV cache (prefill_q8.hip).  q: f32 rows
+// [n_tokens][n_heads][head_dim] after RoPE / QK norm (score_scale applied in the
+// kernel); k_codes / v_codes: int8 row 0 of the sequence (row stride row_stride
+// bytes, KV head g at g * head_dim); scales of row t: k_scale[t * scale_row_stride]
+// (block = 0) or k_scale[t * scale_row_stride + g * head_dim / 32 + b] (block = 1).
+// Visibility as PrefillLaunch (window, bidirectional).
+struct PrefillQ8Launch {
+    int n_tokens, n_heads, n_kv_heads, head_dim;
+    int64_t base_pos;
+    int window, bidirectional, block;
+    float score_scale;
+    const float* q;
+    const int8_t* k_codes;
+    const int8_t* v_codes;
+    int64_t row_stride;
+    const float* k_scale;
+    const float* v_scale;
+    int64_t scale_row_stride;
+    float* out;
+};
+
+hipError_t launch_prefill_q8(const PrefillQ8Launch& p, hipStream_t st);
+
 // Encoder self-attention (encoder.hip): rows [n_seq * tokens][heads * head_dim] f32.
 struct EncoderLaunch {
     int n_seq, tokens, heads, head_dim;

@@ -241,3 +241,43 @@ def test_q8_decode_layer_batch_slots(orc, dev, block):
         ref = orc.attention_token(q[sq], kq[0], vq[0], fmt, 32, 4, 128, 0, L,
                                   key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
         assert float(np.abs(got[b] - ref).max()) <= TOL, (sq, float(np.abs(got[b] - ref).max()))
+
+
+@pytest.mark.parametrize("block,d,window,image", [
+    (False, 128, None, False), (True, 128, 100, False), (False, 256, None, False),
+    (True, 256, 37, False), (False, 128, None, True), (True, 128, 60, True)])
+def test_q8_prefill_chunk_mfma(orc, dev, block, d, window, image):
+    """One long gr_prefill_attention_chunk (or gr_prefill_image_block) over a Q8 cache
+    after a 40-token history: 300 query rows (three 128-row query blocks of the MFMA
+    prefill kernel, keys in 64-key tiles), global or sliding-window layer, row or block
+    scales, head_dim 128 and 256.  Each output row == the oracle's attention_token over
+    the rows the device wrote, with that row's visible range (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv = (16, 8) if d == 128 else (8, 2)
+    p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=512,
+                  kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE,
+                  layer_windows=[window, window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(31 + d + (window or 0))
+    hist, m, layer = 40, 300, 1
+    n = hist + m
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    rt.prefill_attention_chunk(p, s, layer, 0, q[:hist], k[:hist], v[:hist])
+    call = rt.prefill_image_block if image else rt.prefill_attention_chunk
+    got = call(p, s, layer, hist, q[hist:], k[hist:], v[hist:])
+    kq, vq = rt.read_kv_rows(p, s, layer, 0, n)
+    ks, vs = rt.read_kv_scales(p, s, layer, 0, n)
+    fmt = orc.Q8B if block else orc.Q8
+    worst = 0.0
+    for i in range(m):
+        pos = hist + i
+        start = max(0, pos + 1 - window) if window else 0
+        end = pos + 1
+        if image:
+            start, end = min(start, hist), n
+        ref = orc.attention_token(q[pos], kq, vq, fmt, n_heads, n_kv, d, start, end,
+                                  key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
+        worst = max(worst, float(np.abs(got[i] - ref).max()))
+    assert worst <= TOL, worst
