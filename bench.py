@@ -187,6 +187,22 @@ def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
     return call, flops, (q, k, v, kc, vc, out, fr)
 
 
+def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128):
+    """Run-state prefill of one S-token chunk over a Q8 KV cache (row or 32-element
+    block scales): gr_prefill_attention_chunk with host q / k / v rows, i.e. upload,
+    QK prep, the Q8 cache write, the MFMA flash pass and the download of the outputs."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=S,
+                  kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((S, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((S, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((S, p.kv_dim)).astype(np.float32)
+    flops = 4 * n_heads * d * S * (S + 1) // 2
+    return (lambda: rt.prefill_attention_chunk(p, s, 0, 0, q, k, v)), flops, (p, s)
+
+
 def cpu_baseline(lens, n_heads=32, n_kv=4, d=128, budget_s=10.0):
     """Oracle attention_token on the host cores over a bounded prefix of the decode
     batch (whole sequences, in batch order), as the reference runs it: one sequence
@@ -264,6 +280,12 @@ def run_one(args, dev, stream, lens) -> int:
         call, flops, keep = prefill_workload(dev, S, 8)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only in ("prefill2k_q8", "prefill2k_q8b"):
+        # synchronous host-buffer calls: the wall time per call includes the PCIe
+        # copies; the kernel's own time comes from a kernel trace of this run
+        call, flops, keep = prefill_q8_workload(2048, 8, args.only.endswith("b"))
+        _, wall = _timed(call, args.steps, args.warmup, stream)
+        res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only == "deltanet":
         pcall, keep = deltanet_workload(dev, 4096, 5)
         ms, _ = _timed(pcall, args.steps, args.warmup, stream)
@@ -290,7 +312,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "deltanet", "copy"],
+                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "deltanet", "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:

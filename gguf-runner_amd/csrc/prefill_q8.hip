@@ -6,13 +6,13 @@
 // K / V tile read once per 128 query rows.
 //
 // Workgroup = 128 query rows of one query head (4 row groups of 32) x KH key
-// halves: head_dim 128 runs 8 waves, wave (row group, half) taking sub-tile
-// `half` of every 64-key tile, so each SIMD holds two waves (the MFMAs of one
-// overlap the VALU work of the other); the two halves' (max, sum, O) merge
-// through LDS at the end.  head_dim 256 (more registers) runs 4 waves over
-// both sub-tiles.  The tile goes global -> registers -> LDS (the next tile's
-// loads are in flight while the current one is computed), the int8 codes
-// converted to f16 on the way in (exact: |code| <= 127), K and V row-major with
+// halves: head_dim 128 runs 8 waves over 128-key tiles, wave (row group, half)
+// taking the 32-key sub-tiles 2 j + half, so each SIMD holds two waves (the
+// MFMAs of one overlap the VALU work of the other); the two halves' (max, sum,
+// O) merge through LDS at the end.  head_dim 256 (more registers) runs 4 waves
+// over both sub-tiles of 64-key tiles.  The tile goes global -> registers ->
+// LDS (the next tile's loads are in flight while the current one is computed),
+// the int8 codes converted to f16 on the way in (exact: |code| <= 127), K and V row-major with
 // their 16-byte chunks XOR-swizzled per row like the f16 prefill kernel; the
 // tile's k / v scales go to LDS as [block][key].  Each wave computes, on
 // v_mfma_f32_32x32x16_f16,
@@ -41,13 +41,14 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define Q8P_LDS __attribute__((address_space(3)))
 
 constexpr int kQ8BM = 128;        // query rows per workgroup
-constexpr int kQ8BN = 64;         // keys per tile
 constexpr float kQ8Lazy = 8.0f;   // lazy softmax rescale threshold (log2 units)
 
-// key halves per workgroup: 2 where two waves per SIMD fit the registers
+// KH key halves per workgroup (2 where two waves per SIMD fit the registers),
+// BN keys per tile (each wave takes BN / 32 / KH sub-tiles between barriers)
 template <int D>
-struct Q8Halves {
-    static constexpr int value = D == 128 ? 2 : 1;
+struct Q8Tile {
+    static constexpr int KH = D == 128 ? 2 : 1;
+    static constexpr int BN = D == 128 ? 128 : 64;
 };
 
 __device__ __forceinline__ f32x16 q8p_mma(const uint4& a, const uint4& b, const f32x16& c) {
@@ -98,10 +99,10 @@ __device__ __forceinline__ int q8p_ilog2(float x) { return (int)((__float_as_uin
 __device__ __forceinline__ int q8p_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
 
 template <int D, bool BLOCK>
-__global__ __launch_bounds__(256 * Q8Halves<D>::value, 1) void prefill_q8_kernel(const PrefillQ8Launch p) {
-    constexpr int KH = Q8Halves<D>::value;
+__global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(const PrefillQ8Launch p) {
+    constexpr int KH = Q8Tile<D>::KH;
     constexpr int NT = 256 * KH;          // threads
-    constexpr int BM = kQ8BM, BN = kQ8BN;
+    constexpr int BM = kQ8BM, BN = Q8Tile<D>::BN;
     constexpr int NB = D / 32;            // 32-element blocks per head (k-step pairs, O^T tiles)
     constexpr int NBS = BLOCK ? NB : 1;   // scales per key and head
     constexpr int CPR = D / 16;           // 16-code chunks per cache row
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(256 * Q8Halves<D>::value, 1) void prefill_q8_kernel
         if (it + 1 < n_tiles) load_tile(t0 + BN);
 #pragma unroll
         for (int sb = 0; sb < BN / 32; sb++) {
-            if (KH == 2 && sb != kh) continue;
+            if (KH == 2 && (sb & 1) != kh) continue;
             const int ts = t0 + 32 * sb;
             if (wave_active && ts <= hi_max && ts + 31 >= lo_min) subtile(sb, ts);
         }
@@ -480,7 +481,7 @@ __global__ __launch_bounds__(256 * Q8Halves<D>::value, 1) void prefill_q8_kernel
 template <int D, bool BLOCK>
 hipError_t launch_q8_d(const PrefillQ8Launch& p, hipStream_t st) {
     const int n_qb = (p.n_tokens + kQ8BM - 1) / kQ8BM;
-    prefill_q8_kernel<D, BLOCK><<<dim3(p.n_heads, n_qb), 256 * Q8Halves<D>::value, 0, st>>>(p);
+    prefill_q8_kernel<D, BLOCK><<<dim3(p.n_heads, n_qb), 256 * Q8Tile<D>::KH, 0, st>>>(p);
     return hipGetLastError();
 }
 
