@@ -187,13 +187,16 @@ def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
     return call, flops, (q, k, v, kc, vc, out, fr)
 
 
-def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128):
+def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128, turbo=False):
     """Run-state prefill of one S-token chunk over a Q8 KV cache (row or 32-element
-    block scales): gr_prefill_attention_chunk with host q / k / v rows, i.e. upload,
-    QK prep, the Q8 cache write, the MFMA flash pass and the download of the outputs."""
+    block scales) or a Turbo cache: gr_prefill_attention_chunk with host q / k / v
+    rows, i.e. upload, QK prep, the cache write, the attention (Q8: the MFMA flash
+    pass; Turbo: query rotation, token-packed split kernel, merge + inverse
+    rotations) and the download of the outputs."""
     from gguf_runner_amd import ffi, runtime as rt
     p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=S,
-                  kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE)
+                  kv_dtype=ffi.DTYPE_TURBO if turbo else ffi.DTYPE_Q8, q8_block_scales=block,
+                  rope_mode=ffi.ROPE_NONE)
     s = rt.malloc_run_state(p)
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((S, p.q_dim)).astype(np.float32)
@@ -280,10 +283,11 @@ def run_one(args, dev, stream, lens) -> int:
         call, flops, keep = prefill_workload(dev, S, 8)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
-    elif args.only in ("prefill2k_q8", "prefill2k_q8b"):
+    elif args.only in ("prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo"):
         # synchronous host-buffer calls: the wall time per call includes the PCIe
-        # copies; the kernel's own time comes from a kernel trace of this run
-        call, flops, keep = prefill_q8_workload(2048, 8, args.only.endswith("b"))
+        # copies; the kernels' own times come from a kernel trace of this run
+        call, flops, keep = prefill_q8_workload(2048, 8, args.only.endswith("b"),
+                                                turbo=args.only.endswith("turbo"))
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only == "deltanet":
@@ -312,7 +316,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "deltanet", "copy"],
+                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "deltanet", "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:

@@ -191,8 +191,16 @@ int decode_enqueue(const gr_decode_args* a, hipStream_t st) { return decode_enqu
 
 // seq_slot: optional device map from batch entry to cache sequence slot.
 int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st) {
+    return decode_enqueue_ex(a, seq_slot, st, 0, nullptr, nullptr);
+}
+
+int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st, int tok_pack,
+                      const int32_t* col_start, const int32_t* col_end) {
     int rc = check_decode(a);
     if (rc) return rc;
+    if (tok_pack > 0 && (a->kv_dtype != GR_DTYPE_TURBO || seq_slot || !col_start || !col_end || a->split_keys <= 0 ||
+                         tok_pack * (a->n_heads / a->n_kv_heads) > 16))
+        return fail(GR_ERR_ARG, "token-packed decode: Turbo cache, one sequence, explicit split and <= 16 columns");
     const DecodePlan pl = plan_decode(a);
     DecodeLaunch p{};
     p.n_seq = a->n_seq;
@@ -238,6 +246,9 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
         p.turbo_signs = a->turbo_signs;
         p.turbo_slot_stride = a->turbo_slot_stride;
         p.ws_q = (float*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes);
+        p.tok_pack = tok_pack;
+        p.col_start = col_start;
+        p.col_end = col_end;
     }
     hipError_t e = launch_decode(p, st);
     if (e != hipSuccess) return hip_fail(e, "gr_decode_attention launch");

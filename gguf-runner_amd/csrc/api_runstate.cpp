@@ -464,10 +464,60 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
 // Decode n queries whose prepared f32 q rows are at qdev; entry b reads cache
 // slot slots[b] (or `seq` for all when slots_dev is null) with visible range
 // [starts[b], ends[b]).
+// Token-packed Turbo prefill of n rows of one sequence (DecodeLaunch::tok_pack):
+// groups of tp = 16 / kv_mul consecutive rows share the split kernel's MFMA
+// columns and read every K / V tile (and expand its codes) once.
+struct TurboPack {
+    int tp = 0;
+    int split_keys = 0;
+    int max_len = 1;            // longest group range
+    std::vector<int32_t> host;  // [4][n]: group start, group end, own start, own end
+};
+
+static TurboPack plan_turbo_pack(const gr_run_state* s, int n, const std::vector<int32_t>& starts,
+                                 const std::vector<int32_t>& ends) {
+    TurboPack t;
+    t.tp = std::max(1, 16 / (s->cfg.n_heads / s->cfg.n_kv_heads));
+    t.host.resize(4 * (size_t)n);
+    for (int b = 0; b < n; b += t.tp) {
+        const int e = std::min(n, b + t.tp);
+        int32_t lo = starts[b], hi = ends[b];
+        for (int i = b; i < e; i++) {
+            lo = std::min(lo, starts[i]);
+            hi = std::max(hi, ends[i]);
+        }
+        for (int i = b; i < e; i++) {
+            t.host[i] = lo;
+            t.host[n + i] = hi;
+        }
+        t.max_len = std::max(t.max_len, (int)(hi - lo));
+    }
+    for (int i = 0; i < n; i++) {
+        t.host[2 * (size_t)n + i] = starts[i];
+        t.host[3 * (size_t)n + i] = ends[i];
+    }
+    // ~2048 (group, KV head, split) workgroups; splits in whole 128-key rounds
+    const long units = (long)((n + t.tp - 1) / t.tp) * s->cfg.n_kv_heads;
+    const long want = std::max(1L, (2048 + units - 1) / units);
+    t.split_keys = std::max(128, (int)((t.max_len + want - 1) / want + 127) / 128 * 128);
+    return t;
+}
+
+static gr_decode_args turbo_pack_probe(const gr_run_state* s, int n, const TurboPack& t) {
+    gr_decode_args a{};
+    a.n_seq = n;
+    a.n_heads = s->cfg.n_heads;
+    a.n_kv_heads = s->cfg.n_kv_heads;
+    a.head_dim = s->d;
+    a.kv_dtype = s->cfg.kv_dtype;
+    a.split_keys = t.split_keys;
+    a.max_kv_len = t.max_len;
+    return a;
+}
+
 static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, const int32_t* slots_dev, int seq,
                       const std::vector<int32_t>& starts, const std::vector<int32_t>& ends, float* xb_dev,
-                      Carve& cv) {
-    int32_t* se = cv.take<int32_t>(2 * (size_t)n);
+                      Carve& cv, const TurboPack* pack = nullptr) {
     std::vector<int32_t> host(2 * (size_t)n);
     int max_len = 1;
     for (int b = 0; b < n; b++) {
@@ -475,6 +525,11 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
         host[n + b] = ends[b];
         max_len = std::max(max_len, ends[b] - starts[b]);
     }
+    if (pack) {
+        host = pack->host;
+        max_len = pack->max_len;
+    }
+    int32_t* se = cv.take<int32_t>(host.size());
     int rc = h2d(s, se, host.data(), host.size() * 4);
     if (rc) return rc;
     gr_decode_args a{};
@@ -483,7 +538,7 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
     a.n_kv_heads = s->cfg.n_kv_heads;
     a.head_dim = s->d;
     a.kv_dtype = s->cfg.kv_dtype;
-    a.split_keys = 0;
+    a.split_keys = pack ? pack->split_keys : 0;
     a.max_kv_len = max_len;
     a.score_scale = score_scale(s);
     a.q = qdev;
@@ -519,6 +574,7 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
     }
     const size_t ws = decode_ws_bytes(&a);
     a.workspace = cv.take<char>(ws + 256);
+    if (pack) return decode_enqueue_ex(&a, slots_dev, s->stream, pack->tp, se + 2 * (size_t)n, se + 3 * (size_t)n);
     return decode_enqueue_ex(&a, slots_dev, s->stream);
 }
 
@@ -617,7 +673,12 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
     probe.head_dim = s->d;
     probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = max_len;
-    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m);
+    TurboPack pack;
+    if (is_turbo(s)) {
+        pack = plan_turbo_pack(s, m, starts, ends);
+        probe = turbo_pack_probe(s, m, pack);
+    }
+    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m) + 16 * (size_t)m;
     if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
     Carve cv(s->stage);
     float* qin = cv.take<float>((size_t)m * s->q_dim);
@@ -692,7 +753,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
             pq.out = xo;
             const hipError_t e = launch_prefill_q8(pq, s->stream);
             if (e != hipSuccess) return hip_fail(e, "q8 prefill launch");
-        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv))) {
+        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv, is_turbo(s) ? &pack : nullptr))) {
             return rc;
         }
     }

@@ -51,6 +51,15 @@ struct DecodeLaunch {
     const uint8_t* turbo_signs;
     int64_t turbo_slot_stride;
     float* ws_q;
+    // Token-packed Turbo prefill (tok_pack > 0; one cache sequence, seq_slot
+    // null): batch entries are n_seq consecutive query tokens; the split kernel
+    // runs one workgroup row per group of tok_pack tokens, whose MFMA columns are
+    // (token, query head of the GQA group) pairs.  kv_start / kv_end of every
+    // token hold its group's key range (the split and merge ranges), col_start /
+    // col_end the token's own visible keys.
+    int tok_pack;
+    const int32_t* col_start;
+    const int32_t* col_end;
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);

@@ -295,7 +295,10 @@ constexpr int kTdWaves = kTdThreads / 64;
 // sigma and r = gamma sqrt(pi/2/D) of the tile's keys go through LDS as well
 // (one coalesced load per lane).  Partials: ws_o [s][h][split][2][D] (base,
 // residual), ws_ml as the other decodes.
-template <int D>
+// PACK: token-packed prefill (DecodeLaunch::tok_pack): column c of the MFMAs is
+// token s * tok_pack + c / kv_mul, query head g * kv_mul + c % kv_mul, masked to
+// that token's own visible keys.
+template <int D, bool PACK>
 __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const DecodeLaunch p) {
     static_assert(D == 128, "decode_turbo_kernel: lane layouts are sized for head_dim 128");
     constexpr int TILE = 32;
@@ -313,11 +316,17 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
     constexpr int kMergeBytes = (kTdWaves * 16 * (2 * D + 1) + 2 * kTdWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
     const int split = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
-    const int t_begin = p.kv_start[s] + split * p.split_keys;
-    const int t_limit = p.kv_end[s];
+    const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
+    const int t_begin = p.kv_start[e_rng] + split * p.split_keys;
+    const int t_limit = p.kv_end[e_rng];
     if (t_begin >= t_limit) return;
     const int t_stop = min(t_limit, t_begin + p.split_keys);
     const int kv_mul = p.n_heads / p.n_kv_heads;
+    // MFMA column c: batch entry col_tok(c), query head col_head(c)
+    const int n_col = PACK ? p.tok_pack * kv_mul : kv_mul;
+    auto col_tok = [&](int c) { return PACK ? s * p.tok_pack + c / kv_mul : s; };
+    auto col_head = [&](int c) { return g * kv_mul + (PACK ? c % kv_mul : c); };
+    auto col_ok = [&](int c) { return c < n_col && (!PACK || col_tok(c) < p.n_seq); };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
     uint4* lut_c = (uint4*)smem;
@@ -334,8 +343,9 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
     uint4 bq[KS], bql[KS], bp[KS], bpl[KS];
     float qback_c = 1.0f, qback_r = 1.0f;
     {
-        const bool qv = l16 < kv_mul;
-        const float* qr = p.ws_q + ((size_t)s * p.n_heads + (size_t)g * kv_mul + (qv ? l16 : 0)) * 2 * D;
+        const bool qv = col_ok(l16);
+        const int qc = qv ? l16 : 0;
+        const float* qr = p.ws_q + ((size_t)col_tok(qc) * p.n_heads + col_head(qc)) * 2 * D;
         const float qs = p.score_scale * kLog2e;
         float mr = 0.0f, mp = 0.0f;
 #pragma unroll
@@ -385,6 +395,14 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
     // per-tile registers: K codes / signs of the lane's key in both 16-key sub-tiles,
     // V code / sign bytes for the staging (lane: key lane/2, half lane%2 of the row),
     // the lane's aux pair (key lane%32; K for lanes < 32, V above)
+    // keys [c_lo, c_hi) of this split are visible to the lane's column
+    int c_lo = t_begin, c_hi = t_stop;
+    if constexpr (PACK) {
+        const bool ok = col_ok(l16);
+        c_lo = ok ? p.col_start[col_tok(l16)] : 0;
+        c_hi = ok ? min(p.col_end[col_tok(l16)], t_stop) : 0;
+    }
+
     uint2 kc[2];
     uint32_t ksb[2];
     uint4 vcw;
@@ -479,7 +497,8 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
                 const int key = t0 + 16 * sb + 4 * g4 + j;
                 const float base = (kTqC0 * s1[sb][j] + (kTqC1 - kTqC0) * s2[sb][j]) * qback_c;
                 const float v = ksv[j] * base + krv[j] * (sr[sb][j] * qback_r);
-                sv[e] = (!tail || key < t_stop) ? v : -INFINITY;
+                if constexpr (PACK) sv[e] = (key >= c_lo && key < c_hi) ? v : -INFINITY;
+                else sv[e] = (!tail || key < t_stop) ? v : -INFINITY;
                 vsg[e] = vsv[j];
                 vrr[e] = vrv[j];
             }
@@ -608,8 +627,9 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
         }
     __syncthreads();
     const int n_splits = p.n_splits;
-    for (int idx = tid; idx < kv_mul * 2 * D; idx += kTdThreads) {
+    for (int idx = tid; idx < n_col * 2 * D; idx += kTdThreads) {
         const int q = idx / (2 * D), i = idx % (2 * D);
+        if (!col_ok(q)) continue;
         float mx = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kTdWaves; w++) mx = fmaxf(mx, sh_m[w][q]);
@@ -620,7 +640,7 @@ __global__ __launch_bounds__(kTdThreads, 2) void decode_turbo_kernel(const Decod
             lt += sh_l[w][q] * a;
             ot += sh_o[w][q][i] * a;
         }
-        const size_t part = ((size_t)s * p.n_heads + (size_t)g * kv_mul + q) * n_splits + split;
+        const size_t part = ((size_t)col_tok(q) * p.n_heads + col_head(q)) * n_splits + split;
         p.ws_o[part * 2 * D + i] = ot;
         if (i == 0) {
             p.ws_ml[part * 2 + 0] = mx;
@@ -688,7 +708,11 @@ hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st) {
     turbo_query_kernel<128><<<dim3(p.n_heads, p.n_seq), 64, 0, st>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    decode_turbo_kernel<128><<<dim3(p.n_splits, p.n_kv_heads, p.n_seq), kTdThreads, 0, st>>>(p);
+    if (p.tok_pack > 0)
+        decode_turbo_kernel<128, true><<<dim3(p.n_splits, p.n_kv_heads, (p.n_seq + p.tok_pack - 1) / p.tok_pack),
+                                         kTdThreads, 0, st>>>(p);
+    else
+        decode_turbo_kernel<128, false><<<dim3(p.n_splits, p.n_kv_heads, p.n_seq), kTdThreads, 0, st>>>(p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     turbo_combine_kernel<128><<<dim3(p.n_heads, p.n_seq), 64, 0, st>>>(p);
     return hipGetLastError();

@@ -189,3 +189,43 @@ def test_turbo_decode_layer_batch_slots(orc, dev):
         c = _oracle_cache(orc, caches[sq][0], caches[sq][1], table, 0, 4, 128)
         ref = orc.attention_token_turbo(q[sq], c, table, 0, 32, 0, lens[sq] + 1)
         assert float(np.abs(got[b] - ref).max()) <= TOL, (sq, float(np.abs(got[b] - ref).max()))
+
+
+@pytest.mark.parametrize("n_heads,n_kv,window,image", [
+    (16, 8, None, False), (32, 4, 70, False), (16, 1, None, False), (16, 8, 45, True), (32, 4, None, True)])
+def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image):
+    """A 200-row gr_prefill_attention_chunk (or gr_prefill_image_block) over a Turbo
+    cache after a 40-token history: the split kernel packs 16 / kv_mul consecutive
+    rows into its MFMA columns (kv_mul 2, 8 and 16: 8, 2 and 1 rows), each column
+    masked to its own visible keys; global or sliding-window layer.  Each output row ==
+    the oracle's attention_token_turbo over the oracle's encoding of the same rows,
+    with that row's visible range (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    d = 128
+    p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=320,
+                  kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE, layer_windows=[window, window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(41 + n_kv + (window or 0))
+    hist, m, layer = 40, 200, 1
+    n = hist + m
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    rt.prefill_attention_chunk(p, s, layer, 0, q[:hist], k[:hist], v[:hist])
+    call = rt.prefill_image_block if image else rt.prefill_attention_chunk
+    got = call(p, s, layer, hist, q[hist:], k[hist:], v[hist:])
+    table = orc.turbo_sign_table(2, n_kv, d)
+    c = orc.TurboCache(n, n_kv, d)
+    for t in range(n):
+        orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
+    _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 0, n), c, 0, n, n_kv, d)
+    worst = 0.0
+    for i in range(m):
+        pos = hist + i
+        start = max(0, pos + 1 - window) if window else 0
+        end = pos + 1
+        if image:
+            start, end = min(start, hist), n
+        ref = orc.attention_token_turbo(q[pos], c, table, layer, n_heads, start, end)
+        worst = max(worst, float(np.abs(got[i] - ref).max()))
+    assert worst <= TOL, worst
