@@ -75,22 +75,22 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 // int8 -> f16, exact: with u = c + 128 (flip the sign bit), the f16 with
 // exponent byte 0x64 and low byte u is 1024 + u, and (1024 + u) - 1152 = c.
-__device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t two_bytes_spread) {
-    const half2_t h = __builtin_bit_cast(half2_t, two_bytes_spread | 0x64006400u) - half2_t{1152.0f16, 1152.0f16};
-    return __builtin_bit_cast(uint32_t, h);
-}
 
 template <bool BLOCK>
 struct KvQ8 {
     using M = Mfma16<F16>;
     using Raw = uint2;
     static constexpr bool kQ8 = true, kBlock = BLOCK;
+    // v_perm places the sign-flipped codes under the exponent byte 0x64 (selector
+    // bytes 0..3 pick bytes of the code word, 4 a byte of 0x64646464)
     static __device__ __forceinline__ uint4 to16(const uint2& r) {
         const uint32_t a = r.x ^ 0x80808080u, b = r.y ^ 0x80808080u;
-        return make_uint4(i8x2_to_f16x2((a & 0xffu) | ((a & 0xff00u) << 8)),
-                          i8x2_to_f16x2(((a >> 16) & 0xffu) | ((a >> 8) & 0xff0000u)),
-                          i8x2_to_f16x2((b & 0xffu) | ((b & 0xff00u) << 8)),
-                          i8x2_to_f16x2(((b >> 16) & 0xffu) | ((b >> 8) & 0xff0000u)));
+        auto two = [](uint32_t w, uint32_t sel) {
+            const half2_t h = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, w, sel)) -
+                              half2_t{1152.0f16, 1152.0f16};
+            return __builtin_bit_cast(uint32_t, h);
+        };
+        return make_uint4(two(a, 0x04010400u), two(a, 0x04030402u), two(b, 0x04010400u), two(b, 0x04030402u));
     }
 };
 
