@@ -281,3 +281,34 @@ def test_q8_prefill_chunk_mfma(orc, dev, block, d, window, image):
                                   key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
         worst = max(worst, float(np.abs(got[i] - ref).max()))
     assert worst <= TOL, worst
+
+
+@pytest.mark.parametrize("block,m,window,hist", [
+    (False, 1, None, 7), (True, 31, 1, 0), (False, 33, 5, 90), (True, 97, None, 415)])
+def test_q8_prefill_chunk_edges(orc, dev, block, m, window, hist):
+    """Q8 prefill edge cases: one-row and ragged chunks (1, 31, 33, 97 rows: partial
+    32-row groups and a partial 128-row query block), window 1 (each row sees only
+    itself) and 5, a chunk that ends exactly at seq_len (history 415 + 97 = 512)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv, d = 16, 8, 128
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=512,
+                  kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE,
+                  layer_windows=[window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(7 + m)
+    n = hist + m
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    if hist:
+        rt.prefill_attention_chunk(p, s, 0, 0, q[:hist], k[:hist], v[:hist])
+    got = rt.prefill_attention_chunk(p, s, 0, hist, q[hist:], k[hist:], v[hist:])
+    kq, vq = rt.read_kv_rows(p, s, 0, 0, n)
+    ks, vs = rt.read_kv_scales(p, s, 0, 0, n)
+    fmt = orc.Q8B if block else orc.Q8
+    for i in range(m):
+        pos = hist + i
+        start = max(0, pos + 1 - window) if window else 0
+        ref = orc.attention_token(q[pos], kq, vq, fmt, n_heads, n_kv, d, start, pos + 1,
+                                  key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
+        assert float(np.abs(got[i] - ref).max()) <= TOL, (i, float(np.abs(got[i] - ref).max()))

@@ -229,3 +229,32 @@ def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image
         ref = orc.attention_token_turbo(q[pos], c, table, layer, n_heads, start, end)
         worst = max(worst, float(np.abs(got[i] - ref).max()))
     assert worst <= TOL, worst
+
+
+@pytest.mark.parametrize("n_kv,m,window,hist", [(8, 3, None, 5), (8, 11, 1, 20), (2, 1, None, 0), (4, 37, 3, 60)])
+def test_turbo_prefill_chunk_partial_groups(orc, dev, n_kv, m, window, hist):
+    """Token-packed Turbo prefill with partial row groups (3 and 11 rows with 8 rows
+    per group, 37 with 4), a one-row chunk (8 rows per group at 16 / 2 heads), and
+    windows 1 and 3 (rows of one group see different keys)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, d = 16, 128
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=128,
+                  kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE, layer_windows=[window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(17 + m)
+    n = hist + m
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    if hist:
+        rt.prefill_attention_chunk(p, s, 0, 0, q[:hist], k[:hist], v[:hist])
+    got = rt.prefill_attention_chunk(p, s, 0, hist, q[hist:], k[hist:], v[hist:])
+    table = orc.turbo_sign_table(1, n_kv, d)
+    c = orc.TurboCache(n, n_kv, d)
+    for t in range(n):
+        orc.kv_write_turbo(c, t, k[t], v[t], table, 0)
+    for i in range(m):
+        pos = hist + i
+        start = max(0, pos + 1 - window) if window else 0
+        ref = orc.attention_token_turbo(q[pos], c, table, 0, n_heads, start, pos + 1)
+        assert float(np.abs(got[i] - ref).max()) <= TOL, (i, float(np.abs(got[i] - ref).max()))
