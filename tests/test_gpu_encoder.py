@@ -76,3 +76,21 @@ def test_encoder_attention_sizes(dev):
     assert L.gr_encoder_self_attention(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
                                        1, 4, 2, 160, None) < 0
     assert b"head_dim 160 unsupported" in ffi.lib().gr_last_error()
+
+
+def test_encoder_attention_gemma3_siglip_shape(dev):
+    """Gemma 3's SigLIP vision attention (multimodal/gemma3_attention.rs:141-192: one
+    noncausal sequence, q.k / sqrt(d), softmax, . V) is the same op at n_seq = 1:
+    4096 patches (896 / 14 squared), 16 heads of dim 72, against a float64 evaluation
+    of the textbook formula."""
+    ns, tps, hc, hd = 1, 4096, 16, 72
+    rng = np.random.default_rng(4096)
+    q, k, v = (rng.standard_normal((tps, hc * hd)).astype(np.float32) for _ in range(3))
+    got = _run(dev, q, k, v, n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
+    ref = np.empty((tps, hc * hd))
+    for h in range(hc):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = (q[:, sl].astype(np.float64) @ k[:, sl].astype(np.float64).T) / np.sqrt(hd)
+        s = np.exp(s - s.max(axis=1, keepdims=True))
+        ref[:, sl] = (s / s.sum(axis=1, keepdims=True)) @ v[:, sl].astype(np.float64)
+    assert _within(got, ref), f"max abs {np.abs(got - ref).max():.3e}"
