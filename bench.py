@@ -290,6 +290,20 @@ def run_one(args, dev, stream, lens) -> int:
                                                 turbo=args.only.endswith("turbo"))
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "encoder":
+        # Gemma 3 SigLIP vision attention: one noncausal sequence of 4096 patches,
+        # 16 heads of dim 72, f32 (gr_encoder_self_attention)
+        import torch
+        from gguf_runner_amd import ops
+        g = torch.Generator(device=dev)
+        g.manual_seed(9)
+        q, k, v = (torch.randn((4096, 16 * 72), generator=g, device=dev) for _ in range(3))
+        out = torch.empty_like(q)
+        call = lambda: ops.encoder_self_attention(q, k, v, n_seq=1, tokens=4096, heads=16, head_dim=72,
+                                                  out=out, stream=stream)
+        flops = 4 * 16 * 72 * 4096 * 4096
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only == "deltanet":
         pcall, keep = deltanet_workload(dev, 4096, 5)
         ms, _ = _timed(pcall, args.steps, args.warmup, stream)
@@ -316,7 +330,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "deltanet", "copy"],
+                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "encoder", "deltanet", "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
