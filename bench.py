@@ -290,6 +290,28 @@ def run_one(args, dev, stream, lens) -> int:
                                                 turbo=args.only.endswith("turbo"))
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "prefill8k_d256":
+        # config 4 shape (Gemma-3-4B): 8 Q / 4 KV heads, d256, QK RMSNorm, NeoX RoPE,
+        # bf16, 8192 tokens; the sliding-window (1024) and the global layer
+        import torch
+        from gguf_runner_amd import ffi, ops
+        S, Hq, Hk, d = 8192, 8, 4, 256
+        g = torch.Generator(device=dev)
+        g.manual_seed(4)
+        q = torch.randn((S, Hq, d), generator=g, device=dev, dtype=torch.bfloat16)
+        k = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
+        v = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
+        kc, vc = torch.empty_like(k), torch.empty_like(v)
+        out = torch.empty((S, Hq, d), device=dev, dtype=torch.float32)
+        qn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
+        kn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
+        fr = torch.tensor(ops.rope_freqs(1e4, d), dtype=torch.float32, device=dev)
+        for W, key in ((1024, "local"), (0, "global")):
+            call = ops.PrefillCall(q, k, v, kc, vc, out, window=W, rope_mode=ffi.ROPE_NEOX, rope_dim=d,
+                                   rope_freqs=fr, q_norm=qn, k_norm=kn, is_gemma3=True)
+            ms, _ = _timed(call, args.steps, args.warmup, stream)
+            flops = 4 * Hq * d * sum(min(i + 1, W) if W else i + 1 for i in range(S))
+            res[key] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gflop": flops / 1e9}
     elif args.only == "encoder":
         # Gemma 3 SigLIP vision attention: one noncausal sequence of 4096 patches,
         # 16 heads of dim 72, f32 (gr_encoder_self_attention)
@@ -330,7 +352,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "encoder", "deltanet", "copy"],
+                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
+                             "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
