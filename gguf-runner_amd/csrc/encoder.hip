@@ -3,7 +3,8 @@
 // n_seq sequences of `tokens` tokens each; every token attends to all tokens of
 // its own sequence (no cache, no mask), scores scaled by 1/sqrt(d).
 //
-// fp32 throughout (the reference's f32 dot / axpy / exp): one lane per query,
+// fp32 throughout (the reference's f32 dot / axpy / exp).  VALU kernel (sequences
+// under 64 tokens; the f32 MFMA kernel below takes longer ones): one lane per query,
 // 256 queries of one (sequence, head) per workgroup.  Key / value rows go
 // through LDS in tiles of 32 and every lane reads the same row (broadcast, no
 // bank conflicts).  Per tile: 32 scores in registers, the tile maximum raises
@@ -99,10 +100,206 @@ __global__ __launch_bounds__(kEncThreads, 1) void encoder_attention_kernel(const
         if (i < d) orow[i] = o[i] * inv;
 }
 
+// ---------------------------------------------------------------- f32 MFMA path
+//
+// Sequences of kEmMinTokens or more run on v_mfma_f32_32x32x2_f32: f32 operands,
+// f32 products and sums (no 16-bit rounding anywhere).  Workgroup = 4 waves x 32
+// queries of one (sequence, head); keys in tiles of 64 (two 32-key sub-tiles),
+// K row-major and V transposed in LDS, zero beyond the head dim.  Per sub-tile
+//   S^T = K . Q^T   k-step s: lane half lg carries dim lg * DP/2 + s, so a lane
+//                   reads its K operands for 4 k-steps with one ds_read_b128;
+//   O^T += V^T . P^T  k-step t pairs key 8 (t/4) + 4 lg + t%4 with lane half lg,
+//                   which is exactly accumulator element t of S^T: the B operand
+//                   is the lane's own P value, and the A operand (V^T row d,
+//                   4 consecutive keys) one ds_read_b128 per 4 k-steps.
+// Online softmax per query (lanes l and l ^ 32) with the lazy rescale.
+
+typedef float em_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kEmThreads = 256;
+constexpr int kEmBM = 128;         // queries per workgroup
+constexpr int kEmBN = 64;          // keys per tile
+constexpr int kEmMinTokens = 64;   // shorter sequences take the VALU kernel
+constexpr float kEmLazy = 8.0f;    // log2 units
+
+__device__ __forceinline__ float em_xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float em_xsum32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int DP>
+__global__ __launch_bounds__(kEmThreads, 2) void encoder_mfma_kernel(const EncoderLaunch p) {
+    constexpr int BN = kEmBN;
+    constexpr int KS = DP / 2;           // k-steps over the head dim
+    constexpr int DT = (DP + 31) / 32;   // O^T tiles of 32 dims
+    constexpr int DP32 = DT * 32;
+    constexpr int KST = DP + 4;          // K tile row stride (floats)
+    constexpr int VST = BN + 4;          // V^T tile row stride (floats)
+    static_assert(KS % 4 == 0, "head dims in multiples of 8");
+    __shared__ __attribute__((aligned(16))) float Kt[BN * KST];
+    __shared__ __attribute__((aligned(16))) float Vt[DP32 * VST];
+
+    const int d = p.head_dim;
+    const int dim = p.heads * d;
+    const int h = blockIdx.y;
+    const size_t seq0 = (size_t)blockIdx.z * p.tokens;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = lane & 31, lg = lane >> 5;
+    const int qi = (int)blockIdx.x * kEmBM + wave * 32 + ln;
+    const bool q_ok = qi < p.tokens;
+    const float qscale = kLog2e / sqrtf((float)d);  // scores in log2 units
+
+    float qv[KS];  // B operand of k-step s: dim lg * KS + s of this lane's query
+    {
+        const float* qr = p.q + (seq0 + (q_ok ? qi : p.tokens - 1)) * dim + (size_t)h * d;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const int i = lg * KS + s;
+            qv[s] = i < d ? qr[i] * qscale : 0.0f;
+        }
+    }
+    em_f32x16 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[dt][e] = 0.0f;
+    float mrow = -1e30f, lrow = 0.0f;
+
+    // Tile staging: thread tid holds the 4-dim groups tid + 256 u (row c / (DP32/4),
+    // dims 4 (c % (DP32/4)) .. +3) of K and V; the next tile's loads are in flight
+    // while the current one is computed.  Rows past the sequence and dims past d
+    // are zero.  float4 loads when the rows are 16-byte aligned (d % 4 == 0).
+    constexpr int G4 = DP32 / 4;
+    constexpr int NV4 = BN * G4 / kEmThreads;
+    static_assert(BN * G4 % kEmThreads == 0, "tile staging");
+    const bool vec = (d & 3) == 0;
+    float4 kst[NV4], vst[NV4];
+    auto load_tile = [&](int t0) {
+        const int nk = min(BN, p.tokens - t0);
+#pragma unroll
+        for (int u = 0; u < NV4; u++) {
+            const int c = tid + kEmThreads * u;
+            const int r = c / G4, i = 4 * (c % G4);
+            const bool rok = r < nk;
+            const size_t src = (seq0 + t0 + (rok ? r : 0)) * dim + (size_t)h * d;
+            if (vec) {
+                const bool ok = rok && i < d;
+                kst[u] = ok ? *(const float4*)(p.k + src + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vst[u] = ok ? *(const float4*)(p.v + src + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+                float kx[4], vx[4];
+#pragma unroll
+                for (int x = 0; x < 4; x++) {
+                    const bool ok = rok && i + x < d;
+                    kx[x] = ok ? p.k[src + i + x] : 0.0f;
+                    vx[x] = ok ? p.v[src + i + x] : 0.0f;
+                }
+                kst[u] = make_float4(kx[0], kx[1], kx[2], kx[3]);
+                vst[u] = make_float4(vx[0], vx[1], vx[2], vx[3]);
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int u = 0; u < NV4; u++) {
+            const int c = tid + kEmThreads * u;
+            const int r = c / G4, i = 4 * (c % G4);
+            if (i < DP) *(float4*)(Kt + r * KST + i) = kst[u];
+            Vt[(i + 0) * VST + r] = vst[u].x;
+            Vt[(i + 1) * VST + r] = vst[u].y;
+            Vt[(i + 2) * VST + r] = vst[u].z;
+            Vt[(i + 3) * VST + r] = vst[u].w;
+        }
+    };
+
+    load_tile(0);
+    for (int t0 = 0; t0 < p.tokens; t0 += BN) {
+        const int nk = min(BN, p.tokens - t0);
+        __syncthreads();  // the previous tile is consumed
+        store_tile();
+        __syncthreads();
+        if (t0 + BN < p.tokens) load_tile(t0 + BN);
+#pragma unroll
+        for (int sb = 0; sb < BN / 32; sb++) {
+            const int ts = 32 * sb;  // first key of the sub-tile within the tile
+            if (ts >= nk) break;
+            em_f32x16 acc;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+            const float* krow = Kt + (ts + ln) * KST + lg * KS;
+#pragma unroll
+            for (int j = 0; j < KS / 4; j++) {
+                const float4 kx = *(const float4*)(krow + 4 * j);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kx.x, qv[4 * j + 0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kx.y, qv[4 * j + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kx.z, qv[4 * j + 2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kx.w, qv[4 * j + 3], acc, 0, 0, 0);
+            }
+            // element e is key ts + 8 (e / 4) + 4 lg + e % 4 of the tile
+            if (ts + 32 > nk) {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    if (ts + 8 * (e >> 2) + 4 * lg + (e & 3) >= nk) acc[e] = -INFINITY;
+            }
+            float mx = acc[0];
+#pragma unroll
+            for (int e = 1; e < 16; e++) mx = fmaxf(mx, acc[e]);
+            mx = em_xmax32(mx);
+            if (__any(mx > mrow + kEmLazy)) {
+                const float mnew = fmaxf(mrow, mx);
+                const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+                mrow = mnew;
+                lrow *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++) o[dt] *= alpha;
+            }
+            float pv[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                pv[e] = __builtin_amdgcn_exp2f(acc[e] - mrow);
+                lrow += pv[e];
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const float* vrow = Vt + (32 * dt + ln) * VST + ts + 4 * lg;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 vx = *(const float4*)(vrow + 8 * j);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vx.x, pv[4 * j + 0], o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vx.y, pv[4 * j + 1], o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vx.z, pv[4 * j + 2], o[dt], 0, 0, 0);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vx.w, pv[4 * j + 3], o[dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+    const float lsum = em_xsum32(lrow);
+    if (!q_ok) return;
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    float* orow = p.out + (seq0 + qi) * dim + (size_t)h * d;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int i = 32 * dt + 8 * (e >> 2) + 4 * lg + (e & 3);
+            if (i < d) orow[i] = o[dt][e] * inv;
+        }
+}
+
 template <int DP>
 static hipError_t launch_encoder_dp(const EncoderLaunch& p, hipStream_t st) {
-    dim3 grid((p.tokens + kEncThreads - 1) / kEncThreads, p.heads, p.n_seq);
-    encoder_attention_kernel<DP><<<grid, kEncThreads, 0, st>>>(p);
+    if (p.tokens >= kEmMinTokens) {
+        dim3 grid((p.tokens + kEmBM - 1) / kEmBM, p.heads, p.n_seq);
+        encoder_mfma_kernel<DP><<<grid, kEmThreads, 0, st>>>(p);
+    } else {
+        dim3 grid((p.tokens + kEncThreads - 1) / kEncThreads, p.heads, p.n_seq);
+        encoder_attention_kernel<DP><<<grid, kEncThreads, 0, st>>>(p);
+    }
     return hipGetLastError();
 }
 
