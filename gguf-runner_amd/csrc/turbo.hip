@@ -222,11 +222,14 @@ __device__ __forceinline__ f32x4 mma16(const uint4& a, const uint4& b, const f32
                                                   c, 0, 0, 0);
 }
 
-// f16 hi/lo words of two floats
+typedef _Float16 tq_half2 __attribute__((ext_vector_type(2)));
+typedef float tq_float2 __attribute__((ext_vector_type(2)));
+
+// f16 hi/lo words of two floats (round to nearest even; one v_cvt_pk_f16_f32 each)
 __device__ __forceinline__ void split2(float a0, float a1, uint32_t& hi, uint32_t& lo) {
-    const uint16_t h0 = f32_to_f16(a0), h1 = f32_to_f16(a1);
-    hi = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    lo = (uint32_t)f32_to_f16(a0 - f16_to_f32(h0)) | ((uint32_t)f32_to_f16(a1 - f16_to_f32(h1)) << 16);
+    const tq_half2 h = __builtin_convertvector(tq_float2{a0, a1}, tq_half2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(tq_float2{a0 - (float)h[0], a1 - (float)h[1]}, tq_half2));
 }
 
 // Lookup tables of the +-1 / 0 MFMA operands (f16 +1 = 0x3C00, -1 = 0xBC00):
