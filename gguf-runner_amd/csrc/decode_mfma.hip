@@ -47,8 +47,17 @@ struct Mfma16<F16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
                                                       __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
     }
-    static __device__ __forceinline__ uint16_t cvt(float x) { return f32_to_f16(x); }
-    static __device__ __forceinline__ float back(uint16_t x) { return f16_to_f32(x); }
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    // f16 words of (a0, a1) (one v_cvt_pk_f16_f32, round to nearest even), and the
+    // words of the residuals a - f16(a) given those words
+    static __device__ __forceinline__ uint32_t pack2(float a0, float a1) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a0, a1}, h2));
+    }
+    static __device__ __forceinline__ uint32_t rest2(uint32_t hi, float a0, float a1) {
+        const h2 h = __builtin_bit_cast(h2, hi);
+        return pack2(a0 - (float)h[0], a1 - (float)h[1]);
+    }
 };
 template <>
 struct Mfma16<BF16> {
@@ -57,8 +66,12 @@ struct Mfma16<BF16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
     }
-    static __device__ __forceinline__ uint16_t cvt(float x) { return f32_to_bf16(x); }
-    static __device__ __forceinline__ float back(uint16_t x) { return bf16_to_f32(x); }
+    static __device__ __forceinline__ uint32_t pack2(float a0, float a1) {
+        return (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
+    }
+    static __device__ __forceinline__ uint32_t rest2(uint32_t hi, float a0, float a1) {
+        return pack2(a0 - bf16_to_f32((uint16_t)hi), a1 - bf16_to_f32((uint16_t)(hi >> 16)));
+    }
 };
 
 // KV storage formats: Raw = one lane's 8-element chunk as loaded from HBM,
@@ -297,11 +310,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 const int d0 = 32 * k + 8 * g4 + 2 * w;
                 const float x0 = qv ? qrow[d0] * qscale : 0.0f;
                 const float x1 = qv ? qrow[d0 + 1] * qscale : 0.0f;
-                const uint16_t h0 = M::cvt(x0), h1 = M::cvt(x1);
-                hw[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                if constexpr (kSplit) {
-                    lw[w] = (uint32_t)M::cvt(x0 - M::back(h0)) | ((uint32_t)M::cvt(x1 - M::back(h1)) << 16);
-                }
+                hw[w] = M::pack2(x0, x1);
+                if constexpr (kSplit) lw[w] = M::rest2(hw[w], x0, x1);
             }
             qf[k] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
             if constexpr (kSplit) qfl[k] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
@@ -632,10 +642,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                         a0 *= vscale_of(vb, kk, 2 * w) * pw[vb];
                         a1 *= vscale_of(vb, kk, 2 * w + 1) * pw[vb];
                     }
-                    const uint16_t h0 = M::cvt(a0), h1 = M::cvt(a1);
-                    ph[w] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                    if constexpr (kSplitP)
-                        pl[w] = (uint32_t)M::cvt(a0 - M::back(h0)) | ((uint32_t)M::cvt(a1 - M::back(h1)) << 16);
+                    ph[w] = M::pack2(a0, a1);
+                    if constexpr (kSplitP) pl[w] = M::rest2(ph[w], a0, a1);
                 }
                 pf[kk] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
                 if constexpr (kSplitP) pfl[kk] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
