@@ -312,3 +312,58 @@ def test_q8_prefill_chunk_edges(orc, dev, block, m, window, hist):
         ref = orc.attention_token(q[pos], kq, vq, fmt, n_heads, n_kv, d, start, pos + 1,
                                   key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
         assert float(np.abs(got[i] - ref).max()) <= TOL, (i, float(np.abs(got[i] - ref).max()))
+
+
+@pytest.mark.parametrize("kv", ["q8", "q8b", "turbo"])
+def test_quantised_prefill_into_a_middle_sequence_slot(orc, dev, kv):
+    """Q8 (row / block scales) and Turbo prefill into sequence slot 1 of a 3-slot,
+    2-layer run state whose slots 0 and 2 hold other rows: the outputs match the
+    oracle over slot 1's own rows (cache and scale offsets of slot and layer), and
+    the neighbouring slots are left byte-for-byte unchanged."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv, d, L = 16, 4, 128, 160
+    turbo = kv == "turbo"
+    p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=L, n_seq=3,
+                  kv_dtype=ffi.DTYPE_TURBO if turbo else ffi.DTYPE_Q8, q8_block_scales=kv == "q8b",
+                  rope_mode=ffi.ROPE_NONE)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(123)
+    rows = {sq: [rng.standard_normal((L, w)).astype(np.float32) for w in (p.q_dim, p.kv_dim, p.kv_dim)]
+            for sq in range(3)}
+    layer = 1
+    for sq in (0, 2):
+        q, k, v = rows[sq]
+        rt.prefill_attention_chunk(p, s, layer, 0, q[:100], k[:100], v[:100], seq=sq)
+    snap = lambda sq: (rt.read_turbo_rows(p, s, layer, 0, 100, seq=sq) if turbo
+                       else (rt.read_kv_rows(p, s, layer, 0, 100, seq=sq), rt.read_kv_scales(p, s, layer, 0, 100, seq=sq)))
+    before = {sq: snap(sq) for sq in (0, 2)}
+    q, k, v = rows[1]
+    hist, m = 30, 130
+    rt.prefill_attention_chunk(p, s, layer, 0, q[:hist], k[:hist], v[:hist], seq=1)
+    got = rt.prefill_attention_chunk(p, s, layer, hist, q[hist:hist + m], k[hist:hist + m], v[hist:hist + m], seq=1)
+    n = hist + m
+    if turbo:
+        table = orc.turbo_sign_table(2, n_kv, d)
+        c = orc.TurboCache(n, n_kv, d)
+        for t in range(n):
+            orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
+        refs = [orc.attention_token_turbo(q[hist + i], c, table, layer, n_heads, 0, hist + i + 1) for i in range(m)]
+    else:
+        kq, vq = rt.read_kv_rows(p, s, layer, 0, n, seq=1)
+        ks, vs = rt.read_kv_scales(p, s, layer, 0, n, seq=1)
+        fmt = orc.Q8B if kv == "q8b" else orc.Q8
+        for t in range(n):  # slot 1's rows are the oracle's quantisation of its own k / v
+            ek, eks = orc.kv_quantize_row(k[t], kv == "q8b")
+            assert np.array_equal(kq[t], ek) and np.array_equal(ks[t], eks), t
+        refs = [orc.attention_token(q[hist + i], kq, vq, fmt, n_heads, n_kv, d, 0, hist + i + 1,
+                                    key_scale=ks.reshape(-1), value_scale=vs.reshape(-1)) for i in range(m)]
+    worst = max(float(np.abs(got[i] - refs[i]).max()) for i in range(m))
+    assert worst <= TOL, worst
+    for sq in (0, 2):
+        after = snap(sq)
+        if turbo:
+            for key in after:
+                assert np.array_equal(after[key], before[sq][key]), (sq, key)
+        else:
+            assert np.array_equal(after[0][0], before[sq][0][0]) and np.array_equal(after[0][1], before[sq][0][1])
+            assert np.array_equal(after[1][0], before[sq][1][0]) and np.array_equal(after[1][1], before[sq][1][1])
