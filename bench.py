@@ -18,6 +18,12 @@ Also reported in the same line:
   prefill      -- config 2 (Llama-3-8B-shaped causal prefill, 2048 tokens, f16,
                   RoPE fused) and the 8k target run, in TFLOP/s with
                   flops = 4 * Hq * d * sum_q visible(q)
+  deltanet     -- config 5 (gated DeltaNet, 16 heads, d128): 4096-token chunked
+                  prefill and one recurrent decode step
+  prefill_2048_quantised_cache -- run-state prefill of a 2048-token chunk over a
+                  Q8 and a Turbo cache, wall time per call with host buffers
+  encoder_siglip -- encoder self-attention at the Gemma 3 SigLIP shape (4096
+                  patches, 16 heads, d72, f32)
   roofline     -- the dominant kernel (decode) against 8 TB/s HBM
   cpu_baseline -- the CPU oracle (a C restatement of the reference's
                   attention_token, oracle/oracle.c) timed on this host's cores on
@@ -206,6 +212,20 @@ def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128, turbo=False):
     return (lambda: rt.prefill_attention_chunk(p, s, 0, 0, q, k, v)), flops, (p, s)
 
 
+def encoder_workload(dev, stream):
+    """Gemma 3 SigLIP vision attention: one noncausal sequence of 4096 patches, 16
+    heads of dim 72, f32 rows (gr_encoder_self_attention)."""
+    import torch
+    from gguf_runner_amd import ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    q, k, v = (torch.randn((4096, 16 * 72), generator=g, device=dev) for _ in range(3))
+    out = torch.empty_like(q)
+    call = lambda: ops.encoder_self_attention(q, k, v, n_seq=1, tokens=4096, heads=16, head_dim=72,
+                                              out=out, stream=stream)
+    return call, 4 * 16 * 72 * 4096 * 4096, (q, k, v, out)
+
+
 def cpu_baseline(lens, n_heads=32, n_kv=4, d=128, budget_s=10.0):
     """Oracle attention_token on the host cores over a bounded prefix of the decode
     batch (whole sequences, in batch order), as the reference runs it: one sequence
@@ -313,17 +333,7 @@ def run_one(args, dev, stream, lens) -> int:
             flops = 4 * Hq * d * sum(min(i + 1, W) if W else i + 1 for i in range(S))
             res[key] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gflop": flops / 1e9}
     elif args.only == "encoder":
-        # Gemma 3 SigLIP vision attention: one noncausal sequence of 4096 patches,
-        # 16 heads of dim 72, f32 (gr_encoder_self_attention)
-        import torch
-        from gguf_runner_amd import ops
-        g = torch.Generator(device=dev)
-        g.manual_seed(9)
-        q, k, v = (torch.randn((4096, 16 * 72), generator=g, device=dev) for _ in range(3))
-        out = torch.empty_like(q)
-        call = lambda: ops.encoder_self_attention(q, k, v, n_seq=1, tokens=4096, heads=16, head_dim=72,
-                                                  out=out, stream=stream)
-        flops = 4 * 16 * 72 * 4096 * 4096
+        call, flops, keep = encoder_workload(dev, stream)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only == "deltanet":
@@ -438,6 +448,31 @@ def main() -> int:
         "prefill": pre,
         "wall_ms_per_step": round(dec_wall, 5),
     }
+
+    # config 5: gated DeltaNet, 4096-token chunked prefill and one recurrent step
+    pcall, _keep_d = deltanet_workload(dev, 4096, 5)
+    d_ms, _ = _timed(pcall, max(5, args.steps // 5), 2, stream)
+    scall, _keep_s = deltanet_workload(dev, 1, 6)
+    s_ms, _ = _timed(scall, args.steps, args.warmup, stream)
+    line["deltanet"] = {"prefill_ms": round(d_ms, 4), "prefill_tok_s": round(4096 / (d_ms * 1e-3)),
+                        "decode_step_ms": round(s_ms, 5)}
+    del _keep_d, _keep_s, pcall, scall
+
+    # prefill of a 2048-token chunk over Q8 and Turbo run-state caches (host q / k / v
+    # rows: the wall time includes their upload and the download of the outputs)
+    qpre = {}
+    for key, blk, tb in (("q8", False, False), ("turbo", False, True)):
+        qcall, flops, _keep_q = prefill_q8_workload(2048, 8, blk, turbo=tb)
+        _, w_ms = _timed(qcall, max(5, args.steps // 5), 2, stream)
+        qpre[key] = {"call_ms": round(w_ms, 4), "gflop": round(flops / 1e9, 3)}
+        del _keep_q, qcall
+    line["prefill_2048_quantised_cache"] = qpre
+
+    ecall, eflops, _keep_e = encoder_workload(dev, stream)
+    e_ms, _ = _timed(ecall, max(5, args.steps // 5), 2, stream)
+    line["encoder_siglip"] = {"ms": round(e_ms, 4), "tflops": round(eflops / (e_ms * 1e-3) / 1e12, 2)}
+    del _keep_e, ecall
+
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(lens)
     print(json.dumps(line), flush=True)
