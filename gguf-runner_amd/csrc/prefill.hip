@@ -241,6 +241,10 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
     __shared__ __attribute__((aligned(16))) uint16_t Ks1[BN * D];
     __shared__ __attribute__((aligned(16))) uint16_t Vs0[BN * D];
     __shared__ __attribute__((aligned(16))) uint16_t Vs1[BN * D];
+    // bf16 d256: the Q residual fragments live in LDS (per wave, [k-step][lane])
+    // instead of 64 VGPRs, which the d256 accumulators need
+    constexpr bool kQloLds = kSplit && D == 256;
+    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? NW * (D / 16) * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
 
         // Q fragments (B operand): lane (query ln, group lg) holds d = 16 s + 8 lg .. +7.
         uint4 qf[D / 16];
-        uint4 qfl[kSplit ? D / 16 : 1];
+        uint4 qfl[kSplit && !kQloLds ? D / 16 : 1];
         bool q_done = false;
         if constexpr (D == 128) {
             if (p.q_raw) {
@@ -341,7 +345,11 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
             if constexpr (kSplit) {
                 const uint16_t* qrl = (const uint16_t*)p.q_lo + qoff;
 #pragma unroll
-                for (int s = 0; s < D / 16; s++) qfl[s] = *(const uint4*)(qrl + 16 * s);
+                for (int s = 0; s < D / 16; s++) {
+                    const uint4 x = *(const uint4*)(qrl + 16 * s);
+                    if constexpr (kQloLds) Qlo[(wave * (D / 16) + s) * 64 + lane] = x;
+                    else qfl[s] = x;
+                }
             }
         }
 
@@ -405,7 +413,8 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                 const int c = (2 * s + lg) ^ swz_k;
                 const uint4 a = *(const uint4*)(krow + c * 8);
                 sacc = M::mma(a, qf[s], s == 0 ? (kFold ? negm : zero) : sacc);
-                if constexpr (kSplit) sacc = M::mma(a, qfl[s], sacc);
+                if constexpr (kQloLds) sacc = M::mma(a, Qlo[(wave * (D / 16) + s) * 64 + lane], sacc);
+                else if constexpr (kSplit) sacc = M::mma(a, qfl[s], sacc);
             }
             // V^T fragment (dt, t) of this sub-tile: two transpose reads
             auto load_va = [&](int dt, int t) {
