@@ -118,6 +118,10 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
     constexpr int kMs = KH == 2 ? 4 * (2 + NBS) * 64 : 1;
     __shared__ float Mo[kMo];
     __shared__ float Ms[kMs];
+    // head_dim 256: the Q residual fragments live in LDS (per wave, [k-step][lane])
+    // instead of 64 VGPRs, which the accumulators need
+    constexpr bool kQloLds = D == 256;
+    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? 4 * (D / 16) * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -161,7 +165,7 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
 
     // Q (B operand): lane (row ln, half lg) holds d = 16 s + 8 lg .. +7 of k-step s,
     // scaled by score_scale * log2(e) and a per-row power of two 2^eq.
-    uint4 qf[D / 16], qfl[D / 16];
+    uint4 qf[D / 16], qfl[kQloLds ? 1 : D / 16];
     float qfac;
     {
         const float* qrow = p.q + ((size_t)my_row_c * p.n_heads + h) * D + 8 * lg;
@@ -190,9 +194,16 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
 #pragma unroll
             for (int w = 0; w < 4; w++) hw[w] = q8p_split2(qv[s][2 * w] * up, qv[s][2 * w + 1] * up, &lw[w]);
             qf[s] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            qfl[s] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            const uint4 lo4 = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            if constexpr (kQloLds) Qlo[(rg * (D / 16) + s) * 64 + lane] = lo4;
+            else qfl[s] = lo4;
         }
     }
+
+    auto qlo = [&](int s) -> uint4 {
+        if constexpr (kQloLds) return Qlo[(rg * (D / 16) + s) * 64 + lane];
+        else return qfl[s];
+    };
 
     // keys [kbeg, kend) are visible to some row of this block
     const int kend = p.bidirectional ? P0 + m : P0 + min(q0 + BM, m);
@@ -287,7 +298,7 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
             for (int s = 0; s < D / 16; s++) {
                 const uint4 a = kop(s);
                 acc = q8p_mma(a, qf[s], acc);
-                acc = q8p_mma(a, qfl[s], acc);
+                acc = q8p_mma(a, qlo(s), acc);
             }
             float ks[16];
             lane_scales(0, 0, ks);
@@ -299,9 +310,9 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
             for (int u = 0; u < NB; u++) {
                 const uint4 a0 = kop(2 * u), a1 = kop(2 * u + 1);
                 f32x16 acc = q8p_mma(a0, qf[2 * u], zero);
-                acc = q8p_mma(a0, qfl[2 * u], acc);
+                acc = q8p_mma(a0, qlo(2 * u), acc);
                 acc = q8p_mma(a1, qf[2 * u + 1], acc);
-                acc = q8p_mma(a1, qfl[2 * u + 1], acc);
+                acc = q8p_mma(a1, qlo(2 * u + 1), acc);
                 float ks[16];
                 lane_scales(0, u, ks);
 #pragma unroll
