@@ -3,14 +3,14 @@
 // kv_write_token, inference.rs:1886-1917) on gfx950 MFMA.  Replaces the
 // token-serial attention of the prefill loop (inference.rs:2981-3017, one
 // attention_token per token) for Q8 run states: one launch per chunk, every
-// K / V tile read once per 128 query rows.
+// K / V tile read once per 128 (d128) or 64 (d256) query rows.
 //
-// Workgroup = 128 query rows of one query head (4 row groups of 32) x KH key
-// halves: head_dim 128 runs 8 waves over 128-key tiles, wave (row group, half)
-// taking the 32-key sub-tiles 2 j + half, so each SIMD holds two waves (the
-// MFMAs of one overlap the VALU work of the other); the two halves' (max, sum,
-// O) merge through LDS at the end.  head_dim 256 (more registers) runs 4 waves
-// over both sub-tiles of 64-key tiles.  The tile goes global -> registers ->
+// Workgroup = row groups of 32 query rows of one query head x 2 key halves,
+// wave (row group, half) taking the 32-key sub-tiles 2 j + half of every tile;
+// the two halves' (max, sum, O) merge through LDS at the end.  head_dim 128: 4
+// row groups, 128-key tiles, 8 waves (two per SIMD: the MFMAs of one overlap
+// the VALU work of the other).  head_dim 256: 2 row groups, 64-key tiles, 4
+// waves (one per SIMD, for the registers).  The tile goes global -> registers ->
 // LDS (the next tile's loads are in flight while the current one is computed),
 // the int8 codes converted to f16 on the way in (exact: |code| <= 127), K and V row-major with
 // their 16-byte chunks XOR-swizzled per row like the f16 prefill kernel; the
@@ -40,15 +40,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define Q8P_LDS __attribute__((address_space(3)))
 
-constexpr int kQ8BM = 128;        // query rows per workgroup
 constexpr float kQ8Lazy = 8.0f;   // lazy softmax rescale threshold (log2 units)
 
-// KH key halves per workgroup (2 where two waves per SIMD fit the registers),
-// BN keys per tile (each wave takes BN / 32 / KH sub-tiles between barriers)
+// RG row groups of 32 query rows x KH key halves per workgroup (one wave each),
+// BN keys per tile (each wave takes BN / 32 / KH sub-tiles between barriers).
+// d128: 128 rows, 8 waves (two per SIMD).  d256: 64 rows, 4 waves (one per
+// SIMD, which its registers need), so that 8-head models still launch one
+// workgroup per CU for a 2048-token chunk.
 template <int D>
 struct Q8Tile {
-    static constexpr int KH = D == 128 ? 2 : 1;
+    static constexpr int RG = D == 128 ? 4 : 2;
+    static constexpr int KH = 2;
     static constexpr int BN = D == 128 ? 128 : 64;
+    static constexpr int BM = 32 * RG;
+    static constexpr int NT = 64 * RG * KH;
 };
 
 __device__ __forceinline__ f32x16 q8p_mma(const uint4& a, const uint4& b, const f32x16& c) {
@@ -99,10 +104,10 @@ __device__ __forceinline__ int q8p_ilog2(float x) { return (int)((__float_as_uin
 __device__ __forceinline__ int q8p_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
 
 template <int D, bool BLOCK>
-__global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(const PrefillQ8Launch p) {
-    constexpr int KH = Q8Tile<D>::KH;
-    constexpr int NT = 256 * KH;          // threads
-    constexpr int BM = kQ8BM, BN = Q8Tile<D>::BN;
+__global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const PrefillQ8Launch p) {
+    constexpr int KH = Q8Tile<D>::KH, RG = Q8Tile<D>::RG;
+    constexpr int NT = Q8Tile<D>::NT;     // threads
+    constexpr int BM = Q8Tile<D>::BM, BN = Q8Tile<D>::BN;
     constexpr int NB = D / 32;            // 32-element blocks per head (k-step pairs, O^T tiles)
     constexpr int NBS = BLOCK ? NB : 1;   // scales per key and head
     constexpr int CPR = D / 16;           // 16-code chunks per cache row
@@ -110,23 +115,24 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
     constexpr int SCL = (2 * NBS * BN + NT - 1) / NT;  // scales per thread per tile
     static_assert(KCH >= 1 && BN * CPR % NT == 0, "tile");
 
-    __shared__ __attribute__((aligned(16))) uint16_t Kt[BN * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[BN * D];
+    __shared__ __attribute__((aligned(16))) uint16_t KVt[2 * BN * D];
+    uint16_t* const Kt = KVt;
+    uint16_t* const Vt = KVt + BN * D;
     __shared__ __attribute__((aligned(16))) float Sc[2 * NBS * BN];  // [k|v][block][key]
     // key-half merge: O^T accumulators [row group][dt][e][lane], (m, l, pw) [row group][lane]
-    constexpr int kMo = KH == 2 ? 4 * NB * 16 * 64 : 1;
-    constexpr int kMs = KH == 2 ? 4 * (2 + NBS) * 64 : 1;
-    __shared__ float Mo[kMo];
-    __shared__ float Ms[kMs];
+    // (O^T goes into the K / V tiles, free once the key loop is done)
+    static_assert(RG * NB * 16 * 64 * 4 <= 2 * BN * D * 2, "merge buffer fits the tiles");
+    float* const Mo = (float*)KVt;
+    __shared__ float Ms[RG * (2 + NBS) * 64];
     // head_dim 256: the Q residual fragments live in LDS (per wave, [k-step][lane])
     // instead of 64 VGPRs, which the accumulators need
     constexpr bool kQloLds = D == 256;
-    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? 4 * (D / 16) * 64 : 1];
+    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? RG * (D / 16) * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rg = wave & 3, kh = wave >> 2;  // row group, key half
+    const int rg = wave % RG, kh = wave / RG;  // row group, key half
     const int ln = lane & 31, lg = lane >> 5;
     const int m = p.n_tokens;
     const int P0 = (int)p.base_pos;
@@ -432,6 +438,7 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
     // the same rows over disjoint keys.  A half with no keys has pw = 0, l = 0.
     float wa[NBS];  // final factor on O per block (1 / pw, or 1 after the merge)
     if constexpr (KH == 2) {
+        __syncthreads();  // every wave is done with the tiles that Mo overlays
         if (kh == 1) {
 #pragma unroll
             for (int dt = 0; dt < NB; dt++)
@@ -491,8 +498,8 @@ __global__ __launch_bounds__(256 * Q8Tile<D>::KH, 1) void prefill_q8_kernel(cons
 
 template <int D, bool BLOCK>
 hipError_t launch_q8_d(const PrefillQ8Launch& p, hipStream_t st) {
-    const int n_qb = (p.n_tokens + kQ8BM - 1) / kQ8BM;
-    prefill_q8_kernel<D, BLOCK><<<dim3(p.n_heads, n_qb), 256 * Q8Tile<D>::KH, 0, st>>>(p);
+    const int n_qb = (p.n_tokens + Q8Tile<D>::BM - 1) / Q8Tile<D>::BM;
+    prefill_q8_kernel<D, BLOCK><<<dim3(p.n_heads, n_qb), Q8Tile<D>::NT, 0, st>>>(p);
     return hipGetLastError();
 }
 
