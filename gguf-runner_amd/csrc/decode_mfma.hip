@@ -175,6 +175,10 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     constexpr int kLoopBytes = kVtBytes + kScBytes + kKBytes;
     constexpr int kMergeBytes = (kMdWaves * 16 * (D + 1) + 2 * kMdWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
+    // d256 with block scales: the Q residual fragments live in LDS (per wave,
+    // [k-step][lane]) instead of 32 VGPRs, which the per-block chains need
+    constexpr bool kQloLds = kSplit && kBlock && D == 256;
+    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? kMdWaves * KS * 64 : 1];
 
     const int kv_mul = p.n_heads / p.n_kv_heads;
     const int tid = threadIdx.x;
@@ -280,7 +284,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // f16: each query row is also multiplied by a power of two 2^e that puts its
     // largest element near 2^14, so that the lo halves of the hi/lo split stay
     // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
-    uint4 qf[KS], qfl[kSplit ? KS : 1];
+    uint4 qf[KS], qfl[kSplit && !kQloLds ? KS : 1];
     float qback = 1.0f;
     {
         const bool qv = l16 < kv_mul;
@@ -314,7 +318,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 if constexpr (kSplit) lw[w] = M::rest2(hw[w], x0, x1);
             }
             qf[k] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            if constexpr (kSplit) qfl[k] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            if constexpr (kQloLds) Qlo[(wave * KS + k) * 64 + lane] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            else if constexpr (kSplit) qfl[k] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
         }
     }
 
@@ -530,7 +535,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 if constexpr (kBlock) {
                     // k-step k is scale block k: its own product, then scaled
                     f32x4 part = M::mma(ka, qf[k], zero);
-                    if constexpr (kSplit) part = M::mma(ka, qfl[k], part);
+                    if constexpr (kQloLds) part = M::mma(ka, Qlo[(wave * KS + k) * 64 + lane], part);
+                    else if constexpr (kSplit) part = M::mma(ka, qfl[k], part);
                     const float4 k4 = *(const float4*)(sct + k * TILE + 16 * sb + 4 * g4);
                     const float kb[4] = {k4.x, k4.y, k4.z, k4.w};
 #pragma unroll
@@ -538,7 +544,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                         sacc[sb][j] = k == 0 ? part[j] * kb[j] : fmaf(part[j], kb[j], sacc[sb][j]);
                 } else {
                     sacc[sb] = M::mma(ka, qf[k], k == 0 ? zero : sacc[sb]);
-                    if constexpr (kSplit) sacc[sb] = M::mma(ka, qfl[k], sacc[sb]);
+                    if constexpr (kQloLds) sacc[sb] = M::mma(ka, Qlo[(wave * KS + k) * 64 + lane], sacc[sb]);
+                    else if constexpr (kSplit) sacc[sb] = M::mma(ka, qfl[k], sacc[sb]);
                 }
             }
             if constexpr (kQ8 && !kBlock) {
