@@ -425,7 +425,8 @@ uint16_t orc_f32_to_f16(float f) {
     memcpy(&x, &f, 4);
     uint32_t sign = (x >> 16) & 0x8000u;
     uint32_t ax = x & 0x7fffffffu;
-    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0));
+    if (ax >= 0x7f800000u) /* inf, or NaN keeping its top payload bits, quieted (gguf.rs:78-84) */
+        return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? (((ax & 0x7fffffu) >> 13) | 0x200u) : 0));
     if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to inf */
     if (ax < 0x38800000u) {                                   /* subnormal / zero in f16 */
         if (ax < 0x33000000u) return (uint16_t)sign;          /* < half the smallest subnormal */
@@ -451,6 +452,20 @@ uint16_t orc_f32_to_bf16(float f) {
     uint32_t lsb = (x >> 16) & 1u;
     x += 0x7fffu + lsb;
     return (uint16_t)(x >> 16);
+}
+
+/* Array forms of the four conversions (element-wise, for the pinning tests). */
+void orc_f32_to_f16_n(const float* x, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(x[i]);
+}
+void orc_f32_to_bf16_n(const float* x, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_bf16(x[i]);
+}
+void orc_f16_to_f32_n(const uint16_t* h, float* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_f16_to_f32(h[i]);
+}
+void orc_bf16_to_f32_n(const uint16_t* h, float* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_bf16_to_f32(h[i]);
 }
 
 static void store_kv(void* base, size_t idx, int fmt, float v) {

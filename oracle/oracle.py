@@ -52,6 +52,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_f32_to_f16.restype = ctypes.c_uint16
     L.orc_f32_to_bf16.argtypes = [_f]
     L.orc_f32_to_bf16.restype = ctypes.c_uint16
+    for name in ("orc_f32_to_f16_n", "orc_f32_to_bf16_n", "orc_f16_to_f32_n", "orc_bf16_to_f32_n"):
+        getattr(L, name).argtypes = [_p, _p, _sz]
     L.orc_rope_freqs.argtypes = [_f, _i, _p]
     L.orc_rope_cache.argtypes = [_p, _i, _i64, _f, _p, _p]
     L.orc_apply_rope_qk.argtypes = [_p, _p, _i, _i, _i, _i, _p, _p, _i, _i, _f]
@@ -388,6 +390,38 @@ def bf16_bits(x) -> np.ndarray:
     r = ((a + 0x7FFF + ((a >> 16) & 1)) >> 16).astype(np.uint16)
     r[nan] = ((a[nan] >> 16) | 0x40).astype(np.uint16)
     return r
+
+
+def c_f32_to_f16(x) -> np.ndarray:
+    """orc_f32_to_f16 element-wise (the raw f16 cache rounding, gguf.rs:72-106)."""
+    x = _f32(x).reshape(-1)
+    out = np.empty(x.size, np.uint16)
+    lib().orc_f32_to_f16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def c_f32_to_bf16(x) -> np.ndarray:
+    """orc_f32_to_bf16 element-wise (gguf.rs:108-117)."""
+    x = _f32(x).reshape(-1)
+    out = np.empty(x.size, np.uint16)
+    lib().orc_f32_to_bf16_n(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def c_f16_to_f32(bits) -> np.ndarray:
+    """orc_f16_to_f32 element-wise (gguf.rs:26-53)."""
+    b = np.ascontiguousarray(np.asarray(bits, np.uint16)).reshape(-1)
+    out = np.empty(b.size, np.float32)
+    lib().orc_f16_to_f32_n(_ptr(b), _ptr(out), b.size)
+    return out
+
+
+def c_bf16_to_f32(bits) -> np.ndarray:
+    """orc_bf16_to_f32 element-wise (gguf.rs:55-58)."""
+    b = np.ascontiguousarray(np.asarray(bits, np.uint16)).reshape(-1)
+    out = np.empty(b.size, np.float32)
+    lib().orc_bf16_to_f32_n(_ptr(b), _ptr(out), b.size)
+    return out
 
 
 def bf16_to_f32(bits) -> np.ndarray:
