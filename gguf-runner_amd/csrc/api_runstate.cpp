@@ -239,6 +239,10 @@ int validate_config(const gr_attn_config* c) {
         return fail(GR_ERR_ARG, "q_norm and k_norm must be both set or both NULL");
     if (c->ssm_n_heads < 0 || (c->ssm_n_heads > 0 && c->ssm_head_dim != 128))
         return fail(GR_ERR_ARG, "DeltaNet state needs ssm_head_dim 128");
+    // One SSM state and conv history per layer, as one reference RunState holds:
+    // the SSM entry points and the prefill-cache sections take no sequence slot.
+    if (c->ssm_n_heads > 0 && c->n_seq != 1)
+        return fail(GR_ERR_ARG, "an SSM state (ssm_n_heads > 0) needs n_seq == 1: the state has no sequence slots");
     if (c->ssm_conv1d) {
         if (c->ssm_n_heads <= 0 || c->ssm_n_k_heads <= 0 || c->ssm_conv_kernel < 1 || c->ssm_conv_kernel > 9)
             return fail(GR_ERR_ARG, "invalid qwen3next SSM config");
@@ -686,9 +690,8 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
     float* vin = cv.take<float>((size_t)m * s->kv_dim);
     float* xo = cv.take<float>((size_t)m * s->q_dim);
     if ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb))) return rc;
-    const size_t eb = elem_bytes(s->cfg.kv_dtype);
-    void* kc = (char*)layer_k(s, layer) + (size_t)seq * s->seq_stride * eb;
-    void* vc = (char*)layer_v(s, layer) + (size_t)seq * s->seq_stride * eb;
+    void* kc = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
+    void* vc = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     if (mfma) {
         gr_prefill_args a{};
         a.n_tokens = m;

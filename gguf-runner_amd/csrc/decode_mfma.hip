@@ -27,6 +27,7 @@
 //                 exactly one block), scaled and summed; one P operand per
 //                 V block, scaled by that block's v scale.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "gr_common.hpp"
@@ -741,20 +742,28 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     }
 }
 
-// Workgroups of kernel k that fit on the device at once (CUs x occupancy).
+// Workgroups of kernel k that fit on the current device at once (CUs x
+// occupancy).  A device property: computed once per (template instance, device)
+// and cached read-only; concurrent first calls compute the same value.
 template <typename KV, int D>
 static int resident_wgs() {
-    static int cached = 0;  // per template instance; same value for every device of a node
-    if (cached == 0) {
-        int dev = 0, n_cu = 0, occ = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_mfma_kernel<KV, D, 1>, MdWaves<KV, D>::value * 64, 0) !=
-                hipSuccess)
-            return 256;
-        cached = std::max(1, n_cu * std::max(1, occ));
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cached[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    const int slot = dev >= 0 && dev < kMaxDev ? dev : -1;
+    if (slot >= 0) {
+        const int c = cached[slot].load(std::memory_order_relaxed);
+        if (c > 0) return c;
     }
-    return cached;
+    int n_cu = 0, occ = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_mfma_kernel<KV, D, 1>, MdWaves<KV, D>::value * 64, 0) !=
+            hipSuccess)
+        return 256;
+    const int v = std::max(1, n_cu * std::max(1, occ));
+    if (slot >= 0) cached[slot].store(v, std::memory_order_relaxed);
+    return v;
 }
 
 template <typename KV, int D>

@@ -125,3 +125,17 @@ def test_ssm_config_validation(pkg):
         assert "missing qwen3next SSM tensors" in str(e)
     else:
         raise AssertionError("accepted missing ssm_a")
+
+
+def test_ssm_state_needs_one_sequence_slot(pkg):
+    """The SSM state and conv history exist once per layer, as in one reference
+    RunState (types.rs:745-809); a multi-slot state with an SSM is refused before any
+    device work."""
+    from gguf_runner_amd import ffi, runtime as rt
+    try:
+        rt.malloc_run_state(rt.Config(n_layers=1, n_heads=2, n_kv_heads=1, head_dim=128, seq_len=8,
+                                      n_seq=2, ssm_n_heads=2, ssm_head_dim=128))
+    except ffi.GrError as e:
+        assert e.code == ffi.GR_ERR_ARG and "n_seq == 1" in str(e)
+    else:
+        raise AssertionError("accepted an SSM state with two sequence slots")

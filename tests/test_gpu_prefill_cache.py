@@ -47,6 +47,8 @@ def _fill(rt, p, s, seq, rows, seed):
         for t in range(rows):
             s.k[:], s.v[:] = kr[l, t], vr[l, t]
             rt.kv_write_token(p, s, l, t, seq=seq)
+    if not p.ssm_n_heads:
+        return kr, vr, None, None
     conv = rng.standard_normal((L, CONV_K - 1, CONV_DIM)).astype(np.float32)
     state = rng.standard_normal((L, SSM_H, D, D)).astype(np.float32)
     for l in range(L):
@@ -58,7 +60,7 @@ def _fill(rt, p, s, seq, rows, seed):
 def _expected_host_state(orc, fmt, block, seq_len, kr, vr, conv, state):
     g = orc.gpfc
     st = g.HostState(g.TURBO if fmt == "turbo" else g.Q8, block, L, seq_len, NKV, D,
-                     conv.size, state.size)
+                     0 if conv is None else conv.size, 0 if state is None else state.size)
     kv = NKV * D
     if fmt == "q8":
         spr = kv // 32 if block else 1
@@ -80,8 +82,9 @@ def _expected_host_state(orc, fmt, block, seq_len, kr, vr, conv, state):
                               ("key_rnorm", c.kres), ("value_rnorm", c.vres)):
                 n = arr.size
                 st.a[name][l * n:(l + 1) * n] = arr
-    st.a["ssm_conv"][:] = conv.reshape(-1)
-    st.a["ssm_state"][:] = state.reshape(-1)
+    if conv is not None:
+        st.a["ssm_conv"][:] = conv.reshape(-1)
+        st.a["ssm_state"][:] = state.reshape(-1)
     return st
 
 
@@ -107,43 +110,55 @@ def _same_rows(a, b):
                     assert np.array_equal(uu, vv)
 
 
+# (sequence slots, snapshot slot, SSM state): an SSM state has one slot (as one
+# reference RunState), so the two-slot cases carry KV sections only.
+SLOTS = [(2, 1, False), (1, 0, True)]
+
+
+@pytest.mark.parametrize("n_seq,slot,ssm", SLOTS)
 @pytest.mark.parametrize("fmt,block", FORMATS)
-def test_snapshot_matches_oracle_bytes(orc, dev, fmt, block):
-    """Slot 1 of a two-slot state (slot 0 holds other rows): the device blob is the
-    oracle's blob of the same rows, codes, scales and SSM arrays, byte for byte."""
+def test_snapshot_matches_oracle_bytes(orc, dev, fmt, block, n_seq, slot, ssm):
+    """The last slot of the state (slot 0 of a two-slot state holds other rows): the
+    device blob is the oracle's blob of the same rows, codes, scales and SSM arrays,
+    byte for byte."""
     from gguf_runner_amd import ffi, runtime as rt
-    p, s = _config(rt, ffi, fmt, block, seq_len=48, n_seq=2)
-    _fill(rt, p, s, 0, 40, seed=10)
-    kr, vr, conv, state = _fill(rt, p, s, 1, K, seed=11)
+    p, s = _config(rt, ffi, fmt, block, seq_len=48, n_seq=n_seq, ssm=ssm)
+    if slot:
+        _fill(rt, p, s, 0, 40, seed=10)
+    kr, vr, conv, state = _fill(rt, p, s, slot, K, seed=11)
     toks = list(range(1000, 1000 + K))
-    blob = rt.snapshot(p, s, toks, 4_000_000_123, 0xFEEDFACECAFEBEEF, seq=1)
+    blob = rt.snapshot(p, s, toks, 4_000_000_123, 0xFEEDFACECAFEBEEF, seq=slot)
     ref = orc.gpfc.snapshot(_expected_host_state(orc, fmt, block, 48, kr, vr, conv, state),
                             toks, 4_000_000_123, 0xFEEDFACECAFEBEEF)
     assert len(blob) == len(ref)
     assert blob == ref
 
 
+@pytest.mark.parametrize("n_seq,slot,ssm", SLOTS)
 @pytest.mark.parametrize("fmt,block", FORMATS)
-def test_inject_restrides_and_decode_continues(orc, dev, fmt, block):
-    """The blob of slot 1 (context 48) injected into slot 1 of a state with context 80:
-    the rows and SSM arrays read back equal the source's, slot 0 is untouched, the
-    new state's snapshot differs only in seq_len_at_render, and the next token's
-    attention over the injected rows equals the source state's."""
+def test_inject_restrides_and_decode_continues(orc, dev, fmt, block, n_seq, slot, ssm):
+    """The blob of the last slot (context 48) injected into the same slot of a state
+    with context 80: the rows and SSM arrays read back equal the source's, slot 0 of
+    a two-slot state is untouched, the new state's snapshot differs only in
+    seq_len_at_render, and the next token's attention over the injected rows equals
+    the source state's."""
     from gguf_runner_amd import ffi, runtime as rt
-    pa, sa = _config(rt, ffi, fmt, block, seq_len=48, n_seq=2)
-    _fill(rt, pa, sa, 1, K, seed=12)
+    pa, sa = _config(rt, ffi, fmt, block, seq_len=48, n_seq=n_seq, ssm=ssm)
+    _fill(rt, pa, sa, slot, K, seed=12)
     toks = list(range(7, 7 + K))
-    blob = rt.snapshot(pa, sa, toks, 1, 2, seq=1)
-    pb, sb = _config(rt, ffi, fmt, block, seq_len=80, n_seq=2)
-    _fill(rt, pb, sb, 0, 5, seed=13)
-    slot0 = _rows(rt, pb, sb, fmt, 0, 5)
-    assert rt.inject(pb, sb, blob, seq=1) == K
-    _same_rows(_rows(rt, pb, sb, fmt, 1, K), _rows(rt, pa, sa, fmt, 1, K))
-    _same_rows(_rows(rt, pb, sb, fmt, 0, 5), slot0)
-    for l in range(L):
+    blob = rt.snapshot(pa, sa, toks, 1, 2, seq=slot)
+    pb, sb = _config(rt, ffi, fmt, block, seq_len=80, n_seq=n_seq, ssm=ssm)
+    if slot:
+        _fill(rt, pb, sb, 0, 5, seed=13)
+        slot0 = _rows(rt, pb, sb, fmt, 0, 5)
+    assert rt.inject(pb, sb, blob, seq=slot) == K
+    _same_rows(_rows(rt, pb, sb, fmt, slot, K), _rows(rt, pa, sa, fmt, slot, K))
+    if slot:
+        _same_rows(_rows(rt, pb, sb, fmt, 0, 5), slot0)
+    for l in range(L if ssm else 0):
         assert np.array_equal(rt.read_ssm_state(pb, sb, l), rt.read_ssm_state(pa, sa, l))
         assert np.array_equal(rt.read_ssm_conv_state(pb, sb, l), rt.read_ssm_conv_state(pa, sa, l))
-    blob_b = rt.snapshot(pb, sb, toks, 1, 2, seq=1)
+    blob_b = rt.snapshot(pb, sb, toks, 1, 2, seq=slot)
     assert blob_b[:24] + blob_b[28:] == blob[:24] + blob[28:]
     assert int.from_bytes(blob_b[24:28], "little") == 80
     rng = np.random.default_rng(14)
@@ -153,7 +168,7 @@ def test_inject_restrides_and_decode_continues(orc, dev, fmt, block):
     outs = []
     for p, s in ((pa, sa), (pb, sb)):
         s.q[:], s.k[:], s.v[:] = q, k, v
-        rt.attention_layer_token(p, s, 2, K, seq=1)
+        rt.attention_layer_token(p, s, 2, K, seq=slot)
         outs.append(s.xb.copy())
     assert float(np.abs(outs[0] - outs[1]).max()) <= 1e-5
 
