@@ -122,6 +122,8 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     return pl;
 }
 
+}  // namespace
+
 int check_decode(const gr_decode_args* a) {
     if (!a) return fail(GR_ERR_ARG, "gr_decode_attention: null args");
     if (a->n_seq <= 0 || a->n_heads <= 0 || a->n_kv_heads <= 0)
@@ -184,8 +186,6 @@ int check_decode(const gr_decode_args* a) {
         return fail(GR_ERR_ARG, "gr_decode_attention: workspace must be 256-byte aligned");
     return GR_OK;
 }
-
-}  // namespace
 
 int decode_enqueue(const gr_decode_args* a, hipStream_t st) { return decode_enqueue_ex(a, nullptr, st); }
 

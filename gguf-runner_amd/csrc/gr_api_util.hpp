@@ -15,6 +15,8 @@ void clear_error();
 size_t align_up(size_t x, size_t a);
 
 int check_decode_shape_only(const gr_decode_args* a);
+// Full argument check of gr_decode_attention (no HIP calls); GR_OK or the error.
+int check_decode(const gr_decode_args* a);
 int decode_enqueue(const gr_decode_args* a, hipStream_t st);
 int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st);
 // Turbo caches only: token-packed split kernel (DecodeLaunch::tok_pack).

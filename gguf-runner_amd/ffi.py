@@ -109,6 +109,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.gr_decode_workspace_size.restype = ctypes.c_size_t
     L.gr_decode_attention.argtypes = [ctypes.POINTER(DecodeArgs), _p]
     L.gr_decode_attention.restype = ctypes.c_int
+    L.gr_decode_attention_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _p]
+    L.gr_decode_attention_noalloc.restype = ctypes.c_int
     L.gr_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs)]
     L.gr_prefill_workspace_size.restype = ctypes.c_size_t
     L.gr_prefill_attention.argtypes = [ctypes.POINTER(PrefillArgs), _p]

@@ -119,6 +119,19 @@ size_t gr_decode_workspace_size(const gr_decode_args* a);
 /* Enqueue split-K flash decoding on `stream` (a hipStream_t, NULL = default). */
 int gr_decode_attention(const gr_decode_args* a, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc):
+ * gr_decode_attention with the split-K partials in a library-owned device array
+ * of GR_DECODE_NOALLOC_MAX_WORKSPACE bytes per GPU (held until the process
+ * ends) instead of a caller workspace.  a->workspace is ignored; everything
+ * else, the kernels and the results are those of gr_decode_attention.  Calls
+ * whose gr_decode_workspace_size exceeds the maximum fail with GR_ERR_ARG
+ * before any launch.  Allocates nothing.  Every call on one GPU uses the same
+ * array: calls that overlap on one GPU (other streams or threads) race, so
+ * serialise them. */
+#define GR_DECODE_NOALLOC_MAX_WORKSPACE (64u << 20)
+int gr_decode_attention_noalloc(const gr_decode_args* a, void* stream);
+
 /* ======================================================================
  * Prefill: a chunk of m new tokens of one sequence and one layer.
  * Replaces the serial per-token loop of transformer_prefill_batch
