@@ -117,7 +117,7 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     pl.ws_o_bytes = align_up(parts * per_part * a->head_dim * sizeof(float), 256);
     pl.ws_ml_bytes = align_up(parts * 2 * sizeof(float), 256);
     pl.ws_q_bytes = a->kv_dtype == GR_DTYPE_TURBO
-                        ? align_up((size_t)a->n_seq * a->n_heads * 2 * a->head_dim * sizeof(float), 256)
+                        ? align_up((size_t)a->n_seq * a->n_heads * turbo_query_ws_dwords(a->head_dim) * 4, 256)
                         : 0;
     return pl;
 }
@@ -133,9 +133,15 @@ int check_decode(const gr_decode_args* a) {
                     a->n_heads, a->n_kv_heads);
     const int kv_mul = a->n_heads / a->n_kv_heads;
     const bool pow2 = kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 8;
-    if (a->kv_dtype == GR_DTYPE_F32 ? !pow2 : (kv_mul > 16 || (a->head_dim == 64 && !pow2)))
+    // f32 caches and 16-bit caches at head_dim 64 run the VALU split kernel (kv_mul
+    // a power of two up to 8); the MFMA kernels (16-bit / Q8 at 128 / 256, Turbo at
+    // any head size) take up to 16 query heads per KV head.
+    const bool valu = a->kv_dtype == GR_DTYPE_F32 ||
+                      ((a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16) && a->head_dim == 64);
+    if (valu ? !pow2 : kv_mul > 16)
         return fail(GR_ERR_ARG,
-                    "gr_decode_attention: kv_mul %d unsupported (f32 KV: 1,2,4,8; 16-bit / Q8 KV: <= 16)",
+                    "gr_decode_attention: kv_mul %d unsupported (f32 KV and 16-bit KV at head_dim 64: 1,2,4,8; "
+                    "otherwise <= 16)",
                     kv_mul);
     if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
         return fail(GR_ERR_ARG, "gr_decode_attention: head_dim %d unsupported (64,128,256)",
@@ -143,15 +149,15 @@ int check_decode(const gr_decode_args* a) {
     if (a->kv_dtype < GR_DTYPE_F32 || a->kv_dtype > GR_DTYPE_TURBO)
         return fail(GR_ERR_ARG, "gr_decode_attention: bad kv_dtype %d", a->kv_dtype);
     if (a->kv_dtype == GR_DTYPE_TURBO) {
-        if (a->head_dim != 128) return fail(GR_ERR_ARG, "gr_decode_attention: Turbo KV needs head_dim 128");
         if (!a->k_sign || !a->v_sign || !a->k_scale || !a->v_scale || !a->k_rnorm || !a->v_rnorm ||
             !a->turbo_signs)
             return fail(GR_ERR_ARG, "gr_decode_attention: Turbo KV needs sign, scale, rnorm and sign-table arrays");
-        if (a->row_stride % 128 != 0 || a->seq_stride % 128 != 0 ||
+        const int64_t al = a->head_dim / 2;  // elements: code rows stay 4*(D/64)-byte, sign rows 2*(D/64)-byte aligned
+        if (a->row_stride % al != 0 || a->seq_stride % al != 0 ||
             ((uintptr_t)a->k_cache | (uintptr_t)a->v_cache | (uintptr_t)a->k_sign | (uintptr_t)a->v_sign) % 16 != 0)
             return fail(GR_ERR_ARG,
                         "gr_decode_attention: Turbo arrays must be 16-byte aligned with element strides "
-                        "that are multiples of 128");
+                        "that are multiples of head_dim / 2");
         if (a->scale_row_stride < a->n_kv_heads || a->scale_seq_stride < 0 || a->turbo_slot_stride <= 0)
             return fail(GR_ERR_ARG, "gr_decode_attention: bad Turbo aux or sign-table strides");
     }

@@ -224,8 +224,6 @@ int validate_config(const gr_attn_config* c) {
     if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "head_dim %d unsupported (64, 128, 256)", c->head_dim);
     if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_TURBO) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
-    if (c->kv_dtype == GR_DTYPE_TURBO && c->head_dim != 128)
-        return fail(GR_ERR_ARG, "Turbo KV cache needs head_dim 128");
     if (c->kv_dtype == GR_DTYPE_Q8 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "Q8 KV cache needs head_dim 128 or 256");
     if (c->rope_mode < GR_ROPE_NONE || c->rope_mode > GR_ROPE_NEOX) return fail(GR_ERR_ARG, "bad rope_mode %d", c->rope_mode);
@@ -469,7 +467,7 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
 // slot slots[b] (or `seq` for all when slots_dev is null) with visible range
 // [starts[b], ends[b]).
 // Token-packed Turbo prefill of n rows of one sequence (DecodeLaunch::tok_pack):
-// groups of tp = 16 / kv_mul consecutive rows share the split kernel's MFMA
+// groups of tp = turbo_pack_rows consecutive rows share the split kernel's MFMA
 // columns and read every K / V tile (and expand its codes) once.
 struct TurboPack {
     int tp = 0;
@@ -481,7 +479,7 @@ struct TurboPack {
 static TurboPack plan_turbo_pack(const gr_run_state* s, int n, const std::vector<int32_t>& starts,
                                  const std::vector<int32_t>& ends) {
     TurboPack t;
-    t.tp = std::max(1, 16 / (s->cfg.n_heads / s->cfg.n_kv_heads));
+    t.tp = turbo_pack_rows(s->d, s->cfg.n_heads / s->cfg.n_kv_heads);
     t.host.resize(4 * (size_t)n);
     for (int b = 0; b < n; b += t.tp) {
         const int e = std::min(n, b + t.tp);

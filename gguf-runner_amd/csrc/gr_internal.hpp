@@ -43,7 +43,8 @@ struct DecodeLaunch {
     // k_rnorm / v_rnorm gamma of (slot, row t, kv head g) at
     // slot*scale_seq_stride + t*scale_row_stride + g; turbo_signs the layer's sign
     // table rows (slot i at turbo_signs + i*turbo_slot_stride, kv head g at + g*d/8);
-    // ws_q the rotated / projected queries [n_seq][n_heads][2][d].
+    // ws_q the prepared query operands, turbo_query_ws_dwords(d) dwords per
+    // (batch entry, head).
     const void* k_sign;
     const void* v_sign;
     const float* k_rnorm;
@@ -186,6 +187,10 @@ hipError_t launch_ssm_pre(const SsmLaunch& p, hipStream_t st);
 hipError_t launch_ssm_post(const SsmLaunch& p, hipStream_t st);
 bool decode_turbo_supported(const DecodeLaunch& p);
 hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st);
+// ws_q dwords per (batch entry, head) of the Turbo decode (prepared query operands).
+size_t turbo_query_ws_dwords(int head_dim);
+// Rows per group of the token-packed Turbo prefill (DecodeLaunch::tok_pack).
+int turbo_pack_rows(int head_dim, int kv_mul);
 
 // Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
 // [m][n_heads][d] already multiplied by score_scale*log2(e); for bf16, q_lo

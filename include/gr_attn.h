@@ -51,7 +51,7 @@ typedef enum gr_dtype {
     GR_DTYPE_Q8 = 3,
     GR_DTYPE_TURBO = 4 /* KvCacheFormat::Turbo (inference.rs:346-1334, the reference's
                         * default): per kv head 2-bit codes + residual sign bits + sigma,
-                        * gamma; head_dim 128 */
+                        * gamma; head_dim 64, 128 or 256 */
 } gr_dtype;
 
 /* RoPE pairing (apply_rope_qk, inference.rs:1817-1874). */

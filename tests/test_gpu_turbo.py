@@ -78,6 +78,18 @@ def test_turbo_decode_ragged_gqa8_tails_and_windows(orc, dev):
     assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
 
 
+@pytest.mark.parametrize("d,n_heads,n_kv", [(64, 16, 8), (64, 32, 2), (256, 8, 4), (256, 16, 1), (128, 32, 2)])
+def test_turbo_decode_head_dims_and_groups(orc, dev, d, n_heads, n_kv):
+    """Every head size the reference's codec takes (inference.rs:363-365, 822-831),
+    with GQA groups of 2 and 8 query heads (hi / lo query pieces as MFMA columns) and
+    16 (one column per head); lengths ending inside a 32-key tile and a window."""
+    ends = [1, 33, 700]
+    starts = [0, 2, 700 - 300]
+    got, ref = _decode_case(orc, dev, n_heads=n_heads, n_kv=n_kv, d=d, starts=starts, ends=ends,
+                            seq_len=700, seed=1300 + d + n_kv)
+    assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
+
+
 def _turbo_state(rt, ffi, *, rope=False, n_seq=1, seq_len=256, n_heads=16, n_kv=8, d=128):
     rng = np.random.default_rng(78)
     if rope:
@@ -101,14 +113,15 @@ def _assert_rows_equal(dev_rows, c, row0, n, n_kv, d):
         assert np.array_equal(dev_rows[side + "_rnorm"], rn.reshape(-1, n_kv)[row0:row0 + n]), side
 
 
-def test_turbo_kv_write_token_bit_exact(orc, dev):
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_turbo_kv_write_token_bit_exact(orc, dev, d):
     """gr_kv_write_token into a Turbo cache writes the oracle's codes, sign bits, sigma
     and gamma bit for bit: random rows of several magnitudes, an all-zero row (sigma 0),
     a row with one silent head, and a row whose rotation is one centroid exactly."""
     from gguf_runner_amd import ffi, runtime as rt
-    p, s = _turbo_state(rt, ffi, seq_len=128)
+    p, s = _turbo_state(rt, ffi, seq_len=128, d=d)
     rng = np.random.default_rng(9)
-    n, layer, d = 24, 1, 128
+    n, layer = 24, 1
     k = (rng.standard_normal((n, p.kv_dim)) * rng.uniform(0.01, 30, size=(n, 1))).astype(np.float32)
     v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
     k[2] = 0.0
@@ -191,17 +204,18 @@ def test_turbo_decode_layer_batch_slots(orc, dev):
         assert float(np.abs(got[b] - ref).max()) <= TOL, (sq, float(np.abs(got[b] - ref).max()))
 
 
-@pytest.mark.parametrize("n_heads,n_kv,window,image", [
-    (16, 8, None, False), (32, 4, 70, False), (16, 1, None, False), (16, 8, 45, True), (32, 4, None, True)])
-def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image):
+@pytest.mark.parametrize("n_heads,n_kv,window,image,d", [
+    (16, 8, None, False, 128), (32, 4, 70, False, 128), (16, 1, None, False, 128), (16, 8, 45, True, 128),
+    (32, 4, None, True, 128), (8, 4, 50, False, 256), (8, 4, None, True, 256), (16, 8, None, False, 64)])
+def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image, d):
     """A 200-row gr_prefill_attention_chunk (or gr_prefill_image_block) over a Turbo
     cache after a 40-token history: the split kernel packs 16 / kv_mul consecutive
-    rows into its MFMA columns (kv_mul 2, 8 and 16: 8, 2 and 1 rows), each column
-    masked to its own visible keys; global or sliding-window layer.  Each output row ==
-    the oracle's attention_token_turbo over the oracle's encoding of the same rows,
-    with that row's visible range (1e-5)."""
+    rows into its MFMA columns (kv_mul 2, 8 and 16: 8, 2 and 1 rows; at d256 8 / kv_mul
+    rows, each with an f16 hi and a lo query column), each column masked to its own
+    visible keys; global or sliding-window layer; head_dim 64, 128 and 256.  Each
+    output row == the oracle's attention_token_turbo over the oracle's encoding of
+    the same rows, with that row's visible range (1e-5)."""
     from gguf_runner_amd import ffi, runtime as rt
-    d = 128
     p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=320,
                   kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE, layer_windows=[window, window])
     s = rt.malloc_run_state(p)
@@ -233,8 +247,9 @@ def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image
 
 @pytest.mark.parametrize("n_kv,m,window,hist", [(8, 3, None, 5), (8, 11, 1, 20), (2, 1, None, 0), (4, 37, 3, 60)])
 def test_turbo_prefill_chunk_partial_groups(orc, dev, n_kv, m, window, hist):
-    """Token-packed Turbo prefill with partial row groups (3 and 11 rows with 8 rows
-    per group, 37 with 4), a one-row chunk (8 rows per group at 16 / 2 heads), and
+    """Token-packed Turbo prefill with partial row groups (16 query heads: kv_mul 2
+    packs 8 rows per group, so chunks of 3 and 11 rows end inside a group; kv_mul 4
+    packs 4, so 37 rows do), a one-row chunk (kv_mul 8: two rows per group), and
     windows 1 and 3 (rows of one group see different keys)."""
     from gguf_runner_amd import ffi, runtime as rt
     n_heads, d = 16, 128
