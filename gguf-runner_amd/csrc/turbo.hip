@@ -139,11 +139,13 @@ hipError_t launch_turbo_write(const TurboWriteLaunch& p, hipStream_t st) {
 // finalize_turboquant_value_head (inference.rs:1323-1334): residual <- R'^-1
 // residual, base += residual, out = R^-1 base.
 template <int D>
-__global__ __launch_bounds__(64) void turbo_combine_kernel(const DecodeLaunch p) {
+__global__ __launch_bounds__(256) void turbo_combine_kernel(const DecodeLaunch p) {
     constexpr int J = D / 64, U = 8;
-    __shared__ float wsh[64];
-    const int lane = threadIdx.x;
-    const int h = blockIdx.x, s = blockIdx.y;
+    __shared__ float wsh_all[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float* wsh = wsh_all[wave];
+    const int h = 4 * blockIdx.x + wave, s = blockIdx.y;  // four heads per workgroup
+    if (h >= p.n_heads) return;  // whole wave; only wave-level synchronisation below
     const int g = h / (p.n_heads / p.n_kv_heads);
     const int t_len = p.kv_end[s] - p.kv_start[s];
     const int n_used = t_len > 0 ? (t_len + p.split_keys - 1) / p.split_keys : 0;
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(64) void turbo_combine_kernel(const DecodeLaunch p)
             lt += p.ws_ml[pt * 2 + 1] * w;
         }
         wsh[lane] = w;
-        __syncthreads();  // one-wave workgroup: weights visible
+        tq::wave_lds_sync();  // the wave's weights visible to all its lanes
         const float* o = p.ws_o + (part0 + c0) * 2 * D;
         int i = 0;
         for (; i + U <= nc; i += U) {  // U partials' loads in flight together
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(64) void turbo_combine_kernel(const DecodeLaunch p)
                 b[j] += o[i * 2 * D + lane + 64 * j] * wsh[i];
                 r[j] += o[i * 2 * D + D + lane + 64 * j] * wsh[i];
             }
-        __syncthreads();  // wsh reads done before the next chunk's stores
+        tq::wave_lds_sync();  // wsh reads done before the next chunk's stores
     }
     lt = wave_sum<64>(lt);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -212,11 +214,11 @@ __global__ __launch_bounds__(64) void turbo_combine_kernel(const DecodeLaunch p)
 }
 
 hipError_t launch_turbo_combine(const DecodeLaunch& p, hipStream_t st) {
-    const dim3 grid(p.n_heads, p.n_seq);
+    const dim3 grid((p.n_heads + 3) / 4, p.n_seq);
     switch (p.head_dim) {
-        case 64: turbo_combine_kernel<64><<<grid, 64, 0, st>>>(p); break;
-        case 128: turbo_combine_kernel<128><<<grid, 64, 0, st>>>(p); break;
-        case 256: turbo_combine_kernel<256><<<grid, 64, 0, st>>>(p); break;
+        case 64: turbo_combine_kernel<64><<<grid, 256, 0, st>>>(p); break;
+        case 128: turbo_combine_kernel<128><<<grid, 256, 0, st>>>(p); break;
+        case 256: turbo_combine_kernel<256><<<grid, 256, 0, st>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

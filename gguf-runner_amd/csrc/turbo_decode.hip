@@ -198,12 +198,14 @@ __device__ __forceinline__ void load_dwords(__amdgpu_buffer_rsrc_t r, int off, u
 //      E = E_code for code k-steps, E_sign for sign k-steps (max |value| in [2^13, 2^14))
 //   then 2^-E_code, 2^-E_sign, (alpha + beta) sum_i q_rot_i s, sum_i q_proj_i s.
 template <int D>
-__global__ __launch_bounds__(64) void turbo_query_kernel(const DecodeLaunch p) {
+__global__ __launch_bounds__(256) void turbo_query_kernel(const DecodeLaunch p) {
     using S = Tq<D>;
     constexpr int J = D / 64, KS = S::KS, NB = 16 * KS;
-    __shared__ float qsh[2][D];
-    const int lane = threadIdx.x;
-    const int h = blockIdx.x, s = blockIdx.y;
+    __shared__ float qsh_all[4][2][D];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float (*qsh)[D] = qsh_all[wave];
+    const int h = 4 * blockIdx.x + wave, s = blockIdx.y;  // four heads per workgroup
+    if (h >= p.n_heads) return;  // whole wave; no workgroup barrier below
     const int g = h / (p.n_heads / p.n_kv_heads);
     const uint8_t* sg = p.turbo_signs + (size_t)g * (D / 8);
     const int64_t ss = p.turbo_slot_stride;
@@ -229,34 +231,44 @@ __global__ __launch_bounds__(64) void turbo_query_kernel(const DecodeLaunch p) {
     }
     sr = wave_sum<64>(sr);
     sp = wave_sum<64>(sp);
-    __syncthreads();  // one-wave workgroup: qsh complete
+    tq::wave_lds_sync();  // the wave's qsh stores precede its reads
 
-    auto slot_value = [&](int idx, int half, bool& is_sign) {
-        const int g4 = idx / (4 * KS), rem = idx % (4 * KS);
-        int dim, pp;
-        float coef;
-        score_slot<D>(g4, rem >> 2, rem & 3, half, is_sign, dim, pp, coef);
-        return coef * qsh[is_sign ? 1 : 0][dim] * ldexpf(1.0f, -bit_exp(pp));
-    };
+    // one pass over the lane's slots (idx = lane + 64 i): values kept, maxima per plane
+    constexpr int NI = (NB + 63) / 64;
+    float v0[NI], v1[NI];
+    bool sgn[NI];
     float mc = 0.0f, ms = 0.0f;
-    for (int idx = lane; idx < NB; idx += 64)
 #pragma unroll
-        for (int half = 0; half < 2; half++) {
+    for (int i = 0; i < NI; i++) {
+        const int idx = lane + 64 * i;
+        v0[i] = v1[i] = 0.0f;
+        sgn[i] = false;
+        if (idx < NB) {
+            const int g4 = idx / (4 * KS), rem = idx % (4 * KS);
+            int dim, pp;
+            float coef;
             bool is_sign;
-            const float v = fabsf(slot_value(idx, half, is_sign));
-            if (is_sign) ms = fmaxf(ms, v);
-            else mc = fmaxf(mc, v);
+            score_slot<D>(g4, rem >> 2, rem & 3, 0, is_sign, dim, pp, coef);
+            v0[i] = coef * qsh[is_sign ? 1 : 0][dim] * ldexpf(1.0f, -bit_exp(pp));
+            score_slot<D>(g4, rem >> 2, rem & 3, 1, is_sign, dim, pp, coef);
+            v1[i] = coef * qsh[is_sign ? 1 : 0][dim] * ldexpf(1.0f, -bit_exp(pp));
+            sgn[i] = is_sign;
+            const float m = fmaxf(fabsf(v0[i]), fabsf(v1[i]));
+            if (is_sign) ms = fmaxf(ms, m);
+            else mc = fmaxf(mc, m);
         }
+    }
     const float ec = tq::pow2_for(wave_max<64>(mc), 14), es = tq::pow2_for(wave_max<64>(ms), 14);
-    for (int idx = lane; idx < NB; idx += 64) {
-        bool is_sign;
-        const float v0 = slot_value(idx, 0, is_sign);
-        const float v1 = slot_value(idx, 1, is_sign);
-        const float sc = is_sign ? es : ec;
-        uint32_t hi, lo;
-        split2(v0 * sc, v1 * sc, hi, lo);
-        out[idx] = hi;
-        out[NB + idx] = lo;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int idx = lane + 64 * i;
+        if (idx < NB) {
+            const float sc = sgn[i] ? es : ec;
+            uint32_t hi, lo;
+            split2(v0[i] * sc, v1[i] * sc, hi, lo);
+            out[idx] = hi;
+            out[NB + idx] = lo;
+        }
     }
     if (lane == 0) {
         float* c = (float*)(out + 2 * NB);
@@ -301,7 +313,10 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     constexpr int NF = D == 256 ? 2 : 1;  // 16-bit code fields per lane row in the value pass
     constexpr float kLazy = 8.0f;
     constexpr int kWaveBytes = TILE * RB + 4 * TILE * 4;  // V rows | aux [4][TILE]
-    constexpr int kLoopBytes = kTsWaves * kWaveBytes;
+    // !SPLIT: the lo pieces of the query operand, [g4][k-step][l16] uint4, in LDS
+    // once for the four waves (they share the columns), read per MFMA
+    constexpr int kBloBytes = SPLIT ? 0 : 4 * KS * 16 * 16;
+    constexpr int kLoopBytes = kBloBytes + kTsWaves * kWaveBytes;
     constexpr int kMergeBytes = (kTsWaves * 16 * (2 * D + 1) + 2 * kTsWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
@@ -320,11 +335,12 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     const int l16 = lane & 15, g4 = lane >> 4;
     const int qc = SPLIT ? l16 >> 1 : l16;  // the lane's query column
     const bool qv = col_ok(qc);
-    uint8_t* vrow = (uint8_t*)smem + wave * kWaveBytes;  // [TILE][RB]
+    uint4* blo = (uint4*)smem;                                       // !SPLIT: [4][KS][16]
+    uint8_t* vrow = (uint8_t*)smem + kBloBytes + wave * kWaveBytes;  // [TILE][RB]
     float* auxT = (float*)(vrow + TILE * RB);            // [4][TILE]: sigma_k, r_k, sigma_v, r_v
 
     // query operands and constants of the lane's column
-    uint4 bq[KS], bql[SPLIT ? 1 : KS];
+    uint4 bq[KS];
     float cback, pback, qcorr, pcorr;
     {
         const int c0 = qv ? qc : 0;
@@ -334,9 +350,12 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
 #pragma unroll
         for (int k = 0; k < KS; k++) bq[k] = qv ? bh[k] : z;
         if constexpr (!SPLIT) {
-            const uint4* bl = (const uint4*)(qb + (4 + g4) * 4 * KS);
+            if (wave == 0) {
+                const uint4* bl = (const uint4*)(qb + (4 + g4) * 4 * KS);
 #pragma unroll
-            for (int k = 0; k < KS; k++) bql[k] = qv ? bl[k] : z;
+                for (int k = 0; k < KS; k++) blo[(g4 * KS + k) * 16 + l16] = qv ? bl[k] : z;
+            }
+            __syncthreads();
         }
         const float* cst = (const float*)(qb + 32 * KS);
         // SPLIT: the two piece columns each subtract half of the corrections
@@ -362,6 +381,8 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     const uint32_t rsc = (uint32_t)(p.row_stride / 4), rss = (uint32_t)(p.row_stride / 8);
     const uint32_t ars = (uint32_t)p.scale_row_stride;
     const float rfac = sqrtf(tq::kFracPi2 / (float)D);
+
+    auto blo_at = [&](int k) { return blo[(g4 * KS + k) * 16 + l16]; };
 
     int c_lo = t_begin, c_hi = t_stop;  // keys visible to the lane's column
     if constexpr (PACK) {
@@ -458,13 +479,13 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
             auto word4 = [&](uint32_t W, int ks0, f32x4& acc) {
                 const uint4 A0 = score_a<0>(W), A1 = score_a<1>(W), A2 = score_a<2>(W), A3 = score_a<3>(W);
                 acc = mma16(A0, bq[ks0], acc);
-                if constexpr (!SPLIT) acc = mma16(A0, bql[ks0], acc);
+                if constexpr (!SPLIT) acc = mma16(A0, blo_at(ks0), acc);
                 acc = mma16(A1, bq[ks0 + 1], acc);
-                if constexpr (!SPLIT) acc = mma16(A1, bql[ks0 + 1], acc);
+                if constexpr (!SPLIT) acc = mma16(A1, blo_at(ks0 + 1), acc);
                 acc = mma16(A2, bq[ks0 + 2], acc);
-                if constexpr (!SPLIT) acc = mma16(A2, bql[ks0 + 2], acc);
+                if constexpr (!SPLIT) acc = mma16(A2, blo_at(ks0 + 2), acc);
                 acc = mma16(A3, bq[ks0 + 3], acc);
-                if constexpr (!SPLIT) acc = mma16(A3, bql[ks0 + 3], acc);
+                if constexpr (!SPLIT) acc = mma16(A3, blo_at(ks0 + 3), acc);
             };
 #pragma unroll
             for (int w = 0; w < NCW; w++) word4(kcw[sb][w], 4 * w, sc[sb]);
@@ -476,9 +497,9 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
                 const uint32_t H = (h & 0xffu) | ((h & 0xff00u) << 8);  // dims 0..7 | 8..15 at bits 0..7 | 16..23
                 const uint4 A0 = score_a<0>(H), A1 = score_a<1>(H);
                 ssg[sb] = mma16(A0, bq[KSC], ssg[sb]);
-                if constexpr (!SPLIT) ssg[sb] = mma16(A0, bql[KSC], ssg[sb]);
+                if constexpr (!SPLIT) ssg[sb] = mma16(A0, blo_at(KSC), ssg[sb]);
                 ssg[sb] = mma16(A1, bq[KSC + 1], ssg[sb]);
-                if constexpr (!SPLIT) ssg[sb] = mma16(A1, bql[KSC + 1], ssg[sb]);
+                if constexpr (!SPLIT) ssg[sb] = mma16(A1, blo_at(KSC + 1), ssg[sb]);
             }
         }
         __builtin_amdgcn_wave_barrier();  // aux stores precede the reads below (in-order LDS)
@@ -750,7 +771,7 @@ bool decode_turbo_supported(const DecodeLaunch& p) {
 
 template <int D>
 static hipError_t launch_turbo_d(const DecodeLaunch& p, hipStream_t st) {
-    turbo_query_kernel<D><<<dim3(p.n_heads, p.n_seq), 64, 0, st>>>(p);
+    turbo_query_kernel<D><<<dim3((p.n_heads + 3) / 4, p.n_seq), 256, 0, st>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int kv_mul = p.n_heads / p.n_kv_heads;
