@@ -24,10 +24,16 @@ Also reported in the same line:
                   Q8 and a Turbo cache, wall time per call with host buffers
   encoder_siglip -- encoder self-attention at the Gemma 3 SigLIP shape (4096
                   patches, 16 heads, d72, f32)
-  roofline     -- the dominant kernel (decode) against 8 TB/s HBM
-  cpu_baseline -- the CPU oracle (a C restatement of the reference's
-                  attention_token, oracle/oracle.c) timed on this host's cores on
-                  the decode workload.
+  config1_decode -- config 1 (Qwen3-0.6B-shaped decode, f32 KV, 1024 keys)
+  config4      -- config 4 (Gemma-3-4B-shaped, d256, bf16): the 8192-token prefill
+                  of a sliding-window (1024) and the global layer, the 5 : 1 stack
+                  of six layers, and one decode step over the six layers after it
+  roofline     -- the dominant kernel (decode) against 8 TB/s HBM; prefill.roofline
+                  the 8k prefill against the dense f16 MFMA peak
+  cpu_baseline -- the CPU oracle (a C restatement of the reference's loops,
+                  oracle/oracle.c) timed on this host's cores: the config-3 decode
+                  (headline unit) plus Q8 decode, token-serial prefill and serial
+                  DeltaNet legs (median of 3 runs after one warm-up each).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -42,7 +48,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0
-MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense f16)
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X published dense f16 / bf16 MFMA peak
 METRIC = "decode attn GB/s (% of 8 TB/s) + prefill attn TFLOP/s (% MFMA), 1×MI355X"
 
 
@@ -107,21 +113,23 @@ def measured_traffic(name="decode_mfma_f16_d128_config3.md"):
     return None
 
 
-def decode_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
+def decode_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128, kv_dtype=None, starts=None):
     import torch
     from gguf_runner_amd import ops
+    kv_dtype = kv_dtype or torch.float16
     n_seq = len(lens)
     max_len = int(max(lens))
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     q = torch.randn((n_seq, n_heads, d), generator=g, device=dev, dtype=torch.float32)
-    kc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=torch.float16)
-    vc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=torch.float16)
-    st = torch.zeros(n_seq, dtype=torch.int32, device=dev)
+    kc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=kv_dtype)
+    vc = torch.randn((n_seq, max_len, n_kv, d), generator=g, device=dev, dtype=kv_dtype)
+    st = torch.tensor(starts or [0] * n_seq, dtype=torch.int32, device=dev)
     en = torch.tensor(lens, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
-    call = ops.DecodeCall(q, kc, vc, st, en, out, max_kv_len=max_len)
-    nbytes = int(sum(lens)) * n_kv * d * 2 * 2
+    call = ops.DecodeCall(q, kc, vc, st, en, out, max_kv_len=max(e - b for e, b in zip(lens, starts or [0] * n_seq)))
+    esz = torch.finfo(kv_dtype).bits // 8
+    nbytes = int(sum(e - b for e, b in zip(lens, starts or [0] * n_seq))) * n_kv * d * 2 * esz
     return call, nbytes, (q, kc, vc, st, en, out)
 
 
@@ -212,6 +220,30 @@ def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128, turbo=False):
     return (lambda: rt.prefill_attention_chunk(p, s, 0, 0, q, k, v)), flops, (p, s)
 
 
+def config4_prefill_workload(dev, W, S=8192, seed=4):
+    """Config 4 (Gemma-3-4B-shaped attention layer): 8 Q / 4 KV heads, d256, bf16 q/k/v,
+    QK RMSNorm (eps 1e-6, weights ~N(1, 0.1)), NeoX RoPE, Gemma q scale, an 8192-token
+    prefill; W = 1024 for the sliding-window layers, 0 for the global one."""
+    import torch
+    from gguf_runner_amd import ffi, ops
+    Hq, Hk, d = 8, 4, 256
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((S, Hq, d), generator=g, device=dev, dtype=torch.bfloat16)
+    k = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
+    v = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
+    kc, vc = torch.empty_like(k), torch.empty_like(v)
+    out = torch.empty((S, Hq, d), device=dev, dtype=torch.float32)
+    qn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
+    kn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
+    theta, scale = (1e4, 1.0) if W else (1e6, 0.125)
+    fr = torch.tensor(ops.rope_freqs(theta, d), dtype=torch.float32, device=dev)
+    call = ops.PrefillCall(q, k, v, kc, vc, out, window=W, rope_mode=ffi.ROPE_NEOX, rope_dim=d,
+                           rope_freqs=fr, rope_scale=scale, q_norm=qn, k_norm=kn, is_gemma3=True)
+    flops = 4 * Hq * d * sum(min(i + 1, W) if W else i + 1 for i in range(S))
+    return call, flops, (q, k, v, kc, vc, out, qn, kn, fr)
+
+
 def encoder_workload(dev, stream):
     """Gemma 3 SigLIP vision attention: one noncausal sequence of 4096 patches, 16
     heads of dim 72, f32 rows (gr_encoder_self_attention)."""
@@ -226,38 +258,115 @@ def encoder_workload(dev, stream):
     return call, 4 * 16 * 72 * 4096 * 4096, (q, k, v, out)
 
 
-def cpu_baseline(lens, n_heads=32, n_kv=4, d=128, budget_s=10.0):
-    """Oracle attention_token on the host cores over a bounded prefix of the decode
-    batch (whole sequences, in batch order), as the reference runs it: one sequence
-    at a time, parallel over heads."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_runs(run, n=3):
+    """One untimed warm-up, then the median of n timed runs of run() -> (units, seconds)."""
+    run()
+    rates, secs = [], []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        units = run()
+        dt = time.perf_counter() - t0
+        rates.append(units / dt)
+        secs.append(dt)
+    return float(np.median(rates)), float(sum(secs))
+
+
+def cpu_baseline(lens, n_heads=32, n_kv=4, d=128):
+    """The CPU oracle (oracle/oracle.c, a C restatement of the reference's x86 loops)
+    on this host's cores, each leg a bounded sample of a benchmark configuration, the
+    median of 3 runs after one warm-up:
+      value (decode_f16) -- attention_token over f16 raw KV on the first config-3
+          sequences in batch order (one sequence at a time, parallel over heads, as
+          the reference's rayon pool runs it);
+      decode_q8 -- the same over the reference's Q8 storage (int8 rows + one f32 scale
+          per row, dot_q8_row / axpy_q8_row, inference.rs:1337-1366);
+      prefill_token_serial -- transformer_prefill_batch's per-token loop
+          (inference.rs:2981-3017: QK-norm, RoPE, KV write, attention_token) over the
+          first 1024 tokens of config 2 (32 / 8 heads, d128, adjacent RoPE theta 5e5);
+      deltanet_scan -- the serial gated-delta-rule scan of the SSM prefill
+          (inference.rs:2866-2885, qwen3next_state_head_step per head) over the 4096
+          tokens of config 5 (16 heads, d128), parallel over heads."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     import __graft_entry__ as ge
     orc = ge.load_oracle()
     threads = orc.max_threads()
     rng = np.random.default_rng(1003)
-    # one KV buffer sized for the longest sequence, reused (the timed region is the
-    # attention itself, not the data generation)
-    Lmax = max(lens)
-    kc = orc.f16_bits(rng.standard_normal((Lmax, n_kv * d), dtype=np.float32))
-    vc = orc.f16_bits(rng.standard_normal((Lmax, n_kv * d), dtype=np.float32))
+    # decode legs: the 16 config-3 sequences, whole, in batch order
+    seqs = list(lens)
+    Lmax = max(seqs)
+    kf = rng.standard_normal((Lmax, n_kv * d), dtype=np.float32)
+    vf = rng.standard_normal((Lmax, n_kv * d), dtype=np.float32)
+    kc, vc = orc.f16_bits(kf), orc.f16_bits(vf)
     q = rng.standard_normal(n_heads * d, dtype=np.float32)
-    done_bytes = 0
-    elapsed = 0.0
-    n_done = 0
-    keys = 0
-    while elapsed < budget_s and n_done < 64 * len(lens):
-        L = lens[n_done % len(lens)]
-        t0 = time.perf_counter()
-        orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
-        elapsed += time.perf_counter() - t0
-        done_bytes += L * n_kv * d * 2 * 2
-        keys += L
-        n_done += 1
-    return {"value": round(done_bytes / elapsed / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax, parallel over "
-                      f"heads) on {n_done} config-3 sequences in batch order, cycling "
-                      f"({keys} keys, {elapsed:.2f} s)"}
+
+    def dec_f16():
+        for L in seqs:
+            orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
+        return sum(seqs) * n_kv * d * 2 * 2
+    f16_rate, f16_s = _median_runs(dec_f16)
+    k8 = [orc.kv_quantize_row(r, False) for r in kf]
+    v8 = [orc.kv_quantize_row(r, False) for r in vf]
+    kq = np.stack([c for c, _ in k8]); ks = np.concatenate([sc for _, sc in k8]).astype(np.float32)
+    vq = np.stack([c for c, _ in v8]); vs = np.concatenate([sc for _, sc in v8]).astype(np.float32)
+
+    def dec_q8():
+        for L in seqs:
+            orc.attention_token(q, kq, vq, orc.Q8, n_heads, n_kv, d, 0, L, key_scale=ks, value_scale=vs,
+                                n_threads=threads)
+        return sum(seqs) * (n_kv * d * 2 + 2 * 4)
+    q8_rate, q8_s = _median_runs(dec_q8)
+    # token-serial prefill: first M tokens of config 2
+    M, Hq2, Hk2 = 1024, 32, 8
+    qp = rng.standard_normal((M, Hq2 * d), dtype=np.float32)
+    kp = rng.standard_normal((M, Hk2 * d), dtype=np.float32)
+    vp = rng.standard_normal((M, Hk2 * d), dtype=np.float32)
+    freqs = orc.rope_freqs(5e5, d)
+    pairs = M * (M + 1) // 2
+
+    def prefill():
+        orc.prefill_layer(qp, kp, vp, n_heads=Hq2, n_kv_heads=Hk2, head_size=d, seq_len=M, fmt=orc.F16,
+                          rope_dim=d, neox=False, rope_freqs_tab=freqs, rope_scale=1.0, n_threads=threads)
+        return pairs
+    pf_rate, pf_s = _median_runs(prefill)
+    # serial DeltaNet scan: first T tokens of config 5
+    T, H = 4096, 16
+    qd = rng.standard_normal((T, H, d), dtype=np.float32)
+    kd = rng.standard_normal((T, H, d), dtype=np.float32)
+    vd = rng.standard_normal((T, H, d), dtype=np.float32)
+    gate = (-0.1 * rng.random((T, H))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, H))))).astype(np.float32)
+    st0 = np.zeros((H, d, d), np.float32)
+
+    def scan():
+        orc.deltanet_scan(qd, kd, vd, gate, beta, st0, n_threads=threads)
+        return T
+    dn_rate, dn_s = _median_runs(scan)
+    return {"value": round(f16_rate / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax, parallel over heads) on "
+                      f"the {len(seqs)} config-3 sequences ({sum(seqs)} keys), median of 3 runs "
+                      f"after one warm-up ({f16_s:.2f} s timed)",
+            "legs": {
+                "decode_q8": {"gbs": round(q8_rate / 1e9, 3),
+                              "sample": f"the same sequences over Q8 rows + row scales ({q8_s:.2f} s timed)"},
+                "prefill_token_serial": {
+                    "visible_pairs_per_s": round(pf_rate), "tflops": round(pf_rate * 4 * Hq2 * d / 1e12, 5),
+                    "sample": f"first {M} tokens of config 2 (f16 KV, {pairs} (query, key) pairs per "
+                              f"head, {pf_s:.2f} s timed)"},
+                "deltanet_scan": {"tok_s": round(dn_rate, 1),
+                                  "sample": f"the {T} tokens of config 5, 16 heads ({dn_s:.2f} s timed)"},
+            }}
 
 
 def deltanet_workload(dev, T, seed, H=16, d=128):
@@ -311,27 +420,12 @@ def run_one(args, dev, stream, lens) -> int:
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only == "prefill8k_d256":
-        # config 4 shape (Gemma-3-4B): 8 Q / 4 KV heads, d256, QK RMSNorm, NeoX RoPE,
-        # bf16, 8192 tokens; the sliding-window (1024) and the global layer
-        import torch
-        from gguf_runner_amd import ffi, ops
-        S, Hq, Hk, d = 8192, 8, 4, 256
-        g = torch.Generator(device=dev)
-        g.manual_seed(4)
-        q = torch.randn((S, Hq, d), generator=g, device=dev, dtype=torch.bfloat16)
-        k = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
-        v = torch.randn((S, Hk, d), generator=g, device=dev, dtype=torch.bfloat16)
-        kc, vc = torch.empty_like(k), torch.empty_like(v)
-        out = torch.empty((S, Hq, d), device=dev, dtype=torch.float32)
-        qn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
-        kn = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).float()
-        fr = torch.tensor(ops.rope_freqs(1e4, d), dtype=torch.float32, device=dev)
+        # config 4 shape (Gemma-3-4B): the sliding-window (1024) and the global layer
         for W, key in ((1024, "local"), (0, "global")):
-            call = ops.PrefillCall(q, k, v, kc, vc, out, window=W, rope_mode=ffi.ROPE_NEOX, rope_dim=d,
-                                   rope_freqs=fr, q_norm=qn, k_norm=kn, is_gemma3=True)
+            call, flops, keep = config4_prefill_workload(dev, W)
             ms, _ = _timed(call, args.steps, args.warmup, stream)
-            flops = 4 * Hq * d * sum(min(i + 1, W) if W else i + 1 for i in range(S))
             res[key] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gflop": flops / 1e9}
+            del keep, call
     elif args.only == "encoder":
         call, flops, keep = encoder_workload(dev, stream)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
@@ -418,6 +512,46 @@ def main() -> int:
                         "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                         "gflop": round(flops / 1e9, 3)}
         del _keep_p, pcall
+    tf8 = pre["S8192"]["tflops"]
+    pre["roofline"] = {"bound": "mfma", "achieved": tf8, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": round(tf8 / MFMA_F16_PEAK_TFLOPS, 4),
+                       "kernel": "gr_prefill_attention, S = 8192, 32 / 8 heads, d128, f16: qkv_prep_kernel + "
+                                 "prefill_kernel<f16, 128, 8>, hipEvent-timed (4 * Hq * d * sum visible FLOP)"}
+
+    # config 1: Qwen3-0.6B-shaped single-layer decode, f32 KV, 1024 keys (latency-bound)
+    c1call, c1bytes, _keep_c1 = rotating(
+        lambda sd: decode_workload(dev, [1024], sd, n_heads=16, n_kv=8, kv_dtype=torch.float32), 41)
+    c1_ms, _ = _timed(c1call, args.steps, args.warmup, stream)
+    del _keep_c1, c1call
+
+    # config 4: Gemma-3-4B-shaped, 5 local (W = 1024) : 1 global layers, bf16, d256
+    c4 = {}
+    for key, W in (("local", 1024), ("global", 0)):
+        ccall, cflops, _keep_c = config4_prefill_workload(dev, W)
+        c_ms, _ = _timed(ccall, max(5, args.steps // 5), 2, stream)
+        c4[f"prefill_{key}_layer"] = {"ms": round(c_ms, 4), "tflops": round(cflops / (c_ms * 1e-3) / 1e12, 2),
+                                      "gflop": round(cflops / 1e9, 3)}
+        del _keep_c, ccall
+    six = 5 * c4["prefill_local_layer"]["ms"] + c4["prefill_global_layer"]["ms"]
+    six_flops = 1e9 * (5 * c4["prefill_local_layer"]["gflop"] + c4["prefill_global_layer"]["gflop"])
+    c4["prefill_6_layers"] = {"ms": round(six, 4), "tflops": round(six_flops / (six * 1e-3) / 1e12, 2),
+                              "frac_of_mfma_peak": round(six_flops / (six * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    # one decode step after the 8192-token prefill: position 8192 sees 1024 keys in a
+    # local layer and 8193 in the global one
+    dsteps = {}
+    for key, (b, e) in (("local", (8193 - 1024, 8193)), ("global", (0, 8193))):
+        dcall4, dbytes4, _keep_d4 = rotating(
+            lambda sd: decode_workload(dev, [e], sd, n_heads=8, n_kv=4, d=256, kv_dtype=torch.bfloat16,
+                                       starts=[b]), 43)
+        d4_ms, _ = _timed(dcall4, args.steps, args.warmup, stream)
+        dsteps[key] = (d4_ms, dbytes4)
+        del _keep_d4, dcall4
+    step_ms = 5 * dsteps["local"][0] + dsteps["global"][0]
+    step_bytes = 5 * dsteps["local"][1] + dsteps["global"][1]
+    c4["decode_step_6_layers"] = {"ms": round(step_ms, 5), "gbs": round(step_bytes / (step_ms * 1e-3) / 1e9, 2),
+                                  "bytes": step_bytes,
+                                  "local_layer_ms": round(dsteps["local"][0], 5),
+                                  "global_layer_ms": round(dsteps["global"][0], 5)}
 
     line = {
         "metric": METRIC,
@@ -446,6 +580,9 @@ def main() -> int:
         "decode_32k_turbo": {"gbs": round(u_gbs, 2), "ms": round(u_ms, 5), "bytes": ubytes,
                              "f16_equivalent_gbs": round(tbytes / (u_ms * 1e-3) / 1e9, 2)},
         "prefill": pre,
+        "config1_decode": {"ms": round(c1_ms, 5), "gbs": round(c1bytes / (c1_ms * 1e-3) / 1e9, 2),
+                           "bytes": c1bytes, "shape": "1 seq, 16 Q / 8 KV heads, d128, 1024 keys, f32 KV"},
+        "config4": c4,
         "wall_ms_per_step": round(dec_wall, 5),
     }
 
