@@ -4,20 +4,30 @@
 //   S *= g;  kv_i = sum_j k_j S[j][i];  delta_i = beta (v_i - kv_i);
 //   S[j][i] += k_j delta_i;  o_i = sum_j q_j S[j][i]
 // q/k are optionally L2-normalised first (q also * 1/sqrt(d)), math.rs:833-846.
-// Columns i are independent, which is how both kernels parallelise.
+// Columns i are independent (the reference's guards are per element too), which
+// is how every kernel here parallelises.
 //
 // 1. deltanet_step_kernel: the recurrence token by token with a 32-column
-//    slice of the state in registers (decode, and the serial scan).
-// 2. Chunked prefill (chunk C = 64), WY form of the same recurrence:
-//      gamma_t = prod_{s<=t} g_s (in-chunk),  A[t][s] = beta_t (gamma_t/gamma_s) k_t.k_s (s<t)
-//      Delta = (I + A)^-1 [beta V - beta gamma K S0] = U - W S0
-//      O     = diag(gamma) Q S0 + (Gamma-mask . Q K^T) Delta
-//      S_C   = gamma_last S0 + Kd^T Delta,  Kd_s = (gamma_last/gamma_s) k_s
-//    deltanet_chunk_prep_kernel builds U, W, P, Qg, Kd^T per (chunk, head) in
-//    parallel; deltanet_chunk_scan_kernel carries S across chunks with the
-//    state columns split over blocks of 4 (512 workgroups for 16 heads, two per
-//    CU: the chunk steps are sequential and latency-bound, so more, smaller
-//    blocks run faster even though each re-reads the chunk's W / Qg / P / Kd^T).
+//    slice of the state in registers (decode, the recurrent algorithm, and the
+//    chunked algorithm's continuation after a chunk with non-finite values).
+// 2. Chunked prefill (chunk C = 64).  With S0 the state before the chunk,
+//    gamma_t = prod_{s<=t} g_s (in-chunk) and the normalised rows q_t, k_t:
+//      A[t][s] = beta_t (gamma_t / gamma_s) k_t.k_s  (s < t),   T = (I + A)^-1
+//      X       = diag(beta) (V - diag(gamma) K S0)
+//      Delta   = T X                      (row t = the token's delta)
+//      O       = diag(gamma) Q S0 + P Delta,  P[t][s] = (gamma_t / gamma_s) q_t.k_s  (s <= t)
+//      S_C     = gamma_last S0 + sum_s (gamma_last / gamma_s) k_s Delta_s^T
+//    which is the token recurrence whenever every guard of the reference is a
+//    no-op (all values finite).
+//    deltanet_chunk_prep_kernel (chunk, head): T, P and per-row scales; the
+//    Gram products on v_mfma_f32_16x16x4_f32, T by forward substitution.
+//    deltanet_chunk_scan_kernel (head, 16 state columns): the sequential chunk
+//    steps, every product on v_mfma_f32_16x16x4_f32 with the raw q / k rows as
+//    operands and their row scales applied to the products' rows.
+//    Non-finite values: the prep flags a chunk whose inputs, T or P are not all
+//    finite, the scan one whose X, Delta, O or new state are not.  The scan stops
+//    before such a chunk, keeping the state it started from, and the step kernel
+//    runs from there token by token with the reference's guards.
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -29,9 +39,15 @@ __device__ __forceinline__ float dn_load(const void* p, size_t i, int dt) {
     return dt == GR_DTYPE_F16 ? f16_to_f32(b) : bf16_to_f32(b);
 }
 
+constexpr int kChunk = 64;
+constexpr int kChunkThreads = 256;
+constexpr int kScanCols = 16;                 // state columns per scan workgroup
+constexpr int kScanBlocks = 128 / kScanCols;  // scan workgroups per head
+
 // ------------------------------------------------------------------ recurrent step
 constexpr int kStepThreads = 256;
 constexpr int kStepCols = 32;
+static_assert(kStepCols == 2 * kScanCols, "a step block covers two scan blocks");
 
 template <int D>
 __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const DeltaNetLaunch p) {
@@ -48,12 +64,23 @@ __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const Delta
     const int H = p.n_heads;
     float* Sh = p.state + (size_t)h * D * D;
 
+    // After a chunked scan (first_bad set): column i continues from the first
+    // token of the first chunk its scan block did not complete.
+    int start = 0, t_begin = 0;
+    if (p.first_bad) {
+        const int* fb = p.first_bad + h * kScanBlocks + blockIdx.x * (kStepCols / kScanCols);
+        start = fb[ci / kScanCols] * kChunk;
+        t_begin = min(fb[0], fb[1]) * kChunk;
+        if (t_begin >= p.n_tokens) return;  // uniform: the scan completed every chunk
+    }
+
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = Sh[(size_t)(jg * R + r) * D + i];
 
     const float inv_scale_q = 1.0f / sqrtf((float)D);
-    for (int t = 0; t < p.n_tokens; t++) {
+    for (int t = t_begin; t < p.n_tokens; t++) {
+        const bool act = t >= start;
         const size_t row = ((size_t)t * H + h) * D;
         if (wave < 2) {
             const void* src = wave == 0 ? p.q : p.k;
@@ -77,8 +104,8 @@ __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const Delta
             }
         }
         const float gv = p.gate[(size_t)t * H + h];
-        const float g = finite_or_zero(p.gate_is_log ? expf(gv) : gv);
-        const float beta = finite_or_zero(p.beta[(size_t)t * H + h]);
+        const float g = act ? finite_or_zero(p.gate_is_log ? expf(gv) : gv) : 1.0f;
+        const float beta = act ? finite_or_zero(p.beta[(size_t)t * H + h]) : 0.0f;
         const float vi = finite_or_zero(dn_load(p.v, row + i, p.in_dtype));
         __syncthreads();
         float part = 0.0f;
@@ -108,7 +135,7 @@ __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const Delta
         __syncthreads();
         if (lane < 32) red[wave][ci] = po;
         __syncthreads();
-        if (tid < kStepCols) {
+        if (tid < kStepCols && act) {
             float o = 0.0f;
 #pragma unroll
             for (int w = 0; w < kStepThreads / 64; w++) o += red[w][ci];
@@ -120,169 +147,229 @@ __global__ __launch_bounds__(kStepThreads) void deltanet_step_kernel(const Delta
 }
 
 // ------------------------------------------------------------------ chunked prefill
-constexpr int kChunk = 64;
-constexpr int kChunkThreads = 256;
+typedef float dn_f32x4 __attribute__((ext_vector_type(4)));
 
-// Per (chunk, head) workspace block, floats: U, W, Qg [C][D]; KdT [D][C]; P [C][C]; gamma_last.
-template <int D>
-struct ChunkWs {
-    static constexpr size_t U = 0;
-    static constexpr size_t W = U + (size_t)kChunk * D;
-    static constexpr size_t QG = W + (size_t)kChunk * D;
-    static constexpr size_t KDT = QG + (size_t)kChunk * D;
-    static constexpr size_t P = KDT + (size_t)D * kChunk;
-    static constexpr size_t GL = P + (size_t)kChunk * kChunk;
-    static constexpr size_t SIZE = (GL + 1 + 63) / 64 * 64;
-};
+// Per (chunk, head) block of the workspace, the unit the scan copies into LDS:
+//   T, P: the ten 16x16 tiles on and below the diagonal of the 64x64 matrix,
+//     tile (r, q) at index r (r + 1) / 2 + q; a tile is 16 rows of four 16-byte
+//     pieces, piece g of row m at position 4 m + (g ^ (m / 4 % 4)), so the 16
+//     lanes that read one piece column of 16 rows hit 16 distinct bank groups;
+//   row scales [4][64] f32: beta_t;  beta_t gamma_t / |k_t|;
+//     gamma_t / (|q_t| sqrt(d));  (gamma_last / gamma_t) / |k_t|   (|.| = 1
+//     without l2norm, 0 for rows past the end of the sequence);
+//   gamma_last (f32) and the chunk's non-finite flag (i32).
+constexpr int kTpTiles = 10;
+constexpr int kTpT = 0;
+constexpr int kTpP = kTpT + kTpTiles * 1024;
+constexpr int kTpScale = kTpP + kTpTiles * 1024;
+constexpr int kTpGl = kTpScale + 4 * kChunk * 4;
+constexpr int kTpBytes = 22 * 1024;  // 22 DMA rounds of 1 KB
+static_assert(kTpGl + 8 <= kTpBytes, "block layout");
 
+// Workspace: [H][kScanBlocks] i32 chunks completed by each scan block (256-byte
+// aligned), then the (chunk, head) blocks.
+__host__ __device__ constexpr size_t dn_ws_head(int H) { return ((size_t)H * kScanBlocks * 4 + 255) / 256 * 256; }
+
+__device__ __forceinline__ int tp_tri(int r, int q) { return r * (r + 1) / 2 + q; }
+// float offset of element (m, k) in a tile
+__device__ __forceinline__ int tp_elem(int m, int k) { return (4 * m + ((k >> 2) ^ ((m >> 2) & 3))) * 4 + (k & 3); }
+
+__device__ __forceinline__ dn_f32x4 mfma4(float a, float b, dn_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Sum over the four lanes of a quad (DPP quad_perm [1,0,3,2] then [2,3,0,1]).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
+// MFMA 16x16x4 f32 operands: lane l holds A[l % 16][l / 16] and B[l / 16][l % 16];
+// the result holds D[4 (l / 16) + i][l % 16] in element i.  Every product below
+// gives lane group g = l / 16 the reduction indices 16 q + 4 g + i (i = 0..3)
+// in A and B alike, so 4 consecutive indices come from one 16-byte read.
 template <int D>
-__global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_prep_kernel(const DeltaNetLaunch p) {
+__global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(const DeltaNetLaunch p) {
+    static_assert(D == 128, "head_dim 128");
     constexpr int C = kChunk;
-    constexpr int DS = D + 4;  // padded LDS row stride
-    extern __shared__ float smem[];
-    float* qs = smem;                   // [C][DS] normalised q
-    float* ks = qs + C * DS;            // [C][DS] normalised k
-    constexpr int AS = C + 4;           // A row stride (16-byte aligned rows)
-    float* As = ks + C * DS;            // [C][AS] strictly lower-triangular A
-    // [C] in-chunk cumulative log decay, in double: with strong decays the prefix
-    // sums reach ~-100 within a chunk, and a decay exp(lg[t] - lg[s]) taken from two
+    constexpr int RS = D + 4;   // qn / kn row stride (floats): rows 4 banks apart
+    constexpr int AMS = C + 4;  // A row stride
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float* qn = smem;           // [C][RS] normalised q rows
+    float* kn = qn + C * RS;    // [C][RS] normalised k rows
+    float* am = qn;             // [C][AMS] A (strictly lower), over qn once the products are done
+    // in-chunk cumulative log decay in double: with strong decays the prefix sums
+    // reach ~-100 within a chunk, and a decay exp(lg[t] - lg[s]) taken from two
     // f32 prefix sums would carry ~100 ulp of absolute error in its exponent
-    double* lg = (double*)(As + C * AS);
-    float* bt = (float*)(lg + C);       // [C] beta
-    float* gm = bt + C;                 // [C] gamma_t = exp(lg[t])
-    float* kf = gm + C;                 // [C] gamma_last / gamma_s = exp(lg[C-1] - lg[s])
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int c = blockIdx.x, h = blockIdx.y;
-    const int H = p.n_heads;
+    __shared__ double lg[C];
+    __shared__ float bt[C], gm[C], kf[C], qi[C], ki[C];
+    __shared__ int bad;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int c = blockIdx.x, h = blockIdx.y, H = p.n_heads;
     const int t0 = c * C;
-    const int Cn = min(C, p.n_tokens - t0);  // tokens in this chunk
-    float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
+    const int Cn = min(C, p.n_tokens - t0);
+    char* blk = (char*)p.ws + dn_ws_head(H) + ((size_t)c * H + h) * kTpBytes;
+    if (tid == 0) bad = 0;
+    __syncthreads();
 
-    // 1. normalised q, k rows (zero rows past the end of the sequence)
+    // 1. normalised rows (as math.rs:833-846) and the norms for the row scales
     const float inv_scale_q = 1.0f / sqrtf((float)D);
     for (int r = wave; r < 2 * C; r += kChunkThreads / 64) {
-        const int t = r % C;
+        const int t = r & (C - 1);
         const bool isq = r < C;
-        float x[D / 64];
-        float ss = 0.0f;
         const bool valid = t < Cn;
         const size_t row = ((size_t)(t0 + t) * H + h) * D;
-#pragma unroll
-        for (int e = 0; e < D / 64; e++) {
-            x[e] = valid ? dn_load(isq ? p.q : p.k, row + lane + 64 * e, p.in_dtype) : 0.0f;
-            ss += x[e] * x[e];
-        }
-        float* dst = (isq ? qs : ks) + t * DS;
+        const float x0 = valid ? dn_load(isq ? p.q : p.k, row + lane, p.in_dtype) : 0.0f;
+        const float x1 = valid ? dn_load(isq ? p.q : p.k, row + lane + 64, p.in_dtype) : 0.0f;
+        const float ss = wave_sum<64>(x0 * x0 + x1 * x1);
+        float* dst = (isq ? qn : kn) + t * RS;
+        float nrm = valid ? 1.0f : 0.0f;
         if (p.l2norm) {
-            ss = wave_sum<64>(ss);
             const float inv = 1.0f / sqrtf(ss + p.eps);
-#pragma unroll
-            for (int e = 0; e < D / 64; e++)
-                dst[lane + 64 * e] = valid ? finite_or_zero(isq ? x[e] * inv * inv_scale_q : x[e] * inv) : 0.0f;
+            dst[lane] = valid ? finite_or_zero(isq ? x0 * inv * inv_scale_q : x0 * inv) : 0.0f;
+            dst[lane + 64] = valid ? finite_or_zero(isq ? x1 * inv * inv_scale_q : x1 * inv) : 0.0f;
+            nrm = valid ? (isq ? inv * inv_scale_q : inv) : 0.0f;
         } else {
-#pragma unroll
-            for (int e = 0; e < D / 64; e++) dst[lane + 64 * e] = x[e];
+            dst[lane] = x0;
+            dst[lane + 64] = x1;
+        }
+        if (lane == 0) {
+            (isq ? qi : ki)[t] = nrm;
+            if (valid && !is_finite_f(ss)) bad = 1;
         }
     }
-    // in-chunk cumulative log decay (inclusive) and beta; padded tokens: gate 0, beta 0
+    // gates: padded tokens get log decay 0 and beta 0
     if (wave == 0) {
         const bool valid = lane < Cn;
-        double gl = valid ? (double)p.gate[(size_t)(t0 + lane) * H + h] : 0.0;
-        // inclusive prefix sum over the 64 lanes
+        const float gv = valid ? p.gate[(size_t)(t0 + lane) * H + h] : 0.0f;
+        const float bv = valid ? p.beta[(size_t)(t0 + lane) * H + h] : 0.0f;
+        if (!is_finite_f(gv) || !is_finite_f(bv)) bad = 1;
+        double gl = (double)gv;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const double o = __shfl_up(gl, off, 64);
             if (lane >= off) gl += o;
         }
         lg[lane] = gl;
-        gm[lane] = expf((float)gl);
         const double gl_last = __shfl(gl, 63, 64);
+        gm[lane] = expf((float)gl);
         kf[lane] = expf((float)(gl_last - gl));
-        bt[lane] = valid ? finite_or_zero(p.beta[(size_t)(t0 + lane) * H + h]) : 0.0f;
+        bt[lane] = bv;
     }
     __syncthreads();
 
-    // 2. A (LDS) and P (workspace): thread -> row t, 16 columns s
+    // 2. K K^T (tiles 0..9) and Q K^T (10..19) on and below the diagonal, five per wave
+    dn_f32x4 acc[5];
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+        const int ti = wave + 4 * u;
+        const int tt = ti < kTpTiles ? ti : ti - kTpTiles;
+        const int r = tt < 1 ? 0 : tt < 3 ? 1 : tt < 6 ? 2 : 3;
+        const int q = tt - r * (r + 1) / 2;
+        const float* ar = (ti < kTpTiles ? kn : qn) + (16 * r + l16) * RS + 4 * g;
+        const float* br = kn + (16 * q + l16) * RS + 4 * g;
+        dn_f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kk = 0; kk < D / 16; kk++) {
+            const float4 a = *(const float4*)(ar + 16 * kk);
+            const float4 b = *(const float4*)(br + 16 * kk);
+            a4 = mfma4(a.x, b.x, a4);
+            a4 = mfma4(a.y, b.y, a4);
+            a4 = mfma4(a.z, b.z, a4);
+            a4 = mfma4(a.w, b.w, a4);
+        }
+        acc[u] = a4;
+    }
+    __syncthreads();  // every read of qn is done: A goes over it
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+        const int ti = wave + 4 * u;
+        const int tt = ti < kTpTiles ? ti : ti - kTpTiles;
+        const int r = tt < 1 ? 0 : tt < 3 ? 1 : tt < 6 ? 2 : 3;
+        const int q = tt - r * (r + 1) / 2;
+        const int s = 16 * q + l16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tl = 4 * g + i;
+            const int t = 16 * r + tl;
+            const float dec = s <= t ? expf((float)(lg[t] - lg[s])) : 0.0f;
+            if (ti < kTpTiles) {
+                am[t * AMS + s] = s < t ? bt[t] * dec * acc[u][i] : 0.0f;
+            } else {
+                const float v = s <= t ? dec * acc[u][i] : 0.0f;
+                if (!is_finite_f(v)) bad = 1;
+                *(float*)(blk + kTpP + tt * 1024 + 4 * tp_elem(tl, l16)) = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. T = (I + A)^-1, column col = 16 wave + lane / 4 by forward substitution
+    //    x[t] = [t == col] - sum_{s<t} A[t][s] x[s]; the four lanes of a quad
+    //    take the 4-blocks of s with (s / 4) % 4 == part and sum by DPP.
     {
-        const int t = tid >> 2;
-        const int sb = (tid & 3) * 16;
-        float akk[16], aqk[16];
+        const int col = 16 * wave + (lane >> 2), part = lane & 3;
+        float x[16];  // x[s] for s = 16 u + 4 part + e at x[4 u + e]
 #pragma unroll
-        for (int u = 0; u < 16; u++) akk[u] = aqk[u] = 0.0f;
-        for (int j = 0; j < D; j += 4) {
-            const float4 kt = *(const float4*)(ks + t * DS + j);
-            const float4 qt = *(const float4*)(qs + t * DS + j);
+        for (int e = 0; e < 16; e++) x[e] = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const float4 kk = *(const float4*)(ks + (sb + u) * DS + j);
-                akk[u] = fmaf(kt.x, kk.x, fmaf(kt.y, kk.y, fmaf(kt.z, kk.z, fmaf(kt.w, kk.w, akk[u]))));
-                aqk[u] = fmaf(qt.x, kk.x, fmaf(qt.y, kk.y, fmaf(qt.z, kk.z, fmaf(qt.w, kk.w, aqk[u]))));
+        for (int t = 0; t < C; t++) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (16 * u < t) {  // A[t][s >= t] is 0 and x[s >= t] is still 0
+                    const float4 a = *(const float4*)(am + t * AMS + 16 * u + 4 * part);
+                    sum = fmaf(a.x, x[4 * u + 0], sum);
+                    sum = fmaf(a.y, x[4 * u + 1], sum);
+                    sum = fmaf(a.z, x[4 * u + 2], sum);
+                    sum = fmaf(a.w, x[4 * u + 3], sum);
+                }
+            }
+            sum = quad_sum(sum);
+            const float val = (t == col ? 1.0f : 0.0f) - sum;
+            if (((t >> 2) & 3) == part) x[(t >> 4) * 4 + (t & 3)] = val;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (u < wave) continue;  // T[s][col] = 0 above the diagonal tiles
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v = x[4 * u + e];
+                if (!is_finite_f(v)) bad = 1;
+                *(float*)(blk + kTpT + tp_tri(u, wave) * 1024 + 4 * tp_elem(4 * part + e, lane >> 2)) = v;
             }
         }
-        const double lt = lg[t];
-        const float bet = bt[t];
-#pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int s = sb + u;
-            const float decay = s <= t ? expf((float)(lt - lg[s])) : 0.0f;
-            As[t * AS + s] = s < t ? bet * decay * akk[u] : 0.0f;
-            ws[ChunkWs<D>::P + t * C + s] = s <= t ? decay * aqk[u] : 0.0f;
+    }
+    // 4. row scales, gamma_last, flag
+    if (tid < C) {
+        const int t = tid;
+        float* sc = (float*)(blk + kTpScale);
+        const float v0 = bt[t], v1 = bt[t] * gm[t] * ki[t], v2 = gm[t] * qi[t], v3 = kf[t] * ki[t];
+        sc[t] = v0;
+        sc[C + t] = v1;
+        sc[2 * C + t] = v2;
+        sc[3 * C + t] = v3;
+        if (!is_finite_f(v0) || !is_finite_f(v1) || !is_finite_f(v2) || !is_finite_f(v3)) bad = 1;
+        if (t == C - 1) {
+            const float gl = gm[C - 1];
+            if (!is_finite_f(gl)) bad = 1;
+            *(float*)(blk + kTpGl) = gl;
         }
     }
     __syncthreads();
-
-    // 3. Qg = gamma_t q_t and Kd^T[j][s] = (gamma_last / gamma_s) k_s[j]
-    const double lglast = lg[C - 1];
-    for (int e = tid; e < C * D; e += kChunkThreads) {
-        const int t = e / D, j = e % D;
-        ws[ChunkWs<D>::QG + e] = gm[t] * qs[t * DS + j];
-    }
-    for (int e = tid; e < D * C; e += kChunkThreads) {
-        const int j = e / C, s2 = e % C;
-        ws[ChunkWs<D>::KDT + e] = kf[s2] * ks[s2 * DS + j];
-    }
-
-    // 4. [U | W] = (I + A)^-1 [beta V | beta gamma K] by forward substitution,
-    //    one right-hand-side column per thread, the whole column in registers:
-    //    x[t] -= A[t][s] x[s] for s = 0 .. t-1 in order.
-    for (int col = tid; col < 2 * D; col += kChunkThreads) {
-        const bool isv = col < D;
-        const int cc = isv ? col : col - D;
-        float* dst = ws + (isv ? ChunkWs<D>::U : ChunkWs<D>::W);
-        float x[C];
-#pragma unroll
-        for (int t = 0; t < C; t++)
-            x[t] = isv ? (t < Cn ? bt[t] * finite_or_zero(dn_load(p.v, ((size_t)(t0 + t) * H + h) * D + cc, p.in_dtype))
-                                 : 0.0f)
-                       : bt[t] * gm[t] * ks[t * DS + cc];
-#pragma unroll
-        for (int t = 1; t < C; t++) {
-            const float* arow = As + t * AS;
-#pragma unroll
-            for (int s4 = 0; s4 < t; s4 += 4) {
-                const float4 a4 = *(const float4*)(arow + s4);
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    if (s4 + k < t) x[t] = fmaf(-av[k], x[s4 + k], x[t]);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < C; t++) dst[t * D + cc] = x[t];
-    }
-    if (tid == 0) ws[ChunkWs<D>::GL] = expf((float)lglast);
+    if (tid == 0) *(int*)(blk + kTpGl + 4) = bad;
 }
-
-constexpr int kScanCols = 4;
 
 // Raw buffer access (wave-uniform base in a scalar descriptor, 32-bit byte
-// offsets per lane) and 16 bytes per lane straight into LDS at lds + 16 * lane
-// (lds wave-uniform).  The builtin exists for the device pass only.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dn_rsrc(const void* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)0xffffffff, 0x00020000);
+// offsets per lane, offsets at or past `bytes` read as zero) and 16 bytes per lane
+// straight into LDS at lds + 16 * lane (lds wave-uniform).  The builtin exists
+// for the device pass only.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dn_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ void dn_dma16(__amdgpu_buffer_rsrc_t r, float* lds, int voff) {
+__device__ __forceinline__ void dn_dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
 #if defined(__HIP_DEVICE_COMPILE__)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
 #endif
@@ -290,159 +377,336 @@ __device__ __forceinline__ void dn_dma16(__amdgpu_buffer_rsrc_t r, float* lds, i
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void dn_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// The chunk steps are sequential, so every step's memory latency is exposed
-// unless it is requested early: W and Qg (read only by phase A) go by DMA into
-// LDS, the next chunk's as soon as phase A is done, and the P and Kd^T rows a
-// thread needs in phases B and C are loaded into registers when the step starts.
-// W / Qg tiles are [C][D] f32 rows of 32 16-byte chunks, chunk q of row r at
-// position q ^ (r & 15), so the 16 rows a wave reads at once hit distinct banks.
-template <int D>
-__global__ __launch_bounds__(kChunkThreads) void deltanet_chunk_scan_kernel(const DeltaNetLaunch p) {
-    constexpr int C = kChunk;
-    constexpr int NC = kScanCols;
-    constexpr int RQ = D / 4;                 // 16-byte chunks per W / Qg row
-    static_assert(RQ == 32 && C * D * 4 == 4 * 8 * 1024, "tile DMA covers [C][D] in 4 waves x 8 KB");
-    __shared__ __attribute__((aligned(16))) float Ss[D][NC];
-    __shared__ __attribute__((aligned(16))) float Dl[C][NC];
-    __shared__ __attribute__((aligned(16))) float Wl[C * D];
-    __shared__ __attribute__((aligned(16))) float Ql[C * D];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    // blockIdx.x = head so that the column blocks of one head (linear ids
-    // h + H*cb) land on the same XCD and share its L2 copy of the workspace.
-    const int h = blockIdx.x;
-    const int c0 = blockIdx.y * NC;
-    const int H = p.n_heads;
-    float* Sh = p.state + (size_t)h * D * D;
-    for (int e = tid; e < D * NC; e += kChunkThreads) Ss[e / NC][e % NC] = Sh[(size_t)(e / NC) * D + c0 + e % NC];
+template <int DT>
+__device__ __forceinline__ float dn_h2f(uint32_t b) {
+    return DT == GR_DTYPE_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
+}
 
-    const int n_chunks = (p.n_tokens + C - 1) / C;
-    // DMA: instruction k of wave w fills LDS bytes [1 KB (8 w + k), +1 KB): lane l
-    // writes row 2 (8 w + k) + l / 32, position l % 32, which holds chunk
-    // (l % 32) ^ (row & 15) of that row.
-    int dma_off[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int r = 2 * (8 * wave + k) + (lane >> 5);
-        dma_off[k] = (r * RQ + ((lane & 31) ^ (r & 15))) * 16;
+// q / k chunk tiles in LDS: row t (D elements) as 16-byte pieces, piece p at
+// position p ^ (t % 16).  Four consecutive elements 16 q + 4 g .. + 3 of row t:
+template <int DT>
+__device__ __forceinline__ void dn_arow(const char* tile, int t, int q, int g, float* a) {
+    if constexpr (DT == GR_DTYPE_F32) {
+        const int pos = (4 * q + g) ^ (t & 15);
+        const float4 v = *(const float4*)(tile + t * 512 + pos * 16);
+        a[0] = v.x;
+        a[1] = v.y;
+        a[2] = v.z;
+        a[3] = v.w;
+    } else {
+        const int pos = (2 * q + (g >> 1)) ^ (t & 15);
+        const uint2 v = *(const uint2*)(tile + t * 256 + pos * 16 + (g & 1) * 8);
+        a[0] = dn_h2f<DT>(v.x & 0xffffu);
+        a[1] = dn_h2f<DT>(v.x >> 16);
+        a[2] = dn_h2f<DT>(v.y & 0xffffu);
+        a[3] = dn_h2f<DT>(v.y >> 16);
     }
-    auto dma_wq = [&](int c) {
-        const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
-        const __amdgpu_buffer_rsrc_t rw = dn_rsrc(ws + ChunkWs<D>::W);
-        const __amdgpu_buffer_rsrc_t rq = dn_rsrc(ws + ChunkWs<D>::QG);
+}
+// element j of row s
+template <int DT>
+__device__ __forceinline__ float dn_elem(const char* tile, int s, int j) {
+    if constexpr (DT == GR_DTYPE_F32) {
+        return *(const float*)(tile + s * 512 + (((j >> 2) ^ (s & 15)) * 16) + (j & 3) * 4);
+    } else {
+        return dn_h2f<DT>(*(const uint16_t*)(tile + s * 256 + (((j >> 3) ^ (s & 15)) * 16) + (j & 7) * 2));
+    }
+}
+
+template <int DT>
+constexpr size_t dn_scan_lds() {
+    constexpr size_t KB = (size_t)kChunk * 128 * (DT == GR_DTYPE_F32 ? 4 : 2);
+    return 2 * KB + (DT == GR_DTYPE_F32 ? 1 : 2) * KB + 2 * (size_t)kTpBytes +
+           (size_t)(128 * kScanCols + 2 * kChunk * kScanCols) * 4 + 16;
+}
+
+// One workgroup per (head, 16 state columns), the chunks in order.  LDS holds the
+// state slice, the chunk's raw K and Q tiles and its T / P / scale block, all
+// copied by DMA (buffer_load ... lds) one chunk ahead (Q of f32 inputs after its
+// last read in the chunk before: two f32 Q tiles do not fit beside the rest).
+// Wave w computes rows 16 w .. 16 w + 15 of the chunk's X, Delta and O and state
+// rows 32 w .. 32 w + 31.  Per chunk:
+//   b: K S0 and Q S0 (raw rows; K = 128)
+//   c: X = beta V - (beta gamma / |k|) (K S0)                    -> LDS
+//   d: Delta = T X (the tiles on and below the diagonal)        -> LDS
+//   e: O = (gamma / |q| sqrt(d)) (Q S0) + P Delta               -> out
+//      S' = gamma_last S0 + K^T ((gamma_last / gamma) / |k| Delta) -> LDS (own rows)
+template <int DT>
+__global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(const DeltaNetLaunch p) {
+    constexpr int C = kChunk, D = 128, NC = kScanCols;
+    constexpr int ES = DT == GR_DTYPE_F32 ? 4 : 2;
+    constexpr int KB = C * D * ES;        // one K / Q tile (bytes)
+    constexpr int QBUF = ES == 2 ? 2 : 1;
+    constexpr int PPR = D * ES / 16;      // 16-byte pieces per row
+    constexpr int RPK = 1024 / (D * ES);  // rows per 1 KB DMA round
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    char* kbuf = lds;                           // [2][KB]
+    char* qbuf = kbuf + 2 * KB;                 // [QBUF][KB]
+    char* tpbuf = qbuf + QBUF * KB;             // [2][kTpBytes]
+    // S[16 q + 4 g + i][n] at ((16 q + n) * 4 + g) * 4 + i: one MFMA B operand (or
+    // result) per 16-byte read (write); X and Delta rows the same way
+    float* Sl = (float*)(tpbuf + 2 * kTpBytes);
+    float* Xl = Sl + D * NC;
+    float* Dl = Xl + C * NC;
+    int* flag = (int*)(Dl + C * NC);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l16 = lane & 15, g = lane >> 4;
+    // blockIdx.x = head so that the column blocks of one head (linear ids
+    // h + H * cb) share an XCD and its L2 copy of the chunk's rows and block
+    const int h = blockIdx.x, cb = blockIdx.y;
+    const int c0 = cb * NC;
+    const int H = p.n_heads;
+    const int rowstride = H * D * ES;  // bytes between token rows of q / k
+    float* Sh = p.state + (size_t)h * D * D;
+    const int n_chunks = (p.n_tokens + C - 1) / C;
+    const char* tpg = (const char*)p.ws + dn_ws_head(H);
+
+    for (int e = tid; e < D * NC; e += kChunkThreads) {
+        const int i = e & 3, gg = (e >> 2) & 3, n = (e >> 4) & 15, q = e >> 8;
+        Sl[e] = Sh[(size_t)(16 * q + 4 * gg + i) * D + c0 + n];
+    }
+    if (tid == 0) *flag = 0;
+
+    // DMA round I (1 KB) of a tile: lane l fills position l % PPR of row
+    // I * RPK + l / PPR with the piece that belongs there
+    auto dma_rows = [&](char* dst, const void* src, int c) {
+        const int r0 = c * C;
+        const int cn = min(C, p.n_tokens - r0);
+        const char* base = (const char*)src + ((size_t)r0 * H + h) * D * ES;
+        const __amdgpu_buffer_rsrc_t rs = dn_rsrc(base, (uint32_t)((cn - 1) * rowstride + D * ES));
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            dn_dma16(rw, Wl + (8 * wave + k) * 256, dma_off[k]);
-            dn_dma16(rq, Ql + (8 * wave + k) * 256, dma_off[k]);
+        for (int k = 0; k < KB / 1024 / 4; k++) {
+            const int I = wave + 4 * k;
+            const int r = I * RPK + lane / PPR;
+            const int pc = (lane % PPR) ^ (r & 15);
+            dn_dma16(rs, dst + 1024 * I, r * rowstride + pc * 16);
         }
     };
-    if (n_chunks > 0) dma_wq(0);
+    auto dma_tp = [&](char* dst, int c) {
+        const __amdgpu_buffer_rsrc_t rs = dn_rsrc(tpg + ((size_t)c * H + h) * kTpBytes, kTpBytes);
+#pragma unroll
+        for (int k = 0; k < (kTpBytes / 1024 + 3) / 4; k++) {
+            const int I = wave + 4 * k;
+            if (I < kTpBytes / 1024) dn_dma16(rs, dst + 1024 * I, 1024 * I + 16 * lane);
+        }
+    };
+    // V[t][c0 + n] for the rows of this lane's X elements
+    auto load_v = [&](float* vr, int c) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = c * C + 16 * wave + 4 * g + i;
+            vr[i] = t < p.n_tokens ? dn_load(p.v, ((size_t)t * H + h) * D + c0 + l16, DT) : 0.0f;
+        }
+    };
 
-    const int ta = tid >> 2;          // phases A/B: row t
-    const int ia = tid & 3;           //             column
-    const int jc = tid >> 1;          // phase C: state row j (D = 128 rows over 256 threads / 2)
-    const int ic = (tid & 1) * (NC / 2);
-    const int swa = ta & 15;
-    for (int c = 0; c < n_chunks; c++) {
-        const float* ws = p.ws + ((size_t)c * H + h) * ChunkWs<D>::SIZE;
-        dn_wait_vmem();   // this thread's part of chunk c's W / Qg is in LDS
-        __syncthreads();  // ... everyone's (and the initial Ss)
-        // the P and Kd^T rows for phases B and C, U and gamma_last
-        float4 kd[C / 4], pr[C / 4];
+    int done = n_chunks;     // chunks completed
+    bool restore = false;    // state = s0own (the start of chunk done)
+    dn_f32x4 s0own[2];
+    float vcur[4], vnext[4];
+    dma_rows(kbuf, p.k, 0);
+    dma_rows(qbuf, p.q, 0);
+    dma_tp(tpbuf, 0);
+    load_v(vcur, 0);
+    int c = 0;
+    for (; c < n_chunks; c++) {
+        const int kb = c & 1, qb = QBUF == 2 ? (c & 1) : 0;
+        char* kt = kbuf + kb * KB;
+        char* qt = qbuf + qb * KB;
+        const char* tp = tpbuf + kb * kTpBytes;
+        dn_wait_vmem();   // this thread's DMA rounds for chunk c are in LDS
+        __syncthreads();  // ... everyone's; the state rows of chunk c - 1 are written
+        if (*flag) {      // chunk c - 1 met a non-finite value: resume from its start
+            done = c - 1;
+            restore = true;
+            break;
+        }
+        if (*(const int*)(tp + kTpGl + 4)) {  // the prep flagged chunk c
+            done = c;
+            break;
+        }
+        const int Cn = min(C, p.n_tokens - c * C);
+        if (Cn < C) {  // rows past the end of the sequence: zero
+            for (int e = Cn * D * ES / 16 + tid; e < KB / 16; e += kChunkThreads) {
+                ((uint4*)kt)[e] = make_uint4(0, 0, 0, 0);
+                ((uint4*)qt)[e] = make_uint4(0, 0, 0, 0);
+            }
+            __syncthreads();
+        }
+        if (c + 1 < n_chunks) {  // the next chunk's tiles into the other buffers
+            dma_rows(kbuf + (kb ^ 1) * KB, p.k, c + 1);
+            if (QBUF == 2) dma_rows(qbuf + (qb ^ 1) * KB, p.q, c + 1);
+            dma_tp(tpbuf + (kb ^ 1) * kTpBytes, c + 1);
+            load_v(vnext, c + 1);
+        }
+        const float* scl = (const float*)(tp + kTpScale);
+        bool nf = false;
+        // b: K S0, Q S0 for rows 16 w + (0..15)
+        dn_f32x4 ak = {0.0f, 0.0f, 0.0f, 0.0f}, aq = ak;
         {
-            const float* kr = ws + ChunkWs<D>::KDT + jc * C;
-            const float* prr = ws + ChunkWs<D>::P + ta * C;
+            const int ta = 16 * wave + l16;
 #pragma unroll
-            for (int u = 0; u < C / 4; u++) {
-                kd[u] = *(const float4*)(kr + 4 * u);
-                pr[u] = *(const float4*)(prr + 4 * u);
+            for (int q = 0; q < D / 16; q++) {
+                const float4 sb = *(const float4*)(Sl + ((q * 16 + l16) * 4 + g) * 4);
+                float ka[4], qa[4];
+                dn_arow<DT>(kt, ta, q, g, ka);
+                dn_arow<DT>(qt, ta, q, g, qa);
+                ak = mfma4(ka[0], sb.x, ak);
+                aq = mfma4(qa[0], sb.x, aq);
+                ak = mfma4(ka[1], sb.y, ak);
+                aq = mfma4(qa[1], sb.y, aq);
+                ak = mfma4(ka[2], sb.z, ak);
+                aq = mfma4(qa[2], sb.z, aq);
+                ak = mfma4(ka[3], sb.w, ak);
+                aq = mfma4(qa[3], sb.w, aq);
             }
         }
-        const float gl = ws[ChunkWs<D>::GL];
-        const float u0 = ws[ChunkWs<D>::U + ta * D + c0 + ia];
-        // A: Delta[t][i] = U[t][i] - sum_j W[t][j] S[j][i], and the first part of
-        //    O[t][i], sum_j Qg[t][j] S[j][i], in the same pass over S
-        float acc = 0.0f, acc_o = 0.0f;
-#pragma unroll 8
-        for (int q = 0; q < RQ; q++) {
-            const int pos = (ta * RQ + (q ^ swa)) * 4;
-            const float4 w4 = *(const float4*)(Wl + pos);
-            const float4 q4 = *(const float4*)(Ql + pos);
-            const int j = 4 * q;
-            const float s0 = Ss[j][ia], s1 = Ss[j + 1][ia], s2 = Ss[j + 2][ia], s3 = Ss[j + 3][ia];
-            acc = fmaf(-w4.x, s0, acc);
-            acc = fmaf(-w4.y, s1, acc);
-            acc = fmaf(-w4.z, s2, acc);
-            acc = fmaf(-w4.w, s3, acc);
-            acc_o = fmaf(q4.x, s0, acc_o);
-            acc_o = fmaf(q4.y, s1, acc_o);
-            acc_o = fmaf(q4.z, s2, acc_o);
-            acc_o = fmaf(q4.w, s3, acc_o);
-        }
-        Dl[ta][ia] = u0 + acc;
-        __syncthreads();  // Delta is complete; W / Qg of chunk c are no longer read
-        if (c + 1 < n_chunks) dma_wq(c + 1);
-        // B: O[t][i] += sum_{s<=t} P[t][s] Delta[s][i]
+        // c: X
         {
+            float xv[4];
 #pragma unroll
-            for (int u = 0; u < C / 4; u++) {
-                const float pv[4] = {pr[u].x, pr[u].y, pr[u].z, pr[u].w};
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    if (4 * u + k <= ta) acc_o = fmaf(pv[k], Dl[4 * u + k][ia], acc_o);
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * wave + 4 * g + i;
+                xv[i] = scl[t] * vcur[i] - scl[C + t] * ak[i];
+                nf |= !is_finite_f(xv[i]);
             }
-            const int t = c * C + ta;
-            if (t < p.n_tokens) p.out[((size_t)t * H + h) * D + c0 + ia] = finite_or_zero(acc_o);
+            *(float4*)(Xl + ((wave * 16 + l16) * 4 + g) * 4) = make_float4(xv[0], xv[1], xv[2], xv[3]);
         }
-        // C: S'[j][i] = gamma_last S[j][i] + sum_s KdT[j][s] Delta[s][i]
-        float nv[NC / 2];
+        if (nf) *flag = 1;
+        __syncthreads();  // X complete; Q of chunk c read
+        if (QBUF == 1 && c + 1 < n_chunks) dma_rows(qbuf, p.q, c + 1);
+        // d: Delta = T X
+        dn_f32x4 dl = {0.0f, 0.0f, 0.0f, 0.0f};
+        const int apos = 16 * (4 * l16 + (g ^ ((l16 >> 2) & 3)));  // this lane's piece in a T / P tile
+        for (int tq = 0; tq <= wave; tq++) {
+            const float4 a = *(const float4*)(tp + kTpT + tp_tri(wave, tq) * 1024 + apos);
+            const float4 b = *(const float4*)(Xl + ((tq * 16 + l16) * 4 + g) * 4);
+            dl = mfma4(a.x, b.x, dl);
+            dl = mfma4(a.y, b.y, dl);
+            dl = mfma4(a.z, b.z, dl);
+            dl = mfma4(a.w, b.w, dl);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) nf |= !is_finite_f(dl[i]);
+        *(float4*)(Dl + ((wave * 16 + l16) * 4 + g) * 4) = make_float4(dl[0], dl[1], dl[2], dl[3]);
+        if (nf) *flag = 1;
+        __syncthreads();  // Delta complete
+        // e: O
         {
+            dn_f32x4 ov = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int tq = 0; tq <= wave; tq++) {
+                const float4 a = *(const float4*)(tp + kTpP + tp_tri(wave, tq) * 1024 + apos);
+                const float4 b = *(const float4*)(Dl + ((tq * 16 + l16) * 4 + g) * 4);
+                ov = mfma4(a.x, b.x, ov);
+                ov = mfma4(a.y, b.y, ov);
+                ov = mfma4(a.z, b.z, ov);
+                ov = mfma4(a.w, b.w, ov);
+            }
 #pragma unroll
-            for (int u = 0; u < NC / 2; u++) nv[u] = gl * Ss[jc][ic + u];
-#pragma unroll
-            for (int q = 0; q < C / 4; q++) {
-                const float kv[4] = {kd[q].x, kd[q].y, kd[q].z, kd[q].w};
-#pragma unroll
-                for (int w = 0; w < 4; w++)
-#pragma unroll
-                    for (int u = 0; u < NC / 2; u++) nv[u] = fmaf(kv[w], Dl[4 * q + w][ic + u], nv[u]);
+            for (int i = 0; i < 4; i++) {
+                const int t = 16 * wave + 4 * g + i;
+                const float o = scl[2 * C + t] * aq[i] + ov[i];
+                nf |= !is_finite_f(o);
+                if (c * C + t < p.n_tokens) p.out[((size_t)(c * C + t) * H + h) * D + c0 + l16] = o;
             }
         }
-        __syncthreads();  // every read of Ss / Dl for this chunk is done
+        // e: S' for state rows 32 w .. 32 w + 31 (two tiles)
+        {
+            const float gl = *(const float*)(tp + kTpGl);
 #pragma unroll
-        for (int u = 0; u < NC / 2; u++) Ss[jc][ic + u] = nv[u];
+            for (int r2 = 0; r2 < 2; r2++) {
+                const int rt = 2 * wave + r2;
+                float* srow = Sl + ((rt * 16 + l16) * 4 + g) * 4;
+                const float4 s0 = *(const float4*)srow;
+                s0own[r2] = dn_f32x4{s0.x, s0.y, s0.z, s0.w};
+                dn_f32x4 acc = {gl * s0.x, gl * s0.y, gl * s0.z, gl * s0.w};
+                const int j = 16 * rt + l16;
+#pragma unroll
+                for (int q = 0; q < C / 16; q++) {
+                    const float4 b = *(const float4*)(Dl + ((q * 16 + l16) * 4 + g) * 4);
+                    const float4 sk = *(const float4*)(scl + 3 * C + 16 * q + 4 * g);
+                    const int s = 16 * q + 4 * g;
+                    acc = mfma4(dn_elem<DT>(kt, s + 0, j) * sk.x, b.x, acc);
+                    acc = mfma4(dn_elem<DT>(kt, s + 1, j) * sk.y, b.y, acc);
+                    acc = mfma4(dn_elem<DT>(kt, s + 2, j) * sk.z, b.z, acc);
+                    acc = mfma4(dn_elem<DT>(kt, s + 3, j) * sk.w, b.w, acc);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) nf |= !is_finite_f(acc[i]);
+                *(float4*)srow = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            }
+        }
+        if (nf) *flag = 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) vcur[i] = vnext[i];
     }
-    __syncthreads();
-    for (int e = tid; e < D * NC; e += kChunkThreads) Sh[(size_t)(e / NC) * D + c0 + e % NC] = Ss[e / NC][e % NC];
+    if (c == n_chunks) {
+        __syncthreads();
+        if (*flag) {  // the last chunk met a non-finite value
+            done = n_chunks - 1;
+            restore = true;
+        }
+    }
+#pragma unroll
+    for (int r2 = 0; r2 < 2; r2++) {
+        const int rt = 2 * wave + r2;
+        const float4 sv = *(const float4*)(Sl + ((rt * 16 + l16) * 4 + g) * 4);
+        const float v[4] = {restore ? s0own[r2][0] : sv.x, restore ? s0own[r2][1] : sv.y,
+                            restore ? s0own[r2][2] : sv.z, restore ? s0own[r2][3] : sv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) Sh[(size_t)(16 * rt + 4 * g + i) * D + c0 + l16] = v[i];
+    }
+    if (tid == 0) ((int*)p.ws)[h * kScanBlocks + cb] = done;
 }
 
 size_t deltanet_chunked_ws_bytes(int n_tokens, int n_heads, int head_dim, int chunk) {
-    if (head_dim != 128 || chunk != kChunk) return 0;
+    if (head_dim != 128 || chunk != kChunk || n_tokens <= 0 || n_heads <= 0) return 0;
     const size_t n_chunks = (size_t)(n_tokens + kChunk - 1) / kChunk;
-    return n_chunks * n_heads * ChunkWs<128>::SIZE * sizeof(float);
+    return dn_ws_head(n_heads) + n_chunks * n_heads * kTpBytes;
 }
 
 hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     if (p.head_dim != 128) return hipErrorInvalidValue;
+    DeltaNetLaunch q = p;
+    q.first_bad = nullptr;
     dim3 grid(128 / kStepCols, p.n_heads);
-    deltanet_step_kernel<128><<<grid, kStepThreads, 0, st>>>(p);
+    deltanet_step_kernel<128><<<grid, kStepThreads, 0, st>>>(q);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t launch_scan_dt(const DeltaNetLaunch& p, hipStream_t st) {
+    constexpr size_t lds = dn_scan_lds<DT>();
+    static_assert(lds <= 160 * 1024, "scan LDS");
+    hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_scan_kernel<DT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    deltanet_chunk_scan_kernel<DT><<<dim3(p.n_heads, kScanBlocks), kChunkThreads, lds, st>>>(p);
     return hipGetLastError();
 }
 
 hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
-    if (p.head_dim != 128) return hipErrorInvalidValue;
+    if (p.head_dim != 128 || !p.ws) return hipErrorInvalidValue;
     constexpr int D = 128;
-    constexpr size_t lds = (size_t)(2 * kChunk * (D + 4) + kChunk * (kChunk + 4) + 5 * kChunk) * sizeof(float);
-    hipError_t ea = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (ea != hipSuccess) return ea;
+    constexpr size_t lds = (size_t)2 * kChunk * (D + 4) * sizeof(float);
+    hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
     const int n_chunks = (p.n_tokens + kChunk - 1) / kChunk;
     deltanet_chunk_prep_kernel<D><<<dim3(n_chunks, p.n_heads), kChunkThreads, lds, st>>>(p);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
-    deltanet_chunk_scan_kernel<D><<<dim3(p.n_heads, D / kScanCols), kChunkThreads, 0, st>>>(p);
+    switch (p.in_dtype) {
+        case GR_DTYPE_F32: e = launch_scan_dt<GR_DTYPE_F32>(p, st); break;
+        case GR_DTYPE_F16: e = launch_scan_dt<GR_DTYPE_F16>(p, st); break;
+        case GR_DTYPE_BF16: e = launch_scan_dt<GR_DTYPE_BF16>(p, st); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    // columns whose scan stopped at a chunk with non-finite values continue token by token
+    DeltaNetLaunch f = p;
+    f.first_bad = (const int*)p.ws;
+    deltanet_step_kernel<D><<<dim3(D / kStepCols, p.n_heads), kStepThreads, 0, st>>>(f);
     return hipGetLastError();
 }
 

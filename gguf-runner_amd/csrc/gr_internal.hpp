@@ -271,6 +271,9 @@ struct DeltaNetLaunch {
     float* ws;   // chunked algorithm workspace
     int chunk;
     int gate_is_log;  // 1: g = exp(gate[t][h]); 0: gate already holds the decay factor g
+    // step kernel after a chunked scan: [H][128 / 16] chunks each 16-column scan
+    // block completed; column i starts at token 64 * first_bad[h][i / 16]
+    const int* first_bad = nullptr;
 };
 
 hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st);

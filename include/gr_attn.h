@@ -214,11 +214,14 @@ int gr_encoder_self_attention(float* out, const float* q, const float* k, const 
  * With l2norm = 1 the per-head normalisation of math.rs:833-846 is fused:
  * q <- q / sqrt(sum q^2 + eps) / sqrt(d), k <- k / sqrt(sum k^2 + eps).
  * q/k/v are the per-value-head rows (after the K->V head tiling, math.rs:826).
+ * The reference's guards apply: finite_or_zero on the normalised q / k, on v
+ * (math.rs:845), on exp(gate) and beta (869-874), on kv, delta and o (523-545).
  * ====================================================================== */
 typedef enum gr_deltanet_algo {
     GR_DELTANET_AUTO = 0,      /* chunked for n_tokens >= 64, recurrent otherwise */
     GR_DELTANET_RECURRENT = 1, /* token by token, state slice in registers */
-    GR_DELTANET_CHUNKED = 2    /* chunks of 64 tokens (WY form); finite inputs assumed */
+    GR_DELTANET_CHUNKED = 2    /* chunks of 64 tokens; from a chunk with a non-finite input or
+                                  intermediate on, token by token with the guards above */
 } gr_deltanet_algo;
 
 typedef struct gr_deltanet_args {

@@ -1022,14 +1022,18 @@ void orc_deltanet_scan(const float* q, const float* k, const float* v, const flo
             size_t off = ((size_t)t * n_heads + h) * d;
             float* qq = (float*)malloc(sizeof(float) * (size_t)d);
             float* kk = (float*)malloc(sizeof(float) * (size_t)d);
+            float* vv = (float*)malloc(sizeof(float) * (size_t)d);
             memcpy(qq, q + off, sizeof(float) * (size_t)d);
             memcpy(kk, k + off, sizeof(float) * (size_t)d);
+            /* v_dst = finite_or_zero(v_src), math.rs:845 */
+            for (int i = 0; i < d; i++) vv[i] = finite_or_zero(v[off + i]);
             if (l2norm) orc_deltanet_l2norm(qq, kk, d, eps);
             float g = finite_or_zero(expf(gate[(size_t)t * n_heads + h]));
             float b = finite_or_zero(beta[(size_t)t * n_heads + h]);
-            orc_deltanet_head_step(state + (size_t)h * d * d, out + off, qq, kk, v + off, g, b, d);
+            orc_deltanet_head_step(state + (size_t)h * d * d, out + off, qq, kk, vv, g, b, d);
             free(qq);
             free(kk);
+            free(vv);
         }
     }
 }

@@ -379,6 +379,62 @@ def qwen3next_ssm_tokens(qkv, z, gate_a, gate_b, *, n_k_heads, n_v_heads, head_d
     return out, hist, st
 
 
+def qwen3next_ssm_tokens_f64(qkv, z, gate_a, gate_b, *, n_k_heads, n_v_heads, head_dim, conv_kernel,
+                             conv_w, dt_bias, ssm_a, ssm_norm, eps, conv_hist=None, state=None):
+    """The same layer as qwen3next_ssm_tokens evaluated in float64 (numpy), stage by
+    stage from the reference's formulas (math.rs:766-953): depthwise causal conv over
+    the K - 1 history rows + the token (776-812) and SiLU; periodic K -> V head tiling
+    (824-826); q / |q| / sqrt(d), k / |k| (833-846); beta = sigmoid, decay
+    exp(softplus(alpha + dt_bias) * a) (848-874); the delta rule (math.rs:492-546);
+    gated RMSNorm with SiLU(z) (936-951).  All values are assumed finite (no guards).
+    A reference point for fp32 evaluations: returns (out [T][n_v*d] f64,
+    conv_hist [(K-1)][conv_dim] f32, state [n_v][d][d] f64)."""
+    qkv = np.asarray(qkv, np.float32)
+    T = qkv.shape[0]
+    nk, nv, d, K = n_k_heads, n_v_heads, head_dim, conv_kernel
+    d_inner = nv * d
+    conv_dim = d_inner + 2 * nk * d
+    hist = (np.zeros((K - 1, conv_dim), np.float32) if conv_hist is None
+            else np.asarray(conv_hist, np.float32))
+    x = np.concatenate([hist, qkv]).astype(np.float64)
+    cw = np.asarray(conv_w, np.float64).reshape(conv_dim, K)
+    db, sa = np.asarray(dt_bias, np.float64), np.asarray(ssm_a, np.float64)
+    sn = np.asarray(ssm_norm, np.float64)
+    ga = np.asarray(gate_a, np.float64)
+    gb = None if gate_b is None else np.asarray(gate_b, np.float64)
+    zz = np.asarray(z, np.float64).reshape(T, nv, d)
+    S = (np.zeros((nv, d, d)) if state is None else np.asarray(state, np.float64)).copy()
+    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
+    softplus = lambda v: np.where(v > 20, v, np.where(v < -20, np.exp(np.minimum(v, 20)),
+                                                     np.log1p(np.exp(np.minimum(v, 20)))))
+    heads = np.arange(nv)
+    src = heads % nk
+    hpg = nv // nk
+    out = np.zeros((T, nv, d))
+    for t in range(T):
+        acc = (x[t:t + K] * cw.T).sum(axis=0)            # window oldest first, token last
+        conv = acc * sig(acc)
+        q = conv[:nk * d].reshape(nk, d)[src]
+        k = conv[nk * d:2 * nk * d].reshape(nk, d)[src]
+        v = conv[2 * nk * d:].reshape(nv, d)
+        q = q / np.sqrt((q * q).sum(-1, keepdims=True) + eps) / np.sqrt(d)
+        k = k / np.sqrt((k * k).sum(-1, keepdims=True) + eps)
+        if gb is None:
+            base = (heads // hpg) * 2 * hpg + heads % hpg
+            beta, alpha = sig(ga[t, base]), ga[t, base + hpg] + db
+        else:
+            beta, alpha = sig(gb[t]), ga[t] + db
+        g = np.exp(softplus(alpha) * sa)
+        S *= g[:, None, None]
+        delta = beta[:, None] * (v - np.einsum("hji,hj->hi", S, k))
+        S += k[:, :, None] * delta[:, None, :]
+        o = np.einsum("hji,hj->hi", S, q)
+        inv = 1.0 / np.sqrt((o * o).mean(-1, keepdims=True) + eps)
+        out[t] = sn * (o * inv) * (zz[t] * sig(zz[t]))
+    new_hist = np.concatenate([hist, qkv])[T:T + K - 1] if K > 1 else hist
+    return out.reshape(T, d_inner), np.ascontiguousarray(new_hist, np.float32), S
+
+
 def f16_bits(x) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(x, np.float32).astype(np.float16)).view(np.uint16)
 

@@ -67,9 +67,11 @@ def test_config5_deltanet_prefill_4096(orc, dev, algo):
 
 
 def test_config5_deltanet_decode_steps_after_prefill(orc, dev):
-    """Config 5 decode: after a chunked prefill, 512 single-token recurrent steps."""
-    got, ref, S, Sref = _run(orc, dev, 1024 + 512, 16, 128, 1015, orc.BF16, 0,
-                             chunks=[1024] + [1] * 512)
+    """Config 5 as one sequence: the 4096-token chunked prefill, then 512 single-token
+    recurrent decode steps on the state it leaves, against one token-serial scan
+    over all 4608 tokens."""
+    got, ref, S, Sref = _run(orc, dev, 4096 + 512, 16, 128, 1015, orc.BF16, 0,
+                             chunks=[4096] + [1] * 512)
     assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
     assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
 
@@ -84,3 +86,36 @@ def test_deltanet_ragged_lengths(orc, dev, T, algo):
     got, ref, S, Sref = _run(orc, dev, T, 4, 128, 77 + T, orc.F32, algo, state0=S0)
     assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
     assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
+
+
+def test_deltanet_nonfinite_inputs_follow_reference_guards(orc, dev):
+    """Non-finite inputs take the reference's per-token guards (math.rs:523-545 and
+    833-874: finite_or_zero on the normalised q / k, on v, on exp(gate), on beta, on
+    kv, delta and o) on the chunked path too: the scan stops before a chunk with a
+    non-finite value and the step kernel continues from its first token.  One event
+    per head: NaN v element, inf k element, NaN q element, NaN gate, inf beta,
+    gate +100 (exp overflows, g = 0 zeroes the state), one in the ragged last chunk."""
+    T, H, d = 1000, 16, 128
+    q, k, v, gate, beta = _inputs(orc, T, H, d, 4242, orc.F32)
+    v[100, 3, 7] = np.nan
+    k[300, 5, 11] = np.inf
+    q[450, 7, 0] = np.nan
+    gate[500, 9] = np.nan
+    beta[700, 11] = np.inf
+    gate[400, 1] = 100.0
+    beta[990, 13] = np.nan
+    S0 = (0.05 * np.random.default_rng(1).standard_normal((H, d, d))).astype(np.float32)
+    ref, Sref = orc.deltanet_scan(q, k, v, gate, beta, S0, eps=1e-6, n_threads=orc.env_threads())
+    assert np.isfinite(ref).all() and np.isfinite(Sref).all()
+    from gguf_runner_amd import ops
+    st = torch.from_numpy(S0.copy()).to(dev)
+    out = torch.empty((T, H, d), dtype=torch.float32, device=dev)
+    ops.DeltaNetCall(*(torch.from_numpy(x).to(dev) for x in (q, k, v, gate, beta)), st, out,
+                     algo=2)()
+    torch.cuda.synchronize()
+    got, S = out.cpu().numpy(), st.cpu().numpy()
+    assert np.isfinite(got).all() and np.isfinite(S).all()
+    assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
+    assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
+    # the events matter: the state of head 1 restarts from zero at token 400
+    assert float(np.abs(Sref[1]).max()) < float(np.abs(Sref[0]).max())

@@ -34,6 +34,36 @@ def test_rope_scaling_switches_local_and_global_layers_at_the_same_position(dev)
             assert abs(values[1] - math.sin(angle)) < 1e-7
 
 
+def test_swa_pattern_selects_local_rope_without_layer_windows(dev, orc):
+    """is_swa_layer's swa_pattern branch (inference.rs:1820-1825; Gemma period 6, no
+    layer_windows): layers l % 6 < 5 rotate with the local theta and scale, every sixth
+    layer with the global ones (rebuild_rope_cache, 1485-1510), through gr_apply_rope_qk
+    against the oracle's apply_rope_qk for the branch the pattern names."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_layers, d, pos = 13, 128, 37
+    p = rt.Config(n_layers=n_layers, n_heads=2, n_kv_heads=1, head_dim=d, seq_len=64,
+                  rope_mode=ffi.ROPE_NEOX, rope_theta=1e6, rope_theta_swa=1e4, swa_pattern=6,
+                  is_gemma3=True, rope_scale_global=0.125, rope_scale_local=1.0)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(6)
+    q0 = rng.standard_normal(p.q_dim).astype(np.float32)
+    k0 = rng.standard_normal(p.kv_dim).astype(np.float32)
+    want = {}
+    for swa in (False, True):
+        c, sn = orc.rope_cache(orc.rope_freqs(1e4 if swa else 1e6, d), pos, 1.0 if swa else 0.125)
+        want[swa] = orc.apply_rope_qk(q0, k0, 2, 1, d, c, sn, neox=True, gemma_q_scale=True)
+    # the two branches differ well beyond the tolerance, so the check names the branch
+    assert np.abs(want[True][1] - want[False][1]).max() > 0.1
+    for layer in list(range(n_layers)) + [5, 0]:
+        swa = layer % 6 < 5
+        s.q[:] = q0
+        s.k[:] = k0
+        rt.apply_rope_qk(p, s, layer, pos)
+        qr, kr = want[swa]
+        assert np.abs(s.q - qr).max() <= TOL_F32, (layer, swa)
+        assert np.abs(s.k - kr).max() <= TOL_F32, (layer, swa)
+
+
 def test_neox_rope_partial_tail_through_device(dev, orc):
     """NeoX pairing with rope_dim < head_dim leaves the tail untouched (4133-4182) and
     matches the oracle's apply_rope_qk to 1 ulp-level."""

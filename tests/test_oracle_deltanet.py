@@ -98,46 +98,6 @@ def test_scan_thread_invariant(orc):
 
 # ---- the SSM layer around the recurrence (math.rs:766-953) ---------------------
 
-def _ssm_f64(qkv, z, ga, gb, nk, nv, d, K, cw, db, sa, sn, eps):
-    """Float64 statement of the layer, stage by stage, from the reference's formulas."""
-    T = qkv.shape[0]
-    d_inner = nv * d
-    conv_dim = d_inner + 2 * nk * d
-    x = np.concatenate([np.zeros((K - 1, conv_dim)), qkv.astype(np.float64)])
-    cw = cw.reshape(conv_dim, K).astype(np.float64)
-    sig = lambda v: 1.0 / (1.0 + np.exp(-v))
-    softplus = lambda v: v if v > 20 else (np.exp(v) if v < -20 else np.log1p(np.exp(v)))
-    S = np.zeros((nv, d, d))
-    out = np.zeros((T, d_inner))
-    hpg = nv // nk
-    for t in range(T):
-        win = x[t:t + K]                                  # K rows, oldest first
-        acc = (win * cw.T).sum(axis=0)                    # depthwise causal conv
-        conv = acc * sig(acc)
-        for h in range(nv):
-            sh = h % nk                                   # periodic K -> V tiling
-            q = conv[sh * d:(sh + 1) * d]
-            k = conv[nk * d + sh * d:nk * d + (sh + 1) * d]
-            v = conv[2 * nk * d + h * d:2 * nk * d + (h + 1) * d]
-            q = q / np.sqrt((q * q).sum() + eps) / np.sqrt(d)
-            k = k / np.sqrt((k * k).sum() + eps)
-            if gb is None:
-                grp, idx = h // hpg, h % hpg
-                beta = sig(ga[t, grp * 2 * hpg + idx])
-                alpha = ga[t, grp * 2 * hpg + hpg + idx] + db[h]
-            else:
-                beta = sig(gb[t, h])
-                alpha = ga[t, h] + db[h]
-            g = np.exp(softplus(float(alpha)) * sa[h])
-            S[h] *= g
-            delta = beta * (v - S[h].T @ k)
-            S[h] += np.outer(k, delta)
-            o = S[h].T @ q
-            inv = 1.0 / np.sqrt((o * o).mean() + eps)
-            out[t, h * d:(h + 1) * d] = sn * (o * inv) * (z[t, h * d:(h + 1) * d] * sig(z[t, h * d:(h + 1) * d]))
-    return out, x[T:T + K - 1], S
-
-
 @pytest.mark.parametrize("fused", [True, False])
 def test_qwen3next_ssm_token_loop_closed_form(orc, fused):
     rng = np.random.default_rng(60 + int(fused))
@@ -156,9 +116,12 @@ def test_qwen3next_ssm_token_loop_closed_form(orc, fused):
     out, hist, st = orc.qwen3next_ssm_tokens(qkv, z, ga, gb, n_k_heads=nk, n_v_heads=nv, head_dim=d,
                                             conv_kernel=K, conv_w=cw, dt_bias=db, ssm_a=sa, ssm_norm=sn,
                                             eps=eps)
-    e_out, e_hist, e_st = _ssm_f64(qkv, z, ga, gb, nk, nv, d, K, cw, db, sa, sn, eps)
+    e_out, e_hist, e_st = orc.qwen3next_ssm_tokens_f64(
+        qkv, z, ga, gb, n_k_heads=nk, n_v_heads=nv, head_dim=d, conv_kernel=K, conv_w=cw,
+        dt_bias=db, ssm_a=sa, ssm_norm=sn, eps=eps)
     assert np.allclose(out, e_out, rtol=2e-5, atol=2e-5)
     assert np.array_equal(hist, qkv[T - (K - 1):])        # history = the last K-1 raw inputs
+    assert np.array_equal(e_hist, hist)
     assert np.allclose(st, e_st, rtol=2e-5, atol=2e-5)
 
 
@@ -183,3 +146,62 @@ def test_qwen3next_ssm_tiling_is_periodic(orc):
                                         eps=1e-6)
     o = out.reshape(3, nv, d)
     assert np.array_equal(o[:, 2:], o[:, :2]) and not np.allclose(o[:, 0], o[:, 1])
+
+
+def _ssm_case(rng, nk, nv, d, K, T, fused):
+    conv_dim = nv * d + 2 * nk * d
+    return dict(
+        qkv=rng.standard_normal((T, conv_dim)).astype(np.float32),
+        z=rng.standard_normal((T, nv * d)).astype(np.float32),
+        gate_a=rng.standard_normal((T, 2 * nv if fused else nv)).astype(np.float32),
+        gate_b=None if fused else rng.standard_normal((T, nv)).astype(np.float32))
+
+
+@pytest.mark.parametrize("nk,fused", [(8, True), (16, False)])
+def test_qwen3next_ssm_f64_statement_at_config5_shape(orc, nk, fused):
+    """The float64 statement (the reference point of the GPU SSM test) against the
+    oracle's fp32 token loop at the config-5 shape, over two consecutive calls that
+    carry the conv history and the state: they agree to fp32 rounding, and splitting
+    the tokens over two calls changes neither."""
+    rng = np.random.default_rng(90 + nk)
+    nv, d, K, eps = 16, 128, 4, 1e-6
+    conv_dim = nv * d + 2 * nk * d
+    w = dict(conv_w=(0.3 * rng.standard_normal((conv_dim, K))).astype(np.float32),
+             dt_bias=(0.1 * rng.standard_normal(nv)).astype(np.float32),
+             ssm_a=-rng.uniform(0.2, 1.2, nv).astype(np.float32),
+             ssm_norm=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    shape = dict(n_k_heads=nk, n_v_heads=nv, head_dim=d, conv_kernel=K, eps=eps)
+    a = _ssm_case(rng, nk, nv, d, K, 9, fused)
+    b = _ssm_case(rng, nk, nv, d, K, 6, fused)
+    o1, h1, s1 = orc.qwen3next_ssm_tokens(**a, **shape, **w)
+    o2, h2, s2 = orc.qwen3next_ssm_tokens(**b, **shape, **w, conv_hist=h1, state=s1)
+    e1, eh1, es1 = orc.qwen3next_ssm_tokens_f64(**a, **shape, **w)
+    e2, eh2, es2 = orc.qwen3next_ssm_tokens_f64(**b, **shape, **w, conv_hist=eh1, state=es1)
+    for o, e in ((o1, e1), (o2, e2)):
+        assert np.abs(o - e).max() <= 2e-5 * max(1.0, np.abs(e).max())
+    assert np.array_equal(h2, eh2)
+    assert np.abs(s2 - es2).max() <= 1e-5
+    cat = {key: (None if a[key] is None else np.concatenate([a[key], b[key]])) for key in a}
+    ec, ehc, esc = orc.qwen3next_ssm_tokens_f64(**cat, **shape, **w)
+    assert np.allclose(ec, np.concatenate([e1, e2]), rtol=1e-12, atol=1e-12)
+    assert np.array_equal(ehc, eh2) and np.allclose(esc, es2, rtol=1e-12, atol=1e-12)
+
+
+def test_scan_sanitises_nonfinite_v_elements(orc):
+    """v_dst = finite_or_zero(v_src) (math.rs:845): a NaN or inf value element acts as 0."""
+    rng = np.random.default_rng(7)
+    T, H, d = 6, 2, 16
+    q, k, v = (rng.standard_normal((T, H, d)).astype(np.float32) for _ in range(3))
+    gate = rng.uniform(-0.2, 0.0, (T, H)).astype(np.float32)
+    beta = rng.uniform(0.2, 1.0, (T, H)).astype(np.float32)
+    S0 = np.zeros((H, d, d), np.float32)
+    vz = v.copy()
+    vz[2, 1, 3] = 0.0
+    vz[4, 0, 0] = 0.0
+    vn = v.copy()
+    vn[2, 1, 3] = np.nan
+    vn[4, 0, 0] = -np.inf
+    a = orc.deltanet_scan(q, k, vz, gate, beta, S0)
+    b = orc.deltanet_scan(q, k, vn, gate, beta, S0)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    assert not np.array_equal(a[0], orc.deltanet_scan(q, k, v, gate, beta, S0)[0])
