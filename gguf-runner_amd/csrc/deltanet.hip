@@ -28,6 +28,8 @@
 //    finite, the scan one whose X, Delta, O or new state are not.  The scan stops
 //    before such a chunk, keeping the state it started from, and the step kernel
 //    runs from there token by token with the reference's guards.
+#include <type_traits>
+
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -189,9 +191,20 @@ __device__ __forceinline__ float quad_sum(float v) {
 // the result holds D[4 (l / 16) + i][l % 16] in element i.  Every product below
 // gives lane group g = l / 16 the reduction indices 16 q + 4 g + i (i = 0..3)
 // in A and B alike, so 4 consecutive indices come from one 16-byte read.
-template <int D>
+template <int DT>
+__device__ __forceinline__ float2 dn_load2(const void* p, size_t i) {  // elements i, i + 1 (i even)
+    if constexpr (DT == GR_DTYPE_F32) {
+        return *(const float2*)((const float*)p + i);
+    } else {
+        const uint32_t b = *(const uint32_t*)((const uint16_t*)p + i);
+        if constexpr (DT == GR_DTYPE_F16) return make_float2(f16_to_f32(b & 0xffffu), f16_to_f32(b >> 16));
+        return make_float2(__uint_as_float(b << 16), __uint_as_float(b & 0xffff0000u));
+    }
+}
+
+template <int DT>
 __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(const DeltaNetLaunch p) {
-    static_assert(D == 128, "head_dim 128");
+    constexpr int D = 128;
     constexpr int C = kChunk;
     constexpr int RS = D + 4;   // qn / kn row stride (floats): rows 4 banks apart
     constexpr int AMS = C + 4;  // A row stride
@@ -214,30 +227,36 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
     if (tid == 0) bad = 0;
     __syncthreads();
 
-    // 1. normalised rows (as math.rs:833-846) and the norms for the row scales
-    const float inv_scale_q = 1.0f / sqrtf((float)D);
-    for (int r = wave; r < 2 * C; r += kChunkThreads / 64) {
-        const int t = r & (C - 1);
-        const bool isq = r < C;
-        const bool valid = t < Cn;
-        const size_t row = ((size_t)(t0 + t) * H + h) * D;
-        const float x0 = valid ? dn_load(isq ? p.q : p.k, row + lane, p.in_dtype) : 0.0f;
-        const float x1 = valid ? dn_load(isq ? p.q : p.k, row + lane + 64, p.in_dtype) : 0.0f;
-        const float ss = wave_sum<64>(x0 * x0 + x1 * x1);
-        float* dst = (isq ? qn : kn) + t * RS;
-        float nrm = valid ? 1.0f : 0.0f;
-        if (p.l2norm) {
-            const float inv = 1.0f / sqrtf(ss + p.eps);
-            dst[lane] = valid ? finite_or_zero(isq ? x0 * inv * inv_scale_q : x0 * inv) : 0.0f;
-            dst[lane + 64] = valid ? finite_or_zero(isq ? x1 * inv * inv_scale_q : x1 * inv) : 0.0f;
-            nrm = valid ? (isq ? inv * inv_scale_q : inv) : 0.0f;
-        } else {
-            dst[lane] = x0;
-            dst[lane + 64] = x1;
+    // 1. normalised rows (as math.rs:833-846) and the norms for the row scales:
+    //    wave w takes q and k rows 16 w .. 16 w + 15, all 32 loads issued first
+    {
+        const float inv_scale_q = 1.0f / sqrtf((float)D);
+        float2 x[32];
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int t = 16 * wave + (k & 15);
+            x[k] = t < Cn ? dn_load2<DT>(k < 16 ? p.q : p.k, ((size_t)(t0 + t) * H + h) * D + 2 * lane)
+                          : make_float2(0.0f, 0.0f);
         }
-        if (lane == 0) {
-            (isq ? qi : ki)[t] = nrm;
-            if (valid && !is_finite_f(ss)) bad = 1;
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int t = 16 * wave + (k & 15);
+            const bool isq = k < 16, valid = t < Cn;
+            const float ss = wave_sum<64>(x[k].x * x[k].x + x[k].y * x[k].y);
+            float2* dst = (float2*)((isq ? qn : kn) + t * RS) + lane;
+            float nrm = valid ? 1.0f : 0.0f;
+            if (p.l2norm) {
+                const float inv = 1.0f / sqrtf(ss + p.eps);
+                *dst = isq ? make_float2(finite_or_zero(x[k].x * inv * inv_scale_q), finite_or_zero(x[k].y * inv * inv_scale_q))
+                           : make_float2(finite_or_zero(x[k].x * inv), finite_or_zero(x[k].y * inv));
+                nrm = valid ? (isq ? inv * inv_scale_q : inv) : 0.0f;
+            } else {
+                *dst = x[k];
+            }
+            if (lane == 0) {
+                (isq ? qi : ki)[t] = nrm;
+                if (valid && !is_finite_f(ss)) bad = 1;
+            }
         }
     }
     // gates: padded tokens get log decay 0 and beta 0
@@ -316,18 +335,18 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
         for (int e = 0; e < 16; e++) x[e] = 0.0f;
 #pragma unroll
         for (int t = 0; t < C; t++) {
-            float sum = 0.0f;
+            float su[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four short chains instead of one long one
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 if (16 * u < t) {  // A[t][s >= t] is 0 and x[s >= t] is still 0
                     const float4 a = *(const float4*)(am + t * AMS + 16 * u + 4 * part);
-                    sum = fmaf(a.x, x[4 * u + 0], sum);
-                    sum = fmaf(a.y, x[4 * u + 1], sum);
-                    sum = fmaf(a.z, x[4 * u + 2], sum);
-                    sum = fmaf(a.w, x[4 * u + 3], sum);
+                    su[u] = a.x * x[4 * u + 0];
+                    su[u] = fmaf(a.y, x[4 * u + 1], su[u]);
+                    su[u] = fmaf(a.z, x[4 * u + 2], su[u]);
+                    su[u] = fmaf(a.w, x[4 * u + 3], su[u]);
                 }
             }
-            sum = quad_sum(sum);
+            const float sum = quad_sum((su[0] + su[1]) + (su[2] + su[3]));
             const float val = (t == col ? 1.0f : 0.0f) - sum;
             if (((t >> 2) & 3) == part) x[(t >> 4) * 4 + (t & 3)] = val;
         }
@@ -362,20 +381,44 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
     if (tid == 0) *(int*)(blk + kTpGl + 4) = bad;
 }
 
-// Raw buffer access (wave-uniform base in a scalar descriptor, 32-bit byte
-// offsets per lane, offsets at or past `bytes` read as zero) and 16 bytes per lane
-// straight into LDS at lds + 16 * lane (lds wave-uniform).  The builtin exists
-// for the device pass only.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dn_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+// Raw buffer access: a buffer descriptor (base, stride 0, num_records = `bytes`:
+// offsets at or past it read as zero) and 16 bytes per lane straight into LDS at
+// lds + 16 * lane (buffer_load_dwordx4 ... lds; lds and the descriptor
+// wave-uniform).  Issued as inline assembly so that the compiler does not see an
+// LDS write: it would otherwise wait for the DMA before every later LDS read it
+// cannot prove disjoint.  Completion is waited for explicitly (dn_wait_vmem)
+// before the data is read; vmcnt waits the compiler places for its own loads
+// count these rounds too and only wait longer, never shorter.
+typedef int dn_i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ dn_i32x4 dn_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    dn_i32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
 }
-__device__ __forceinline__ void dn_dma16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
-#endif
+__device__ __forceinline__ void dn_dma16(dn_i32x4 r, void* lds, int voff) {
+    const int m0 = __builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(r)
+                 : "memory", "m0");
 }
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void dn_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Workgroup barrier for LDS data written with ds_write: waits for this wave's
+// LDS operations (lgkmcnt) only, not for its outstanding global loads, stores and
+// DMA rounds, which __syncthreads() (a fence of all memory, and the DMA rounds
+// write LDS) would wait for too.  DMA rounds are waited for explicitly
+// (dn_wait_vmem) before the barrier that publishes them.  The memory clobber
+// keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void dn_lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 template <int DT>
 __device__ __forceinline__ float dn_h2f(uint32_t b) {
@@ -412,42 +455,45 @@ __device__ __forceinline__ float dn_elem(const char* tile, int s, int j) {
     }
 }
 
-template <int DT>
-constexpr size_t dn_scan_lds() {
-    constexpr size_t KB = (size_t)kChunk * 128 * (DT == GR_DTYPE_F32 ? 4 : 2);
-    return 2 * KB + (DT == GR_DTYPE_F32 ? 1 : 2) * KB + 2 * (size_t)kTpBytes +
-           (size_t)(128 * kScanCols + 2 * kChunk * kScanCols) * 4 + 16;
-}
-
 // One workgroup per (head, 16 state columns), the chunks in order.  LDS holds the
 // state slice, the chunk's raw K and Q tiles and its T / P / scale block, all
-// copied by DMA (buffer_load ... lds) one chunk ahead (Q of f32 inputs after its
-// last read in the chunk before: two f32 Q tiles do not fit beside the rest).
+// copied by DMA (buffer_load ... lds) one chunk ahead into the other of two
+// buffers (f32 inputs: one Q buffer, refilled after its last read in the chunk
+// before, as two f32 Q tiles do not fit beside the rest).  Every buffer is its
+// own array and the chunk loop is unrolled by two, so the compiler sees that a
+// DMA never writes what the same chunk reads and adds no wait for it.
 // Wave w computes rows 16 w .. 16 w + 15 of the chunk's X, Delta and O and state
 // rows 32 w .. 32 w + 31.  Per chunk:
 //   b: K S0 and Q S0 (raw rows; K = 128)
 //   c: X = beta V - (beta gamma / |k|) (K S0)                    -> LDS
 //   d: Delta = T X (the tiles on and below the diagonal)        -> LDS
-//   e: O = (gamma / |q| sqrt(d)) (Q S0) + P Delta               -> out
+//   e: O = (gamma / |q| sqrt(d)) (Q S0) + P Delta               -> out (stored a chunk later)
 //      S' = gamma_last S0 + K^T ((gamma_last / gamma) / |k| Delta) -> LDS (own rows)
+// Each product runs as two or four independent MFMA accumulator chains, and the
+// next chunk's DMA rounds are issued between the MFMAs of steps b, d and e.
 template <int DT>
 __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(const DeltaNetLaunch p) {
     constexpr int C = kChunk, D = 128, NC = kScanCols;
     constexpr int ES = DT == GR_DTYPE_F32 ? 4 : 2;
     constexpr int KB = C * D * ES;        // one K / Q tile (bytes)
-    constexpr int QBUF = ES == 2 ? 2 : 1;
+    constexpr bool Q2 = ES == 2;          // two Q buffers
     constexpr int PPR = D * ES / 16;      // 16-byte pieces per row
     constexpr int RPK = 1024 / (D * ES);  // rows per 1 KB DMA round
-    extern __shared__ __attribute__((aligned(16))) char lds[];
-    char* kbuf = lds;                           // [2][KB]
-    char* qbuf = kbuf + 2 * KB;                 // [QBUF][KB]
-    char* tpbuf = qbuf + QBUF * KB;             // [2][kTpBytes]
-    // S[16 q + 4 g + i][n] at ((16 q + n) * 4 + g) * 4 + i: one MFMA B operand (or
-    // result) per 16-byte read (write); X and Delta rows the same way
-    float* Sl = (float*)(tpbuf + 2 * kTpBytes);
-    float* Xl = Sl + D * NC;
-    float* Dl = Xl + C * NC;
-    int* flag = (int*)(Dl + C * NC);
+    constexpr int KR = KB / 1024 / 4;     // K (or Q) DMA rounds per wave
+    constexpr int TR = (kTpBytes / 1024 + 3) / 4;  // T / P block rounds per wave (the last partly)
+    __shared__ __attribute__((aligned(16))) char K0[KB];
+    __shared__ __attribute__((aligned(16))) char K1[KB];
+    __shared__ __attribute__((aligned(16))) char Q0[KB];
+    __shared__ __attribute__((aligned(16))) char Q1[Q2 ? KB : 16];
+    __shared__ __attribute__((aligned(16))) char TP0[kTpBytes];
+    __shared__ __attribute__((aligned(16))) char TP1[kTpBytes];
+    // S[16 q + 4 g + i][n] at (64 q + 16 g + n) * 4 + i: the four values of one
+    // MFMA B operand (or result) of lane 16 g + n in one 16-byte read (write),
+    // consecutive lanes on consecutive 16-byte words; X and Delta rows the same way
+    __shared__ __attribute__((aligned(16))) float Sl[D * NC];
+    __shared__ __attribute__((aligned(16))) float Xl[C * NC];
+    __shared__ __attribute__((aligned(16))) float Dl[C * NC];
+    __shared__ int flag;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l16 = lane & 15, g = lane >> 4;
     // blockIdx.x = head so that the column blocks of one head (linear ids
@@ -461,67 +507,97 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
     const char* tpg = (const char*)p.ws + dn_ws_head(H);
 
     for (int e = tid; e < D * NC; e += kChunkThreads) {
-        const int i = e & 3, gg = (e >> 2) & 3, n = (e >> 4) & 15, q = e >> 8;
+        const int i = e & 3, n = (e >> 2) & 15, gg = (e >> 6) & 3, q = e >> 8;
         Sl[e] = Sh[(size_t)(16 * q + 4 * gg + i) * D + c0 + n];
     }
-    if (tid == 0) *flag = 0;
+    if (tid == 0) flag = 0;
 
-    // DMA round I (1 KB) of a tile: lane l fills position l % PPR of row
-    // I * RPK + l / PPR with the piece that belongs there
-    auto dma_rows = [&](char* dst, const void* src, int c) {
+    // DMA round k of this wave for a K / Q tile: round I = wave + 4 k (1 KB) fills
+    // position l % PPR of row I * RPK + l / PPR (lane l) with the piece that
+    // belongs there (piece p of row t at position p ^ (t % 16))
+    auto rows_rsrc = [&](const void* src, int c) {
         const int r0 = c * C;
         const int cn = min(C, p.n_tokens - r0);
-        const char* base = (const char*)src + ((size_t)r0 * H + h) * D * ES;
-        const __amdgpu_buffer_rsrc_t rs = dn_rsrc(base, (uint32_t)((cn - 1) * rowstride + D * ES));
-#pragma unroll
-        for (int k = 0; k < KB / 1024 / 4; k++) {
-            const int I = wave + 4 * k;
-            const int r = I * RPK + lane / PPR;
-            const int pc = (lane % PPR) ^ (r & 15);
-            dn_dma16(rs, dst + 1024 * I, r * rowstride + pc * 16);
-        }
+        return dn_rsrc((const char*)src + ((size_t)r0 * H + h) * D * ES,
+                       (uint32_t)((cn - 1) * rowstride + D * ES));
     };
-    auto dma_tp = [&](char* dst, int c) {
-        const __amdgpu_buffer_rsrc_t rs = dn_rsrc(tpg + ((size_t)c * H + h) * kTpBytes, kTpBytes);
-#pragma unroll
-        for (int k = 0; k < (kTpBytes / 1024 + 3) / 4; k++) {
-            const int I = wave + 4 * k;
-            if (I < kTpBytes / 1024) dn_dma16(rs, dst + 1024 * I, 1024 * I + 16 * lane);
-        }
+    auto dma_row_round = [&](dn_i32x4 rs, char* dst, int k) {
+        const int I = wave + 4 * k;
+        const int r = I * RPK + lane / PPR;
+        dn_dma16(rs, dst + 1024 * I, r * rowstride + (((lane % PPR) ^ (r & 15)) * 16));
+    };
+    auto tp_rsrc = [&](int c) { return dn_rsrc(tpg + ((size_t)c * H + h) * kTpBytes, kTpBytes); };
+    auto dma_tp_round = [&](dn_i32x4 rs, char* dst, int k) {
+        const int I = wave + 4 * k;
+        if (I < kTpBytes / 1024) dn_dma16(rs, dst + 1024 * I, 1024 * I + 16 * lane);
     };
     // V[t][c0 + n] for the rows of this lane's X elements
-    auto load_v = [&](float* vr, int c) {
+    //   as raw bits, converted where chunk c uses them (rows past the end are read
+    //   from the last row and zeroed then): no branch and no arithmetic on the
+    //   loaded registers here, so the compiler does not wait for the loads here
+    auto load_v = [&](uint32_t* vr, int c) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = c * C + 16 * wave + 4 * g + i;
-            vr[i] = t < p.n_tokens ? dn_load(p.v, ((size_t)t * H + h) * D + c0 + l16, DT) : 0.0f;
+            const size_t e = ((size_t)min(t, p.n_tokens - 1) * H + h) * D + c0 + l16;
+            vr[i] = DT == GR_DTYPE_F32 ? __float_as_uint(((const float*)p.v)[e]) : ((const uint16_t*)p.v)[e];
         }
+    };
+    auto v_value = [&](uint32_t raw, int t) {
+        const float x = DT == GR_DTYPE_F32 ? __uint_as_float(raw) : dn_h2f<DT>(raw);
+        return t < p.n_tokens ? x : 0.0f;
     };
 
     int done = n_chunks;     // chunks completed
     bool restore = false;    // state = s0own (the start of chunk done)
     dn_f32x4 s0own[2];
-    float vcur[4], vnext[4];
-    dma_rows(kbuf, p.k, 0);
-    dma_rows(qbuf, p.q, 0);
-    dma_tp(tpbuf, 0);
-    load_v(vcur, 0);
-    int c = 0;
-    for (; c < n_chunks; c++) {
-        const int kb = c & 1, qb = QBUF == 2 ? (c & 1) : 0;
-        char* kt = kbuf + kb * KB;
-        char* qt = qbuf + qb * KB;
-        const char* tp = tpbuf + kb * kTpBytes;
+    // O rows of chunk `pend` wait in registers and are stored after the next
+    // chunk's wait for its DMA rounds (which counts stores too), a chunk before
+    // the wait that covers them
+    float opend[4];
+    int pend = -1;
+    auto store_pending = [&]() {
+        if (pend < 0) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = pend * C + 16 * wave + 4 * g + i;
+            if (t < p.n_tokens) p.out[((size_t)t * H + h) * D + c0 + l16] = opend[i];
+        }
+        pend = -1;
+    };
+    uint32_t vcur[4], vnext[4];
+    {
+        const dn_i32x4 rk = rows_rsrc(p.k, 0), rq = rows_rsrc(p.q, 0), rt = tp_rsrc(0);
+#pragma unroll
+        for (int k = 0; k < KR; k++) {
+            dma_row_round(rk, K0, k);
+            dma_row_round(rq, Q0, k);
+        }
+#pragma unroll
+        for (int k = 0; k < TR; k++) dma_tp_round(rt, TP0, k);
+        load_v(vcur, 0);
+    }
+
+    // one chunk; PAR selects the buffers (compile time); false = stop the scan
+    auto chunk = [&](const int c, auto par) -> bool {
+        constexpr int P = decltype(par)::value;
+        char* kt = P ? K1 : K0;
+        char* qt = (Q2 && P) ? Q1 : Q0;
+        const char* tp = P ? TP1 : TP0;
+        char* kn = P ? K0 : K1;                // next chunk's buffers
+        char* qn = Q2 ? (P ? Q0 : Q1) : Q0;
+        char* tpn = P ? TP0 : TP1;
         dn_wait_vmem();   // this thread's DMA rounds for chunk c are in LDS
-        __syncthreads();  // ... everyone's; the state rows of chunk c - 1 are written
-        if (*flag) {      // chunk c - 1 met a non-finite value: resume from its start
+        dn_lds_barrier();  // ... everyone's; the state rows of chunk c - 1 are written
+        store_pending();
+        if (flag) {       // chunk c - 1 met a non-finite value: resume from its start
             done = c - 1;
             restore = true;
-            break;
+            return false;
         }
         if (*(const int*)(tp + kTpGl + 4)) {  // the prep flagged chunk c
             done = c;
-            break;
+            return false;
         }
         const int Cn = min(C, p.n_tokens - c * C);
         if (Cn < C) {  // rows past the end of the sequence: zero
@@ -529,34 +605,37 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
                 ((uint4*)kt)[e] = make_uint4(0, 0, 0, 0);
                 ((uint4*)qt)[e] = make_uint4(0, 0, 0, 0);
             }
-            __syncthreads();
+            dn_lds_barrier();
         }
-        if (c + 1 < n_chunks) {  // the next chunk's tiles into the other buffers
-            dma_rows(kbuf + (kb ^ 1) * KB, p.k, c + 1);
-            if (QBUF == 2) dma_rows(qbuf + (qb ^ 1) * KB, p.q, c + 1);
-            dma_tp(tpbuf + (kb ^ 1) * kTpBytes, c + 1);
-            load_v(vnext, c + 1);
-        }
+        const bool more = c + 1 < n_chunks;
+        if (more) load_v(vnext, c + 1);
         const float* scl = (const float*)(tp + kTpScale);
         bool nf = false;
-        // b: K S0, Q S0 for rows 16 w + (0..15)
-        dn_f32x4 ak = {0.0f, 0.0f, 0.0f, 0.0f}, aq = ak;
+        // b: K S0, Q S0 for rows 16 w + (0..15); four chains (K / Q x even / odd i);
+        //    the next chunk's K (and 16-bit Q) rounds between the MFMAs
+        dn_f32x4 ak0 = {0.0f, 0.0f, 0.0f, 0.0f}, ak1 = ak0, aq0 = ak0, aq1 = ak0;
         {
+            const dn_i32x4 rk = rows_rsrc(p.k, more ? c + 1 : c);
+            const dn_i32x4 rq = rows_rsrc(p.q, more ? c + 1 : c);
             const int ta = 16 * wave + l16;
 #pragma unroll
             for (int q = 0; q < D / 16; q++) {
-                const float4 sb = *(const float4*)(Sl + ((q * 16 + l16) * 4 + g) * 4);
+                const float4 sb = *(const float4*)(Sl + (q * 64 + lane) * 4);
                 float ka[4], qa[4];
                 dn_arow<DT>(kt, ta, q, g, ka);
                 dn_arow<DT>(qt, ta, q, g, qa);
-                ak = mfma4(ka[0], sb.x, ak);
-                aq = mfma4(qa[0], sb.x, aq);
-                ak = mfma4(ka[1], sb.y, ak);
-                aq = mfma4(qa[1], sb.y, aq);
-                ak = mfma4(ka[2], sb.z, ak);
-                aq = mfma4(qa[2], sb.z, aq);
-                ak = mfma4(ka[3], sb.w, ak);
-                aq = mfma4(qa[3], sb.w, aq);
+                ak0 = mfma4(ka[0], sb.x, ak0);
+                aq0 = mfma4(qa[0], sb.x, aq0);
+                ak1 = mfma4(ka[1], sb.y, ak1);
+                aq1 = mfma4(qa[1], sb.y, aq1);
+                ak0 = mfma4(ka[2], sb.z, ak0);
+                aq0 = mfma4(qa[2], sb.z, aq0);
+                ak1 = mfma4(ka[3], sb.w, ak1);
+                aq1 = mfma4(qa[3], sb.w, aq1);
+                if (more && q < KR) {
+                    dma_row_round(rk, kn, q);
+                    if (Q2) dma_row_round(rq, qn, q);
+                }
             }
         }
         // c: X
@@ -565,82 +644,117 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * wave + 4 * g + i;
-                xv[i] = scl[t] * vcur[i] - scl[C + t] * ak[i];
+                xv[i] = scl[t] * v_value(vcur[i], c * C + t) - scl[C + t] * (ak0[i] + ak1[i]);
                 nf |= !is_finite_f(xv[i]);
             }
-            *(float4*)(Xl + ((wave * 16 + l16) * 4 + g) * 4) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+            *(float4*)(Xl + (wave * 64 + lane) * 4) = make_float4(xv[0], xv[1], xv[2], xv[3]);
         }
-        if (nf) *flag = 1;
-        __syncthreads();  // X complete; Q of chunk c read
-        if (QBUF == 1 && c + 1 < n_chunks) dma_rows(qbuf, p.q, c + 1);
-        // d: Delta = T X
-        dn_f32x4 dl = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (nf) flag = 1;
+        dn_lds_barrier();  // X complete; Q of chunk c read
+        // d: Delta = T X (two chains); the next chunk's T / P block rounds
         const int apos = 16 * (4 * l16 + (g ^ ((l16 >> 2) & 3)));  // this lane's piece in a T / P tile
-        for (int tq = 0; tq <= wave; tq++) {
-            const float4 a = *(const float4*)(tp + kTpT + tp_tri(wave, tq) * 1024 + apos);
-            const float4 b = *(const float4*)(Xl + ((tq * 16 + l16) * 4 + g) * 4);
-            dl = mfma4(a.x, b.x, dl);
-            dl = mfma4(a.y, b.y, dl);
-            dl = mfma4(a.z, b.z, dl);
-            dl = mfma4(a.w, b.w, dl);
+        dn_f32x4 dl;
+        {
+            const dn_i32x4 rt = tp_rsrc(more ? c + 1 : c);
+            dn_f32x4 d0 = {0.0f, 0.0f, 0.0f, 0.0f}, d1 = d0;
+#pragma unroll
+            for (int tq = 0; tq < 4; tq++) {
+                if (tq <= wave) {
+                    const float4 a = *(const float4*)(tp + kTpT + tp_tri(wave, tq) * 1024 + apos);
+                    const float4 b = *(const float4*)(Xl + (tq * 64 + lane) * 4);
+                    d0 = mfma4(a.x, b.x, d0);
+                    d1 = mfma4(a.y, b.y, d1);
+                    d0 = mfma4(a.z, b.z, d0);
+                    d1 = mfma4(a.w, b.w, d1);
+                }
+                if (more) {
+                    dma_tp_round(rt, tpn, tq);
+                    if (tq < TR - 4) dma_tp_round(rt, tpn, tq + 4);
+                }
+            }
+            dl = d0 + d1;
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) nf |= !is_finite_f(dl[i]);
-        *(float4*)(Dl + ((wave * 16 + l16) * 4 + g) * 4) = make_float4(dl[0], dl[1], dl[2], dl[3]);
-        if (nf) *flag = 1;
-        __syncthreads();  // Delta complete
-        // e: O
+        *(float4*)(Dl + (wave * 64 + lane) * 4) = make_float4(dl[0], dl[1], dl[2], dl[3]);
+        if (nf) flag = 1;
+        dn_lds_barrier();  // Delta complete
+        if (!Q2 && more) {  // the single f32 Q buffer: its reads ended with step b
+            const dn_i32x4 rq = rows_rsrc(p.q, c + 1);
+#pragma unroll
+            for (int k = 0; k < KR; k++) dma_row_round(rq, qn, k);
+        }
+        // e: O (two chains)
         {
-            dn_f32x4 ov = {0.0f, 0.0f, 0.0f, 0.0f};
-            for (int tq = 0; tq <= wave; tq++) {
-                const float4 a = *(const float4*)(tp + kTpP + tp_tri(wave, tq) * 1024 + apos);
-                const float4 b = *(const float4*)(Dl + ((tq * 16 + l16) * 4 + g) * 4);
-                ov = mfma4(a.x, b.x, ov);
-                ov = mfma4(a.y, b.y, ov);
-                ov = mfma4(a.z, b.z, ov);
-                ov = mfma4(a.w, b.w, ov);
+            dn_f32x4 o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = o0;
+#pragma unroll
+            for (int tq = 0; tq < 4; tq++) {
+                if (tq <= wave) {
+                    const float4 a = *(const float4*)(tp + kTpP + tp_tri(wave, tq) * 1024 + apos);
+                    const float4 b = *(const float4*)(Dl + (tq * 64 + lane) * 4);
+                    o0 = mfma4(a.x, b.x, o0);
+                    o1 = mfma4(a.y, b.y, o1);
+                    o0 = mfma4(a.z, b.z, o0);
+                    o1 = mfma4(a.w, b.w, o1);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = 16 * wave + 4 * g + i;
-                const float o = scl[2 * C + t] * aq[i] + ov[i];
-                nf |= !is_finite_f(o);
-                if (c * C + t < p.n_tokens) p.out[((size_t)(c * C + t) * H + h) * D + c0 + l16] = o;
+                opend[i] = scl[2 * C + t] * (aq0[i] + aq1[i]) + (o0[i] + o1[i]);
+                nf |= !is_finite_f(opend[i]);
             }
+            pend = c;
         }
-        // e: S' for state rows 32 w .. 32 w + 31 (two tiles)
+        // e: S' for state rows 32 w .. 32 w + 31 (two tiles x even / odd i chains)
         {
             const float gl = *(const float*)(tp + kTpGl);
+            float* srow0 = Sl + ((2 * wave) * 64 + lane) * 4;
+            float* srow1 = Sl + ((2 * wave + 1) * 64 + lane) * 4;
+            const float4 s0a = *(const float4*)srow0, s0b = *(const float4*)srow1;
+            s0own[0] = dn_f32x4{s0a.x, s0a.y, s0a.z, s0a.w};
+            s0own[1] = dn_f32x4{s0b.x, s0b.y, s0b.z, s0b.w};
+            dn_f32x4 a0 = gl * s0own[0], a1 = gl * s0own[1];
+            dn_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = b0;
+            const int j0 = 32 * wave + l16, j1 = j0 + 16;
 #pragma unroll
-            for (int r2 = 0; r2 < 2; r2++) {
-                const int rt = 2 * wave + r2;
-                float* srow = Sl + ((rt * 16 + l16) * 4 + g) * 4;
-                const float4 s0 = *(const float4*)srow;
-                s0own[r2] = dn_f32x4{s0.x, s0.y, s0.z, s0.w};
-                dn_f32x4 acc = {gl * s0.x, gl * s0.y, gl * s0.z, gl * s0.w};
-                const int j = 16 * rt + l16;
-#pragma unroll
-                for (int q = 0; q < C / 16; q++) {
-                    const float4 b = *(const float4*)(Dl + ((q * 16 + l16) * 4 + g) * 4);
-                    const float4 sk = *(const float4*)(scl + 3 * C + 16 * q + 4 * g);
-                    const int s = 16 * q + 4 * g;
-                    acc = mfma4(dn_elem<DT>(kt, s + 0, j) * sk.x, b.x, acc);
-                    acc = mfma4(dn_elem<DT>(kt, s + 1, j) * sk.y, b.y, acc);
-                    acc = mfma4(dn_elem<DT>(kt, s + 2, j) * sk.z, b.z, acc);
-                    acc = mfma4(dn_elem<DT>(kt, s + 3, j) * sk.w, b.w, acc);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++) nf |= !is_finite_f(acc[i]);
-                *(float4*)srow = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            for (int q = 0; q < C / 16; q++) {
+                const float4 b = *(const float4*)(Dl + (q * 64 + lane) * 4);
+                const float4 sk = *(const float4*)(scl + 3 * C + 16 * q + 4 * g);
+                const int s = 16 * q + 4 * g;
+                const float bs[4] = {b.x * sk.x, b.y * sk.y, b.z * sk.z, b.w * sk.w};
+                a0 = mfma4(dn_elem<DT>(kt, s + 0, j0), bs[0], a0);
+                a1 = mfma4(dn_elem<DT>(kt, s + 0, j1), bs[0], a1);
+                b0 = mfma4(dn_elem<DT>(kt, s + 1, j0), bs[1], b0);
+                b1 = mfma4(dn_elem<DT>(kt, s + 1, j1), bs[1], b1);
+                a0 = mfma4(dn_elem<DT>(kt, s + 2, j0), bs[2], a0);
+                a1 = mfma4(dn_elem<DT>(kt, s + 2, j1), bs[2], a1);
+                b0 = mfma4(dn_elem<DT>(kt, s + 3, j0), bs[3], b0);
+                b1 = mfma4(dn_elem<DT>(kt, s + 3, j1), bs[3], b1);
             }
+            a0 += b0;
+            a1 += b1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) nf |= !is_finite_f(a0[i]) || !is_finite_f(a1[i]);
+            *(float4*)srow0 = make_float4(a0[0], a0[1], a0[2], a0[3]);
+            *(float4*)srow1 = make_float4(a1[0], a1[1], a1[2], a1[3]);
         }
-        if (nf) *flag = 1;
+        if (nf) flag = 1;
 #pragma unroll
         for (int i = 0; i < 4; i++) vcur[i] = vnext[i];
+        return true;
+    };
+
+    int c = 0;
+    bool all = true;
+    for (; c < n_chunks; c += 2) {
+        if (!chunk(c, std::integral_constant<int, 0>{})) { all = false; break; }
+        if (c + 1 < n_chunks && !chunk(c + 1, std::integral_constant<int, 1>{})) { all = false; break; }
     }
-    if (c == n_chunks) {
-        __syncthreads();
-        if (*flag) {  // the last chunk met a non-finite value
+    store_pending();
+    if (all) {
+        dn_lds_barrier();
+        if (flag) {  // the last chunk met a non-finite value
             done = n_chunks - 1;
             restore = true;
         }
@@ -648,7 +762,7 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
 #pragma unroll
     for (int r2 = 0; r2 < 2; r2++) {
         const int rt = 2 * wave + r2;
-        const float4 sv = *(const float4*)(Sl + ((rt * 16 + l16) * 4 + g) * 4);
+        const float4 sv = *(const float4*)(Sl + (rt * 64 + lane) * 4);
         const float v[4] = {restore ? s0own[r2][0] : sv.x, restore ? s0own[r2][1] : sv.y,
                             restore ? s0own[r2][2] : sv.z, restore ? s0own[r2][3] : sv.w};
 #pragma unroll
@@ -674,13 +788,16 @@ hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st) {
 }
 
 template <int DT>
-static hipError_t launch_scan_dt(const DeltaNetLaunch& p, hipStream_t st) {
-    constexpr size_t lds = dn_scan_lds<DT>();
-    static_assert(lds <= 160 * 1024, "scan LDS");
-    hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_scan_kernel<DT>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+static hipError_t launch_chunked_dt(const DeltaNetLaunch& p, hipStream_t st) {
+    constexpr size_t lds_prep = (size_t)2 * kChunk * (128 + 4) * sizeof(float);
+    hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<DT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_prep);
     if (e != hipSuccess) return e;
-    deltanet_chunk_scan_kernel<DT><<<dim3(p.n_heads, kScanBlocks), kChunkThreads, lds, st>>>(p);
+    const int n_chunks = (p.n_tokens + kChunk - 1) / kChunk;
+    deltanet_chunk_prep_kernel<DT><<<dim3(n_chunks, p.n_heads), kChunkThreads, lds_prep, st>>>(p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    deltanet_chunk_scan_kernel<DT><<<dim3(p.n_heads, kScanBlocks), kChunkThreads, 0, st>>>(p);
     return hipGetLastError();
 }
 
@@ -688,18 +805,11 @@ hipError_t launch_deltanet_chunked(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     if (p.head_dim != 128 || !p.ws) return hipErrorInvalidValue;
     constexpr int D = 128;
-    constexpr size_t lds = (size_t)2 * kChunk * (D + 4) * sizeof(float);
-    hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<D>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    const int n_chunks = (p.n_tokens + kChunk - 1) / kChunk;
-    deltanet_chunk_prep_kernel<D><<<dim3(n_chunks, p.n_heads), kChunkThreads, lds, st>>>(p);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
     switch (p.in_dtype) {
-        case GR_DTYPE_F32: e = launch_scan_dt<GR_DTYPE_F32>(p, st); break;
-        case GR_DTYPE_F16: e = launch_scan_dt<GR_DTYPE_F16>(p, st); break;
-        case GR_DTYPE_BF16: e = launch_scan_dt<GR_DTYPE_BF16>(p, st); break;
+        case GR_DTYPE_F32: e = launch_chunked_dt<GR_DTYPE_F32>(p, st); break;
+        case GR_DTYPE_F16: e = launch_chunked_dt<GR_DTYPE_F16>(p, st); break;
+        case GR_DTYPE_BF16: e = launch_chunked_dt<GR_DTYPE_BF16>(p, st); break;
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
