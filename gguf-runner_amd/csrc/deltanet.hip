@@ -203,15 +203,50 @@ __device__ __forceinline__ float2 dn_load2(const void* p, size_t i) {  // elemen
 }
 
 template <int DT>
-__global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(const DeltaNetLaunch p) {
+__device__ __forceinline__ float dn_h2f(uint32_t b) {
+    return DT == GR_DTYPE_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
+}
+
+typedef _Float16 dn_h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 dn_b8 __attribute__((ext_vector_type(8)));
+
+// 16x16x32 MFMA on 16-bit operands (8 consecutive reduction indices per lane,
+// lane group g = l / 16 taking 8 g .. 8 g + 7): products of 16-bit values are
+// exact and accumulate in fp32.
+template <int DT>
+__device__ __forceinline__ dn_f32x4 mfma32(const uint4& a, const uint4& b, dn_f32x4 c) {
+    if constexpr (DT == GR_DTYPE_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(dn_h8, a), __builtin_bit_cast(dn_h8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dn_b8, a), __builtin_bit_cast(dn_b8, b), c,
+                                                       0, 0, 0);
+}
+
+template <int DT>
+constexpr size_t dn_prep_lds() {
+    // f32 inputs: normalised q, k rows [C][D + 4] f32; 16-bit inputs: raw q, k rows
+    // [C][D + 8] (272-byte rows: 16 rows 4 banks apart); both hold A [C][C + 4] f32
+    // once the products are done
+    return DT == GR_DTYPE_F32 ? (size_t)2 * kChunk * (128 + 4) * 4 : (size_t)2 * kChunk * (128 + 8) * 2;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kChunkThreads, DT == GR_DTYPE_F32 ? 2 : 4) void deltanet_chunk_prep_kernel(
+    const DeltaNetLaunch p) {
     constexpr int D = 128;
     constexpr int C = kChunk;
-    constexpr int RS = D + 4;   // qn / kn row stride (floats): rows 4 banks apart
+    constexpr bool RAW = DT != GR_DTYPE_F32;  // 16-bit rows, Gram products on 16-bit MFMA
+    constexpr int RS = D + 4;   // f32 row stride (floats): rows 4 banks apart
+    constexpr int RS16 = D + 8; // 16-bit row stride (elements)
     constexpr int AMS = C + 4;  // A row stride
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float* qn = smem;           // [C][RS] normalised q rows
-    float* kn = qn + C * RS;    // [C][RS] normalised k rows
-    float* am = qn;             // [C][AMS] A (strictly lower), over qn once the products are done
+    float* qn = smem;                          // f32: [C][RS] normalised q rows
+    float* kn = qn + C * RS;                   // f32: [C][RS] normalised k rows
+    uint16_t* qr = (uint16_t*)smem;            // 16-bit: [C][RS16] raw q rows
+    uint16_t* kr = qr + C * RS16;              // 16-bit: [C][RS16] raw k rows
+    float* am = smem;                          // [C][AMS] A (strictly lower), over the rows once the products are done
+    static_assert(C * AMS * 4 <= dn_prep_lds<DT>(), "A fits over the rows");
     // in-chunk cumulative log decay in double: with strong decays the prefix sums
     // reach ~-100 within a chunk, and a decay exp(lg[t] - lg[s]) taken from two
     // f32 prefix sums would carry ~100 ulp of absolute error in its exponent
@@ -227,10 +262,42 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
     if (tid == 0) bad = 0;
     __syncthreads();
 
-    // 1. normalised rows (as math.rs:833-846) and the norms for the row scales:
-    //    wave w takes q and k rows 16 w .. 16 w + 15, all 32 loads issued first
-    {
-        const float inv_scale_q = 1.0f / sqrtf((float)D);
+    const float inv_scale_q = 1.0f / sqrtf((float)D);
+    if constexpr (RAW) {
+        // 1. raw rows into LDS and their norms: wave w takes q and k rows
+        //    16 w .. 16 w + 15, four rows per 16-byte load round (16 lanes a row)
+        uint4 x[8];
+#pragma unroll
+        for (int r4 = 0; r4 < 8; r4++) {
+            const int t = 16 * wave + 4 * (r4 & 3) + g;
+            x[r4] = t < Cn ? *(const uint4*)((const uint16_t*)(r4 < 4 ? p.q : p.k) + ((size_t)(t0 + t) * H + h) * D +
+                                             8 * l16)
+                           : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r4 = 0; r4 < 8; r4++) {
+            const int t = 16 * wave + 4 * (r4 & 3) + g;
+            const bool isq = r4 < 4, valid = t < Cn;
+            const uint32_t w[4] = {x[r4].x, x[r4].y, x[r4].z, x[r4].w};
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float lo = dn_h2f<DT>(w[e] & 0xffffu), hi = dn_h2f<DT>(w[e] >> 16);
+                ss = fmaf(lo, lo, ss);
+                ss = fmaf(hi, hi, ss);
+            }
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) ss += shfl_xor(ss, m);
+            *(uint4*)((isq ? qr : kr) + t * RS16 + 8 * l16) = x[r4];
+            if (l16 == 0) {
+                const float inv = 1.0f / sqrtf(ss + p.eps);
+                (isq ? qi : ki)[t] = !valid ? 0.0f : !p.l2norm ? 1.0f : isq ? inv * inv_scale_q : inv;
+                if (valid && !is_finite_f(ss)) bad = 1;
+            }
+        }
+    } else {
+        // 1. normalised rows (as math.rs:833-846) and the norms for the row scales:
+        //    wave w takes q and k rows 16 w .. 16 w + 15, all 32 loads issued first
         float2 x[32];
 #pragma unroll
         for (int k = 0; k < 32; k++) {
@@ -279,7 +346,9 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
     }
     __syncthreads();
 
-    // 2. K K^T (tiles 0..9) and Q K^T (10..19) on and below the diagonal, five per wave
+    // 2. K K^T (tiles 0..9) and Q K^T (10..19) on and below the diagonal, five per
+    //    wave: of the normalised f32 rows, or exactly of the raw 16-bit rows (the
+    //    norms are applied below)
     dn_f32x4 acc[5];
 #pragma unroll
     for (int u = 0; u < 5; u++) {
@@ -287,21 +356,29 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
         const int tt = ti < kTpTiles ? ti : ti - kTpTiles;
         const int r = tt < 1 ? 0 : tt < 3 ? 1 : tt < 6 ? 2 : 3;
         const int q = tt - r * (r + 1) / 2;
-        const float* ar = (ti < kTpTiles ? kn : qn) + (16 * r + l16) * RS + 4 * g;
-        const float* br = kn + (16 * q + l16) * RS + 4 * g;
         dn_f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (RAW) {
+            const uint16_t* ar = (ti < kTpTiles ? kr : qr) + (16 * r + l16) * RS16 + 8 * g;
+            const uint16_t* br = kr + (16 * q + l16) * RS16 + 8 * g;
 #pragma unroll
-        for (int kk = 0; kk < D / 16; kk++) {
-            const float4 a = *(const float4*)(ar + 16 * kk);
-            const float4 b = *(const float4*)(br + 16 * kk);
-            a4 = mfma4(a.x, b.x, a4);
-            a4 = mfma4(a.y, b.y, a4);
-            a4 = mfma4(a.z, b.z, a4);
-            a4 = mfma4(a.w, b.w, a4);
+            for (int ks = 0; ks < D / 32; ks++)
+                a4 = mfma32<DT>(*(const uint4*)(ar + 32 * ks), *(const uint4*)(br + 32 * ks), a4);
+        } else {
+            const float* ar = (ti < kTpTiles ? kn : qn) + (16 * r + l16) * RS + 4 * g;
+            const float* br = kn + (16 * q + l16) * RS + 4 * g;
+#pragma unroll
+            for (int kk = 0; kk < D / 16; kk++) {
+                const float4 a = *(const float4*)(ar + 16 * kk);
+                const float4 b = *(const float4*)(br + 16 * kk);
+                a4 = mfma4(a.x, b.x, a4);
+                a4 = mfma4(a.y, b.y, a4);
+                a4 = mfma4(a.z, b.z, a4);
+                a4 = mfma4(a.w, b.w, a4);
+            }
         }
         acc[u] = a4;
     }
-    __syncthreads();  // every read of qn is done: A goes over it
+    __syncthreads();  // every read of the rows is done: A goes over them
 #pragma unroll
     for (int u = 0; u < 5; u++) {
         const int ti = wave + 4 * u;
@@ -315,9 +392,11 @@ __global__ __launch_bounds__(kChunkThreads, 2) void deltanet_chunk_prep_kernel(c
             const int t = 16 * r + tl;
             const float dec = s <= t ? expf((float)(lg[t] - lg[s])) : 0.0f;
             if (ti < kTpTiles) {
-                am[t * AMS + s] = s < t ? bt[t] * dec * acc[u][i] : 0.0f;
+                const float gr = RAW ? ki[t] * ki[s] * acc[u][i] : acc[u][i];
+                am[t * AMS + s] = s < t ? bt[t] * dec * gr : 0.0f;
             } else {
-                const float v = s <= t ? dec * acc[u][i] : 0.0f;
+                const float pr = RAW ? qi[t] * ki[s] * acc[u][i] : acc[u][i];
+                const float v = s <= t ? dec * pr : 0.0f;
                 if (!is_finite_f(v)) bad = 1;
                 *(float*)(blk + kTpP + tt * 1024 + 4 * tp_elem(tl, l16)) = v;
             }
@@ -418,11 +497,6 @@ __device__ __forceinline__ void dn_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F
 // keeps the compiler from moving memory accesses across it.
 __device__ __forceinline__ void dn_lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-template <int DT>
-__device__ __forceinline__ float dn_h2f(uint32_t b) {
-    return DT == GR_DTYPE_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
 }
 
 // q / k chunk tiles in LDS: row t (D elements) as 16-byte pieces, piece p at
@@ -789,7 +863,7 @@ hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st) {
 
 template <int DT>
 static hipError_t launch_chunked_dt(const DeltaNetLaunch& p, hipStream_t st) {
-    constexpr size_t lds_prep = (size_t)2 * kChunk * (128 + 4) * sizeof(float);
+    constexpr size_t lds_prep = dn_prep_lds<DT>();
     hipError_t e = hipFuncSetAttribute((const void*)deltanet_chunk_prep_kernel<DT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_prep);
     if (e != hipSuccess) return e;

@@ -119,3 +119,35 @@ def test_deltanet_nonfinite_inputs_follow_reference_guards(orc, dev):
     assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
     # the events matter: the state of head 1 restarts from zero at token 400
     assert float(np.abs(Sref[1]).max()) < float(np.abs(Sref[0]).max())
+
+
+@pytest.mark.parametrize("fmt", ["F16", "BF16"])
+@pytest.mark.parametrize("l2norm", [True, False])
+def test_deltanet_16bit_inputs_chunked(orc, dev, fmt, l2norm):
+    """16-bit q/k/v on the chunked path (exact 16-bit Gram products, raw-row MFMA
+    operands), a ragged last chunk, non-zero initial state, with and without the
+    fused normalisation (without it the oracle gets rows of norm ~1 so the
+    recurrence stays in range)."""
+    f = getattr(orc, fmt)
+    T, H, d = 200, 4, 128
+    q, k, v, gate, beta = _inputs(orc, T, H, d, 300 + int(l2norm), f)
+    if not l2norm:  # unit-norm-ish rows stored in the 16-bit format
+        conv = orc.f16_bits if f == orc.F16 else orc.bf16_bits
+        rng = np.random.default_rng(9)
+        qq = rng.standard_normal((T, H, d)).astype(np.float32)
+        kk = rng.standard_normal((T, H, d)).astype(np.float32)
+        q = conv(qq / np.linalg.norm(qq, axis=-1, keepdims=True) / np.sqrt(d))
+        k = conv(kk / np.linalg.norm(kk, axis=-1, keepdims=True))
+    S0 = (0.1 * np.random.default_rng(3).standard_normal((H, d, d))).astype(np.float32)
+    ref, Sref = orc.deltanet_scan(orc.upcast(q, f), orc.upcast(k, f), orc.upcast(v, f), gate, beta, S0,
+                                  l2norm=l2norm, eps=1e-6, n_threads=orc.env_threads())
+    from gguf_runner_amd import ops
+    st = torch.from_numpy(S0.copy()).to(dev)
+    out = torch.empty((T, H, d), dtype=torch.float32, device=dev)
+    ops.DeltaNetCall(_to_dev(q, f, orc, dev), _to_dev(k, f, orc, dev), _to_dev(v, f, orc, dev),
+                     torch.from_numpy(gate).to(dev), torch.from_numpy(beta).to(dev), st, out,
+                     l2norm=l2norm, algo=2)()
+    torch.cuda.synchronize()
+    got, S = out.cpu().numpy(), st.cpu().numpy()
+    assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
+    assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
