@@ -176,6 +176,8 @@ int check_decode(const gr_decode_args* a) {
             return fail(GR_ERR_ARG, "gr_decode_attention: negative scale stride");
     }
     if (a->max_kv_len <= 0) return fail(GR_ERR_ARG, "gr_decode_attention: max_kv_len must be > 0");
+    if (a->out_gate && (a->out_gate_row_stride < 0 || a->out_gate_head_stride < 0))
+        return fail(GR_ERR_ARG, "gr_decode_attention: negative out_gate stride");
     if (a->split_keys < 0) return fail(GR_ERR_ARG, "gr_decode_attention: split_keys < 0");
     if (!a->q || !a->k_cache || !a->v_cache || !a->kv_start || !a->kv_end || !a->out ||
         !a->workspace)
@@ -226,6 +228,9 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
     p.kv_end = a->kv_end;
     p.seq_slot = seq_slot;
     p.out = a->out;
+    p.gate.gate = a->out_gate;
+    p.gate.row_stride = a->out_gate_row_stride;
+    p.gate.head_stride = a->out_gate_head_stride;
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
     p.use_mfma = 1;

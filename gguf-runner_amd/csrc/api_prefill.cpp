@@ -41,6 +41,8 @@ int check_prefill(const gr_prefill_args* a) {
     if (a->n_tokens > 0 && (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache || !a->out ||
                             !a->workspace))
         return fail(GR_ERR_ARG, "gr_prefill_attention: null buffer");
+    if (a->out_gate && (a->out_gate_row_stride < 0 || a->out_gate_head_stride < 0))
+        return fail(GR_ERR_ARG, "gr_prefill_attention: negative out_gate stride");
     if (a->cache_row_stride < (int64_t)a->n_kv_heads * a->head_dim || (a->cache_row_stride * 2) % 16)
         return fail(GR_ERR_ARG, "gr_prefill_attention: cache_row_stride must be >= n_kv_heads*head_dim and 16-byte aligned");
     if (((uintptr_t)a->k_cache | (uintptr_t)a->v_cache) % 16 || (uintptr_t)a->out % 16)
@@ -148,6 +150,9 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pf.v_cache = a->v_cache;
     pf.cache_row_stride = a->cache_row_stride;
     pf.out = a->out;
+    pf.gate.gate = a->out_gate;
+    pf.gate.row_stride = a->out_gate_row_stride;
+    pf.gate.head_stride = a->out_gate_head_stride;
     e = launch_prefill(pf, st);
     if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention launch");
     return GR_OK;

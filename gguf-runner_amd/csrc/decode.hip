@@ -223,6 +223,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     }
     const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
     float* out = p.out + ((size_t)s * p.n_heads + h) * D;
+    const float* gt = p.gate.at(s, h);  // Qwen3.5 output gate, or null
     constexpr int EPL = D / 64;
     // Few partials (the usual case): every lane loads all (m, l) pairs and its
     // own o values at once and reduces them itself, one round trip to memory.
@@ -256,7 +257,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
         }
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) out[lane + 64 * e] = acc[e] * inv;
+        for (int e = 0; e < EPL; e++) {
+            const float o = acc[e] * inv;
+            out[lane + 64 * e] = gt ? gate_mul(o, gt[lane + 64 * e]) : o;
+        }
         return;
     }
     // pass 1: global max and denominator, lanes over splits
@@ -301,7 +305,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
         __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
-    for (int e = 0; e < EPL; e++) out[lane + 64 * e] = acc[e] * inv;
+    for (int e = 0; e < EPL; e++) {
+        const float o = acc[e] * inv;
+        out[lane + 64 * e] = gt ? gate_mul(o, gt[lane + 64 * e]) : o;
+    }
 }
 
 template <typename KV, int D>

@@ -114,4 +114,11 @@ __device__ __forceinline__ bool is_finite_f(float x) {
 }
 __device__ __forceinline__ float finite_or_zero(float x) { return is_finite_f(x) ? x : 0.0f; }
 
+// sigmoid_mul_inplace for one element (math.rs:396-403, the x86 branch):
+// x * (1 / (1 + exp(-g))), non-finite results to 0.
+__device__ __forceinline__ float gate_mul(float x, float g) {
+    const float s = 1.0f / (1.0f + expf(-g));
+    return finite_or_zero(x * s);
+}
+
 }  // namespace gr

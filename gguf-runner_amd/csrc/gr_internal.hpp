@@ -8,6 +8,17 @@ namespace gr {
 
 // Split-K decode.  Partials: ws_o [n_seq][n_heads][n_splits][head_dim],
 // ws_ml [n_seq][n_heads][n_splits][2] = (m, l) in log2 units.
+// Qwen3.5 output gate of output row r (decode: batch entry, prefill: token), head
+// h: out *= sigmoid(gate[r * row_stride + h * head_stride + i]) (gate null = none).
+struct OutGate {
+    const float* gate = nullptr;
+    int64_t row_stride = 0;
+    int head_stride = 0;
+    __device__ __forceinline__ const float* at(int64_t r, int h) const {
+        return gate ? gate + r * row_stride + (int64_t)h * head_stride : nullptr;
+    }
+};
+
 struct DecodeLaunch {
     int n_seq, n_heads, n_kv_heads, head_dim, kv_dtype;
     int split_keys, n_splits;
@@ -61,6 +72,7 @@ struct DecodeLaunch {
     int tok_pack;
     const int32_t* col_start;
     const int32_t* col_end;
+    OutGate gate;  // written by the combine kernels
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);
@@ -219,6 +231,7 @@ struct PrefillLaunch {
     const void* v_cache;
     int64_t cache_row_stride;
     float* out;
+    OutGate gate;
 };
 
 hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st);
@@ -242,6 +255,7 @@ struct PrefillQ8Launch {
     const float* v_scale;
     int64_t scale_row_stride;
     float* out;
+    OutGate gate;
 };
 
 hipError_t launch_prefill_q8(const PrefillQ8Launch& p, hipStream_t st);

@@ -559,6 +559,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         if (row_ok) {
             float* orow = p.out + ((size_t)my_row * p.n_heads + h) * D;
+            const float* gt = p.gate.at(my_row, h);  // Qwen3.5 output gate, or null
 #pragma unroll
             for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
@@ -569,6 +570,12 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                     v.y = o[dt][4 * jb + 1] * inv;
                     v.z = o[dt][4 * jb + 2] * inv;
                     v.w = o[dt][4 * jb + 3] * inv;
+                    if (gt) {
+                        v.x = gate_mul(v.x, gt[d0 + 0]);
+                        v.y = gate_mul(v.y, gt[d0 + 1]);
+                        v.z = gate_mul(v.z, gt[d0 + 2]);
+                        v.w = gate_mul(v.w, gt[d0 + 3]);
+                    }
                     *(float4*)(orow + d0) = v;
                 }
         }

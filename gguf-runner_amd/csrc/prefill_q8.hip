@@ -478,6 +478,7 @@ __global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const Pref
     const float lsum = q8p_xsum32(lrow);
     if (row_ok) {
         float* orow = p.out + ((size_t)my_row * p.n_heads + h) * D;
+        const float* gt = p.gate.at(my_row, h);  // Qwen3.5 output gate, or null
         const float il = lsum > 0.0f ? 1.0f / lsum : 0.0f;
 #pragma unroll
         for (int dt = 0; dt < NB; dt++) {
@@ -490,6 +491,12 @@ __global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const Pref
                 v.y = o[dt][4 * jb + 1] * inv;
                 v.z = o[dt][4 * jb + 2] * inv;
                 v.w = o[dt][4 * jb + 3] * inv;
+                if (gt) {
+                    v.x = gate_mul(v.x, gt[d0 + 0]);
+                    v.y = gate_mul(v.y, gt[d0 + 1]);
+                    v.z = gate_mul(v.z, gt[d0 + 2]);
+                    v.w = gate_mul(v.w, gt[d0 + 3]);
+                }
                 *(float4*)(orow + d0) = v;
             }
         }

@@ -209,8 +209,9 @@ __global__ __launch_bounds__(256) void turbo_combine_kernel(const DecodeLaunch p
     for (int j = 0; j < J; j++) b[j] += r[j];
     tq::wave_transform<D>(b, sg + ss, sg, lane);  // rot_post, rot_pre: inverse
     float* out = p.out + ((size_t)s * p.n_heads + h) * D;
+    const float* gt = p.gate.at(s, h);  // Qwen3.5 output gate, or null
 #pragma unroll
-    for (int j = 0; j < J; j++) out[lane + 64 * j] = b[j];
+    for (int j = 0; j < J; j++) out[lane + 64 * j] = gt ? gate_mul(b[j], gt[lane + 64 * j]) : b[j];
 }
 
 hipError_t launch_turbo_combine(const DecodeLaunch& p, hipStream_t st) {

@@ -47,6 +47,7 @@ class DecodeArgs(ctypes.Structure):
         ("k_scale", _p), ("v_scale", _p), ("scale_seq_stride", _i64), ("scale_row_stride", _i64),
         ("q8_block", _i32), ("k_sign", _p), ("v_sign", _p), ("k_rnorm", _p), ("v_rnorm", _p),
         ("turbo_signs", _p), ("turbo_slot_stride", _i64),
+        ("out_gate", _p), ("out_gate_row_stride", _i64), ("out_gate_head_stride", _i32),
     ]
 
 
@@ -58,6 +59,7 @@ class PrefillArgs(ctypes.Structure):
         ("k_norm", _p), ("norm_eps", _f), ("is_gemma3", _i32), ("q", _p), ("k", _p), ("v", _p),
         ("k_cache", _p), ("v_cache", _p), ("cache_row_stride", _i64), ("out", _p),
         ("workspace", _p), ("bidirectional", _i32),
+        ("out_gate", _p), ("out_gate_row_stride", _i64), ("out_gate_head_stride", _i32),
     ]
 
 

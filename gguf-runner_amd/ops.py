@@ -38,6 +38,17 @@ def _aligned(ws: torch.Tensor) -> int:
     return (p + 255) // 256 * 256
 
 
+def _set_gate(a, gate, row_stride, head_stride) -> None:
+    """The optional Qwen3.5 output gate (an f32 device tensor, or None): element
+    (row r, head h, i) at r * row_stride + h * head_stride + i of gate's storage."""
+    if gate is None:
+        return
+    assert gate.dtype == torch.float32 and gate.is_cuda
+    a.out_gate = _ptr(gate)
+    a.out_gate_row_stride = int(row_stride)
+    a.out_gate_head_stride = int(head_stride)
+
+
 class DecodeCall:
     """A prepared gr_decode_attention call (args + workspace), reusable for timing.
 
@@ -48,7 +59,8 @@ class DecodeCall:
     """
 
     def __init__(self, q, k_cache, v_cache, kv_start, kv_end, out, *, max_kv_len,
-                 score_scale=None, split_keys=0, k_scale=None, v_scale=None, q8_block=False):
+                 score_scale=None, split_keys=0, k_scale=None, v_scale=None, q8_block=False,
+                 out_gate=None, out_gate_row_stride=0, out_gate_head_stride=0):
         n_seq, n_heads, d = q.shape
         _, seq_len, n_kv, d2 = k_cache.shape
         assert d2 == d and v_cache.shape == k_cache.shape and out.shape == q.shape
@@ -75,6 +87,8 @@ class DecodeCall:
             a.scale_seq_stride = seq_len * per_row
             a.scale_row_stride = per_row
             a.q8_block = int(bool(q8_block))
+        _set_gate(a, out_gate, out_gate_row_stride, out_gate_head_stride)
+        self._keep = self._keep + (out_gate,)
         L = ffi.lib()
         nbytes = L.gr_decode_workspace_size(ctypes.byref(a))
         self.ws = _workspace(nbytes, q.device)
@@ -166,7 +180,8 @@ class PrefillCall:
 
     def __init__(self, q, k, v, k_cache, v_cache, out, *, base_pos=0, window=0,
                  rope_mode=ffi.ROPE_NONE, rope_dim=0, rope_scale=1.0, rope_freqs=None,
-                 q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False, bidirectional=False):
+                 q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False, bidirectional=False,
+                 out_gate=None, out_gate_row_stride=0, out_gate_head_stride=0):
         m, n_heads, d = q.shape
         _, n_kv, d2 = k.shape
         assert d2 == d and v.shape == k.shape and out.shape == (m, n_heads, d)
@@ -174,7 +189,7 @@ class PrefillCall:
         assert out.dtype == torch.float32
         for t in (q, k, v, k_cache, v_cache, out):
             assert t.is_contiguous()
-        self._keep = (q, k, v, k_cache, v_cache, out, rope_freqs, q_norm, k_norm)
+        self._keep = (q, k, v, k_cache, v_cache, out, rope_freqs, q_norm, k_norm, out_gate)
         a = ffi.PrefillArgs()
         a.n_tokens, a.base_pos, a.n_heads, a.n_kv_heads, a.head_dim = m, base_pos, n_heads, n_kv, d
         a.dtype = _DT[q.dtype]
@@ -189,6 +204,7 @@ class PrefillCall:
         a.k_cache, a.v_cache = _ptr(k_cache), _ptr(v_cache)
         a.cache_row_stride = n_kv * d
         a.out = _ptr(out)
+        _set_gate(a, out_gate, out_gate_row_stride, out_gate_head_stride)
         nbytes = ffi.lib().gr_prefill_workspace_size(ctypes.byref(a))
         self.ws = _workspace(nbytes, q.device)
         a.workspace = _aligned(self.ws)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define GR_ATTN_ABI_VERSION 3
+#define GR_ATTN_ABI_VERSION 4
 
 /* Status codes. */
 #define GR_OK 0
@@ -113,6 +113,16 @@ typedef struct gr_decode_args {
     const float* v_rnorm;
     const uint8_t* turbo_signs;
     int64_t turbo_slot_stride;
+    /* Qwen3.5 packed-q output gate (qwen3next_packed_q_gate, inference.rs:3509-3519
+     * decode, 3003-3016 batched prefill), fused into the kernel that writes out: when
+     * non-NULL, out[r][h][i] = finite_or_zero(out[r][h][i] * sigmoid(g)) with
+     * g = out_gate[r*out_gate_row_stride + h*out_gate_head_stride + i]
+     * (sigmoid_mul_inplace, math.rs:396-403), r = the sequence.  The reference's packed
+     * rows [q_h | gate_h] give out_gate = rows + head_dim, head stride 2*head_dim and
+     * row stride 2*n_heads*head_dim.  NULL = no gate. */
+    const float* out_gate;
+    int64_t out_gate_row_stride;
+    int32_t out_gate_head_stride;
 } gr_decode_args;
 
 size_t gr_decode_workspace_size(const gr_decode_args* a);
@@ -175,6 +185,16 @@ typedef struct gr_prefill_args {
                             * pos + 1 - window (saturating) or 0, i.e. every key of the
                             * block plus its causal / window history
                             * (LanguageAttentionPolicy::visible_keys, attention.rs:74-96). */
+    /* Qwen3.5 packed-q output gate (qwen3next_packed_q_gate, inference.rs:3509-3519
+     * decode, 3003-3016 batched prefill), fused into the kernel that writes out: when
+     * non-NULL, out[r][h][i] = finite_or_zero(out[r][h][i] * sigmoid(g)) with
+     * g = out_gate[r*out_gate_row_stride + h*out_gate_head_stride + i]
+     * (sigmoid_mul_inplace, math.rs:396-403), r = the token.  The reference's packed
+     * rows [q_h | gate_h] give out_gate = rows + head_dim, head stride 2*head_dim and
+     * row stride 2*n_heads*head_dim.  NULL = no gate. */
+    const float* out_gate;
+    int64_t out_gate_row_stride;
+    int32_t out_gate_head_stride;
 } gr_prefill_args;
 
 size_t gr_prefill_workspace_size(const gr_prefill_args* a);

@@ -1038,6 +1038,17 @@ void orc_deltanet_scan(const float* q, const float* k, const float* v, const flo
     }
 }
 
+/* sigmoid_mul_inplace, math.rs:396-403 (the x86 / portable branch): the Qwen3.5
+ * packed-q output gate, d[i] = finite_or_zero(d[i] * (1 / (1 + exp(-g[i])))).
+ * Pinned by: float64 sigmoid (closed form), g = +-inf and NaN special cases
+ * (tests/test_oracle_attention.py). */
+void orc_sigmoid_mul(float* d, const float* g, int n) {
+    for (int i = 0; i < n; i++) {
+        const float s = 1.0f / (1.0f + expf(-g[i]));
+        d[i] = finite_or_zero(d[i] * s);
+    }
+}
+
 /* ---------------------------------------------------------------- encoder attention */
 
 /* dot_f32_simd on x86 with AVX2+FMA (quant.rs:741-763 dot_f32_avx2_ptr, via the

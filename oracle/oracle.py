@@ -71,6 +71,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_deltanet_scan.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _i]
     L.orc_max_threads.restype = _i
     L.orc_encoder_self_attention.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _i]
+    L.orc_sigmoid_mul.argtypes = [_p, _p, _i]
     L.orc_qwen3next_ssm_token.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p, _p, _p]
     L.orc_splitmix64.argtypes = [ctypes.c_uint64]
     L.orc_splitmix64.restype = ctypes.c_uint64
@@ -433,6 +434,15 @@ def qwen3next_ssm_tokens_f64(qkv, z, gate_a, gate_b, *, n_k_heads, n_v_heads, he
         out[t] = sn * (o * inv) * (zz[t] * sig(zz[t]))
     new_hist = np.concatenate([hist, qkv])[T:T + K - 1] if K > 1 else hist
     return out.reshape(T, d_inner), np.ascontiguousarray(new_hist, np.float32), S
+
+
+def sigmoid_mul(d, g) -> np.ndarray:
+    """orc_sigmoid_mul on a copy of d (the Qwen3.5 output gate, math.rs:396-403)."""
+    d = _f32(d).copy()
+    g = _f32(g)
+    assert d.shape == g.shape
+    lib().orc_sigmoid_mul(_ptr(d), _ptr(g), d.size)
+    return d
 
 
 def f16_bits(x) -> np.ndarray:

@@ -289,3 +289,18 @@ def test_encoder_attention_float64_closed_form(orc, hd):
             p = np.exp(sc - sc.max(axis=1, keepdims=True))
             ref = (p / p.sum(axis=1, keepdims=True)) @ v[rows, cols].astype(np.float64)
             np.testing.assert_allclose(got[rows, cols], ref, rtol=0, atol=2e-5)
+
+
+def test_sigmoid_mul_matches_float64_and_special_cases(orc):
+    """orc_sigmoid_mul (the Qwen3.5 output gate, math.rs:396-403): x / (1 + exp(-g))
+    against float64 to fp32 rounding over the exp range; g = +inf gives x, g = -inf
+    gives 0 (exp(inf) = inf), a NaN gate or a product that overflows gives 0."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(50_000).astype(np.float32) * 10
+    g = rng.uniform(-90, 90, 50_000).astype(np.float32)
+    got = orc.sigmoid_mul(x, g)
+    exp = x.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    assert np.all(np.abs(got - exp) <= 4e-7 * np.maximum(np.abs(exp), 1e-30) + 1e-37)
+    xs = np.array([3.0, 3.0, 3.0, 3.0, np.inf, 3.4e38, -2.0], np.float32)
+    gs = np.array([np.inf, -np.inf, np.nan, 0.0, 1.0, 100.0, 0.0], np.float32)
+    assert orc.sigmoid_mul(xs, gs).tolist() == [3.0, 0.0, 0.0, 1.5, 0.0, np.float32(3.4e38), -1.0]
