@@ -91,8 +91,10 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     const int kv_mul = a->n_kv_heads > 0 ? a->n_heads / a->n_kv_heads : 0;
     pl.stream = split <= 0 &&
                 (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16 || a->kv_dtype == GR_DTYPE_Q8) &&
-                kv_mul >= 1 && kv_mul <= 16 && (a->head_dim == 128 || a->head_dim == 256) &&
-                a->n_seq <= kStreamMaxSeq && (int64_t)a->n_seq * max_len * a->n_kv_heads < (int64_t)1 << 30;
+                kv_mul >= 1 &&
+                (a->head_dim == 128 || a->head_dim == 256 || (a->head_dim == 64 && a->kv_dtype == GR_DTYPE_Q8)) &&
+                a->n_seq <= kStreamMaxSeq &&
+                (int64_t)a->n_seq * max_len * a->n_kv_heads * ((kv_mul + 15) / 16) < (int64_t)1 << 30;
     if (pl.stream) {
         pl.split_keys = kStreamMinKeys;
         pl.n_splits = (max_len + kStreamMinKeys - 1) / kStreamMinKeys + 1;
@@ -131,18 +133,6 @@ int check_decode(const gr_decode_args* a) {
     if (a->n_heads % a->n_kv_heads != 0)
         return fail(GR_ERR_ARG, "gr_decode_attention: n_heads %d not a multiple of n_kv_heads %d",
                     a->n_heads, a->n_kv_heads);
-    const int kv_mul = a->n_heads / a->n_kv_heads;
-    const bool pow2 = kv_mul == 1 || kv_mul == 2 || kv_mul == 4 || kv_mul == 8;
-    // f32 caches and 16-bit caches at head_dim 64 run the VALU split kernel (kv_mul
-    // a power of two up to 8); the MFMA kernels (16-bit / Q8 at 128 / 256, Turbo at
-    // any head size) take up to 16 query heads per KV head.
-    const bool valu = a->kv_dtype == GR_DTYPE_F32 ||
-                      ((a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16) && a->head_dim == 64);
-    if (valu ? !pow2 : kv_mul > 16)
-        return fail(GR_ERR_ARG,
-                    "gr_decode_attention: kv_mul %d unsupported (f32 KV and 16-bit KV at head_dim 64: 1,2,4,8; "
-                    "otherwise <= 16)",
-                    kv_mul);
     if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
         return fail(GR_ERR_ARG, "gr_decode_attention: head_dim %d unsupported (64,128,256)",
                     a->head_dim);
@@ -162,16 +152,12 @@ int check_decode(const gr_decode_args* a) {
             return fail(GR_ERR_ARG, "gr_decode_attention: bad Turbo aux or sign-table strides");
     }
     if (a->kv_dtype == GR_DTYPE_Q8) {
-        if (a->head_dim != 128 && a->head_dim != 256)
-            return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs head_dim 128 or 256");
+        if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+            return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs head_dim 64, 128 or 256");
         if (!a->k_scale || !a->v_scale)
             return fail(GR_ERR_ARG, "gr_decode_attention: Q8 KV needs k_scale and v_scale");
-        if (a->q8_block &&
-            (((uintptr_t)a->k_scale | (uintptr_t)a->v_scale) % 16 != 0 || a->scale_row_stride % 4 != 0 ||
-             a->scale_seq_stride % 4 != 0 || a->scale_row_stride < (int64_t)a->n_kv_heads * a->head_dim / 32))
-            return fail(GR_ERR_ARG,
-                        "gr_decode_attention: Q8 block scales need 16-byte aligned scale arrays and "
-                        "strides (multiples of 4 floats, row stride >= kv_dim/32)");
+        if (a->q8_block && a->scale_row_stride < (int64_t)a->n_kv_heads * a->head_dim / 32)
+            return fail(GR_ERR_ARG, "gr_decode_attention: Q8 block scales need scale_row_stride >= kv_dim/32");
         if (a->scale_row_stride < 0 || a->scale_seq_stride < 0)
             return fail(GR_ERR_ARG, "gr_decode_attention: negative scale stride");
     }

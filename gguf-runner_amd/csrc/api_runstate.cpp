@@ -224,8 +224,6 @@ int validate_config(const gr_attn_config* c) {
     if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
         return fail(GR_ERR_ARG, "head_dim %d unsupported (64, 128, 256)", c->head_dim);
     if (c->kv_dtype < GR_DTYPE_F32 || c->kv_dtype > GR_DTYPE_TURBO) return fail(GR_ERR_ARG, "bad kv_dtype %d", c->kv_dtype);
-    if (c->kv_dtype == GR_DTYPE_Q8 && c->head_dim != 128 && c->head_dim != 256)
-        return fail(GR_ERR_ARG, "Q8 KV cache needs head_dim 128 or 256");
     if (c->rope_mode < GR_ROPE_NONE || c->rope_mode > GR_ROPE_NEOX) return fail(GR_ERR_ARG, "bad rope_mode %d", c->rope_mode);
     const int rd = c->rope_dim > 0 ? c->rope_dim : c->head_dim;
     if (rd > c->head_dim || (rd & 1)) return fail(GR_ERR_ARG, "rope_dim %d must be even and <= head_dim", rd);
@@ -675,8 +673,9 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
     probe.head_dim = s->d;
     probe.kv_dtype = s->cfg.kv_dtype;
     probe.max_kv_len = max_len;
-    TurboPack pack;
-    if (is_turbo(s)) {
+    TurboPack pack;  // tp = 0: rows decoded one query row each (GQA groups above 16 heads)
+    const int kv_mul = s->cfg.n_heads / s->cfg.n_kv_heads;
+    if (is_turbo(s) && turbo_pack_rows(s->d, kv_mul) * kv_mul <= 16) {
         pack = plan_turbo_pack(s, m, starts, ends);
         probe = turbo_pack_probe(s, m, pack);
     }
@@ -731,8 +730,9 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         p.k_cache = kc;
         p.v_cache = vc;
         if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
-        if (is_q8(s)) {
-            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile)
+        if (is_q8(s) && s->d != 64) {
+            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile);
+            // head_dim 64 runs the rows through the decode kernels instead
             PrefillQ8Launch pq{};
             pq.n_tokens = m;
             pq.n_heads = s->cfg.n_heads;
@@ -754,7 +754,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
             pq.out = xo;
             const hipError_t e = launch_prefill_q8(pq, s->stream);
             if (e != hipSuccess) return hip_fail(e, "q8 prefill launch");
-        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv, is_turbo(s) ? &pack : nullptr))) {
+        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv, pack.tp > 0 ? &pack : nullptr))) {
             return rc;
         }
     }

@@ -30,6 +30,7 @@ struct DecodeGeom {
     static_assert(LPR >= 1 && LPR <= 64 && 64 % LPR == 0, "row must map onto a wave");
 };
 
+// KVMUL: query heads per workgroup (the GQA group, or a slice of it: n_sub > 1).
 template <typename KV, int D, int KVMUL>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const DecodeLaunch p) {
     using G = DecodeGeom<KV, D>;
@@ -37,7 +38,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     constexpr int STEP = kDecodeWaves * kDecodeUnroll * RPW;  // rows per block iteration
 
     const int split = blockIdx.x;
-    const int g = blockIdx.y;
+    const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
+    const int g = blockIdx.y / n_sub;  // KV head
+    const int kv_mul = p.n_heads / p.n_kv_heads;
+    const int h0 = g * kv_mul + (blockIdx.y % n_sub) * KVMUL;  // first query head
+    const int nq = min(KVMUL, g * kv_mul + kv_mul - h0);       // query heads here
     const int s = blockIdx.z;
     const int t_begin = p.kv_start[s] + split * p.split_keys;
     const int t_limit = p.kv_end[s];
@@ -55,9 +60,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     float qv[KVMUL][EPL];
 #pragma unroll
     for (int j = 0; j < KVMUL; j++) {
-        const float* qh = p.q + ((size_t)s * p.n_heads + (size_t)g * KVMUL + j) * D + e0;
+        const float* qh = p.q + ((size_t)s * p.n_heads + h0 + (j < nq ? j : 0)) * D + e0;
 #pragma unroll
-        for (int e = 0; e < EPL; e++) qv[j][e] = qh[e] * qscale;
+        for (int e = 0; e < EPL; e++) qv[j][e] = j < nq ? qh[e] * qscale : 0.0f;
     }
 
     float m[KVMUL], l[KVMUL], o[KVMUL][EPL];
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     __syncthreads();
     // Thread layout for the final merge: KVMUL*D outputs spread over the block.
     const int n_splits = p.n_splits;
-    for (int idx = threadIdx.x; idx < KVMUL * D; idx += kDecodeThreads) {
+    for (int idx = threadIdx.x; idx < nq * D; idx += kDecodeThreads) {
         const int j = idx / D;
         const int i = idx % D;
         float mx = -INFINITY;
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
             lt += sh_l[w][j] * a;
             ot += sh_o[w][j][i] * a;
         }
-        const int h = g * KVMUL + j;
+        const int h = h0 + j;
         const size_t part = ((size_t)s * p.n_heads + h) * n_splits + split;
         p.ws_o[part * D + i] = ot;
         if (i == 0) {
@@ -214,9 +219,12 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     if (h >= p.n_heads) return;
     const int len = p.kv_end[s] - p.kv_start[s];
     int nv;
-    if (p.stream_sched) {  // ranges of stream_sched[n_seq] keys that meet pair (s, h / kv_mul)
+    if (p.stream_sched) {  // ranges of stream_sched[n_seq] keys that meet pair (s, column of h)
         const int q = p.stream_sched[p.n_seq];
-        const int off = p.stream_sched[s] + (h / (p.n_heads / p.n_kv_heads)) * len;
+        const int kv_mul = p.n_heads / p.n_kv_heads;
+        const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
+        const int col = (h / kv_mul) * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0);
+        const int off = p.stream_sched[s] + col * len;
         nv = len > 0 ? min(p.n_splits, (off + len - 1) / q - off / q + 1) : 0;
     } else {
         nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
@@ -311,10 +319,18 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     }
 }
 
+// Query heads per workgroup: the whole GQA group rounded up to 1, 2, 4 or 8
+// (unused slots masked), groups above 8 in slices of 8 (n_sub columns per KV head).
+static int valu_heads_per_block(int kv_mul) { return kv_mul <= 1 ? 1 : kv_mul <= 2 ? 2 : kv_mul <= 4 ? 4 : 8; }
+
 template <typename KV, int D>
-static hipError_t launch_kvmul(const DecodeLaunch& p, int kv_mul, hipStream_t st) {
-    dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
-    switch (kv_mul) {
+static hipError_t launch_kvmul(const DecodeLaunch& p0, int kv_mul, hipStream_t st) {
+    DecodeLaunch p = p0;
+    const int hb = valu_heads_per_block(kv_mul);
+    p.n_sub = (kv_mul + hb - 1) / hb;
+    p.sub_heads = hb;
+    dim3 grid(p.n_splits, p.n_kv_heads * p.n_sub, p.n_seq);
+    switch (hb) {
         case 1: decode_split_kernel<KV, D, 1><<<grid, kDecodeThreads, 0, st>>>(p); break;
         case 2: decode_split_kernel<KV, D, 2><<<grid, kDecodeThreads, 0, st>>>(p); break;
         case 4: decode_split_kernel<KV, D, 4><<<grid, kDecodeThreads, 0, st>>>(p); break;
@@ -348,12 +364,16 @@ static hipError_t launch_combine(const DecodeLaunch& p, hipStream_t st) {
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
     if (p.kv_dtype == GR_DTYPE_TURBO) return decode_turbo_supported(p) ? launch_decode_turbo(p, st) : hipErrorInvalidValue;
-    if (p.use_mfma && decode_mfma_supported(p)) {
-        hipError_t e = launch_decode_mfma_split(p, st);
+    DecodeLaunch pm = p;  // MFMA path: groups above 16 query heads in columns of 16
+    pm.n_sub = (kv_mul + 15) / 16;
+    pm.sub_heads = 16;
+    if (p.use_mfma && decode_mfma_supported(pm)) {
+        hipError_t e = launch_decode_mfma_split(pm, st);
         if (e != hipSuccess) return e;
         switch (p.head_dim) {
-            case 128: return launch_combine<128>(p, st);
-            case 256: return launch_combine<256>(p, st);
+            case 64: return launch_combine<64>(pm, st);
+            case 128: return launch_combine<128>(pm, st);
+            case 256: return launch_combine<256>(pm, st);
             default: return hipErrorInvalidValue;
         }
     }

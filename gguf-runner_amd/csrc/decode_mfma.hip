@@ -2,8 +2,9 @@
 //
 // Same work split and partial format as decode.hip (one workgroup per
 // (sequence, KV head, split); partials merged by decode_combine_kernel), but
-// the scores and the value accumulation run on v_mfma_f32_16x16x32 with the
-// kv_mul (<= 16) query heads of a GQA group on the N axis:
+// the scores and the value accumulation run on v_mfma_f32_16x16x32 with up to 16
+// query heads of a GQA group on the N axis (larger groups: several workgroup
+// columns per KV head, DecodeLaunch::n_sub):
 //   S^T[key][q]  = K . Q^T        A = K rows (16-bit caches: from a per-wave
 //                                 LDS tile; Q8: straight from HBM)
 //   O^T[d][q]   += V^T . P^T      A = V^T from a per-wave LDS tile, B = P from
@@ -182,11 +183,14 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? kMdWaves * KS * 64 : 1];
 
     const int kv_mul = p.n_heads / p.n_kv_heads;
+    // grid / schedule columns: n_sub per KV head, 16 query heads each (DecodeLaunch::n_sub)
+    const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
+    const int n_cols = p.n_kv_heads * n_sub;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
 
-    // Segment = keys [t_begin, t_stop) of sequence s, KV head g; its partial
+    // Segment = keys [t_begin, t_stop) of sequence s, column g (KV head g / n_sub); its partial
     // goes to slot `split` of the (s, head) partial rows.
     int s, g, t_begin, t_stop, split;
     // stream schedule state (DecodeLaunch::stream_sched)
@@ -220,7 +224,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             const int q = tid * C + c;
             const int len = q < n ? max(0, p.kv_end[q] - p.kv_start[q]) : 0;
             loc[c] = tsum;
-            tsum += len * p.n_kv_heads;
+            tsum += len * n_cols;
             if (q < n) st_len[q] = len;
         }
         // inclusive scan of tsum over the workgroup
@@ -250,7 +254,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 const int off = excl + loc[c];
                 st_off[q] = off;
                 if (blockIdx.x == 0) p.stream_sched[q] = off;
-                if (lo >= off && lo < off + st_len[q] * p.n_kv_heads) st_first = q;
+                if (lo >= off && lo < off + st_len[q] * n_cols) st_first = q;
             }
         }
         if (blockIdx.x == 0 && tid == 0) p.stream_sched[n] = st_q;
@@ -276,20 +280,23 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         st_pos = seg_end;
         __syncthreads();  // the previous segment is done with the LDS
     }
+    const int kvh = g / n_sub;                                     // KV head
+    const int h0 = kvh * kv_mul + (g % n_sub) * 16;                // first query head
+    const int nq = min(16, kvh * kv_mul + kv_mul - h0);            // query heads (MFMA columns)
     uint16_t* vt = (uint16_t*)smem + wave * D * VS;
     float* sct = (float*)(smem + kVtBytes) + wave * 2 * NB * TILE;  // block mode: [2][NB][TILE]
     uint4* kst = (uint4*)(smem + kVtBytes + kScBytes) + wave * TILE * DC;  // 16-bit: K tile
 
     // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
-    // d = 32 ks + 8 g4 .. +7, pre-scaled to log2 units; queries >= kv_mul are 0.
+    // d = 32 ks + 8 g4 .. +7, pre-scaled to log2 units; columns >= nq are 0.
     // f16: each query row is also multiplied by a power of two 2^e that puts its
     // largest element near 2^14, so that the lo halves of the hi/lo split stay
     // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
     uint4 qf[KS], qfl[kSplit && !kQloLds ? KS : 1];
     float qback = 1.0f;
     {
-        const bool qv = l16 < kv_mul;
-        const float* qrow = p.q + ((size_t)s * p.n_heads + (size_t)g * kv_mul + (qv ? l16 : 0)) * D;
+        const bool qv = l16 < nq;
+        const float* qrow = p.q + ((size_t)s * p.n_heads + h0 + (qv ? l16 : 0)) * D;
         float qscale = p.score_scale * kLog2e;
         if constexpr (std::is_same<M, Mfma16<F16>>::value) {
             float qmax = 0.0f;
@@ -327,8 +334,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
     // element pointers (one element = sizeof(Raw)/8 bytes)
     typedef typename std::conditional<kQ8, int8_t, uint16_t>::type Elem;
-    const Elem* kc = (const Elem*)p.k_cache + slot * p.seq_stride + (size_t)g * D;
-    const Elem* vc = (const Elem*)p.v_cache + slot * p.seq_stride + (size_t)g * D;
+    const Elem* kc = (const Elem*)p.k_cache + slot * p.seq_stride + (size_t)kvh * D;
+    const Elem* vc = (const Elem*)p.v_cache + slot * p.seq_stride + (size_t)kvh * D;
     const int64_t rs = p.row_stride;
     // Q8 scales: this lane's keys of S^T register j of sub-tile sb are
     // t0 + 16 sb + 4 g4 + j; block mode adds the kv head's block offset.
@@ -336,7 +343,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     const float* vsb = nullptr;
     int64_t srs = 0;
     if constexpr (kQ8) {
-        const size_t so = slot * p.scale_seq_stride + (kBlock ? (size_t)g * NB : 0);
+        const size_t so = slot * p.scale_seq_stride + (kBlock ? (size_t)kvh * NB : 0);
         ksb = p.k_scale + so;
         vsb = p.v_scale + so;
         srs = p.scale_row_stride;
@@ -711,7 +718,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         for (int j = 0; j < 4; j++) sh_o[wave][l16][16 * dt + 4 * g4 + j] = o[dt][j];
     __syncthreads();
     const int n_splits = p.n_splits;
-    for (int idx = tid; idx < kv_mul * D; idx += kMdThreads) {
+    for (int idx = tid; idx < nq * D; idx += kMdThreads) {
         const int q = idx / D, i = idx % D;
         float mx = -INFINITY;
 #pragma unroll
@@ -724,7 +731,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             ot += sh_o[w][q][i] * a;
         }
         if (split >= n_splits) break;  // a sequence longer than max_kv_len: slots end here
-        const size_t part = ((size_t)s * p.n_heads + (size_t)g * kv_mul + q) * n_splits + split;
+        const size_t part = ((size_t)s * p.n_heads + h0 + q) * n_splits + split;
         p.ws_o[part * D + i] = ot;
         if (i == 0) {
             p.ws_ml[part * 2 + 0] = mx;
@@ -733,7 +740,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     }
     if (!p.stream_sched || st_pos >= st_hi) break;
     if (tid == 0) tile_next = kMdWaves;  // ordered before the next segment's claims by its barrier
-    if (++g == p.n_kv_heads) {  // next pair: skip empty sequences
+    if (++g == n_cols) {  // next pair: skip empty sequences
         g = 0;
         do {
             s++;
@@ -768,7 +775,8 @@ static int resident_wgs() {
 
 template <typename KV, int D>
 static hipError_t launch_mfma_kv_d(const DecodeLaunch& p, hipStream_t st) {
-    const dim3 grid = p.stream_sched ? dim3(resident_wgs<KV, D>()) : dim3(p.n_splits, p.n_kv_heads, p.n_seq);
+    const dim3 grid = p.stream_sched ? dim3(resident_wgs<KV, D>())
+                                     : dim3(p.n_splits, p.n_kv_heads * (p.n_sub > 0 ? p.n_sub : 1), p.n_seq);
     decode_mfma_kernel<KV, D, 1><<<grid, MdWaves<KV, D>::value * 64, 0, st>>>(p);
     return hipGetLastError();
 }
@@ -776,6 +784,9 @@ static hipError_t launch_mfma_kv_d(const DecodeLaunch& p, hipStream_t st) {
 template <typename KV>
 static hipError_t launch_mfma_kv(const DecodeLaunch& p, hipStream_t st) {
     switch (p.head_dim) {
+        case 64:  // Q8 only: 16-bit caches at d64 take the VALU kernel (the K tile swizzle needs 16 chunks a row)
+            if constexpr (KV::kQ8) return launch_mfma_kv_d<KV, 64>(p, st);
+            return hipErrorInvalidValue;
         case 128: return launch_mfma_kv_d<KV, 128>(p, st);
         case 256: return launch_mfma_kv_d<KV, 256>(p, st);
         default: return hipErrorInvalidValue;
@@ -785,7 +796,8 @@ static hipError_t launch_mfma_kv(const DecodeLaunch& p, hipStream_t st) {
 bool decode_mfma_supported(const DecodeLaunch& p) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
     return (p.kv_dtype == GR_DTYPE_F16 || p.kv_dtype == GR_DTYPE_BF16 || p.kv_dtype == GR_DTYPE_Q8) &&
-           kv_mul <= 16 && (p.head_dim == 128 || p.head_dim == 256);
+           (kv_mul <= 16 || (p.n_sub > 0 && p.sub_heads == 16)) &&
+           (p.head_dim == 128 || p.head_dim == 256 || (p.head_dim == 64 && p.kv_dtype == GR_DTYPE_Q8));
 }
 
 hipError_t launch_decode_mfma_split(const DecodeLaunch& p, hipStream_t st) {

@@ -73,6 +73,11 @@ struct DecodeLaunch {
     const int32_t* col_start;
     const int32_t* col_end;
     OutGate gate;  // written by the combine kernels
+    // Query heads of a GQA group split over n_sub workgroup columns (kv_mul above
+    // what one workgroup takes: 16 MFMA columns, 8 VALU heads): column vg of the
+    // grid is KV head vg / n_sub with query heads (vg / n_sub) * kv_mul + (vg % n_sub)
+    // * sub_heads .. + min(sub_heads, kv_mul - (vg % n_sub) * sub_heads).  0 = 1.
+    int n_sub = 0, sub_heads = 0;
 };
 
 hipError_t launch_decode(const DecodeLaunch& p, hipStream_t st);

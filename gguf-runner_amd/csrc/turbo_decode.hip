@@ -320,16 +320,21 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     constexpr int kMergeBytes = (kTsWaves * 16 * (2 * D + 1) + 2 * kTsWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
-    const int split = blockIdx.x, g = blockIdx.y, s = blockIdx.z;
+    const int split = blockIdx.x, s = blockIdx.z;
+    // decode: grid column blockIdx.y = KV head g, query heads h0 .. h0 + kv_cols - 1
+    // (DecodeLaunch::n_sub slices groups above 16 query heads)
+    const int n_sub = (!PACK && p.n_sub > 0) ? p.n_sub : 1;
+    const int g = blockIdx.y / n_sub;
     const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
     const int t_begin = p.kv_start[e_rng] + split * p.split_keys;
     const int t_limit = p.kv_end[e_rng];
     if (t_begin >= t_limit) return;
     const int t_stop = min(t_limit, t_begin + p.split_keys);
     const int kv_mul = p.n_heads / p.n_kv_heads;
-    const int n_col = PACK ? p.tok_pack * kv_mul : kv_mul;
+    const int h0 = g * kv_mul + (int)(blockIdx.y % n_sub) * 16;
+    const int n_col = PACK ? p.tok_pack * kv_mul : min(16, g * kv_mul + kv_mul - h0);
     auto col_tok = [&](int c) { return PACK ? s * p.tok_pack + c / kv_mul : s; };
-    auto col_head = [&](int c) { return g * kv_mul + (PACK ? c % kv_mul : c); };
+    auto col_head = [&](int c) { return PACK ? g * kv_mul + c % kv_mul : h0 + c; };
     auto col_ok = [&](int c) { return c < n_col && (!PACK || col_tok(c) < p.n_seq); };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g4 = lane >> 4;
@@ -765,17 +770,20 @@ size_t turbo_query_ws_dwords(int head_dim) {
 }
 
 bool decode_turbo_supported(const DecodeLaunch& p) {
-    return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) && p.n_heads / p.n_kv_heads <= 16 &&
+    return (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256) &&
            (p.tok_pack == 0 || p.tok_pack * (p.n_heads / p.n_kv_heads) <= 16);
 }
 
 template <int D>
-static hipError_t launch_turbo_d(const DecodeLaunch& p, hipStream_t st) {
+static hipError_t launch_turbo_d(const DecodeLaunch& p0, hipStream_t st) {
+    DecodeLaunch p = p0;  // decode: groups above 16 query heads in columns of 16
+    p.n_sub = p.tok_pack > 0 ? 1 : (p.n_heads / p.n_kv_heads + 15) / 16;
+    p.sub_heads = 16;
     turbo_query_kernel<D><<<dim3((p.n_heads + 3) / 4, p.n_seq), 256, 0, st>>>(p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int kv_mul = p.n_heads / p.n_kv_heads;
-    const int n_col = (p.tok_pack > 0 ? p.tok_pack : 1) * kv_mul;
+    const int n_col = p.tok_pack > 0 ? p.tok_pack * kv_mul : std::min(kv_mul, 16);
     const bool split = 2 * n_col <= 16;  // hi / lo pieces as MFMA columns
     if (p.tok_pack > 0) {
         // token-packed prefill (turbo_pack_rows: 16 columns up to d128, 8 at d256)
@@ -783,7 +791,7 @@ static hipError_t launch_turbo_d(const DecodeLaunch& p, hipStream_t st) {
         if (split) turbo_split_kernel<D, true, true><<<grid, kTsThreads, 0, st>>>(p);
         else turbo_split_kernel<D, true, false><<<grid, kTsThreads, 0, st>>>(p);
     } else {
-        const dim3 grid(p.n_splits, p.n_kv_heads, p.n_seq);
+        const dim3 grid(p.n_splits, p.n_kv_heads * p.n_sub, p.n_seq);
         if (split) turbo_split_kernel<D, false, true><<<grid, kTsThreads, 0, st>>>(p);
         else turbo_split_kernel<D, false, false><<<grid, kTsThreads, 0, st>>>(p);
     }

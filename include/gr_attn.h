@@ -75,7 +75,7 @@ int gr_abi_version(void);
 typedef struct gr_decode_args {
     int32_t n_seq;        /* independent sequences in the batch */
     int32_t n_heads;      /* query heads Hq */
-    int32_t n_kv_heads;   /* KV heads Hkv; Hq/Hkv in {1,2,4,8} */
+    int32_t n_kv_heads;   /* KV heads Hkv (Hq % Hkv == 0, any ratio) */
     int32_t head_dim;     /* 64, 128 or 256 */
     int32_t kv_dtype;     /* gr_dtype of the cache */
     int32_t split_keys;   /* keys per split-K partition, 0 = automatic */

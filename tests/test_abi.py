@@ -40,16 +40,16 @@ def test_decode_rejects_bad_q8_args(pkg):
     from gguf_runner_amd import ffi
     L = ffi.lib()
     a = ffi.DecodeArgs()
-    a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_dtype, a.max_kv_len = 1, 8, 4, 64, ffi.DTYPE_Q8, 16
+    a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_dtype, a.max_kv_len = 1, 8, 4, 96, ffi.DTYPE_Q8, 16
     assert L.gr_decode_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
-    assert b"Q8 KV needs head_dim" in L.gr_last_error()
-    a.head_dim = 128
+    assert b"head_dim 96 unsupported" in L.gr_last_error()
+    a.head_dim = 64
     assert L.gr_decode_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
     assert b"k_scale and v_scale" in L.gr_last_error()
-    a.k_scale = a.v_scale = 4  # misaligned, block mode
-    a.q8_block, a.scale_row_stride = 1, 16
+    a.k_scale = a.v_scale = 4
+    a.q8_block, a.scale_row_stride = 1, 7  # block mode needs kv_dim / 32 = 8 scales a row
     assert L.gr_decode_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
-    assert b"16-byte aligned" in L.gr_last_error()
+    assert b"scale_row_stride >= kv_dim/32" in L.gr_last_error()
 
 
 def test_malloc_run_state_rejects_invalid_rope_scales(pkg):
@@ -73,7 +73,7 @@ def test_malloc_run_state_rejects_invalid_rope_scales(pkg):
 def test_malloc_run_state_rejects_bad_windows_and_shapes(pkg):
     from gguf_runner_amd import ffi, runtime
     bad = [dict(layer_windows=[1024, -1]), dict(n_kv_heads=3), dict(head_dim=96),
-           dict(kv_dtype=ffi.DTYPE_Q8, head_dim=64), dict(kv_dtype=7),
+           dict(kv_dtype=ffi.DTYPE_Q8, head_dim=96), dict(kv_dtype=7),
            dict(rope_mode=ffi.ROPE_ADJACENT, rope_dim=32)]
     for kw in bad:
         base = dict(n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, seq_len=8)
