@@ -163,6 +163,11 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     constexpr int KS = D / 32;                   // MFMA k-steps over d
     constexpr int VTASK = (TILE / 4) * DC / 64;  // 4-key x 16-byte V tasks per lane
     constexpr int VS = TILE + 4;                 // V^T row stride (elements)
+    // V^T rows hold TILE / 4 quads of 4 keys; quad q of row d sits at quad
+    // q ^ vswz(d), vswz(d) = ((d / 32) * (256 / D)) % 8: the transposing stores of
+    // one instruction (rows 8 dc + dd, 16 dc values) then hit distinct banks, where
+    // the row stride alone maps every fourth dc to the same banks
+    auto vswz = [](int d) { return ((d >> 5) * (256 / D)) & 7; };
     static_assert(VTASK >= 1, "tile");
 
     // LDS: per-wave V^T tiles during the key loop, then (aliased) the wave merge.
@@ -470,6 +475,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         for (int u = 0; u < VTASK; u++) {
             const int task = lane + 64 * u;
             const int dc = task % DC, kg = task / DC;
+            const int kq = kg ^ vswz(8 * dc);  // this lane's quad of keys, swizzled (rows 8 dc .. 8 dc + 7)
             const uint4 v16[4] = {KV::to16(vr[u][0]), KV::to16(vr[u][1]), KV::to16(vr[u][2]), KV::to16(vr[u][3])};
             const uint32_t w[4][4] = {{v16[0].x, v16[0].y, v16[0].z, v16[0].w},
                                       {v16[1].x, v16[1].y, v16[1].z, v16[1].w},
@@ -486,7 +492,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                     lo = (w[0][wi] >> 16) | (w[1][wi] & 0xffff0000u);
                     hi = (w[2][wi] >> 16) | (w[3][wi] & 0xffff0000u);
                 }
-                *(uint2*)(vt + (8 * dc + dd) * VS + 4 * kg) = make_uint2(lo, hi);
+                *(uint2*)(vt + (8 * dc + dd) * VS + 4 * kq) = make_uint2(lo, hi);
             }
         }
         float vbmax[kBlock ? NB : 1];  // block mode: the tile's largest v scale per block (wave-uniform)
@@ -682,11 +688,12 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
 #pragma unroll
             for (int dd = 0; dd < DTB; dd++) {
                 const int dt = pb * DTB + dd;
-                const uint16_t* vrow = vt + (16 * dt + l16) * VS + 4 * g4;
+                const uint16_t* vrow = vt + (16 * dt + l16) * VS;
+                const int sw = vswz(16 * dt);  // the same for the 16 rows of tile dt
 #pragma unroll
                 for (int kk = 0; kk < NSUB; kk++) {
-                    const uint2 lo = *(const uint2*)(vrow + 32 * kk);
-                    const uint2 hi = *(const uint2*)(vrow + 32 * kk + 16);
+                    const uint2 lo = *(const uint2*)(vrow + 4 * ((8 * kk + g4) ^ sw));
+                    const uint2 hi = *(const uint2*)(vrow + 4 * ((8 * kk + 4 + g4) ^ sw));
                     const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
                     o[dt] = M::mma(a, pf[kk], o[dt]);
                     if constexpr (kSplitP) o[dt] = M::mma(a, pfl[kk], o[dt]);
