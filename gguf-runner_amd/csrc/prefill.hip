@@ -405,7 +405,10 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
         auto subtile = [&](const uint16_t* kb, const uint16_t* vb, int sb, int ts) {
             const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                  0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            // S^T = K Q^T
+            // S^T = K Q^T.  The waves raise their priority over their MFMA
+            // groups (s_setprio 1) so the SIMD's arbiter favours the wave that has
+            // matrix work ready while the other computes its softmax.
+            __builtin_amdgcn_s_setprio(1);
             f32x16 sacc;
             const uint16_t* krow = kb + (32 * sb + ln) * D;
 #pragma unroll
@@ -439,6 +442,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                     for (int t = 0; t < 2; t++) va[dt][t] = load_va(dt, t);
             }
 
+            __builtin_amdgcn_s_setprio(0);
             // element e of the accumulator is key ts + 8 (e/4) + 4 lg + e%4
             const bool need_mask = (ts + 31 > hi_min) || (ts < lo_max);
             if (need_mask) {
@@ -520,6 +524,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                     lrow = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, pf[t].w), one2, lrow, false);
                 }
             }
+            __builtin_amdgcn_s_setprio(1);
             // O^T += V^T P^T; the V^T slot order matches P^T's: slots 0..3 are keys
             // 16 t + 4 lg + 0..3, slots 4..7 keys 16 t + 8 + 4 lg + 0..3.
 #pragma unroll
@@ -530,6 +535,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                     o[dt] = M::mma(a, pf[t], o[dt]);
                     if constexpr (kSplit) o[dt] = M::mma(a, pfl[t], o[dt]);
                 }
+            __builtin_amdgcn_s_setprio(0);
         };
         auto compute_tile = [&](const uint16_t* kb, const uint16_t* vb, int t0) {
 #pragma unroll
