@@ -6,12 +6,29 @@ the ABI version and enum constants agree.  The ctypes binding (ffi.py) is held t
 the same field lists.  CPU only."""
 from __future__ import annotations
 
+import functools
 import pathlib
 import re
 
+import pytest
+
 ROOT = pathlib.Path(__file__).resolve().parents[1]
-HEADER = (ROOT / "include" / "gr_attn.h").read_text()
-RUST = (ROOT / "rust" / "ffi.rs").read_text()
+
+
+@functools.lru_cache(maxsize=None)
+def _text(*parts: str) -> str:
+    path = ROOT.joinpath(*parts)
+    if not path.exists():
+        pytest.skip(f"{path} is not in this checkout")
+    return path.read_text()
+
+
+def _header() -> str:
+    return _text("include", "gr_attn.h")
+
+
+def _rust() -> str:
+    return _text("rust", "ffi.rs")
 
 # C type -> Rust type (parameters and fields)
 C2R = {
@@ -39,7 +56,7 @@ def _norm_ctype(t: str) -> str:
 
 
 def header_structs() -> dict[str, list[tuple[str, str]]]:
-    body = _strip_c_comments(HEADER)
+    body = _strip_c_comments(_header())
     out = {}
     for name in STRUCTS:
         m = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), body, re.S)
@@ -56,7 +73,7 @@ def header_structs() -> dict[str, list[tuple[str, str]]]:
 
 
 def header_functions() -> dict[str, tuple[str, list[str]]]:
-    body = _strip_c_comments(HEADER)
+    body = _strip_c_comments(_header())
     out = {}
     for m in re.finditer(r"^\s*((?:const )?\w+\s*\**)\s*(gr_\w+)\(([^)]*)\);", body, re.M | re.S):
         ret, name, params = _norm_ctype(m.group(1)), m.group(2), m.group(3)
@@ -71,14 +88,15 @@ def header_functions() -> dict[str, tuple[str, list[str]]]:
 
 def rust_structs() -> dict[str, list[tuple[str, str]]]:
     out = {}
-    for m in re.finditer(r"#\[repr\(C\)\]\s*pub struct (\w+) \{(.*?)\n\}", RUST, re.S):
+    for m in re.finditer(r"#\[repr\(C\)\]\s*pub struct (\w+) \{(.*?)\n\}", _rust(), re.S):
         fields = re.findall(r"pub (\w+): ([^,]+),", m.group(2))
         out[m.group(1)] = [(n, re.sub(r"\s+", " ", t.strip())) for n, t in fields]
     return out
 
 
 def rust_functions() -> dict[str, tuple[str, list[str]]]:
-    block = RUST[RUST.index('unsafe extern "C" {'):]
+    rust = _rust()
+    block = rust[rust.index('unsafe extern "C" {'):]
     out = {}
     for m in re.finditer(r"pub fn (gr_\w+)\((.*?)\)(?:\s*->\s*([^;]+))?;", block, re.S):
         params = [re.sub(r"\s+", " ", p.split(":", 1)[1].strip()) for p in m.group(2).split(",") if p.strip()]
@@ -105,18 +123,19 @@ def test_rust_functions_match_header_signatures():
 
 
 def test_rust_constants_match_header():
-    ver = int(re.search(r"#define GR_ATTN_ABI_VERSION (\d+)", HEADER).group(1))
-    assert f"pub const GR_ATTN_ABI_VERSION: i32 = {ver};" in RUST
+    header, rust = _header(), _rust()
+    ver = int(re.search(r"#define GR_ATTN_ABI_VERSION (\d+)", header).group(1))
+    assert f"pub const GR_ATTN_ABI_VERSION: i32 = {ver};" in rust
     for name in ("GR_DTYPE_F32", "GR_DTYPE_F16", "GR_DTYPE_BF16", "GR_DTYPE_Q8", "GR_DTYPE_TURBO",
                  "GR_DELTANET_AUTO", "GR_DELTANET_RECURRENT", "GR_DELTANET_CHUNKED"):
-        v = int(re.search(name + r"\s*=\s*(\d+)", HEADER).group(1))
-        assert f"pub const {name}: i32 = {v};" in RUST, name
+        v = int(re.search(name + r"\s*=\s*(\d+)", header).group(1))
+        assert f"pub const {name}: i32 = {v};" in rust, name
 
 
 def test_build_rs_builds_the_gfx950_library():
-    b = (ROOT / "rust" / "build.rs").read_text()
+    b = _text("rust", "build.rs")
     assert '"-C", &src' in b and "libgr_attn.so" in b and "rustc-link-lib=dylib=gr_attn" in b
-    mk = (ROOT / "gguf-runner_amd" / "Makefile").read_text()
+    mk = _text("gguf-runner_amd", "Makefile")
     assert "--offload-arch=$(ARCH)" in mk and "ARCH ?= gfx950" in mk
 
 
