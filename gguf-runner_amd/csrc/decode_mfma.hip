@@ -296,8 +296,14 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     float* sct = (float*)(smem + kVtBytes) + wave * 2 * NB * TILE;  // block mode: [2][NB][TILE]
     uint4* kst = (uint4*)(smem + kVtBytes + kScBytes) + wave * TILE * DC;  // 16-bit: K tile
 
+    // Element d of the head row behind slot e of k-step k in lane group g4: 32 k +
+    // 8 g4 + e; Q8 with row scales pairs k-steps 2j, 2j + 1 on one 16-byte code
+    // load per lane, d = 64 j + 16 g4 + 8 (k & 1) + e (the sum over d is the same;
+    // block scales keep one 32-element block per k-step).
+    constexpr bool kPairK = kQ8 && !kBlock && KS % 2 == 0;
+    auto dperm = [](int k, int g) { return kPairK ? 64 * (k >> 1) + 16 * g + 8 * (k & 1) : 32 * k + 8 * g; };
     // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
-    // d = 32 ks + 8 g4 .. +7, pre-scaled to log2 units; columns >= nq are 0.
+    // d = dperm(ks, g4) .. +7, pre-scaled to log2 units; columns >= nq are 0.
     // f16: each query row is also multiplied by a power of two 2^e that puts its
     // largest element near 2^14, so that the lo halves of the hi/lo split stay
     // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
@@ -312,7 +318,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
 #pragma unroll
             for (int k = 0; k < KS; k++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, qv ? fabsf(qrow[32 * k + 8 * g4 + e] * qscale) : 0.0f);
+                for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, qv ? fabsf(qrow[dperm(k, g4) + e] * qscale) : 0.0f);
             qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
             qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
             if (qmax > 0.0f && qmax < 3.0e38f) {
@@ -328,7 +334,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             uint32_t hw[4], lw[4];
 #pragma unroll
             for (int w = 0; w < 4; w++) {
-                const int d0 = 32 * k + 8 * g4 + 2 * w;
+                const int d0 = dperm(k, g4) + 2 * w;
                 const float x0 = qv ? qrow[d0] * qscale : 0.0f;
                 const float x1 = qv ? qrow[d0 + 1] * qscale : 0.0f;
                 hw[w] = M::pack2(x0, x1);
@@ -428,22 +434,31 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             }
             return;
         }
-        if (t0 + TILE <= t_stop) {
-            const Elem* kt = kc + (int64_t)t0 * rs + 8 * g4;
+        // this lane's operand chunks of one K row (row = the row's first element)
+        auto load_row = [&](int sb, const Elem* row) {
+            if constexpr (kPairK) {
 #pragma unroll
-            for (int sb = 0; sb < NS16; sb++) {
-                const Elem* row = kt + (int64_t)(16 * sb + l16) * rs;
+                for (int j = 0; j < KS / 2; j++) {
+                    uint4 w;
+                    ld_plain(&w, row + 64 * j + 16 * g4);
+                    kr[sb][2 * j] = make_uint2(w.x, w.y);
+                    kr[sb][2 * j + 1] = make_uint2(w.z, w.w);
+                }
+            } else {
 #pragma unroll
-                for (int k = 0; k < KS; k++) ld_plain(&kr[sb][k], row + 32 * k);
+                for (int k = 0; k < KS; k++) ld_plain(&kr[sb][k], row + 32 * k + 8 * g4);
             }
+        };
+        if (t0 + TILE <= t_stop) {
+            const Elem* kt = kc + (int64_t)t0 * rs;
+#pragma unroll
+            for (int sb = 0; sb < NS16; sb++) load_row(sb, kt + (int64_t)(16 * sb + l16) * rs);
             return;
         }
 #pragma unroll
         for (int sb = 0; sb < NS16; sb++) {
             const int key = min(t0 + 16 * sb + l16, t_stop - 1);
-            const Elem* row = kc + (int64_t)key * rs + 8 * g4;
-#pragma unroll
-            for (int k = 0; k < KS; k++) ld_plain(&kr[sb][k], row + 32 * k);
+            load_row(sb, kc + (int64_t)key * rs);
         }
     };
 
