@@ -115,10 +115,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // 16 lanes (4 rows x 256 B per instruction for d128 f16), and those loads carry
 // the nontemporal hint (streaming policy in the L2): a plain read of that
 // pattern measured 6.0 TB/s with ordinary loads and 6.7 TB/s with the hint on
-// MI355X.  K tiles are loaded in the MFMA operand layout, 64 B (f16) or 32 B
-// (Q8) of each of 16 rows per instruction, i.e. part of a 128-byte line; with
-// the hint the line leaves the L2 before the rest is read (5.8 -> 5.2 TB/s for
-// that pattern), so K and all Q8 rows use plain loads.
+// MI355X.  K tiles are loaded in the MFMA operand layout, 64 B (f16, Q8 row
+// scales) or 32 B (Q8 block scales) of each of 16 rows per instruction, i.e.
+// part of a 128-byte line; with the hint the line leaves the L2 before the rest
+// is read (5.8 -> 5.2 TB/s for that pattern), so K and all Q8 rows use plain loads.
 __device__ __forceinline__ void ld_stream(uint4* r, const void* p) {
     const u32x4_t x = __builtin_nontemporal_load((const u32x4_t*)p);
     *r = make_uint4(x[0], x[1], x[2], x[3]);
@@ -126,6 +126,27 @@ __device__ __forceinline__ void ld_stream(uint4* r, const void* p) {
 __device__ __forceinline__ void ld_stream(uint2* r, const void* p) { *r = *(const uint2*)p; }
 template <typename R>
 __device__ __forceinline__ void ld_plain(R* r, const void* p) { *r = *(const R*)p; }
+
+// Buffer descriptor for a wave-uniform base address (read from lane 0), for raw
+// buffer loads with a scalar base and 32-bit per-lane offsets.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t md_rsrc(const void* p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, (int)0xffffffff,
+                                             0x00020000);
+}
+__device__ __forceinline__ uint2 md_ld8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 md_ld16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float md_ldf(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
 
 // Waves per workgroup: 8 (one workgroup per CU, two waves per SIMD) where the
 // registers (<= 256) and the per-wave LDS tiles allow it, else 4.
@@ -374,8 +395,20 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     Raw kr[kKLds ? 1 : NS16][KS];   // Q8: K in the MFMA operand layout
     Raw krs[kKLds ? VTASK : 1][4];  // 16-bit: K rows in the V row-slice layout
     Raw vr[VTASK][4];
+    // Q8 with row scales: raw buffer loads from the tile's first row (wave-uniform
+    // base), so the lane offsets of a whole tile are the same for every tile and
+    // the loop carries no 64-bit address arithmetic; the last tile of a range
+    // clamps its keys to t_stop - 1.  Block scales keep plain loads.
+    constexpr bool kBufLd = kQ8 && !kBlock;
+    const int srsb = (int)srs * 4;  // scale row stride, bytes
     auto load_scales = [&](int t0) {
+        const int last = t_stop - 1 - t0;  // last valid key, relative to t0
+        const bool whole = t0 + TILE <= t_stop;
+        (void)last;
+        (void)whole;
         if constexpr (kBlock) {
+            // block scales: plain loads (the four extra scalar descriptors of the
+            // buffer path cost the block-scale kernel SGPR spills: 10% slower)
 #pragma unroll
             for (int u = 0; u < NBS; u++) {
                 const int e = lane + 64 * u;
@@ -384,11 +417,19 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 vbs[u] = vsb[(int64_t)key * srs + e % NB];
             }
         } else if constexpr (kQ8) {
+            const __amdgpu_buffer_rsrc_t kr_ = md_rsrc(ksb + (int64_t)t0 * srs);
+            const __amdgpu_buffer_rsrc_t vr_ = md_rsrc(vsb + (int64_t)t0 * srs);
 #pragma unroll
             for (int e = 0; e < NRS; e++) {
-                const int key = min(t0 + 16 * (e >> 2) + 4 * g4 + (e & 3), t_stop - 1);
-                ksc[e] = ksb[(int64_t)key * srs];
-                vsc[e] = vsb[(int64_t)key * srs];
+                const int kk = 16 * (e >> 2) + (e & 3);  // key - 4 g4 - t0
+                if (whole) {
+                    ksc[e] = md_ldf(kr_, 4 * g4 * srsb, kk * srsb);
+                    vsc[e] = md_ldf(vr_, 4 * g4 * srsb, kk * srsb);
+                } else {
+                    const int off = min(kk + 4 * g4, last) * srsb;
+                    ksc[e] = md_ldf(kr_, off, 0);
+                    vsc[e] = md_ldf(vr_, off, 0);
+                }
             }
         }
     };
@@ -396,6 +437,22 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // is in LDS, K (and the Q8 scales) once the current scores are done, so each
     // is in flight for most of an iteration.
     auto load_v = [&](int t0) {
+        if constexpr (kBufLd) {
+            const __amdgpu_buffer_rsrc_t r_ = md_rsrc(vc + (int64_t)t0 * rs);
+            const bool whole = t0 + TILE <= t_stop;
+            const int last = t_stop - 1 - t0;
+#pragma unroll
+            for (int u = 0; u < VTASK; u++) {
+                const int task = lane + 64 * u;
+                const int dc = task % DC, kg = task / DC;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    if (whole) vr[u][r] = md_ld8(r_, 4 * kg * (int)rs + 8 * dc, r * (int)rs);
+                    else vr[u][r] = md_ld8(r_, min(4 * kg + r, last) * (int)rs + 8 * dc, 0);
+                }
+            }
+            return;
+        }
         if (t0 + TILE <= t_stop) {  // whole tile inside the split: plain strided rows
             const Elem* vtp = vc + (int64_t)t0 * rs;
 #pragma unroll
@@ -432,33 +489,40 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                     ld_stream(&krs[u][r], kc + (int64_t)key * rs + 8 * dc);
                 }
             }
-            return;
-        }
-        // this lane's operand chunks of one K row (row = the row's first element)
-        auto load_row = [&](int sb, const Elem* row) {
+        } else if constexpr (!kBufLd) {
+            const Elem* kt = kc + (int64_t)t0 * rs + 8 * g4;
+            const bool whole = t0 + TILE <= t_stop;
+#pragma unroll
+            for (int sb = 0; sb < NS16; sb++) {
+                const int key = whole ? 16 * sb + l16 : min(16 * sb + l16, t_stop - 1 - t0);
+                const Elem* row = kt + (int64_t)key * rs;
+#pragma unroll
+                for (int k = 0; k < KS; k++) ld_plain(&kr[sb][k], row + 32 * k);
+            }
+        } else {
+        // this lane's operand chunks of K row 16 sb + l16 of the tile (row offset
+        // voff + soff bytes from the tile's first row)
+        const __amdgpu_buffer_rsrc_t r_ = md_rsrc(kc + (int64_t)t0 * rs);
+        auto load_row = [&](int sb, int voff, int soff) {
             if constexpr (kPairK) {
 #pragma unroll
                 for (int j = 0; j < KS / 2; j++) {
-                    uint4 w;
-                    ld_plain(&w, row + 64 * j + 16 * g4);
+                    const uint4 w = md_ld16(r_, voff + 64 * j + 16 * g4, soff);
                     kr[sb][2 * j] = make_uint2(w.x, w.y);
                     kr[sb][2 * j + 1] = make_uint2(w.z, w.w);
                 }
             } else {
 #pragma unroll
-                for (int k = 0; k < KS; k++) ld_plain(&kr[sb][k], row + 32 * k + 8 * g4);
+                for (int k = 0; k < KS; k++) kr[sb][k] = md_ld8(r_, voff + 32 * k + 8 * g4, soff);
             }
         };
         if (t0 + TILE <= t_stop) {
-            const Elem* kt = kc + (int64_t)t0 * rs;
 #pragma unroll
-            for (int sb = 0; sb < NS16; sb++) load_row(sb, kt + (int64_t)(16 * sb + l16) * rs);
+            for (int sb = 0; sb < NS16; sb++) load_row(sb, l16 * (int)rs, 16 * sb * (int)rs);
             return;
         }
 #pragma unroll
-        for (int sb = 0; sb < NS16; sb++) {
-            const int key = min(t0 + 16 * sb + l16, t_stop - 1);
-            load_row(sb, kc + (int64_t)key * rs);
+        for (int sb = 0; sb < NS16; sb++) load_row(sb, min(16 * sb + l16, t_stop - 1 - t0) * (int)rs, 0);
         }
     };
 
