@@ -68,11 +68,9 @@ struct Mfma16<BF16> {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                        __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
     }
-    static __device__ __forceinline__ uint32_t pack2(float a0, float a1) {
-        return (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
-    }
+    static __device__ __forceinline__ uint32_t pack2(float a0, float a1) { return pack_bf16x2(a0, a1); }
     static __device__ __forceinline__ uint32_t rest2(uint32_t hi, float a0, float a1) {
-        return pack2(a0 - bf16_to_f32((uint16_t)hi), a1 - bf16_to_f32((uint16_t)(hi >> 16)));
+        return pack2(a0 - __uint_as_float(hi << 16), a1 - __uint_as_float(hi & 0xffff0000u));
     }
 };
 

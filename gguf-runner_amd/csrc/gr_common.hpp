@@ -43,6 +43,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(x >> 16);
 }
 
+// Two floats as a bf16 pair (low half = lo) with one v_cvt_pk_bf16_f32 (round to
+// nearest even, as f32_to_bf16 for finite values); for MFMA operands.
+typedef __bf16 gr_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float gr_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(gr_f32x2_t{lo, hi}, gr_bf16x2_t));
+}
+
 template <typename T>
 __device__ __forceinline__ float to_f32(typename T::storage v);
 template <>
