@@ -479,7 +479,15 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
                 mrow = mnew;
                 lrow *= alpha;
 #pragma unroll
-                for (int dt = 0; dt < D / 32; dt++) o[dt] *= alpha;
+                for (int dt = 0; dt < D / 32; dt++) {
+                    // d = 256: O lives in AGPRs (the MFMAs accumulate there).  The
+                    // empty asm statements move it to VGPRs for the multiply and
+                    // back here, inside this rarely taken branch; otherwise the
+                    // compiler copies all of O out of the AGPRs on every tile.
+                    if constexpr (D == 256) asm volatile("" : "+v"(o[dt]));
+                    o[dt] *= alpha;
+                    if constexpr (D == 256) asm volatile("" : "+a"(o[dt]));
+                }
             }
             float pv[16];
 #pragma unroll
