@@ -149,13 +149,20 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
             float xs[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) xs[e] = x[e] * p.q_out_scale;
-            store8(p.q_out, ob, p.q_out_dtype, xs);
             if (p.q_out_lo) {
-                float hi[8], lo[8];
-                load8(p.q_out, ob, p.q_out_dtype, hi);
+                // bf16 hi + lo pair of the MFMA operand (the hi rounding kept in
+                // registers for the residual)
+                uint32_t hw[4], lw[4];
 #pragma unroll
-                for (int e = 0; e < 8; e++) lo[e] = xs[e] - hi[e];
-                store8(p.q_out_lo, ob, p.q_out_dtype, lo);
+                for (int w = 0; w < 4; w++) {
+                    hw[w] = pack_bf16x2(xs[2 * w], xs[2 * w + 1]);
+                    lw[w] = pack_bf16x2(xs[2 * w] - __uint_as_float(hw[w] << 16),
+                                        xs[2 * w + 1] - __uint_as_float(hw[w] & 0xffff0000u));
+                }
+                *(uint4*)((uint16_t*)p.q_out + ob) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                *(uint4*)((uint16_t*)p.q_out_lo + ob) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            } else {
+                store8(p.q_out, ob, p.q_out_dtype, xs);
             }
         } else {
             void* dst = kind == 1 ? p.k_cache : p.v_cache;
