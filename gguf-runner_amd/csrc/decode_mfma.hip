@@ -230,6 +230,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // (the older wave of a SIMD) take more tiles and the waves finish together.
     __shared__ int tile_next;
     int st_q = 0, st_pos = 0, st_hi = 0;
+    auto seg_ext = [&](int q) { return st_len[q] > 0 ? st_len[q] + p.stream_seg_cost : 0; };
     if (!p.stream_sched) {
         split = blockIdx.x;
         g = blockIdx.y;
@@ -239,10 +240,12 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         if (t_begin >= t_limit) return;
         t_stop = min(t_limit, t_begin + p.split_keys);
     } else {
-        // Flattened key space: pair (s, g) occupies [off_s + g L_s, off_s + (g+1) L_s)
-        // with off_s = n_kv * sum_{s' < s} L_s'.  Workgroup b takes keys
-        // [b Q, (b+1) Q), Q = max(stream_min_keys, ceil(total / #workgroups))
-        // rounded up to 32.  Consecutive sequences per thread, block-wide scan.
+        // Flattened key space: with E_s = L_s + P for a non-empty sequence (0 for
+        // an empty one; P = stream_seg_cost), pair (s, g) occupies
+        // [off_s + g E_s, off_s + (g+1) E_s), off_s = n_cols * sum_{s' < s} E_s',
+        // its keys the last L_s of it.  Workgroup b takes [b Q, (b+1) Q),
+        // Q = max(stream_min_keys, ceil(total / #workgroups)) rounded up to 32.
+        // Consecutive sequences per thread, block-wide scan.
         const int n = p.n_seq;
         constexpr int C = kStreamMaxSeq / kMdThreads;
         int loc[C];
@@ -252,7 +255,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             const int q = tid * C + c;
             const int len = q < n ? max(0, p.kv_end[q] - p.kv_start[q]) : 0;
             loc[c] = tsum;
-            tsum += len * n_cols;
+            tsum += (len > 0 ? len + p.stream_seg_cost : 0) * n_cols;
             if (q < n) st_len[q] = len;
         }
         // inclusive scan of tsum over the workgroup
@@ -282,7 +285,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 const int off = excl + loc[c];
                 st_off[q] = off;
                 if (blockIdx.x == 0) p.stream_sched[q] = off;
-                if (lo >= off && lo < off + st_len[q] * n_cols) st_first = q;
+                if (lo >= off && lo < off + seg_ext(q) * n_cols) st_first = q;
             }
         }
         if (blockIdx.x == 0 && tid == 0) p.stream_sched[n] = st_q;
@@ -291,7 +294,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         st_pos = lo;
         st_hi = min(total, lo + st_q);
         s = st_first;
-        g = (lo - st_off[s]) / st_len[s];
+        g = (lo - st_off[s]) / seg_ext(s);
         t_begin = t_stop = split = 0;  // set per segment below
     }
 
@@ -300,12 +303,16 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     for (;;) {
     if (p.stream_sched) {
         const int len = st_len[s];
-        const int off = st_off[s] + g * len;
+        const int off = st_off[s] + g * seg_ext(s) + p.stream_seg_cost;  // the pair's first key
+        const int seg_beg = max(st_pos, off);
         const int seg_end = min(st_hi, off + len);
+        st_pos = max(st_pos, seg_end);
+        if (seg_beg >= seg_end) {  // the range ends inside the pair's virtual keys: nothing here
+            break;
+        }
         split = (int)blockIdx.x - off / st_q;
-        t_begin = p.kv_start[s] + (st_pos - off);
+        t_begin = p.kv_start[s] + (seg_beg - off);
         t_stop = p.kv_start[s] + (seg_end - off);
-        st_pos = seg_end;
         __syncthreads();  // the previous segment is done with the LDS
     }
     const int kvh = g / n_sub;                                     // KV head

@@ -37,12 +37,17 @@ struct DecodeLaunch {
     // Stream schedule (MFMA split kernel only): when set, the grid is one row of
     // workgroups that cut the flattened (sequence, KV head, key) space into
     // equal ranges of at least stream_min_keys keys; partial slot j of (s, head)
-    // comes from the j-th range that meets pair (s, head / kv_mul), n_splits
+    // comes from the j-th range that meets the keys of pair (s, head / kv_mul), n_splits
     // bounds the slots.  stream_sched[0 .. n_seq) receives the pair offsets
     // off_s of every sequence and stream_sched[n_seq] the range size, for the
     // combine kernel.
     int* stream_sched;
     int stream_min_keys;
+    // Stream schedule: every non-empty (sequence, KV head) pair also counts
+    // stream_seg_cost virtual keys ahead of its own (a segment start costs a
+    // pipeline refill and a partial), so ranges that cross into a pair take
+    // correspondingly fewer keys.  The split and combine kernels share it.
+    int stream_seg_cost;
     // Q8 cache: scale of (seq slot, row t, kv head g, element i) at
     // slot*scale_seq_stride + t*scale_row_stride + (q8_block ? (g*head_dim + i)/32 : 0).
     const float* k_scale;

@@ -152,3 +152,29 @@ def test_decode_16bit_d256_window(orc, dev, fmt_name):
     got, ref = _run_case(orc, dev, n_heads=8, n_kv=4, d=256, starts=[3, 0], ends=[1500, 77],
                          seq_len=1500, fmt=fmt, seed=256, score_scale=1.0)
     _assert_close(got, ref, fmt, orc)
+
+
+@pytest.mark.parametrize("fmt_name,n_heads,n_kv", [("f16", 16, 4), ("bf16", 48, 2), ("q8", 16, 4)])
+def test_decode_stream_many_short_ragged(orc, dev, fmt_name, n_heads, n_kv):
+    """Stream schedule over 40 short ragged sequences, four of them empty and most
+    offset: with ~512 virtual keys charged per (sequence, KV head) pair, workgroup
+    ranges begin and end inside those virtual keys and cross several pairs each;
+    48 / 2 heads put two workgroup columns on each KV head.  An empty range gives
+    zeros, as the oracle's loop over no keys does."""
+    rng = np.random.default_rng(4242 + n_heads)
+    n = 40
+    lens = rng.integers(1, 700, size=n)
+    lens[[3, 4, 17, 39]] = 0
+    starts = rng.integers(0, 100, size=n)
+    ends = starts + lens
+    kw = dict(n_heads=n_heads, n_kv=n_kv, d=128, starts=starts.tolist(), ends=ends.tolist(),
+              seq_len=int(ends.max()), seed=77 + n_heads)
+    if fmt_name == "q8":
+        from test_gpu_q8 import TOL, _decode_case
+        got, ref = _decode_case(orc, dev, block=False, **kw)
+        assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
+    else:
+        fmt = orc.F16 if fmt_name == "f16" else orc.BF16
+        got, ref = _run_case(orc, dev, fmt=fmt, **kw)
+        _assert_close(got, ref, fmt, orc)
+    assert not got[[3, 4, 17, 39]].any()
