@@ -481,10 +481,14 @@ __device__ __forceinline__ dn_i32x4 dn_rsrc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ void dn_dma16(dn_i32x4 r, void* lds, int voff) {
     const int m0 = __builtin_amdgcn_readfirstlane(
         (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
+    // m0 (the LDS destination) is saved and restored inside the statement: the
+    // compiler treats m0 as reserved and would not preserve a value of its own
+    // across a clobber.
+    int saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
                  : "s"(m0), "v"(voff), "s"(r)
-                 : "memory", "m0");
+                 : "memory");
 }
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void dn_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
