@@ -68,14 +68,16 @@ struct DecodePlan {
     int split_keys;
     int n_splits;
     bool stream;  // stream schedule (see DecodeLaunch::stream_sched)
+    int stream_min_keys, stream_seg_cost;
     size_t ws_o_bytes;
     size_t ws_ml_bytes;
     size_t ws_q_bytes;      // Turbo: rotated / projected queries
     size_t ws_sched_bytes;  // stream: pair offsets per sequence + range size
 };
 
-// Keys per workgroup range on the stream schedule never drop below this, which
-// bounds the partial slots per (sequence, head) by ceil(max_kv_len / 256) + 1.
+// Stream schedule of the MFMA split kernel (16-bit and Q8 caches).  Keys per
+// workgroup range never drop below kStreamMinKeys, which bounds the partial
+// slots per (sequence, head) by ceil(max_kv_len / kStreamMinKeys) + 1.
 constexpr int kStreamMinKeys = 256;
 // Virtual keys charged per (sequence, KV head) pair on the stream schedule: what a
 // segment start costs a workgroup (the pipeline refill of its 8 waves, the partial
@@ -83,7 +85,13 @@ constexpr int kStreamMinKeys = 256;
 // ragged batches (+2-10% against no charge, +59% on 64 sequences of 256-4096 keys)
 // and costs 0.5% on 16 equal 32k sequences; 256 and 768 were each below it.
 constexpr int kStreamSegCost = 512;
-constexpr int kStreamMaxSeq = 1024;
+// The same for the Turbo split kernel (whose segment start also loads the
+// prepared query operands of its columns): ranges of at least 1024 keys, 512
+// virtual keys per pair.  Against the fixed 1024-key split grid: 16 x 32k keys
+// 0.120 -> 0.107 ms, config-3 lengths 0.110 -> 0.095 ms, 64 sequences of 256-4096
+// keys 0.081 -> 0.062 ms; charges of 0, 1024 and 2048 keys were within 1-15% of it.
+constexpr int kTurboStreamMinKeys = 1024;
+constexpr int kTurboStreamSegCost = 512;
 
 // Split size: aim for ~2048 (sequence, KV head, split) work units so the 256
 // CUs stay fed even when sequences are ragged; never below 64 keys.
@@ -91,21 +99,30 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     DecodePlan pl{};
     const int max_len = a->max_kv_len > 0 ? a->max_kv_len : 1;
     int split = a->split_keys;
-    // Automatic splitting on the MFMA path (16-bit and Q8 caches) uses the stream
-    // schedule: one workgroup per resident slot, equal key ranges, so ragged
-    // batches leave no tail.  Explicit split_keys keeps the fixed split grid.
+    // Automatic splitting on the MFMA path (16-bit and Q8 caches) and the Turbo
+    // path uses the stream schedule: one workgroup per resident slot, equal key
+    // ranges, so ragged batches leave no tail.  Explicit split_keys keeps the
+    // fixed split grid.
     const int kv_mul = a->n_kv_heads > 0 ? a->n_heads / a->n_kv_heads : 0;
+    const bool turbo = a->kv_dtype == GR_DTYPE_TURBO;
+    pl.stream_min_keys = turbo ? kTurboStreamMinKeys : kStreamMinKeys;
+    pl.stream_seg_cost = turbo ? kTurboStreamSegCost : kStreamSegCost;
     pl.stream = split <= 0 &&
-                (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16 || a->kv_dtype == GR_DTYPE_Q8) &&
+                (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16 || a->kv_dtype == GR_DTYPE_Q8 ||
+                 (turbo && turbo_stream_ok(a->head_dim, turbo_split_pieces(kv_mul)))) &&
                 kv_mul >= 1 &&
-                (a->head_dim == 128 || a->head_dim == 256 || (a->head_dim == 64 && a->kv_dtype == GR_DTYPE_Q8)) &&
+                (a->head_dim == 128 || a->head_dim == 256 ||
+                 (a->head_dim == 64 && (a->kv_dtype == GR_DTYPE_Q8 || turbo))) &&
                 a->n_seq <= kStreamMaxSeq &&
-                (int64_t)a->n_seq * (max_len + kStreamSegCost) * a->n_kv_heads * ((kv_mul + 15) / 16) < (int64_t)1 << 30;
+                (int64_t)a->n_seq * (max_len + pl.stream_seg_cost) * a->n_kv_heads * ((kv_mul + 15) / 16) <
+                    (int64_t)1 << 30;
+    const size_t per_part = turbo ? 2 : 1;  // Turbo: base + residual
+    pl.ws_q_bytes = turbo ? align_up((size_t)a->n_seq * a->n_heads * turbo_query_ws_dwords(a->head_dim) * 4, 256) : 0;
     if (pl.stream) {
-        pl.split_keys = kStreamMinKeys;
-        pl.n_splits = (max_len + kStreamMinKeys - 1) / kStreamMinKeys + 1;
+        pl.split_keys = pl.stream_min_keys;
+        pl.n_splits = (max_len + pl.stream_min_keys - 1) / pl.stream_min_keys + 1;
         const size_t parts = (size_t)a->n_seq * a->n_heads * pl.n_splits;
-        pl.ws_o_bytes = align_up(parts * a->head_dim * sizeof(float), 256);
+        pl.ws_o_bytes = align_up(parts * per_part * a->head_dim * sizeof(float), 256);
         pl.ws_ml_bytes = align_up(parts * 2 * sizeof(float), 256);
         pl.ws_sched_bytes = align_up((size_t)(a->n_seq + 1) * sizeof(int32_t), 256);
         return pl;
@@ -121,12 +138,8 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     pl.split_keys = split;
     pl.n_splits = (max_len + split - 1) / split;
     const size_t parts = (size_t)a->n_seq * a->n_heads * pl.n_splits;
-    const size_t per_part = a->kv_dtype == GR_DTYPE_TURBO ? 2 : 1;  // Turbo: base + residual
     pl.ws_o_bytes = align_up(parts * per_part * a->head_dim * sizeof(float), 256);
     pl.ws_ml_bytes = align_up(parts * 2 * sizeof(float), 256);
-    pl.ws_q_bytes = a->kv_dtype == GR_DTYPE_TURBO
-                        ? align_up((size_t)a->n_seq * a->n_heads * turbo_query_ws_dwords(a->head_dim) * 4, 256)
-                        : 0;
     return pl;
 }
 
@@ -226,10 +239,10 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
     p.use_mfma = 1;
-    if (pl.stream) {
-        p.stream_sched = (int*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes);
-        p.stream_min_keys = kStreamMinKeys;
-        p.stream_seg_cost = kStreamSegCost;
+    if (pl.stream) {  // workspace: partials o | (m, l) | Turbo queries | schedule
+        p.stream_sched = (int*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes + pl.ws_q_bytes);
+        p.stream_min_keys = pl.stream_min_keys;
+        p.stream_seg_cost = pl.stream_seg_cost;
     }
     if (a->kv_dtype == GR_DTYPE_Q8) {
         p.k_scale = a->k_scale;

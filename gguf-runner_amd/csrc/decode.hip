@@ -13,6 +13,7 @@
 // exp(s - m) == exp2(s2 - m2) with one v_exp_f32.
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
+#include "stream_sched.hpp"
 
 namespace gr {
 
@@ -219,13 +220,11 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
     if (h >= p.n_heads) return;
     const int len = p.kv_end[s] - p.kv_start[s];
     int nv;
-    if (p.stream_sched) {  // ranges of stream_sched[n_seq] keys that meet pair (s, column of h)
-        const int q = p.stream_sched[p.n_seq];
+    if (p.stream_sched) {  // ranges that meet pair (s, column of h)
         const int kv_mul = p.n_heads / p.n_kv_heads;
         const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
         const int col = (h / kv_mul) * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0);
-        const int off = p.stream_sched[s] + col * (len + p.stream_seg_cost) + p.stream_seg_cost;  // first key
-        nv = len > 0 ? min(p.n_splits, (off + len - 1) / q - off / q + 1) : 0;
+        nv = stream_partials(p, s, col, len);
     } else {
         nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
     }

@@ -33,6 +33,7 @@
 
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
+#include "stream_sched.hpp"
 
 namespace gr {
 
@@ -152,7 +153,6 @@ template <typename KV, int D>
 struct MdWaves {
     static constexpr int value = D <= 128 && !KV::kBlock ? 8 : 4;
 };
-constexpr int kStreamMaxSeq = 1024;  // sequences per launch on the stream schedule
 
 // Raise a row's reference maximum only when a tile exceeds it by more than
 // this (log2 units); P = 2^(s - m_ref) <= 2^8 meanwhile and O needs no rescale.
@@ -221,16 +221,16 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // Segment = keys [t_begin, t_stop) of sequence s, column g (KV head g / n_sub); its partial
     // goes to slot `split` of the (s, head) partial rows.
     int s, g, t_begin, t_stop, split;
-    // stream schedule state (DecodeLaunch::stream_sched)
+    // stream schedule state (DecodeLaunch::stream_sched, stream_sched.hpp)
     __shared__ int st_len[kStreamMaxSeq];
     __shared__ int st_off[kStreamMaxSeq];
     __shared__ int st_first;
+    __shared__ int st_wsum[kMdWaves];
+    StreamCursor<kMdThreads> cur;
     // Tiles of the current segment: wave w starts with tile w, then claims the
     // next unclaimed one from this counter, so waves that get more issue slots
     // (the older wave of a SIMD) take more tiles and the waves finish together.
     __shared__ int tile_next;
-    int st_q = 0, st_pos = 0, st_hi = 0;
-    auto seg_ext = [&](int q) { return st_len[q] > 0 ? st_len[q] + p.stream_seg_cost : 0; };
     if (!p.stream_sched) {
         split = blockIdx.x;
         g = blockIdx.y;
@@ -240,61 +240,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         if (t_begin >= t_limit) return;
         t_stop = min(t_limit, t_begin + p.split_keys);
     } else {
-        // Flattened key space: with E_s = L_s + P for a non-empty sequence (0 for
-        // an empty one; P = stream_seg_cost), pair (s, g) occupies
-        // [off_s + g E_s, off_s + (g+1) E_s), off_s = n_cols * sum_{s' < s} E_s',
-        // its keys the last L_s of it.  Workgroup b takes [b Q, (b+1) Q),
-        // Q = max(stream_min_keys, ceil(total / #workgroups)) rounded up to 32.
-        // Consecutive sequences per thread, block-wide scan.
-        const int n = p.n_seq;
-        constexpr int C = kStreamMaxSeq / kMdThreads;
-        int loc[C];
-        int tsum = 0;
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-            const int q = tid * C + c;
-            const int len = q < n ? max(0, p.kv_end[q] - p.kv_start[q]) : 0;
-            loc[c] = tsum;
-            tsum += (len > 0 ? len + p.stream_seg_cost : 0) * n_cols;
-            if (q < n) st_len[q] = len;
-        }
-        // inclusive scan of tsum over the workgroup
-        int incl = tsum;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int y = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += y;
-        }
-        __shared__ int wsum[kMdWaves];
-        if (lane == 63) wsum[wave] = incl;
-        __syncthreads();
-        int base = 0, total = 0;
-#pragma unroll
-        for (int w = 0; w < kMdWaves; w++) {
-            base += w < wave ? wsum[w] : 0;
-            total += wsum[w];
-        }
-        const int excl = base + incl - tsum;
-        st_q = max(p.stream_min_keys, (total + (int)gridDim.x - 1) / (int)gridDim.x);
-        st_q = (st_q + 31) / 32 * 32;
-        const int lo = (int)blockIdx.x * st_q;
-#pragma unroll
-        for (int c = 0; c < C; c++) {
-            const int q = tid * C + c;
-            if (q < n) {
-                const int off = excl + loc[c];
-                st_off[q] = off;
-                if (blockIdx.x == 0) p.stream_sched[q] = off;
-                if (lo >= off && lo < off + seg_ext(q) * n_cols) st_first = q;
-            }
-        }
-        if (blockIdx.x == 0 && tid == 0) p.stream_sched[n] = st_q;
-        if (lo >= total) return;
-        __syncthreads();
-        st_pos = lo;
-        st_hi = min(total, lo + st_q);
-        s = st_first;
-        g = (lo - st_off[s]) / seg_ext(s);
+        if (!cur.init(p, n_cols, st_len, st_off, &st_first, st_wsum)) return;
         t_begin = t_stop = split = 0;  // set per segment below
     }
 
@@ -302,17 +248,9 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     __syncthreads();
     for (;;) {
     if (p.stream_sched) {
-        const int len = st_len[s];
-        const int off = st_off[s] + g * seg_ext(s) + p.stream_seg_cost;  // the pair's first key
-        const int seg_beg = max(st_pos, off);
-        const int seg_end = min(st_hi, off + len);
-        st_pos = max(st_pos, seg_end);
-        if (seg_beg >= seg_end) {  // the range ends inside the pair's virtual keys: nothing here
-            break;
-        }
-        split = (int)blockIdx.x - off / st_q;
-        t_begin = p.kv_start[s] + (seg_beg - off);
-        t_stop = p.kv_start[s] + (seg_end - off);
+        if (!cur.segment(p, t_begin, t_stop, split)) break;  // the range ends inside the pair's virtual keys
+        s = cur.s;
+        g = cur.col;
         __syncthreads();  // the previous segment is done with the LDS
     }
     const int kvh = g / n_sub;                                     // KV head
@@ -836,14 +774,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             p.ws_ml[part * 2 + 1] = lt;
         }
     }
-    if (!p.stream_sched || st_pos >= st_hi) break;
+    if (!p.stream_sched || !cur.advance()) break;
     if (tid == 0) tile_next = kMdWaves;  // ordered before the next segment's claims by its barrier
-    if (++g == n_cols) {  // next pair: skip empty sequences
-        g = 0;
-        do {
-            s++;
-        } while (st_len[s] == 0);
-    }
     }
 }
 

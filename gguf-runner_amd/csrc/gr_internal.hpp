@@ -19,6 +19,9 @@ struct OutGate {
     }
 };
 
+// Sequences per launch on the stream schedule (per-workgroup LDS tables).
+constexpr int kStreamMaxSeq = 1024;
+
 struct DecodeLaunch {
     int n_seq, n_heads, n_kv_heads, head_dim, kv_dtype;
     int split_keys, n_splits;
@@ -34,16 +37,16 @@ struct DecodeLaunch {
     float* ws_o;
     float* ws_ml;
     int use_mfma;  // 16-bit / Q8 caches: MFMA split kernel (decode_mfma.hip) instead of VALU
-    // Stream schedule (MFMA split kernel only): when set, the grid is one row of
-    // workgroups that cut the flattened (sequence, KV head, key) space into
-    // equal ranges of at least stream_min_keys keys; partial slot j of (s, head)
-    // comes from the j-th range that meets the keys of pair (s, head / kv_mul), n_splits
-    // bounds the slots.  stream_sched[0 .. n_seq) receives the pair offsets
-    // off_s of every sequence and stream_sched[n_seq] the range size, for the
-    // combine kernel.
+    // Stream schedule (the MFMA and Turbo split kernels, stream_sched.hpp): when
+    // set, the grid is one row of workgroups that cut the flattened (sequence,
+    // column, key) space into equal ranges of at least stream_min_keys keys;
+    // partial slot j of (s, head) comes from the j-th range that meets the keys
+    // of the head's pair, n_splits bounds the slots.  stream_sched[0 .. n_seq)
+    // receives the pair offsets off_s of every sequence and stream_sched[n_seq]
+    // the range size, for the combine kernel.
     int* stream_sched;
     int stream_min_keys;
-    // Stream schedule: every non-empty (sequence, KV head) pair also counts
+    // Stream schedule: every non-empty (sequence, column) pair also counts
     // stream_seg_cost virtual keys ahead of its own (a segment start costs a
     // pipeline refill and a partial), so ranges that cross into a pair take
     // correspondingly fewer keys.  The split and combine kernels share it.
@@ -213,6 +216,13 @@ hipError_t launch_decode_turbo(const DecodeLaunch& p, hipStream_t st);
 size_t turbo_query_ws_dwords(int head_dim);
 // Rows per group of the token-packed Turbo prefill (DecodeLaunch::tok_pack).
 int turbo_pack_rows(int head_dim, int kv_mul);
+// Turbo decode: the split kernel carries the hi and lo query pieces as separate
+// MFMA columns when a workgroup's query heads fit twice in 16 columns.
+constexpr bool turbo_split_pieces(int kv_mul) { return 2 * (kv_mul < 16 ? kv_mul : 16) <= 16; }
+// Turbo decode shapes that run on the stream schedule: every one but head_dim
+// 256 with unsplit pieces (groups above 8 query heads), which keeps the fixed
+// split grid (its stream build faulted on the GPU with no cause found).
+constexpr bool turbo_stream_ok(int head_dim, bool split_pieces) { return head_dim != 256 || split_pieces; }
 
 // Flash prefill over the KV cache (MFMA).  q is the prepared 16-bit Q
 // [m][n_heads][d] already multiplied by score_scale*log2(e); for bf16, q_lo

@@ -20,6 +20,7 @@
 
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
+#include "stream_sched.hpp"
 #include "turbo_common.hpp"
 
 namespace gr {
@@ -146,9 +147,16 @@ __global__ __launch_bounds__(256) void turbo_combine_kernel(const DecodeLaunch p
     float* wsh = wsh_all[wave];
     const int h = 4 * blockIdx.x + wave, s = blockIdx.y;  // four heads per workgroup
     if (h >= p.n_heads) return;  // whole wave; only wave-level synchronisation below
-    const int g = h / (p.n_heads / p.n_kv_heads);
+    const int kv_mul = p.n_heads / p.n_kv_heads;
+    const int g = h / kv_mul;
     const int t_len = p.kv_end[s] - p.kv_start[s];
-    const int n_used = t_len > 0 ? (t_len + p.split_keys - 1) / p.split_keys : 0;
+    int n_used;
+    if (p.stream_sched) {  // ranges that meet pair (s, column of h)
+        const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
+        n_used = stream_partials(p, s, g * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0), t_len);
+    } else {
+        n_used = t_len > 0 ? (t_len + p.split_keys - 1) / p.split_keys : 0;
+    }
     const size_t part0 = ((size_t)s * p.n_heads + h) * p.n_splits;
     float mx = -INFINITY;
     for (int sp = lane; sp < n_used; sp += 64) mx = fmaxf(mx, p.ws_ml[(part0 + sp) * 2]);

@@ -22,9 +22,11 @@
 // prepared once per query by turbo_query_kernel); on the value side it is one
 // exact scale per output row.  Products are exact, sums are f32.
 #include <algorithm>
+#include <atomic>
 
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
+#include "stream_sched.hpp"
 #include "turbo_common.hpp"
 
 namespace gr {
@@ -305,8 +307,11 @@ constexpr int kTsWaves = kTsThreads / 64;
 // PACK: token-packed prefill (DecodeLaunch::tok_pack): query column i is token
 // s * tok_pack + i / kv_mul, head g * kv_mul + i % kv_mul, masked to that
 // token's own visible keys.
-template <int D, bool PACK, bool SPLIT>
+// STREAM: decode on the stream schedule (DecodeLaunch::stream_sched); else the
+// fixed (split, column, entry) grid.
+template <int D, bool PACK, bool SPLIT, bool STREAM>
 __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_kernel(const DecodeLaunch p) {
+    static_assert(!(PACK && STREAM), "the token-packed prefill runs on the fixed grid");
     using S = Tq<D>;
     constexpr int TILE = 32;
     constexpr int NCW = S::NCW, NSW = S::NSW, KS = S::KS, KSC = S::KSC, RT = S::RT, RB = S::RB;
@@ -320,18 +325,43 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     constexpr int kMergeBytes = (kTsWaves * 16 * (2 * D + 1) + 2 * kTsWaves * 16) * 4;
     __shared__ __attribute__((aligned(16))) char smem[kLoopBytes > kMergeBytes ? kLoopBytes : kMergeBytes];
 
-    const int split = blockIdx.x, s = blockIdx.z;
-    // decode: grid column blockIdx.y = KV head g, query heads h0 .. h0 + kv_cols - 1
+    // decode: column col = KV head g * n_sub + slice, query heads h0 .. h0 + n_col - 1
     // (DecodeLaunch::n_sub slices groups above 16 query heads)
     const int n_sub = (!PACK && p.n_sub > 0) ? p.n_sub : 1;
-    const int g = blockIdx.y / n_sub;
-    const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
-    const int t_begin = p.kv_start[e_rng] + split * p.split_keys;
-    const int t_limit = p.kv_end[e_rng];
-    if (t_begin >= t_limit) return;
-    const int t_stop = min(t_limit, t_begin + p.split_keys);
     const int kv_mul = p.n_heads / p.n_kv_heads;
-    const int h0 = g * kv_mul + (int)(blockIdx.y % n_sub) * 16;
+    // Segment = keys [t_begin, t_stop) of entry s, column col; its partials go to
+    // slot `split`.  Fixed grid: (split, column, entry) = blockIdx; decode on the
+    // stream schedule (DecodeLaunch::stream_sched, stream_sched.hpp): the
+    // segments of the workgroup's key range, one after another.
+    constexpr bool stream = STREAM;
+    __shared__ int st_len[STREAM ? kStreamMaxSeq : 1];
+    __shared__ int st_off[STREAM ? kStreamMaxSeq : 1];
+    __shared__ int st_first;
+    __shared__ int st_wsum[kTsWaves];
+    StreamCursor<kTsThreads> cur;
+    int split, s, col, t_begin, t_stop;
+    if (!stream) {
+        split = blockIdx.x;
+        s = blockIdx.z;
+        col = blockIdx.y;
+        const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
+        t_begin = p.kv_start[e_rng] + split * p.split_keys;
+        const int t_limit = p.kv_end[e_rng];
+        if (t_begin >= t_limit) return;
+        t_stop = min(t_limit, t_begin + p.split_keys);
+    } else {
+        if (!cur.init(p, p.n_kv_heads * n_sub, st_len, st_off, &st_first, st_wsum)) return;
+        split = s = col = t_begin = t_stop = 0;  // set per segment below
+    }
+    for (;;) {
+    if constexpr (stream) {
+        if (!cur.segment(p, t_begin, t_stop, split)) break;  // the range ends inside the pair's virtual keys
+        s = cur.s;
+        col = cur.col;
+        __syncthreads();  // the previous segment is done with the LDS
+    }
+    const int g = col / n_sub;
+    const int h0 = g * kv_mul + (col % n_sub) * 16;
     const int n_col = PACK ? p.tok_pack * kv_mul : min(16, g * kv_mul + kv_mul - h0);
     auto col_tok = [&](int c) { return PACK ? s * p.tok_pack + c / kv_mul : s; };
     auto col_head = [&](int c) { return PACK ? g * kv_mul + c % kv_mul : h0 + c; };
@@ -744,12 +774,16 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
             lt += sh_l[w][q] * a;
             ot += sh_o[w][q][i] * a;
         }
+        if (split >= n_splits) break;  // a sequence longer than max_kv_len: slots end here
         const size_t part = ((size_t)col_tok(q) * p.n_heads + col_head(q)) * n_splits + split;
         p.ws_o[part * 2 * D + i] = ot;
         if (i == 0) {
             p.ws_ml[part * 2 + 0] = mx;
             p.ws_ml[part * 2 + 1] = lt;
         }
+    }
+    if constexpr (!stream) break;
+    else if (!cur.advance()) break;
     }
 }
 
@@ -774,6 +808,30 @@ bool decode_turbo_supported(const DecodeLaunch& p) {
            (p.tok_pack == 0 || p.tok_pack * (p.n_heads / p.n_kv_heads) <= 16);
 }
 
+// Workgroups of the decode split kernel that fit on the current device at once
+// (CUs x occupancy): the stream schedule's grid.  A device property, cached per
+// (template instance, device); concurrent first calls compute the same value.
+template <int D, bool SPLIT>
+static int turbo_resident_wgs() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cached[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    const int slot = dev >= 0 && dev < kMaxDev ? dev : -1;
+    if (slot >= 0) {
+        const int c = cached[slot].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n_cu = 0, occ = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, turbo_split_kernel<D, false, SPLIT, true>, kTsThreads, 0) !=
+            hipSuccess)
+        return 256;
+    const int v = std::max(1, n_cu * std::max(1, occ));
+    if (slot >= 0) cached[slot].store(v, std::memory_order_relaxed);
+    return v;
+}
+
 template <int D>
 static hipError_t launch_turbo_d(const DecodeLaunch& p0, hipStream_t st) {
     DecodeLaunch p = p0;  // decode: groups above 16 query heads in columns of 16
@@ -788,12 +846,18 @@ static hipError_t launch_turbo_d(const DecodeLaunch& p0, hipStream_t st) {
     if (p.tok_pack > 0) {
         // token-packed prefill (turbo_pack_rows: 16 columns up to d128, 8 at d256)
         const dim3 grid(p.n_splits, p.n_kv_heads, (p.n_seq + p.tok_pack - 1) / p.tok_pack);
-        if (split) turbo_split_kernel<D, true, true><<<grid, kTsThreads, 0, st>>>(p);
-        else turbo_split_kernel<D, true, false><<<grid, kTsThreads, 0, st>>>(p);
-    } else {
+        if (split) turbo_split_kernel<D, true, true, false><<<grid, kTsThreads, 0, st>>>(p);
+        else turbo_split_kernel<D, true, false, false><<<grid, kTsThreads, 0, st>>>(p);
+    } else if (!p.stream_sched) {
         const dim3 grid(p.n_splits, p.n_kv_heads * p.n_sub, p.n_seq);
-        if (split) turbo_split_kernel<D, false, true><<<grid, kTsThreads, 0, st>>>(p);
-        else turbo_split_kernel<D, false, false><<<grid, kTsThreads, 0, st>>>(p);
+        if (split) turbo_split_kernel<D, false, true, false><<<grid, kTsThreads, 0, st>>>(p);
+        else turbo_split_kernel<D, false, false, false><<<grid, kTsThreads, 0, st>>>(p);
+    } else if (split) {
+        turbo_split_kernel<D, false, true, true><<<dim3(turbo_resident_wgs<D, true>()), kTsThreads, 0, st>>>(p);
+    } else if constexpr (turbo_stream_ok(D, false)) {
+        turbo_split_kernel<D, false, false, true><<<dim3(turbo_resident_wgs<D, false>()), kTsThreads, 0, st>>>(p);
+    } else {
+        return hipErrorInvalidValue;  // the plan keeps this shape on the fixed grid
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     return launch_turbo_combine(p, st);

@@ -273,3 +273,22 @@ def test_turbo_prefill_chunk_partial_groups(orc, dev, n_kv, m, window, hist):
         start = max(0, pos + 1 - window) if window else 0
         ref = orc.attention_token_turbo(q[pos], c, table, 0, n_heads, start, pos + 1)
         assert float(np.abs(got[i] - ref).max()) <= TOL, (i, float(np.abs(got[i] - ref).max()))
+
+
+@pytest.mark.parametrize("d,n_heads,n_kv", [(128, 32, 4), (128, 32, 2), (64, 16, 8), (256, 8, 4)])
+def test_turbo_decode_stream_many_short_ragged(orc, dev, d, n_heads, n_kv):
+    """Stream schedule over 24 short ragged sequences, four of them empty and most
+    offset: workgroup ranges begin and end inside the virtual keys charged per
+    (sequence, KV head) pair and cross several pairs each; GQA groups of 8 (hi / lo
+    query pieces as MFMA columns) and 16 (one column per head).  An empty range
+    gives zeros, as the oracle's loop over no keys does."""
+    rng = np.random.default_rng(5151 + d + n_kv)
+    n = 24
+    lens = rng.integers(1, 600, size=n)
+    lens[[0, 5, 6, 23]] = 0
+    starts = rng.integers(0, 80, size=n)
+    ends = starts + lens
+    got, ref = _decode_case(orc, dev, n_heads=n_heads, n_kv=n_kv, d=d, starts=starts.tolist(),
+                            ends=ends.tolist(), seq_len=int(ends.max()), seed=1400 + d + n_kv)
+    assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
+    assert not got[[0, 5, 6, 23]].any()
