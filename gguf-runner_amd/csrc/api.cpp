@@ -197,6 +197,7 @@ int check_decode(const gr_decode_args* a) {
         return fail(GR_ERR_ARG, "gr_decode_attention: caches and strides must be 16-byte aligned");
     if ((uintptr_t)a->workspace % 256 != 0)
         return fail(GR_ERR_ARG, "gr_decode_attention: workspace must be 256-byte aligned");
+    if ((uintptr_t)a->q % 16 != 0) return fail(GR_ERR_ARG, "gr_decode_attention: q must be 16-byte aligned");
     return GR_OK;
 }
 

@@ -266,50 +266,6 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // block scales keep one 32-element block per k-step).
     constexpr bool kPairK = kQ8 && !kBlock && KS % 2 == 0;
     auto dperm = [](int k, int g) { return kPairK ? 64 * (k >> 1) + 16 * g + 8 * (k & 1) : 32 * k + 8 * g; };
-    // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
-    // d = dperm(ks, g4) .. +7, pre-scaled to log2 units; columns >= nq are 0.
-    // f16: each query row is also multiplied by a power of two 2^e that puts its
-    // largest element near 2^14, so that the lo halves of the hi/lo split stay
-    // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
-    uint4 qf[KS], qfl[kSplit && !kQloLds ? KS : 1];
-    float qback = 1.0f;
-    {
-        const bool qv = l16 < nq;
-        const float* qrow = p.q + ((size_t)s * p.n_heads + h0 + (qv ? l16 : 0)) * D;
-        float qscale = p.score_scale * kLog2e;
-        if constexpr (std::is_same<M, Mfma16<F16>>::value) {
-            float qmax = 0.0f;
-#pragma unroll
-            for (int k = 0; k < KS; k++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, qv ? fabsf(qrow[dperm(k, g4) + e] * qscale) : 0.0f);
-            qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
-            qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-            if (qmax > 0.0f && qmax < 3.0e38f) {
-                int ex;
-                (void)frexpf(qmax, &ex);               // qmax = m 2^ex, m in [0.5, 1)
-                const int e = min(max(14 - ex, -100), 100);
-                qscale *= ldexpf(1.0f, e);
-                qback = ldexpf(1.0f, -e);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < KS; k++) {
-            uint32_t hw[4], lw[4];
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const int d0 = dperm(k, g4) + 2 * w;
-                const float x0 = qv ? qrow[d0] * qscale : 0.0f;
-                const float x1 = qv ? qrow[d0 + 1] * qscale : 0.0f;
-                hw[w] = M::pack2(x0, x1);
-                if constexpr (kSplit) lw[w] = M::rest2(hw[w], x0, x1);
-            }
-            qf[k] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            if constexpr (kQloLds) Qlo[(wave * KS + k) * 64 + lane] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-            else if constexpr (kSplit) qfl[k] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        }
-    }
-
     const size_t slot = (size_t)(p.seq_slot ? p.seq_slot[s] : s);
     // element pointers (one element = sizeof(Raw)/8 bytes)
     typedef typename std::conditional<kQ8, int8_t, uint16_t>::type Elem;
@@ -469,6 +425,70 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         }
     };
 
+    // The segment's first tile is requested before Q is prepared, so the Q
+    // loads and their conversion run while it is in flight.
+    const int n_tiles = (t_stop - t_begin + TILE - 1) / TILE;
+    int it = wave;
+    if (it < n_tiles) {
+        load_scales(t_begin + it * TILE);
+        load_k(t_begin + it * TILE);
+        load_v(t_begin + it * TILE);
+    }
+    // Q fragments (B operand of S^T = K Q^T): lane (query l16, group g4) holds
+    // d = dperm(ks, g4) .. +7, pre-scaled to log2 units; columns >= nq are 0.
+    // f16: each query row is also multiplied by a power of two 2^e that puts its
+    // largest element near 2^14, so that the lo halves of the hi/lo split stay
+    // out of the f16 subnormal range; the scores are multiplied back by 2^-e.
+    uint4 qf[KS], qfl[kSplit && !kQloLds ? KS : 1];
+    float qback = 1.0f;
+    {
+        const bool qv = l16 < nq;
+        const float* qrow = p.q + ((size_t)s * p.n_heads + h0 + (qv ? l16 : 0)) * D;
+        float qscale = p.score_scale * kLog2e;
+        // the lane's 8 consecutive elements per k-step as two 16-byte loads (q is
+        // 16-byte aligned, checked by the API, and rows are D floats)
+        float qx[KS][8];
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const float* src = qrow + dperm(k, g4);
+            const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 a = qv ? *(const float4*)src : z;
+            const float4 b = qv ? *(const float4*)(src + 4) : z;
+            qx[k][0] = a.x, qx[k][1] = a.y, qx[k][2] = a.z, qx[k][3] = a.w;
+            qx[k][4] = b.x, qx[k][5] = b.y, qx[k][6] = b.z, qx[k][7] = b.w;
+        }
+        if constexpr (std::is_same<M, Mfma16<F16>>::value) {
+            float qmax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KS; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, fabsf(qx[k][e] * qscale));
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 16, 64));
+            qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+            if (qmax > 0.0f && qmax < 3.0e38f) {
+                int ex;
+                (void)frexpf(qmax, &ex);               // qmax = m 2^ex, m in [0.5, 1)
+                const int e = min(max(14 - ex, -100), 100);
+                qscale *= ldexpf(1.0f, e);
+                qback = ldexpf(1.0f, -e);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float x0 = qx[k][2 * w] * qscale;
+                const float x1 = qx[k][2 * w + 1] * qscale;
+                hw[w] = M::pack2(x0, x1);
+                if constexpr (kSplit) lw[w] = M::rest2(hw[w], x0, x1);
+            }
+            qf[k] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            if constexpr (kQloLds) Qlo[(wave * KS + k) * 64 + lane] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            else if constexpr (kSplit) qfl[k] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        }
+    }
+
     f32x4 o[D / 16];
 #pragma unroll
     for (int dt = 0; dt < D / 16; dt++) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -483,13 +503,6 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     float pw[kQ8 ? NPB : 1];
     bool pw_set = false;
 
-    const int n_tiles = (t_stop - t_begin + TILE - 1) / TILE;
-    int it = wave;
-    if (it < n_tiles) {
-        load_scales(t_begin + it * TILE);
-        load_k(t_begin + it * TILE);
-        load_v(t_begin + it * TILE);
-    }
     while (it < n_tiles) {
         const int t0 = t_begin + it * TILE;
         // V tile -> LDS, transposed: Vt[d][key]

@@ -81,7 +81,7 @@ typedef struct gr_decode_args {
     int32_t split_keys;   /* keys per split-K partition, 0 = automatic */
     int32_t max_kv_len;   /* >= kv_end[s] - kv_start[s] for every s (sizes the grid) */
     float score_scale;    /* 1/sqrt(head_dim); 1.0 for Gemma3 whose q is pre-scaled */
-    const float* q;       /* [n_seq][n_heads][head_dim] f32, post-RoPE */
+    const float* q;       /* [n_seq][n_heads][head_dim] f32, post-RoPE, 16-byte aligned */
     const void* k_cache;
     const void* v_cache;
     int64_t seq_stride;   /* elements between sequences */

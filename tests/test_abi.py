@@ -139,3 +139,18 @@ def test_ssm_state_needs_one_sequence_slot(pkg):
         assert e.code == ffi.GR_ERR_ARG and "n_seq == 1" in str(e)
     else:
         raise AssertionError("accepted an SSM state with two sequence slots")
+
+
+def test_decode_rejects_misaligned_q(pkg):
+    """q is read as 16-byte vectors: a q pointer off a 16-byte boundary is an
+    argument error, reported before any launch (no GPU needed)."""
+    from gguf_runner_amd import ffi
+    L = ffi.lib()
+    a = ffi.DecodeArgs()
+    a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim, a.kv_dtype, a.max_kv_len = 1, 8, 4, 128, ffi.DTYPE_F16, 16
+    a.row_stride, a.seq_stride = 4 * 128, 16 * 4 * 128
+    a.k_cache = a.v_cache = a.kv_start = a.kv_end = a.out = 1 << 20
+    a.workspace = 1 << 21
+    a.q = (1 << 22) + 4
+    assert L.gr_decode_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
+    assert b"q must be 16-byte aligned" in L.gr_last_error()
