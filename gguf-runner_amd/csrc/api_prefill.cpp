@@ -38,6 +38,8 @@ int check_prefill(const gr_prefill_args* a) {
     }
     if ((a->q_norm == nullptr) != (a->k_norm == nullptr))
         return fail(GR_ERR_ARG, "gr_prefill_attention: q_norm and k_norm must be both set or both NULL");
+    if (((uintptr_t)a->q_norm | (uintptr_t)a->k_norm) % 16)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: q_norm and k_norm must be 16-byte aligned");
     if (a->n_tokens > 0 && (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache || !a->out ||
                             !a->workspace))
         return fail(GR_ERR_ARG, "gr_prefill_attention: null buffer");

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
     constexpr int LPR = D / 8;        // lanes per row
     constexpr int RPW = 64 / LPR;     // rows per wave step
     __shared__ float row_buf[kPrepRowsPerBlock][RPW][D];
-    __shared__ float cs_t[D / 2], sn_t[D / 2];
+    __shared__ __attribute__((aligned(16))) float cs_t[D / 2], sn_t[D / 2];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int rsub = lane / LPR;      // row of this lane within the wave step
@@ -104,8 +104,10 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
             ss = wave_sum<LPR>(ss);  // lanes of other rows never mix: groups are LPR-aligned
             if (w) {
                 const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+                float wv[8];
+                load8(w, c8, GR_DTYPE_F32, wv);
 #pragma unroll
-                for (int e = 0; e < 8; e++) x[e] = w[c8 + e] * (inv * x[e]);
+                for (int e = 0; e < 8; e++) x[e] = wv[e] * (inv * x[e]);
             }
             if (rope) {
                 if (p.rope_mode == GR_ROPE_ADJACENT) {
@@ -118,8 +120,26 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
                         x[e] = v0 * cs - v1 * sn;
                         x[e + 1] = v0 * sn + v1 * cs;
                     }
+                } else if (p.rope_dim == D) {
+                    // NeoX pairs (i, i + D/2) of a fully rotated row: the partner
+                    // elements of this lane's 8 are the 8 of lane ^ (LPR/2), in the
+                    // same row's lane group
+                    const bool first = c8 < half;
+                    const int f0 = first ? c8 : c8 - half;
+                    float csv[8], snv[8];
+                    *(float4*)csv = *(const float4*)(cs_t + f0);
+                    *(float4*)(csv + 4) = *(const float4*)(cs_t + f0 + 4);
+                    *(float4*)snv = *(const float4*)(sn_t + f0);
+                    *(float4*)(snv + 4) = *(const float4*)(sn_t + f0 + 4);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float other = __shfl_xor(x[e], LPR / 2, 64);
+                        // (v0, v1) -> (v0*c - v1*s, v0*s + v1*c)
+                        x[e] = first ? x[e] * csv[e] - other * snv[e] : other * snv[e] + x[e] * csv[e];
+                    }
                 } else {
-                    // NeoX pairs (i, i + rope_dim/2) live in other lanes: stage the row
+                    // NeoX pairs (i, i + rope_dim/2) of a partial rotation live in
+                    // other lanes: stage the row
 #pragma unroll
                     for (int e = 0; e < 8; e++) rb[c8 + e] = x[e];
                     __builtin_amdgcn_wave_barrier();

@@ -166,8 +166,8 @@ typedef struct gr_prefill_args {
     int32_t rope_dim;     /* rotated dims per head, even, <= head_dim */
     float rope_scale;     /* rope_scaling.global or .local of this layer (inference.rs:1502-1506) */
     const float* rope_freqs; /* device [rope_dim/2], see gr_rope_freqs */
-    const float* q_norm;  /* device [head_dim] QK RMSNorm weights, or NULL */
-    const float* k_norm;  /* device [head_dim], or NULL */
+    const float* q_norm;  /* device [head_dim] QK RMSNorm weights, 16-byte aligned, or NULL */
+    const float* k_norm;  /* device [head_dim], 16-byte aligned, or NULL */
     float norm_eps;       /* rms_norm_eps (1e-5 when the model gives 0, inference.rs:2539-2543) */
     int32_t is_gemma3;    /* 1: q *= 1/sqrt(head_dim) after RoPE, scores unscaled (1871-1873, 1982) */
     const void* q;        /* [m][n_heads][head_dim] */

@@ -154,3 +154,15 @@ def test_decode_rejects_misaligned_q(pkg):
     a.q = (1 << 22) + 4
     assert L.gr_decode_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
     assert b"q must be 16-byte aligned" in L.gr_last_error()
+
+
+def test_prefill_rejects_misaligned_norm_weights(pkg):
+    """The QK-norm weights are read as 16-byte vectors: a weight pointer off a
+    16-byte boundary is an argument error, reported before any launch."""
+    from gguf_runner_amd import ffi
+    L = ffi.lib()
+    a = ffi.PrefillArgs()
+    a.n_tokens, a.n_heads, a.n_kv_heads, a.head_dim, a.dtype = 16, 8, 4, 256, ffi.DTYPE_BF16
+    a.q_norm, a.k_norm = (1 << 20) + 8, 1 << 21
+    assert L.gr_prefill_attention(ctypes.byref(a), None) == ffi.GR_ERR_ARG
+    assert b"q_norm and k_norm must be 16-byte aligned" in L.gr_last_error()
