@@ -30,7 +30,8 @@ def _bits(x, fmt, orc):
 
 
 def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_scale=1.0,
-          window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6, rope_dim=None):
+          window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6, rope_dim=None,
+          attend_rows=None):
     from gguf_runner_amd import ffi, ops
     rng = np.random.default_rng(seed)
     qb = _bits(rng.standard_normal((m, n_heads, d), dtype=np.float32), fmt, orc)
@@ -48,7 +49,7 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
         orc.upcast(vb, fmt).reshape(m, -1), n_heads=n_heads, n_kv_heads=n_kv, head_size=d,
         seq_len=m, fmt=fmt, rope_dim=(0 if rope_mode == ffi.ROPE_NONE else rope_dim), neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs,
         rope_scale=rope_scale, is_gemma3=is_gemma3, window=window, q_norm=qn, k_norm=kn, eps=eps,
-        n_threads=orc.env_threads())
+        n_threads=orc.env_threads(), attend_rows=attend_rows)
     # GPU
     q, k, v = (_t16(x, fmt, orc, dev) for x in (qb, kb, vb))
     kc = torch.zeros((m, n_kv, d), dtype=q.dtype, device=dev)
@@ -115,6 +116,22 @@ def test_config2_llama3_8b_prefill_f16(orc, dev):
     got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=32, n_kv=8, d=128, fmt=orc.F16, seed=1002,
                              rope_mode=ffi.ROPE_ADJACENT, theta=5e5)
     _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)
+
+
+def test_config2_shape_prefill_8192_sampled_rows(orc, dev):
+    """The 8k prefill the benchmark times, at full size: 8192 tokens, 32 Q / 8 KV
+    heads, d128, f16, adjacent-pair RoPE theta 5e5, one call (the eight-wave
+    kernel).  The oracle prepares and caches every row and attends a sample of
+    rows: the edges of the 256-row query blocks, the last rows, and random ones;
+    every cache row is checked."""
+    from gguf_runner_amd import ffi
+    m = 8192
+    rows = np.unique(np.concatenate([[0, 1, 31, 32, 255, 256, 257, 511, 4095, 4096, 8063, 8190, 8191],
+                                     np.random.default_rng(88).integers(0, m, 20)]))
+    got, ref, kc, vc = _case(orc, dev, m=m, n_heads=32, n_kv=8, d=128, fmt=orc.F16, seed=8192,
+                             rope_mode=ffi.ROPE_ADJACENT, theta=5e5, attend_rows=rows)
+    _assert_close(got[rows], ref[rows])
     _assert_cache(kc, vc, orc.F16, orc)
 
 
