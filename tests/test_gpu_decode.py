@@ -178,3 +178,18 @@ def test_decode_stream_many_short_ragged(orc, dev, fmt_name, n_heads, n_kv):
         got, ref = _run_case(orc, dev, fmt=fmt, **kw)
         _assert_close(got, ref, fmt, orc)
     assert not got[[3, 4, 17, 39]].any()
+
+
+@pytest.mark.parametrize("n_seq", [1024, 1025])
+def test_decode_stream_sequence_limit(orc, dev, n_seq):
+    """1024 sequences fill the stream schedule's per-workgroup tables (two per
+    thread of the scan); 1025 take the fixed split grid.  Short ragged lengths,
+    some empty, f16, 8 / 2 heads."""
+    rng = np.random.default_rng(n_seq)
+    lens = rng.integers(0, 48, size=n_seq)
+    starts = rng.integers(0, 16, size=n_seq)
+    ends = starts + lens
+    got, ref = _run_case(orc, dev, n_heads=8, n_kv=2, d=128, starts=starts.tolist(), ends=ends.tolist(),
+                         seq_len=int(ends.max()), fmt=orc.F16, seed=n_seq)
+    _assert_close(got, ref, orc.F16, orc)
+    assert not got[lens == 0].any()

@@ -292,3 +292,17 @@ def test_turbo_decode_stream_many_short_ragged(orc, dev, d, n_heads, n_kv):
                             ends=ends.tolist(), seq_len=int(ends.max()), seed=1400 + d + n_kv)
     assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
     assert not got[[0, 5, 6, 23]].any()
+
+
+@pytest.mark.parametrize("n_seq", [1024, 1025])
+def test_turbo_decode_stream_sequence_limit(orc, dev, n_seq):
+    """The Turbo split kernel's stream schedule at its 1024-sequence table limit
+    (four per thread of the scan) and the fixed grid just past it."""
+    rng = np.random.default_rng(n_seq + 7)
+    lens = rng.integers(0, 24, size=n_seq)
+    starts = rng.integers(0, 8, size=n_seq)
+    ends = starts + lens
+    got, ref = _decode_case(orc, dev, n_heads=8, n_kv=4, d=64, starts=starts.tolist(), ends=ends.tolist(),
+                            seq_len=int(ends.max()), seed=1500 + n_seq)
+    assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
+    assert not got[lens == 0].any()
