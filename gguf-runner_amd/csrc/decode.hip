@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
         const int kv_mul = p.n_heads / p.n_kv_heads;
         const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
         const int col = (h / kv_mul) * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0);
-        nv = stream_partials(p, s, col, len);
+        nv = stream_partials(p, s, col);
     } else {
         nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
     }

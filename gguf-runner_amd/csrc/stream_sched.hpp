@@ -15,6 +15,15 @@
 
 namespace gr {
 
+// Keys of sequence i on the schedule: kv_end - kv_start, at least 0 and at most
+// what the partial slots cover ((n_splits - 1) * stream_min_keys >= max_kv_len),
+// so that a length above the max_kv_len the caller declared cannot push the
+// flattened offsets past the range the host checked (its keys past the slots
+// are dropped, as on the fixed grid).
+__device__ __forceinline__ int stream_len(const DecodeLaunch& p, int i) {
+    return min(max(0, p.kv_end[i] - p.kv_start[i]), (p.n_splits - 1) * p.stream_min_keys);
+}
+
 // Per-workgroup cursor over the workgroup's key range.  The per-sequence
 // lengths and offsets live in LDS (len, off: kStreamMaxSeq entries each).
 template <int kThreads>
@@ -45,7 +54,7 @@ struct StreamCursor {
 #pragma unroll
         for (int c = 0; c < C; c++) {
             const int i = tid * C + c;
-            const int l = i < n ? max(0, p.kv_end[i] - p.kv_start[i]) : 0;
+            const int l = i < n ? stream_len(p, i) : 0;
             loc[c] = tsum;
             tsum += (l > 0 ? l + cost : 0) * n_cols;
             if (i < n) len[i] = l;
@@ -119,9 +128,10 @@ struct StreamCursor {
     }
 };
 
-// Partials the split kernel wrote for pair (s, col) of a sequence with len keys,
-// from the offsets and range size workgroup 0 published.
-__device__ __forceinline__ int stream_partials(const DecodeLaunch& p, int s, int col, int len) {
+// Partials the split kernel wrote for pair (s, col), from the offsets and range
+// size workgroup 0 published.
+__device__ __forceinline__ int stream_partials(const DecodeLaunch& p, int s, int col) {
+    const int len = stream_len(p, s);
     if (len <= 0) return 0;
     const int q = p.stream_sched[p.n_seq];
     const int o = p.stream_sched[s] + col * (len + p.stream_seg_cost) + p.stream_seg_cost;

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void turbo_combine_kernel(const DecodeLaunch p
     int n_used;
     if (p.stream_sched) {  // ranges that meet pair (s, column of h)
         const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
-        n_used = stream_partials(p, s, g * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0), t_len);
+        n_used = stream_partials(p, s, g * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0));
     } else {
         n_used = t_len > 0 ? (t_len + p.split_keys - 1) / p.split_keys : 0;
     }

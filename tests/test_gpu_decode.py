@@ -193,3 +193,31 @@ def test_decode_stream_sequence_limit(orc, dev, n_seq):
                          seq_len=int(ends.max()), fmt=orc.F16, seed=n_seq)
     _assert_close(got, ref, orc.F16, orc)
     assert not got[lens == 0].any()
+
+
+def test_decode_stream_length_above_declared_max(orc, dev):
+    """A sequence longer than the max_kv_len the caller declared (a contract
+    violation the host cannot see) stays contained on the stream schedule: its
+    length is capped at what the partial slots cover, the other sequences keep
+    the oracle's answer, and its own output is finite.  The cache holds every
+    key, so no read leaves it."""
+    from gguf_runner_amd import ops
+    rng = np.random.default_rng(31337)
+    n_heads, n_kv, d = 8, 2, 128
+    lens = [300, 5000, 40, 500]
+    declared = 512  # only sequence 1 exceeds it
+    L = max(lens)
+    q = rng.standard_normal((len(lens), n_heads, d), dtype=np.float32)
+    kb = orc.f16_bits(rng.standard_normal((len(lens), L, n_kv * d), dtype=np.float32))
+    vb = orc.f16_bits(rng.standard_normal((len(lens), L, n_kv * d), dtype=np.float32))
+    T16 = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.float16).reshape(len(lens), L, n_kv, d).to(dev)
+    st = torch.zeros(len(lens), dtype=torch.int32, device=dev)
+    en = torch.tensor(lens, dtype=torch.int32, device=dev)
+    out = ops.decode_attention(torch.from_numpy(q).to(dev), T16(kb), T16(vb), st, en, max_kv_len=declared)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    for s in (0, 2, 3):
+        ref = orc.attention_token(q[s].reshape(-1), kb[s], vb[s], orc.F16, n_heads, n_kv, d, 0, lens[s],
+                                  n_threads=orc.env_threads()).reshape(n_heads, d)
+        _assert_close(got[s], ref, orc.F16, orc)
