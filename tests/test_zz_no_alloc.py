@@ -3,8 +3,8 @@ gr_decode_attention on the same inputs, over two calls in a row, the second smal
 than the first, so the second call runs over the first call's partials left in the
 built-in scratch array.
 
-Bar: the decode path's own (f16 cache: |d| <= 2e-3 + 1e-2 |ref|; Q8 cache: 1e-5, the
-fp32 bar).  The two entry points run the same kernels, but the d128 decode's waves
+Bar: the decode path's own (f16 cache: |d| <= 2e-3 + 1e-2 |ref|; Q8 and Turbo caches:
+1e-5, the fp32 bar).  The two entry points run the same kernels, but the d128 decode's waves
 claim key tiles dynamically, so the f16 rounding of P (relative to a running maximum)
 differs from run to run; the test prints that run-to-run difference of the
 workspace entry point beside the no-alloc difference."""
@@ -45,6 +45,27 @@ def _case(torch, dev, rng, n_seq, n_heads, n_kv, d, lens, dtype, q8_block=False)
     return call, out_ref, out_na, (q, kc, vc, ks, vs, kv_start, kv_end)
 
 
+def _turbo_case(torch, dev, rng, n_seq, n_heads, n_kv, d, lens):
+    """A Turbo cache of random codes / signs and sigma, gamma ~U[0.5, 1.5]."""
+    from gguf_runner_amd import ops
+    L = int(max(lens))
+    kv_dim = n_kv * d
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    u8 = lambda w: T(rng.integers(0, 256, (n_seq, L, w), dtype=np.uint8))
+    aux = lambda: T(rng.uniform(0.5, 1.5, (n_seq, L, n_kv)).astype(np.float32))
+    q = T(rng.standard_normal((n_seq, n_heads, d), dtype=np.float32))
+    table = T(ops.turbo_sign_table(1, n_kv, d))
+    kv_start = T(np.zeros(n_seq, np.int32))
+    kv_end = T(np.asarray(lens, np.int32))
+    out_ref = torch.full((n_seq, n_heads, d), float("nan"), device=dev)
+    out_na = torch.full((n_seq, n_heads, d), float("nan"), device=dev)
+    kb, vb, ks, vs = u8(kv_dim // 4), u8(kv_dim // 4), u8(kv_dim // 8), u8(kv_dim // 8)
+    sk, sv, gk, gv = aux(), aux(), aux(), aux()
+    call = ops.TurboDecodeCall(q, kb, vb, ks, vs, sk, sv, gk, gv, table, 0, kv_start, kv_end, out_ref,
+                               max_kv_len=L)
+    return call, out_ref, out_na, (q, kb, vb, ks, vs, sk, sv, gk, gv, table, kv_start, kv_end)
+
+
 def _run_noalloc(call, out_na):
     from gguf_runner_amd import ffi, ops
     a = ffi.DecodeArgs.from_buffer_copy(call.args)
@@ -53,7 +74,7 @@ def _run_noalloc(call, out_na):
     ffi.check(ffi.lib().gr_decode_attention_noalloc(ctypes.byref(a), ops._stream(None)))
 
 
-@pytest.mark.parametrize("kind", ["f16", "q8"])
+@pytest.mark.parametrize("kind", ["f16", "q8", "turbo"])
 def test_noalloc_decode_matches_workspace_decode_twice(dev, kind):
     import torch
     rng = np.random.default_rng(4242)
@@ -64,8 +85,12 @@ def test_noalloc_decode_matches_workspace_decode_twice(dev, kind):
              dict(n_seq=3, n_heads=16, n_kv=8, d=128, lens=[1, 300, 2049])]
     for i, c in enumerate(cases):
         print(f"noalloc case {i} {kind}: {c['n_seq']} seqs, lens {list(map(int, c['lens']))}", flush=True)
-        call, out_ref, out_na, keep = _case(torch, dev, rng, c["n_seq"], c["n_heads"], c["n_kv"], c["d"],
-                                            c["lens"], dt)
+        if kind == "turbo":
+            call, out_ref, out_na, keep = _turbo_case(torch, dev, rng, c["n_seq"], c["n_heads"], c["n_kv"],
+                                                      c["d"], c["lens"])
+        else:
+            call, out_ref, out_na, keep = _case(torch, dev, rng, c["n_seq"], c["n_heads"], c["n_kv"], c["d"],
+                                                c["lens"], dt)
         call()
         torch.cuda.synchronize()
         ref0 = out_ref.cpu().numpy()
