@@ -116,8 +116,8 @@ def _assert_rows_equal(dev_rows, c, row0, n, n_kv, d):
 @pytest.mark.parametrize("d", [64, 128, 256])
 def test_turbo_kv_write_token_bit_exact(orc, dev, d):
     """gr_kv_write_token into a Turbo cache writes the oracle's codes, sign bits, sigma
-    and gamma bit for bit: random rows of several magnitudes, an all-zero row (sigma 0),
-    a row with one silent head, and a row whose rotation is one centroid exactly."""
+    and gamma bit for bit: random rows of several magnitudes, an all-zero row (sigma 0)
+    and a row with one silent head."""
     from gguf_runner_amd import ffi, runtime as rt
     p, s = _turbo_state(rt, ffi, seq_len=128, d=d)
     rng = np.random.default_rng(9)
@@ -134,6 +134,31 @@ def test_turbo_kv_write_token_bit_exact(orc, dev, d):
     for t in range(n):
         orc.kv_write_turbo(c, 60 + t, k[t], v[t], table, layer)
     _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 60, n), c, 60, n, p.n_kv_heads, d)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_turbo_prefill_chunk_write_batched_bit_exact(orc, dev, d):
+    """A 1401-row prefill chunk with 3 KV heads has 8406 K and V units, past the 4096
+    from which the write quantises 4 units per wave (lane u running unit u's
+    sequential norms): the last wave holds 2 units and one wave holds both K and V
+    units (4203 of each).  Codes, sign bits, sigma and gamma equal the oracle's
+    quantize_turboquant_head bit for bit, over rows of several magnitudes, an
+    all-zero K row (sigma 0) and a silent V head."""
+    from gguf_runner_amd import ffi, runtime as rt
+    m, layer = 1401, 1
+    p, s = _turbo_state(rt, ffi, seq_len=1408, n_heads=6, n_kv=3, d=d)
+    rng = np.random.default_rng(31 + d)
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = (rng.standard_normal((m, p.kv_dim)) * rng.uniform(0.01, 30, size=(m, 1))).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    k[2] = 0.0
+    v[5, :d] = 0.0
+    rt.prefill_attention_chunk(p, s, layer, 0, q, k, v)
+    table = orc.turbo_sign_table(2, p.n_kv_heads, d)
+    c = orc.TurboCache(m, p.n_kv_heads, d)
+    for t in range(m):
+        orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
+    _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 0, m), c, 0, m, p.n_kv_heads, d)
 
 
 def test_turbo_layer_token_loop_and_chunked_prefill(orc, dev):
