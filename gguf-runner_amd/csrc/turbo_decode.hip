@@ -342,7 +342,9 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     int split, s, col, t_begin, t_stop;
     if (!stream) {
         split = blockIdx.x;
-        s = blockIdx.z;
+        // token-packed prefill: later row groups see more keys (causal), so they
+        // are dispatched first and the short ones fill in behind them
+        s = PACK ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
         col = blockIdx.y;
         const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
         t_begin = p.kv_start[e_rng] + split * p.split_keys;
