@@ -86,7 +86,8 @@ __device__ __forceinline__ uint32_t shl(uint32_t x) {
 // ka_pos(a).  Sign k-steps do the same over 32-bit sign words (D 64: a 16-bit
 // half whose bits 8..15 are first moved to 16..23).
 template <int D>
-__device__ void score_slot(int g4, int s, int m, int half, bool& is_sign, int& dim, int& p, float& coef) {
+__host__ __device__ constexpr void score_slot(int g4, int s, int m, int half, bool& is_sign, int& dim, int& p,
+                                              float& coef) {
     using S = Tq<D>;
     if (s < S::KSC) {
         const int a = 4 * (s & 3) + m, k = half ? a + 16 : a;
@@ -190,6 +191,53 @@ __device__ __forceinline__ void load_dwords(__amdgpu_buffer_rsrc_t r, int off, u
 
 }  // namespace
 
+// score_slot of every query-operand slot, tabulated at compile time for
+// turbo_query_kernel: slot idx (lane + 64 i) and half h give the flat index
+// (is_sign ? D : 0) + dim into the rotated / projected query and the factor
+// coef * 2^-e(p).  The factor is coef scaled by a power of two (2^14 .. 2^-1), so
+// factor * q rounds exactly as coef * q * 2^-e(p) does.
+template <int D>
+struct QSlots {
+    static constexpr int NB = 16 * Tq<D>::KS;
+    uint16_t idx[2][NB];
+    float f[2][NB];
+};
+
+constexpr float pow2f(int e) {
+    float r = 1.0f;
+    for (; e > 0; e--) r *= 2.0f;
+    for (; e < 0; e++) r *= 0.5f;
+    return r;
+}
+
+template <int D>
+constexpr QSlots<D> make_qslots() {
+    QSlots<D> t{};
+    for (int i = 0; i < QSlots<D>::NB; i++) {
+        const int g4 = i / (4 * Tq<D>::KS), rem = i % (4 * Tq<D>::KS);
+        for (int h = 0; h < 2; h++) {
+            bool is_sign = false;
+            int dim = 0, pp = 0;
+            float coef = 0.0f;
+            score_slot<D>(g4, rem >> 2, rem & 3, h, is_sign, dim, pp, coef);
+            t.idx[h][i] = (uint16_t)((is_sign ? D : 0) + dim);
+            t.f[h][i] = coef * pow2f(-bit_exp(pp));
+        }
+    }
+    return t;
+}
+
+__constant__ QSlots<64> kQSlots64 = make_qslots<64>();
+__constant__ QSlots<128> kQSlots128 = make_qslots<128>();
+__constant__ QSlots<256> kQSlots256 = make_qslots<256>();
+
+template <int D>
+__device__ __forceinline__ const QSlots<D>& qslots() {
+    if constexpr (D == 64) return kQSlots64;
+    else if constexpr (D == 128) return kQSlots128;
+    else return kQSlots256;
+}
+
 // ---------------------------------------------------------------- query preparation
 
 // turboquant_prepare_query (inference.rs:954-968) for (head h, entry s), one wave:
@@ -235,6 +283,7 @@ __global__ __launch_bounds__(256) void turbo_query_kernel(const DecodeLaunch p) 
     sp = wave_sum<64>(sp);
     tq::wave_lds_sync();  // the wave's qsh stores precede its reads
 
+    const float* qflat = &qsh[0][0];  // [rotated | projected]
     // one pass over the lane's slots (idx = lane + 64 i): values kept, maxima per plane
     constexpr int NI = (NB + 63) / 64;
     float v0[NI], v1[NI];
@@ -246,14 +295,11 @@ __global__ __launch_bounds__(256) void turbo_query_kernel(const DecodeLaunch p) 
         v0[i] = v1[i] = 0.0f;
         sgn[i] = false;
         if (idx < NB) {
-            const int g4 = idx / (4 * KS), rem = idx % (4 * KS);
-            int dim, pp;
-            float coef;
-            bool is_sign;
-            score_slot<D>(g4, rem >> 2, rem & 3, 0, is_sign, dim, pp, coef);
-            v0[i] = coef * qsh[is_sign ? 1 : 0][dim] * ldexpf(1.0f, -bit_exp(pp));
-            score_slot<D>(g4, rem >> 2, rem & 3, 1, is_sign, dim, pp, coef);
-            v1[i] = coef * qsh[is_sign ? 1 : 0][dim] * ldexpf(1.0f, -bit_exp(pp));
+            const QSlots<D>& tab = qslots<D>();
+            const int i0 = tab.idx[0][idx], i1 = tab.idx[1][idx];
+            v0[i] = tab.f[0][idx] * qflat[i0];
+            v1[i] = tab.f[1][idx] * qflat[i1];
+            const bool is_sign = i0 >= D;  // the slot's k-step: both halves alike
             sgn[i] = is_sign;
             const float m = fmaxf(fabsf(v0[i]), fabsf(v1[i]));
             if (is_sign) ms = fmaxf(ms, m);
