@@ -395,7 +395,18 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
         const int e_rng = PACK ? s * p.tok_pack : s;  // batch entry holding the key range
         t_begin = p.kv_start[e_rng] + split * p.split_keys;
         const int t_limit = p.kv_end[e_rng];
-        if (t_begin >= t_limit) return;
+        if (t_begin >= t_limit) {
+            if constexpr (PACK) {
+                if (p.n_splits == 1) {  // no keys: the group's rows are zero (as the combine gives)
+                    const int kv_mul = p.n_heads / p.n_kv_heads, n_col = p.tok_pack * kv_mul;
+                    for (int i = threadIdx.x; i < n_col * D; i += kTsThreads) {
+                        const int c = i / D, tok = s * p.tok_pack + c / kv_mul;
+                        if (tok < p.n_seq) p.out[((size_t)tok * p.n_heads + blockIdx.y * kv_mul + c % kv_mul) * D + i % D] = 0.0f;
+                    }
+                }
+            }
+            return;
+        }
         t_stop = min(t_limit, t_begin + p.split_keys);
     } else {
         if (!cur.init(p, p.n_kv_heads * n_sub, st_len, st_off, &st_first, st_wsum)) return;
@@ -809,6 +820,53 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     }
     __syncthreads();
     const int n_splits = p.n_splits;
+    if constexpr (PACK) {
+        if (n_splits == 1) {
+            // One split per row group (long chunks): the merged (O, l) of each
+            // column is final, so the workgroup does turbo_combine_kernel's work
+            // for it (1/l, the inverse residual rotation, the sum, the inverse
+            // rotation, the output gate) and writes no partials; the host skips
+            // the combine launch.
+            constexpr int J = D / 64;
+            const uint8_t* sg = p.turbo_signs + (size_t)g * (D / 8);
+            const int64_t ss = p.turbo_slot_stride;
+            for (int q = wave; q < n_col; q += kTsWaves) {
+                if (!col_ok(q)) continue;  // wave-uniform
+                float mx = -INFINITY;
+#pragma unroll
+                for (int w = 0; w < kTsWaves; w++) mx = fmaxf(mx, sh_m[w][q]);
+                float lt = 0.0f, b[J], r[J];
+#pragma unroll
+                for (int j = 0; j < J; j++) b[j] = r[j] = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kTsWaves; w++) {
+                    const float a = exp2f(sh_m[w][q] - mx);
+                    lt += sh_l[w][q] * a;
+#pragma unroll
+                    for (int j = 0; j < J; j++) {
+                        b[j] += sh_o[w][q][lane + 64 * j] * a;
+                        r[j] += sh_o[w][q][D + lane + 64 * j] * a;
+                    }
+                }
+                const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+                for (int j = 0; j < J; j++) {
+                    b[j] *= inv;
+                    r[j] *= inv;
+                }
+                tq::wave_transform<D>(r, sg + 3 * ss, sg + 2 * ss, lane);  // res_post, res_pre: inverse
+#pragma unroll
+                for (int j = 0; j < J; j++) b[j] += r[j];
+                tq::wave_transform<D>(b, sg + ss, sg, lane);  // rot_post, rot_pre: inverse
+                const int tok = col_tok(q), hh = col_head(q);
+                float* out = p.out + ((size_t)tok * p.n_heads + hh) * D;
+                const float* gt = p.gate.at(tok, hh);  // Qwen3.5 output gate, or null
+#pragma unroll
+                for (int j = 0; j < J; j++) out[lane + 64 * j] = gt ? gate_mul(b[j], gt[lane + 64 * j]) : b[j];
+            }
+            break;
+        }
+    }
     for (int idx = tid; idx < n_col * 2 * D; idx += kTsThreads) {
         const int q = idx / (2 * D), i = idx % (2 * D);
         if (!col_ok(q)) continue;
@@ -908,6 +966,7 @@ static hipError_t launch_turbo_d(const DecodeLaunch& p0, hipStream_t st) {
         return hipErrorInvalidValue;  // the plan keeps this shape on the fixed grid
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (p.tok_pack > 0 && p.n_splits == 1) return hipSuccess;  // the split kernel finished the rows
     return launch_turbo_combine(p, st);
 }
 

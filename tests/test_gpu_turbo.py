@@ -270,6 +270,38 @@ def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image
     assert worst <= TOL, worst
 
 
+@pytest.mark.parametrize("n_heads,n_kv,d,m,window", [(32, 8, 128, 1100, None), (32, 8, 128, 1100, 300),
+                                                     (16, 8, 256, 1100, None), (16, 8, 64, 2100, None)])
+def test_turbo_prefill_chunk_single_split_finished_in_split_kernel(orc, dev, n_heads, n_kv, d, m, window):
+    """Chunks with at least 2048 (row group, KV head) workgroups get one split per
+    group (1100 rows in groups of 4 x 8 KV heads = 2200; d64: 2100 rows in groups of
+    8 = 2104), and the split kernel finishes those rows itself (1/l, the inverse
+    rotations, the output store) with no partials and no combine launch.  Sampled
+    rows (the first two groups, the middle, the end and 12 random rows) == the
+    oracle's attention_token_turbo with each row's causal or window range (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=m + 8,
+                  kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE, layer_windows=[window, window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(7 * d + m + (window or 0))
+    layer = 1
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    got = rt.prefill_attention_chunk(p, s, layer, 0, q, k, v)
+    table = orc.turbo_sign_table(2, n_kv, d)
+    c = orc.TurboCache(m, n_kv, d)
+    for t in range(m):
+        orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
+    rows = sorted(set(range(8)) | {m // 2, m // 2 + 1, m - 2, m - 1} | set(rng.integers(0, m, 12).tolist()))
+    worst = 0.0
+    for i in rows:
+        start = max(0, i + 1 - window) if window else 0
+        ref = orc.attention_token_turbo(q[i], c, table, layer, n_heads, start, i + 1)
+        worst = max(worst, float(np.abs(got[i] - ref).max()))
+    assert worst <= TOL, worst
+
+
 @pytest.mark.parametrize("n_kv,m,window,hist", [(8, 3, None, 5), (8, 11, 1, 20), (2, 1, None, 0), (4, 37, 3, 60)])
 def test_turbo_prefill_chunk_partial_groups(orc, dev, n_kv, m, window, hist):
     """Token-packed Turbo prefill with partial row groups (16 query heads: kv_mul 2
