@@ -479,9 +479,18 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     auto blo_at = [&](int k) { return blo[(g4 * KS + k) * 16 + l16]; };
 
     int c_lo = t_begin, c_hi = t_stop;  // keys visible to the lane's column
+    int vis_lo = c_lo, vis_hi = c_hi;   // PACK: keys visible to every valid column (wave-uniform)
     if constexpr (PACK) {
         c_lo = qv ? p.col_start[col_tok(qc)] : 0;
         c_hi = qv ? min(p.col_end[col_tok(qc)], t_stop) : 0;
+        int lo = qv ? c_lo : INT_MIN, hi = qv ? c_hi : INT_MAX;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            lo = max(lo, __shfl_xor(lo, o, 64));
+            hi = min(hi, __shfl_xor(hi, o, 64));
+        }
+        vis_lo = __builtin_amdgcn_readfirstlane(lo);
+        vis_hi = __builtin_amdgcn_readfirstlane(hi);
     }
 
     // per-tile registers: K code / sign dwords of the lane's key in both
@@ -613,11 +622,19 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
                 const int key = t0 + 16 * sb + 4 * g4 + j;
                 float v = ksv[j] * (cback * sc[sb][j] - qcorr) + krv[j] * (pback * ssg[sb][j] - pcorr);
                 if constexpr (SPLIT) v += dpp_xor1(v);  // the hi and lo columns' halves
-                if constexpr (PACK) sv[e] = (key >= c_lo && key < c_hi) ? v : -INFINITY;
-                else sv[e] = v;
+                sv[e] = v;
                 (void)key;
                 vsg[e] = vsv[j];
                 vrr[e] = vrv[j];
+            }
+        }
+        if constexpr (PACK) {
+            if (!(t0 >= vis_lo && t0 + TILE <= vis_hi)) {  // a column sees only part of the tile
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int key = t0 + 16 * (e >> 2) + 4 * g4 + (e & 3);
+                    sv[e] = (key >= c_lo && key < c_hi) ? sv[e] : -INFINITY;
+                }
             }
         }
         if constexpr (!PACK) {
