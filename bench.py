@@ -15,9 +15,11 @@ Also reported in the same line:
   decode_32k_turbo -- the same over a Turbo cache (2-bit codes + residual signs + 2
                   f32 per kv head and row; compute-bound, so also given as the f16
                   cache bytes per second it replaces)
-  prefill      -- config 2 (Llama-3-8B-shaped causal prefill, 2048 tokens, f16,
-                  RoPE fused) and the 8k target run, in TFLOP/s with
-                  flops = 4 * Hq * d * sum_q visible(q)
+  prefill      -- the 8k prefill target run (config 2's shape at 8192 tokens:
+                  Llama-3-8B-shaped causal prefill, f16, RoPE fused), in TFLOP/s
+                  with flops = 4 * Hq * d * sum_q visible(q), with its roofline
+                  block; also flat as prefill_tflops / prefill_frac_of_mfma_peak
+  prefill_config2_s2048 -- config 2 itself (2048 tokens)
   deltanet     -- config 5 (gated DeltaNet, 16 heads, d128): 4096-token chunked
                   prefill and one recurrent decode step
   prefill_2048_quantised_cache -- run-state prefill of a 2048-token chunk over a
@@ -31,9 +33,12 @@ Also reported in the same line:
   roofline     -- the dominant kernel (decode) against 8 TB/s HBM; prefill.roofline
                   the 8k prefill against the dense f16 MFMA peak
   cpu_baseline -- the CPU oracle (a C restatement of the reference's loops,
-                  oracle/oracle.c) timed on this host's cores: the config-3 decode
-                  (headline unit) plus Q8 decode, token-serial prefill and serial
-                  DeltaNet legs (median of 3 runs after one warm-up each).
+                  oracle/oracle.c) timed on this host's cores.  `value` is the
+                  config-3 decode over the reference's Q8 storage (headline unit);
+                  the legs add the Turbo storage (the reference's default), f16 raw
+                  KV (the GPU headline's format, which the reference never stores),
+                  token-serial prefill and the serial DeltaNet scan (median of 3
+                  runs after one warm-up each).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -285,12 +290,18 @@ def _median_runs(run, n=3):
 def cpu_baseline(lens, n_heads=32, n_kv=4, d=128):
     """The CPU oracle (oracle/oracle.c, a C restatement of the reference's x86 loops)
     on this host's cores, each leg a bounded sample of a benchmark configuration, the
-    median of 3 runs after one warm-up:
-      value (decode_f16) -- attention_token over f16 raw KV on the first config-3
-          sequences in batch order (one sequence at a time, parallel over heads, as
-          the reference's rayon pool runs it);
-      decode_q8 -- the same over the reference's Q8 storage (int8 rows + one f32 scale
-          per row, dot_q8_row / axpy_q8_row, inference.rs:1337-1366);
+    median of 3 runs after one warm-up.  The decode legs run the 16 config-3
+    sequences whole, in batch order, one sequence at a time and parallel over heads
+    (as the reference's rayon pool runs attention_token):
+      value (decode_q8) -- the reference's Q8 storage (int8 rows + one f32 scale per
+          row, dot_q8_row / axpy_q8_row, inference.rs:1337-1366);
+      decode_turbo -- the reference's default storage (switches.rs:233-235): 2-bit
+          codes + residual signs + sigma / gamma per (row, KV head), the query
+          rotations and dot_ / axpy_turboquant_head* (inference.rs:954-968,
+          1246-1334); the cost does not depend on the code values, which are random;
+      decode_f16_raw -- f16 raw KV rows, the GPU headline's storage.  The reference
+          stores only Q8 or Turbo rows (KvCacheFormat, types.rs:811-814): this leg
+          is the oracle's raw-row mode, not a reference configuration;
       prefill_token_serial -- transformer_prefill_batch's per-token loop
           (inference.rs:2981-3017: QK-norm, RoPE, KV write, attention_token) over the
           first 1024 tokens of config 2 (32 / 8 heads, d128, adjacent RoPE theta 5e5);
@@ -302,19 +313,11 @@ def cpu_baseline(lens, n_heads=32, n_kv=4, d=128):
     orc = ge.load_oracle()
     threads = orc.max_threads()
     rng = np.random.default_rng(1003)
-    # decode legs: the 16 config-3 sequences, whole, in batch order
     seqs = list(lens)
     Lmax = max(seqs)
     kf = rng.standard_normal((Lmax, n_kv * d), dtype=np.float32)
     vf = rng.standard_normal((Lmax, n_kv * d), dtype=np.float32)
-    kc, vc = orc.f16_bits(kf), orc.f16_bits(vf)
     q = rng.standard_normal(n_heads * d, dtype=np.float32)
-
-    def dec_f16():
-        for L in seqs:
-            orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
-        return sum(seqs) * n_kv * d * 2 * 2
-    f16_rate, f16_s = _median_runs(dec_f16)
     k8 = [orc.kv_quantize_row(r, False) for r in kf]
     v8 = [orc.kv_quantize_row(r, False) for r in vf]
     kq = np.stack([c for c, _ in k8]); ks = np.concatenate([sc for _, sc in k8]).astype(np.float32)
@@ -326,6 +329,30 @@ def cpu_baseline(lens, n_heads=32, n_kv=4, d=128):
                                 n_threads=threads)
         return sum(seqs) * (n_kv * d * 2 + 2 * 4)
     q8_rate, q8_s = _median_runs(dec_q8)
+    del k8, v8
+
+    tc = orc.TurboCache(Lmax, n_kv, d)
+    for arr in (tc.kbase, tc.vbase, tc.ksign, tc.vsign):
+        arr[:] = rng.integers(0, 256, arr.size, dtype=np.uint8)
+    for arr in (tc.kscale, tc.vscale, tc.kres, tc.vres):
+        arr[:] = (rng.random(arr.size) + 0.5).astype(np.float32)
+    table = orc.turbo_sign_table(1, n_kv, d)
+
+    def dec_turbo():
+        for L in seqs:
+            orc.attention_token_turbo(q, tc, table, 0, n_heads, 0, L, n_threads=threads)
+        return sum(seqs) * n_kv * 2 * (d // 4 + d // 8 + 8)
+    tb_rate, tb_s = _median_runs(dec_turbo)
+    del tc
+
+    kc, vc = orc.f16_bits(kf), orc.f16_bits(vf)
+
+    def dec_f16():
+        for L in seqs:
+            orc.attention_token(q, kc, vc, orc.F16, n_heads, n_kv, d, 0, L, n_threads=threads)
+        return sum(seqs) * n_kv * d * 2 * 2
+    f16_rate, f16_s = _median_runs(dec_f16)
+    del kc, vc, kf, vf
     # token-serial prefill: first M tokens of config 2
     M, Hq2, Hk2 = 1024, 32, 8
     qp = rng.standard_normal((M, Hq2 * d), dtype=np.float32)
@@ -352,14 +379,19 @@ def cpu_baseline(lens, n_heads=32, n_kv=4, d=128):
         orc.deltanet_scan(qd, kd, vd, gate, beta, st0, n_threads=threads)
         return T
     dn_rate, dn_s = _median_runs(scan)
-    return {"value": round(f16_rate / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(q8_rate / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "cpu_model": _cpu_model(),
-            "sample": f"oracle attention_token (f16 raw KV, two-pass softmax, parallel over heads) on "
-                      f"the {len(seqs)} config-3 sequences ({sum(seqs)} keys), median of 3 runs "
-                      f"after one warm-up ({f16_s:.2f} s timed)",
+            "sample": f"oracle attention_token over the reference's Q8 KV storage (int8 rows + row scales, "
+                      f"two-pass softmax, parallel over heads) on the {len(seqs)} config-3 sequences "
+                      f"({sum(seqs)} keys), median of 3 runs after one warm-up ({q8_s:.2f} s timed)",
             "legs": {
-                "decode_q8": {"gbs": round(q8_rate / 1e9, 3),
-                              "sample": f"the same sequences over Q8 rows + row scales ({q8_s:.2f} s timed)"},
+                "decode_turbo": {"gbs": round(tb_rate / 1e9, 3),
+                                 "f16_equivalent_gbs": round(tb_rate / 1e9 * (d * 2 * 2) / (2 * (d // 4 + d // 8 + 8)), 3),
+                                 "sample": f"the same sequences over the Turbo storage, the reference's default "
+                                           f"({tb_s:.2f} s timed)"},
+                "decode_f16_raw": {"gbs": round(f16_rate / 1e9, 3),
+                                   "sample": f"the same sequences over f16 raw KV rows: the GPU headline's format, "
+                                             f"not a reference storage mode ({f16_s:.2f} s timed)"},
                 "prefill_token_serial": {
                     "visible_pairs_per_s": round(pf_rate), "tflops": round(pf_rate * 4 * Hq2 * d / 1e12, 5),
                     "sample": f"first {M} tokens of config 2 (f16 KV, {pairs} (query, key) pairs per "
@@ -508,15 +540,20 @@ def main() -> int:
         pcall, flops, _keep_p = prefill_workload(dev, S, seed)
         p_ms, _ = _timed(pcall, max(5, args.steps // 5), 2, stream)
         tf = flops / (p_ms * 1e-3) / 1e12
-        pre[f"S{S}"] = {"tflops": round(tf, 2), "ms": round(p_ms, 4),
-                        "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                        "gflop": round(flops / 1e9, 3)}
+        pre[S] = {"tflops": round(tf, 2), "ms": round(p_ms, 4),
+                  "frac_of_mfma_peak": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "gflop": round(flops / 1e9, 3)}
         del _keep_p, pcall
-    tf8 = pre["S8192"]["tflops"]
-    pre["roofline"] = {"bound": "mfma", "achieved": tf8, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                       "frac": round(tf8 / MFMA_F16_PEAK_TFLOPS, 4),
-                       "kernel": "gr_prefill_attention, S = 8192, 32 / 8 heads, d128, f16: qkv_prep_kernel + "
-                                 "prefill_kernel<f16, 128, 8>, hipEvent-timed (4 * Hq * d * sum visible FLOP)"}
+    tf8 = pre[8192]["tflops"]
+    # the prefill half of the metric: the 8k target run, flat, with its roofline block
+    prefill_line = dict(pre[8192])
+    prefill_line.update({
+        "value": tf8, "unit": "TFLOP/s",
+        "workload": "config 2 shape at S = 8192: causal GQA prefill, 32 Q / 8 KV heads, d128, f16 Q/K/V, "
+                    "adjacent RoPE theta 5e5 fused on load",
+        "roofline": {"bound": "mfma", "achieved": tf8, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf8 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "kernel": "gr_prefill_attention, S = 8192, 32 / 8 heads, d128, f16: qkv_prep_kernel + "
+                               "prefill_kernel<f16, 128, 8>, hipEvent-timed (4 * Hq * d * sum visible FLOP)"}})
 
     # config 1: Qwen3-0.6B-shaped single-layer decode, f32 KV, 1024 keys (latency-bound)
     c1call, c1bytes, _keep_c1 = rotating(
@@ -579,7 +616,10 @@ def main() -> int:
                           "frac_of_hbm": round(q_gbs / HBM_PEAK_GBS, 4), "bytes": qbytes},
         "decode_32k_turbo": {"gbs": round(u_gbs, 2), "ms": round(u_ms, 5), "bytes": ubytes,
                              "f16_equivalent_gbs": round(tbytes / (u_ms * 1e-3) / 1e9, 2)},
-        "prefill": pre,
+        "prefill": prefill_line,
+        "prefill_tflops": tf8,
+        "prefill_frac_of_mfma_peak": round(tf8 / MFMA_F16_PEAK_TFLOPS, 4),
+        "prefill_config2_s2048": pre[2048],
         "config1_decode": {"ms": round(c1_ms, 5), "gbs": round(c1bytes / (c1_ms * 1e-3) / 1e9, 2),
                            "bytes": c1bytes, "shape": "1 seq, 16 Q / 8 KV heads, d128, 1024 keys, f32 KV"},
         "config4": c4,

@@ -483,9 +483,11 @@ __device__ __forceinline__ void dn_dma16(dn_i32x4 r, void* lds, int voff) {
         (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
     // m0 (the LDS destination) is saved and restored inside the statement: the
     // compiler treats m0 as reserved and would not preserve a value of its own
-    // across a clobber.
+    // across a clobber.  An SALU write of m0 followed by an LDS DMA needs one
+    // wait state on gfx9-family parts, which the compiler cannot insert inside
+    // the statement: hence the s_nop.
     int saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
                  : "s"(m0), "v"(voff), "s"(r)
                  : "memory");
