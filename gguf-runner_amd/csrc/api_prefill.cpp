@@ -2,6 +2,8 @@
 // the two launches (Q/K/V prep -> cache; MFMA flash attention).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <atomic>
 #include <cmath>
 
 #include "gr_api_util.hpp"
@@ -71,11 +73,42 @@ size_t prefill_cs_bytes(const gr_prefill_args* a) {
     return a->rope_mode == GR_ROPE_NONE ? 0 : align_up((size_t)a->n_tokens * a->rope_dim * 4, 256);
 }
 
-// Staging: the (cos, sin) table when Q is fused, else the prepared Q (bf16 as
-// hi + lo residual pairs, two buffers).  Both layouts fit the larger size.
+// Staging: the (cos, sin) table when Q is fused, else the prepared Q (16-bit;
+// for bf16 caches the f16 values of the f16 path).  Both layouts fit the larger
+// size.
+size_t prefill_stage_bytes(const gr_prefill_args* a) {
+    return prefill_q_bytes(a) > prefill_cs_bytes(a) ? prefill_q_bytes(a) : prefill_cs_bytes(a);
+}
+
+// bf16 caches run the f16 MFMA path on an exact f16 copy of the cache rows
+// [f16_row0, base_pos + n_tokens): the first row any query of the launch sees,
+// rounded down to 128 keys (the largest K / V tile, whose first rows the kernel
+// loads and masks).
+int64_t prefill_f16_row0(const gr_prefill_args* a) {
+    const int64_t lo = a->window > 0 ? std::max<int64_t>(0, (int64_t)a->base_pos + 1 - a->window) : 0;
+    return lo / 128 * 128;
+}
+size_t prefill_f16_copy_bytes(const gr_prefill_args* a) {
+    const int64_t rows = (int64_t)a->base_pos + a->n_tokens - prefill_f16_row0(a);
+    return align_up((size_t)rows * a->n_kv_heads * a->head_dim * 2, 256);
+}
+
+// [staging][K copy][V copy][flag, 256 B] for bf16, [staging] for f16.
 size_t prefill_ws_total(const gr_prefill_args* a) {
-    const size_t staged = prefill_q_bytes(a) * (a->dtype == GR_DTYPE_BF16 ? 2 : 1);
-    return staged > prefill_cs_bytes(a) ? staged : prefill_cs_bytes(a);
+    if (a->dtype != GR_DTYPE_BF16) return prefill_stage_bytes(a);
+    return prefill_stage_bytes(a) + 2 * prefill_f16_copy_bytes(a) + 256;
+}
+
+// Per-launch tag of the bf16 range flag: a launch reads "out of f16 range" only
+// from a flag word its own prep pass wrote (a stale word from an earlier launch
+// holds another tag; a word that happens to match sends the launch down the
+// exact bf16 path, which is always correct).
+uint32_t next_f16_epoch() {
+    static std::atomic<uint32_t> ctr{0x6a09e667u};
+    uint32_t e;
+    do e = ctr.fetch_add(0x9e3779b9u) + 0x9e3779b9u;
+    while (e == 0u);
+    return e;
 }
 
 }  // namespace
@@ -110,10 +143,11 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pp.q_row_stride = (int64_t)a->n_heads * a->head_dim;
     pp.kv_row_stride = (int64_t)a->n_kv_heads * a->head_dim;
     const bool fused = prefill_fused_q(a);
+    const bool bf16 = a->dtype == GR_DTYPE_BF16;
     pp.q_out = fused ? nullptr : a->workspace;
-    pp.q_out_lo = !fused && a->dtype == GR_DTYPE_BF16 ? (char*)a->workspace + prefill_q_bytes(a) : nullptr;
+    pp.q_out_lo = nullptr;
     pp.rope_cs_out = fused && a->rope_mode != GR_ROPE_NONE ? (float*)a->workspace : nullptr;
-    pp.q_out_dtype = a->dtype;
+    pp.q_out_dtype = GR_DTYPE_F16;  // bf16 caches too: the f16 path's operand (split exactly on the bf16 path)
     pp.q_out_scale = score_scale * 1.4426950408889634f;
     pp.k_cache = a->k_cache;
     pp.v_cache = a->v_cache;
@@ -122,7 +156,41 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pp.cache_seq = nullptr;
     pp.cache_seq_stride = 0;
     pp.cache_row_stride = a->cache_row_stride;
-    hipError_t e = launch_qkv_prep(pp, st);
+    const int kv_dim = a->n_kv_heads * a->head_dim;
+    const int64_t row0 = prefill_f16_row0(a);
+    uint16_t* k_f16 = nullptr;
+    uint16_t* v_f16 = nullptr;
+    uint32_t* flag = nullptr;
+    uint32_t epoch = 0;
+    hipError_t e = hipSuccess;
+    if (bf16) {
+        char* w = (char*)a->workspace + prefill_stage_bytes(a);
+        k_f16 = (uint16_t*)w;
+        v_f16 = (uint16_t*)(w + prefill_f16_copy_bytes(a));
+        flag = (uint32_t*)(w + 2 * prefill_f16_copy_bytes(a));
+        epoch = next_f16_epoch();
+        pp.k_f16 = k_f16;
+        pp.v_f16 = v_f16;
+        pp.f16_row0 = row0;
+        pp.f16_row_stride = kv_dim;
+        pp.f16_flag = flag;
+        pp.f16_epoch = epoch;
+        // rows of earlier calls that this launch's queries see
+        Bf16CopyLaunch hc{};
+        hc.n_rows = a->base_pos - row0;
+        hc.row0 = row0;
+        hc.kv_dim = kv_dim;
+        hc.k_cache = (const uint16_t*)a->k_cache;
+        hc.v_cache = (const uint16_t*)a->v_cache;
+        hc.cache_row_stride = a->cache_row_stride;
+        hc.k_f16 = k_f16;
+        hc.v_f16 = v_f16;
+        hc.f16_flag = flag;
+        hc.f16_epoch = epoch;
+        e = launch_bf16_rows_to_f16(hc, st);
+        if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention bf16 copy launch");
+    }
+    e = launch_qkv_prep(pp, st);
     if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention prep launch");
 
     PrefillLaunch pf{};
@@ -155,6 +223,14 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pf.gate.gate = a->out_gate;
     pf.gate.row_stride = a->out_gate_row_stride;
     pf.gate.head_stride = a->out_gate_head_stride;
+    if (bf16) {
+        pf.k_f16 = k_f16;
+        pf.v_f16 = v_f16;
+        pf.f16_row0 = row0;
+        pf.f16_row_stride = kv_dim;
+        pf.f16_flag = flag;
+        pf.f16_epoch = epoch;
+    }
     e = launch_prefill(pf, st);
     if (e != hipSuccess) return hip_fail(e, "gr_prefill_attention launch");
     return GR_OK;

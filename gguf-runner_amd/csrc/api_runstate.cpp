@@ -253,6 +253,7 @@ int validate_config(const gr_attn_config* c) {
 }  // namespace
 
 int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st);
+size_t prefill_ws_bytes(const gr_prefill_args* a);
 int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStream_t st);
 int deltanet_enqueue(const gr_deltanet_args* a, hipStream_t st);
 size_t deltanet_ws(const gr_deltanet_args* a);
@@ -679,7 +680,18 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         pack = plan_turbo_pack(s, m, starts, ends);
         probe = turbo_pack_probe(s, m, pack);
     }
-    const size_t extra = mfma ? 2 * qb : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m) + 16 * (size_t)m;
+    gr_prefill_args a{};  // the MFMA prefill's arguments (sizes first: its workspace depends on them)
+    a.n_tokens = m;
+    a.base_pos = (int32_t)base_pos;
+    a.n_heads = s->cfg.n_heads;
+    a.n_kv_heads = s->cfg.n_kv_heads;
+    a.head_dim = s->d;
+    a.dtype = s->cfg.kv_dtype;
+    a.window = (int32_t)w;
+    a.rope_mode = s->cfg.rope_mode;
+    a.rope_dim = s->rope_dim;
+    const size_t pf_ws = mfma ? prefill_ws_bytes(&a) : 0;
+    const size_t extra = mfma ? pf_ws : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m) + 16 * (size_t)m;
     if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
     Carve cv(s->stage);
     float* qin = cv.take<float>((size_t)m * s->q_dim);
@@ -690,16 +702,6 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
     void* kc = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     void* vc = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     if (mfma) {
-        gr_prefill_args a{};
-        a.n_tokens = m;
-        a.base_pos = (int32_t)base_pos;
-        a.n_heads = s->cfg.n_heads;
-        a.n_kv_heads = s->cfg.n_kv_heads;
-        a.head_dim = s->d;
-        a.dtype = s->cfg.kv_dtype;
-        a.window = (int32_t)w;
-        a.rope_mode = s->cfg.rope_mode;
-        a.rope_dim = s->rope_dim;
         const bool swa = is_swa_layer(s, layer);
         a.rope_scale = swa ? s->cfg.rope_scale_local : s->cfg.rope_scale_global;
         a.rope_freqs = (s->cfg.is_gemma3 && swa) ? s->freqs_swa : s->freqs;
@@ -716,7 +718,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         a.v_cache = vc;
         a.cache_row_stride = s->kv_dim;
         a.out = xo;
-        a.workspace = cv.take<char>(2 * qb);
+        a.workspace = cv.take<char>(pf_ws);
         a.bidirectional = block ? 1 : 0;
         if ((rc = prefill_enqueue_ex(&a, GR_DTYPE_F32, s->stream))) return rc;
     } else {

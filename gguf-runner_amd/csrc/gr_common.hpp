@@ -43,6 +43,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return (uint16_t)(x >> 16);
 }
 
+// A bf16 value whose f16 conversion is not exact or not finite: |x| >= 2^16
+// (f16's largest finite value is 65504; bf16 has nothing between 65280 and
+// 65536), inf or NaN.  Below f16's normal range the conversion rounds to a
+// multiple of 2^-24, an absolute change under 2^-25.
+__device__ __forceinline__ bool bf16_outside_f16(uint16_t b) { return (b & 0x7fffu) >= 0x4780u; }
+
 // Two floats as a bf16 pair (low half = lo) with one v_cvt_pk_bf16_f32 (round to
 // nearest even, as f32_to_bf16 for finite values); for MFMA operands.
 typedef __bf16 gr_bf16x2_t __attribute__((ext_vector_type(2)));

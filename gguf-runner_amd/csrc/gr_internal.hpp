@@ -125,9 +125,36 @@ struct QkvPrepLaunch {
     int64_t cache_row_stride;
     int cache_by_index;         // 1: token i's K/V go to row i of the cache (staging), slot 0
     float* rope_cs_out;         // [n_tokens][rope_dim / 2][2] (cos, sin) of each token, or nullptr
+    // bf16 caches feeding the f16 MFMA prefill: each K / V row written to the cache
+    // is also written as f16 (exact: a bf16 significand fits f16's) to row
+    // (cache row - f16_row0) of k_f16 / v_f16 (row stride f16_row_stride
+    // elements); a value f16 cannot hold (|x| >= 65536, inf, NaN) stores f16_epoch
+    // to *f16_flag.  k_f16 = nullptr: no copy.
+    void* k_f16;
+    void* v_f16;
+    int64_t f16_row0, f16_row_stride;
+    uint32_t* f16_flag;
+    uint32_t f16_epoch;
 };
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);
+
+// f16 copies of cache rows [row0, row0 + n_rows) of a bf16 K and V cache (row
+// stride cache_row_stride elements, kv_dim elements per row) into rows 0.. of
+// k_f16 / v_f16 (row stride kv_dim), with the range flag of QkvPrepLaunch.
+struct Bf16CopyLaunch {
+    int64_t n_rows, row0;
+    int kv_dim;
+    const uint16_t* k_cache;
+    const uint16_t* v_cache;
+    int64_t cache_row_stride;
+    uint16_t* k_f16;
+    uint16_t* v_f16;
+    uint32_t* f16_flag;
+    uint32_t f16_epoch;
+};
+
+hipError_t launch_bf16_rows_to_f16(const Bf16CopyLaunch& p, hipStream_t st);
 
 // Q8 KV write (kv_write_token's Q8 branch, inference.rs:1886-1917): n_rows f32
 // rows of kv_dim elements (k_rows / v_rows, row stride kv_dim) are quantised
@@ -252,6 +279,17 @@ struct PrefillLaunch {
     int64_t cache_row_stride;
     float* out;
     OutGate gate;
+    // bf16 caches (dtype BF16): when k_f16 is set, the rows [f16_row0, base_pos +
+    // n_tokens) of the cache are also in k_f16 / v_f16 as exact f16 values (row
+    // stride f16_row_stride), and unless *f16_flag == f16_epoch (a value f16
+    // cannot hold was found) the kernel runs the single-pass f16 MFMA path on them;
+    // otherwise the bf16 hi + lo path on the cache.  q (staged, head_dim 256)
+    // then holds f16 values, which the bf16 path splits exactly into hi + lo.
+    const void* k_f16;
+    const void* v_f16;
+    int64_t f16_row0, f16_row_stride;
+    const uint32_t* f16_flag;
+    uint32_t f16_epoch;
 };
 
 hipError_t launch_prefill(const PrefillLaunch& p, hipStream_t st);

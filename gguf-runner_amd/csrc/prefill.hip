@@ -18,6 +18,8 @@
 // For head_dim 128 the kernel prepares Q itself from the raw rows (QK RMSNorm,
 // RoPE from a per-token (cos, sin) table, softmax_scale*log2(e)); otherwise Q
 // arrives prepared that way by the prep pass.
+#include <type_traits>
+
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -218,8 +220,15 @@ __device__ __forceinline__ void pf_prepare_q(const PrefillLaunch& p, int row, in
     }
 }
 
+// The attention of one workgroup.  K / V rows t of the visible range are rows
+// t - row0 of k_cache / v_cache (row stride rs elements); Ks0 .. Vs1 are the
+// double-buffered tiles (BN * D each) and Qlo the bf16 d256 Q residuals, all in
+// LDS and declared by the kernel (distinct arrays, so the compiler sees that the
+// DMA into one buffer never aliases the reads of another).
 template <typename DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel(const PrefillLaunch p) {
+__device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void* k_cache, const void* v_cache,
+                                             const int64_t rs, const int64_t row0, uint16_t* Ks0, uint16_t* Ks1,
+                                             uint16_t* Vs0, uint16_t* Vs1, uint4* Qlo) {
     constexpr int kPfThreads = NW * 64;
     constexpr int BM = NW * 32, BN = PfTile<D, NW>::BN;
     constexpr int CPR = D / 8;                   // 16-byte chunks per cache row
@@ -233,16 +242,9 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
     // subtraction; the variants with more live registers subtract instead.
     constexpr bool kFold = D == 128 && !kSplit;
 
-    // Double-buffered K and V tiles; four distinct arrays so that the compiler
-    // sees the DMA into one buffer never aliases the reads of the other.
-    __shared__ __attribute__((aligned(16))) uint16_t Ks0[BN * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Ks1[BN * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs0[BN * D];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs1[BN * D];
     // bf16 d256: the Q residual fragments live in LDS (per wave, [k-step][lane])
     // instead of 64 VGPRs, which the d256 accumulators need
     constexpr bool kQloLds = kSplit && D == 256;
-    __shared__ __attribute__((aligned(16))) uint4 Qlo[kQloLds ? NW * (D / 16) * 64 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -265,9 +267,8 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
     const int j = item - h * n_pairs;
     const int kv_mul = p.n_heads / p.n_kv_heads;
     const int g = h / kv_mul;
-    const uint16_t* kc = (const uint16_t*)p.k_cache + (size_t)g * D;
-    const uint16_t* vc = (const uint16_t*)p.v_cache + (size_t)g * D;
-    const int64_t rs = p.cache_row_stride;
+    const uint16_t* kc = (const uint16_t*)k_cache + (size_t)g * D;
+    const uint16_t* vc = (const uint16_t*)v_cache + (size_t)g * D;
     const int rsb = (int)rs * 2;
 
     // DMA: thread tid fills chunk position tid + NW * 64 * u of the tile: row
@@ -341,12 +342,33 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
 #pragma unroll
             for (int s = 0; s < D / 16; s++) qf[s] = *(const uint4*)(qrow + 16 * s);
             if constexpr (kSplit) {
-                const uint16_t* qrl = (const uint16_t*)p.q_lo + qoff;
+                if (p.k_f16) {
+                    // staged f16 values (bf16 cache with an f16 copy): hi = bf16(x)
+                    // and lo = x - hi are exact, an 11-bit significand in two 8-bit ones
 #pragma unroll
-                for (int s = 0; s < D / 16; s++) {
-                    const uint4 x = *(const uint4*)(qrl + 16 * s);
-                    if constexpr (kQloLds) Qlo[(wave * (D / 16) + s) * 64 + lane] = x;
-                    else qfl[s] = x;
+                    for (int s = 0; s < D / 16; s++) {
+                        float xv[8];
+                        unpack16<F16>(qf[s], xv);
+                        uint32_t hw[4], lw[4];
+#pragma unroll
+                        for (int w = 0; w < 4; w++) {
+                            hw[w] = pack_bf16x2(xv[2 * w], xv[2 * w + 1]);
+                            lw[w] = pack_bf16x2(xv[2 * w] - __uint_as_float(hw[w] << 16),
+                                                xv[2 * w + 1] - __uint_as_float(hw[w] & 0xffff0000u));
+                        }
+                        qf[s] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                        const uint4 x = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+                        if constexpr (kQloLds) Qlo[(wave * (D / 16) + s) * 64 + lane] = x;
+                        else qfl[s] = x;
+                    }
+                } else {
+                    const uint16_t* qrl = (const uint16_t*)p.q_lo + qoff;
+#pragma unroll
+                    for (int s = 0; s < D / 16; s++) {
+                        const uint4 x = *(const uint4*)(qrl + 16 * s);
+                        if constexpr (kQloLds) Qlo[(wave * (D / 16) + s) * 64 + lane] = x;
+                        else qfl[s] = x;
+                    }
                 }
             }
         }
@@ -360,8 +382,8 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
         // Issue the DMA of the tile starting at key t0.  Rows past kend - 1 are
         // clamped to it (they are masked; the clamp keeps P.V free of stale data).
         auto dma_tile = [&](int t0, uint16_t* kdst, uint16_t* vdst) {
-            const __amdgpu_buffer_rsrc_t kr = pf_rsrc(kc + (int64_t)t0 * rs);
-            const __amdgpu_buffer_rsrc_t vr = pf_rsrc(vc + (int64_t)t0 * rs);
+            const __amdgpu_buffer_rsrc_t kr = pf_rsrc(kc + (t0 - row0) * rs);
+            const __amdgpu_buffer_rsrc_t vr = pf_rsrc(vc + (t0 - row0) * rs);
             if (t0 + BN <= kend) {
 #pragma unroll
                 for (int u = 0; u < LD; u++) {
@@ -594,12 +616,43 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
     }
 }
 
+// The LDS of one workgroup: double-buffered K and V tiles (four distinct
+// arrays) and, with QLO, the bf16 d256 Q residual fragments.
+#define GR_PF_LDS(D, NW, QLO)                                                          \
+    __shared__ __attribute__((aligned(16))) uint16_t Ks0[PfTile<D, NW>::BN * D];    \
+    __shared__ __attribute__((aligned(16))) uint16_t Ks1[PfTile<D, NW>::BN * D];    \
+    __shared__ __attribute__((aligned(16))) uint16_t Vs0[PfTile<D, NW>::BN * D];    \
+    __shared__ __attribute__((aligned(16))) uint16_t Vs1[PfTile<D, NW>::BN * D];    \
+    __shared__ __attribute__((aligned(16))) uint4 Qlo[(QLO) ? NW * (D / 16) * 64 : 1]
+
+template <typename DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel(const PrefillLaunch p) {
+    GR_PF_LDS(D, NW, Mfma32<DT>::kSplit && D == 256);
+    prefill_body<DT, D, NW>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
+}
+
+// bf16 cache with an exact f16 copy of its visible rows: the single-pass f16
+// path on the copy, or, when the copy could not hold every value (the flag
+// carries this launch's epoch), the bf16 hi + lo path on the cache itself.
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_bf16x_kernel(const PrefillLaunch p) {
+    GR_PF_LDS(D, NW, D == 256);
+    if (*p.f16_flag != p.f16_epoch)
+        prefill_body<F16, D, NW>(p, p.k_f16, p.v_f16, p.f16_row_stride, p.f16_row0, Ks0, Ks1, Vs0, Vs1, Qlo);
+    else
+        prefill_body<BF16, D, NW>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
+}
+#undef GR_PF_LDS
+
 template <typename DT, int D, int NW>
 static hipError_t launch_prefill_d(const PrefillLaunch& p, hipStream_t st) {
     const int n_qb = (p.n_tokens + NW * 32 - 1) / (NW * 32);
     const int n_items = p.n_heads * ((n_qb + 1) / 2);  // query blocks paired heavy + light
     dim3 grid(8 * ((n_items + 7) / 8));
-    prefill_kernel<DT, D, NW><<<grid, NW * 64, 0, st>>>(p);
+    if (std::is_same<DT, BF16>::value && p.k_f16)
+        prefill_bf16x_kernel<D, NW><<<grid, NW * 64, 0, st>>>(p);
+    else
+        prefill_kernel<DT, D, NW><<<grid, NW * 64, 0, st>>>(p);
     return hipGetLastError();
 }
 

@@ -188,9 +188,60 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
             void* dst = kind == 1 ? p.k_cache : p.v_cache;
             const size_t ob = (size_t)sq * p.cache_seq_stride + (size_t)row * p.cache_row_stride +
                               (size_t)head * D + c8;
-            store8(dst, ob, p.cache_dtype, x);
+            if (p.k_f16) {
+                // bf16 cache row plus its exact f16 copy for the f16 MFMA prefill
+                uint32_t wb[4], wh[4];
+                bool bad = false;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint16_t b0 = f32_to_bf16(x[2 * k]), b1 = f32_to_bf16(x[2 * k + 1]);
+                    bad = bad || bf16_outside_f16(b0) || bf16_outside_f16(b1);
+                    wb[k] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+                    wh[k] = (uint32_t)f32_to_f16(bf16_to_f32(b0)) | ((uint32_t)f32_to_f16(bf16_to_f32(b1)) << 16);
+                }
+                *(uint4*)((uint16_t*)dst + ob) = make_uint4(wb[0], wb[1], wb[2], wb[3]);
+                uint16_t* cp = (uint16_t*)(kind == 1 ? p.k_f16 : p.v_f16);
+                *(uint4*)(cp + (size_t)(row - p.f16_row0) * p.f16_row_stride + (size_t)head * D + c8) =
+                    make_uint4(wh[0], wh[1], wh[2], wh[3]);
+                if (bad) *p.f16_flag = p.f16_epoch;
+            } else {
+                store8(dst, ob, p.cache_dtype, x);
+            }
         }
     }
+}
+
+// Existing bf16 cache rows (the history of a prefill chunk) to their f16 copy:
+// 8 elements per thread, K then V.
+__global__ __launch_bounds__(256) void bf16_rows_to_f16_kernel(const Bf16CopyLaunch p) {
+    const int64_t per = (int64_t)p.n_rows * (p.kv_dim / 8);
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= 2 * per) return;
+    const bool is_v = idx >= per;
+    const int64_t j = is_v ? idx - per : idx;
+    const int64_t r = j / (p.kv_dim / 8);
+    const int c8 = (int)(j - r * (p.kv_dim / 8)) * 8;
+    const uint16_t* src = (is_v ? p.v_cache : p.k_cache) + (p.row0 + r) * p.cache_row_stride + c8;
+    uint16_t* dst = (is_v ? p.v_f16 : p.k_f16) + r * p.kv_dim + c8;
+    const uint4 u = *(const uint4*)src;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    uint32_t h[4];
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint16_t b0 = (uint16_t)(w[k] & 0xffffu), b1 = (uint16_t)(w[k] >> 16);
+        bad = bad || bf16_outside_f16(b0) || bf16_outside_f16(b1);
+        h[k] = (uint32_t)f32_to_f16(bf16_to_f32(b0)) | ((uint32_t)f32_to_f16(bf16_to_f32(b1)) << 16);
+    }
+    *(uint4*)dst = make_uint4(h[0], h[1], h[2], h[3]);
+    if (bad) *p.f16_flag = p.f16_epoch;
+}
+
+hipError_t launch_bf16_rows_to_f16(const Bf16CopyLaunch& p, hipStream_t st) {
+    if (p.n_rows <= 0) return hipSuccess;
+    const int64_t threads = 2 * p.n_rows * (p.kv_dim / 8);
+    bf16_rows_to_f16_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(p);
+    return hipGetLastError();
 }
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st) {

@@ -31,7 +31,7 @@ LAYERS = [WINDOW] * 5 + [0]
 
 def _close(got, ref, what):
     err = np.abs(got - ref)
-    bad = err > ATOL + RTOL * np.abs(ref)
+    bad = ~(err <= ATOL + RTOL * np.abs(ref))  # NaN counts as out of tolerance
     assert not bad.any(), f"{what}: {bad.sum()} / {bad.size} out of tolerance; max abs {err.max():.3e}"
 
 

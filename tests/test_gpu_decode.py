@@ -60,7 +60,7 @@ def _assert_close(got, ref, fmt, orc):
     if fmt == orc.F32:
         assert float(err.max()) <= TOL_F32, f"max abs {err.max():.3e}"
     else:
-        bad = err > ATOL_16 + RTOL_16 * np.abs(ref)
+        bad = ~(err <= ATOL_16 + RTOL_16 * np.abs(ref))  # NaN counts as out of tolerance
         assert not bad.any(), f"{bad.sum()} elements out of tolerance, max abs {err.max():.3e}"
 
 

@@ -31,12 +31,15 @@ def _bits(x, fmt, orc):
 
 def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_scale=1.0,
           window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6, rope_dim=None,
-          attend_rows=None):
+          attend_rows=None, patch=None):
     from gguf_runner_amd import ffi, ops
     rng = np.random.default_rng(seed)
-    qb = _bits(rng.standard_normal((m, n_heads, d), dtype=np.float32), fmt, orc)
-    kb = _bits(rng.standard_normal((m, n_kv, d), dtype=np.float32), fmt, orc)
-    vb = _bits(rng.standard_normal((m, n_kv, d), dtype=np.float32), fmt, orc)
+    qf = rng.standard_normal((m, n_heads, d), dtype=np.float32)
+    kf = rng.standard_normal((m, n_kv, d), dtype=np.float32)
+    vf = rng.standard_normal((m, n_kv, d), dtype=np.float32)
+    if patch:
+        patch(qf, kf, vf)
+    qb, kb, vb = (_bits(x, fmt, orc) for x in (qf, kf, vf))
     qn = kn = None
     if norm:
         qn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
@@ -78,7 +81,7 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
 
 def _assert_close(got, ref):
     err = np.abs(got - ref)
-    bad = err > ATOL + RTOL * np.abs(ref)
+    bad = ~(err <= ATOL + RTOL * np.abs(ref))  # NaN counts as out of tolerance
     assert not bad.any(), f"{bad.sum()} / {bad.size} out of tolerance; max abs {err.max():.3e}"
 
 
@@ -266,3 +269,28 @@ def test_prefill_image_block_eight_wave_sampled(orc, dev):
                                  fmt=orc.F16, seed=7, window=0, rope_mode=ffi.ROPE_ADJACENT,
                                  theta=5e5, sample=sample)
     _assert_close(got, ref)
+
+
+@pytest.mark.parametrize("where", ["chunk", "history"])
+@pytest.mark.parametrize("which", ["k", "v"])
+@pytest.mark.parametrize("d", [128, 256])
+def test_bf16_prefill_values_outside_f16_take_the_exact_path(orc, dev, d, which, where):
+    """bf16 caches run the single-pass f16 MFMA path on an exact f16 copy of their rows;
+    a bf16 value f16 cannot hold (V: 70144 and -98304; K: 1e6 and -3e6 before RoPE, of
+    which a rotated pair keeps at least 1/sqrt(2) in one element; in the chunk's own rows
+    or in the history rows an earlier call wrote) sends the launch to the bf16 hi + lo
+    path instead.  On the f16 path these values would become inf and the outputs inf or
+    NaN; here they match the oracle's token-serial prefill."""
+    from gguf_runner_amd import ffi
+    rows = [30, 31] if where == "history" else [150, 260]
+
+    def patch(q, k, v):
+        x, big = (k, (1e6, -3e6)) if which == "k" else (v, (70144.0, -98304.0))
+        x[rows[0], 0, 5] = big[0]
+        x[rows[1], 1, d - 3] = big[1]
+
+    got, ref, kc, vc = _case(orc, dev, m=300, n_heads=8, n_kv=2, d=d, fmt=orc.BF16, seed=77 + d,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6, base_chunks=[100, 200], patch=patch)
+    assert np.isfinite(ref).all()
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.BF16, orc)
