@@ -206,6 +206,23 @@ def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
     return call, flops, (q, k, v, kc, vc, out, fr)
 
 
+def prefill_d64_workload(dev, S, seed, n_heads=14, n_kv=2, d=64):
+    """head_dim-64 causal prefill at the Qwen2-0.5B shape (14 Q / 2 KV heads, f16 Q/K/V,
+    NeoX RoPE theta 1e6 fused on load)."""
+    import torch
+    from gguf_runner_amd import ffi, ops
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    kc, vc = torch.empty_like(k), torch.empty_like(v)
+    out = torch.empty((S, n_heads, d), device=dev, dtype=torch.float32)
+    fr = torch.tensor(ops.rope_freqs(1e6, d), dtype=torch.float32, device=dev)
+    call = ops.PrefillCall(q, k, v, kc, vc, out, rope_mode=ffi.ROPE_NEOX, rope_dim=d, rope_freqs=fr)
+    return call, 4 * n_heads * d * S * (S + 1) // 2, (q, k, v, kc, vc, out, fr)
+
+
 def prefill_q8_workload(S, seed, block, n_heads=32, n_kv=8, d=128, turbo=False):
     """Run-state prefill of one S-token chunk over a Q8 KV cache (row or 32-element
     block scales) or a Turbo cache: gr_prefill_attention_chunk with host q / k / v
@@ -444,6 +461,11 @@ def run_one(args, dev, stream, lens) -> int:
         call, flops, keep = prefill_workload(dev, S, 8)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only in ("prefill2k_d64", "prefill8k_d64"):
+        S = 2048 if args.only == "prefill2k_d64" else 8192
+        call, flops, keep = prefill_d64_workload(dev, S, 64)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only in ("prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo"):
         # synchronous host-buffer calls: the wall time per call includes the PCIe
         # copies; the kernels' own times come from a kernel trace of this run
@@ -488,7 +510,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
+                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()

@@ -21,8 +21,8 @@ int check_prefill(const gr_prefill_args* a) {
     if (a->n_heads <= 0 || a->n_kv_heads <= 0 || a->n_heads % a->n_kv_heads != 0)
         return fail(GR_ERR_ARG, "gr_prefill_attention: n_heads %d must be a positive multiple of n_kv_heads %d",
                     a->n_heads, a->n_kv_heads);
-    if (a->head_dim != 128 && a->head_dim != 256)
-        return fail(GR_ERR_ARG, "gr_prefill_attention: head_dim %d unsupported (128, 256)", a->head_dim);
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: head_dim %d unsupported (64, 128, 256)", a->head_dim);
     if (a->dtype != GR_DTYPE_F16 && a->dtype != GR_DTYPE_BF16)
         return fail(GR_ERR_ARG, "gr_prefill_attention: dtype must be f16 or bf16");
     if (a->window < 0) return fail(GR_ERR_ARG, "gr_prefill_attention: window < 0");

@@ -655,7 +655,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
     DeviceScope dsc(s->device);
     const size_t qb = 4 * (size_t)m * s->q_dim, kb = 4 * (size_t)m * s->kv_dim;
     const bool mfma = (s->cfg.kv_dtype == GR_DTYPE_F16 || s->cfg.kv_dtype == GR_DTYPE_BF16) &&
-                      (s->d == 128 || s->d == 256);
+                      (s->d == 64 || s->d == 128 || s->d == 256);
     const int64_t w = s->windows.empty() ? 0 : s->windows[layer];
     std::vector<int32_t> starts(m), ends(m);
     int max_len = 1;
@@ -732,9 +732,8 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         p.k_cache = kc;
         p.v_cache = vc;
         if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
-        if (is_q8(s) && s->d != 64) {
-            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile);
-            // head_dim 64 runs the rows through the decode kernels instead
+        if (is_q8(s)) {
+            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile)
             PrefillQ8Launch pq{};
             pq.n_tokens = m;
             pq.n_heads = s->cfg.n_heads;

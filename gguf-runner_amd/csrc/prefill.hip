@@ -78,10 +78,17 @@ __device__ __forceinline__ void pf_dma16(__amdgpu_buffer_rsrc_t r, uint16_t* lds
 // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima)
 __device__ __forceinline__ void pf_wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Position of 16-byte chunk c of tile row r: c ^ pf_swz(r & 15).  With it the
+// Position of 16-byte chunk c of tile row r: c ^ pf_swz<D>(r & 15).  With it the
 // K reads (16 consecutive rows, one chunk each) and the V transpose reads (4
-// consecutive rows x 4 chunks per 32 lanes) each touch distinct banks.
-__device__ __forceinline__ int pf_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
+// consecutive rows x 4 chunks per 32 lanes) each touch distinct banks.  A
+// head_dim-64 row is 8 chunks (128 B, half the banks): rows of one parity then
+// need distinct chunk positions (K), and rows r and r + 2 opposite 4-chunk halves
+// (V), which a 3-bit swizzle with bit 2 = bit 1 of r gives.
+template <int D>
+__device__ __forceinline__ int pf_swz(int r) {
+    if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15;
+}
 
 
 // Workgroup = NW waves of 32 query rows each.  Large launches use 8 waves
@@ -91,18 +98,28 @@ template <int D, int NW>
 struct PfTile;
 template <>
 struct PfTile<128, 8> {
-    static constexpr int BN = 128;  // keys per LDS tile
-    static constexpr int kOcc = 1;  // workgroups per CU (2 waves per SIMD, <= 256 VGPRs each)
+    static constexpr int BN = 128;      // keys per LDS tile
+    static constexpr int kWaves = 2;    // waves per SIMD (one workgroup per CU, <= 256 VGPRs each)
 };
 template <>
 struct PfTile<128, 4> {
     static constexpr int BN = 64;
-    static constexpr int kOcc = 2;
+    static constexpr int kWaves = 2;    // two workgroups per CU
+};
+template <>
+struct PfTile<64, 8> {
+    static constexpr int BN = 128;
+    static constexpr int kWaves = 4;    // two workgroups per CU, <= 128 VGPRs each
+};
+template <>
+struct PfTile<64, 4> {
+    static constexpr int BN = 64;
+    static constexpr int kWaves = 4;    // four workgroups per CU
 };
 template <>
 struct PfTile<256, 4> {
     static constexpr int BN = 32;
-    static constexpr int kOcc = 1;
+    static constexpr int kWaves = 1;    // one wave per SIMD (its registers)
 };
 
 // Softmax reference maxima are only raised when a row's tile maximum exceeds
@@ -281,11 +298,11 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
     for (int u = 0; u < LD; u++) {
         const int r = tid / CPR + u * RPU;
         dma_row[u] = r;
-        dma_col[u] = ((tid % CPR) ^ pf_swz(r & 15)) * 16;
+        dma_col[u] = ((tid % CPR) ^ pf_swz<D>(r & 15)) * 16;
         dma_off[u] = r * rsb + dma_col[u];
     }
     // K fragment reads: row 32 sb + ln (row & 15 == ln & 15), chunk 2 s + lg.
-    const int swz_k = pf_swz(ln & 15);
+    const int swz_k = pf_swz<D>(ln & 15);
     // V^T transpose reads (ds_read_b64_tr_b16): lane i of 16-lane group G
     // supplies row k0 + i/4, columns d0 + 4 (i%4) .. +3, with
     // k0 = 32 sb + 16 t + 8 b + 4 lg and d0 = 32 dt + 16 (G & 1); it receives
@@ -297,7 +314,7 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
     for (int b = 0; b < 2; b++) {
         const int r = 8 * b + 4 * lg + (gi >> 2);
         v_base[b] = r * D + (gi & 1) * 4;
-        v_swz[b] = pf_swz(r & 15);
+        v_swz[b] = pf_swz<D>(r & 15);
     }
 
     for (int pass = 0; pass < 2; pass++) {
@@ -451,9 +468,9 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
                 const uint2 hi = __builtin_bit_cast(uint2, part[1]);
                 return make_uint4(lo.x, lo.y, hi.x, hi.y);
             };
-            // d = 128: all V^T fragments are read before the softmax (they do not
+            // d <= 128: all V^T fragments are read before the softmax (they do not
             // depend on it); d = 256 reads them next to their MFMAs (registers).
-            constexpr bool kPreV = D == 128;
+            constexpr bool kPreV = D <= 128;
             uint4 va[kPreV ? D / 32 : 1][2];
             if constexpr (kPreV) {
 #pragma unroll
@@ -626,7 +643,7 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
     __shared__ __attribute__((aligned(16))) uint4 Qlo[(QLO) ? NW * (D / 16) * 64 : 1]
 
 template <typename DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel(const PrefillLaunch p) {
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kWaves)) void prefill_kernel(const PrefillLaunch p) {
     GR_PF_LDS(D, NW, Mfma32<DT>::kSplit && D == 256);
     prefill_body<DT, D, NW>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
 }
@@ -635,7 +652,7 @@ __global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_kernel
 // path on the copy, or, when the copy could not hold every value (the flag
 // carries this launch's epoch), the bf16 hi + lo path on the cache itself.
 template <int D, int NW>
-__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kOcc)) void prefill_bf16x_kernel(const PrefillLaunch p) {
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kWaves)) void prefill_bf16x_kernel(const PrefillLaunch p) {
     GR_PF_LDS(D, NW, D == 256);
     if (*p.f16_flag != p.f16_epoch)
         prefill_body<F16, D, NW>(p, p.k_f16, p.v_f16, p.f16_row_stride, p.f16_row0, Ks0, Ks1, Vs0, Vs1, Qlo);
@@ -659,12 +676,14 @@ static hipError_t launch_prefill_d(const PrefillLaunch& p, hipStream_t st) {
 // Eight-wave workgroups once they alone fill every CU (256 on MI355X), else four.
 static int prefill_pick_waves(const PrefillLaunch& p) {
     const int n_qb8 = (p.n_tokens + 255) / 256;
-    return p.head_dim == 128 && p.n_heads * ((n_qb8 + 1) / 2) >= 256 ? 8 : 4;
+    return p.head_dim <= 128 && p.n_heads * ((n_qb8 + 1) / 2) >= 256 ? 8 : 4;
 }
 
 template <typename DT>
 static hipError_t launch_prefill_dt(const PrefillLaunch& p, hipStream_t st) {
     switch (p.head_dim) {
+        case 64:
+            return prefill_pick_waves(p) == 8 ? launch_prefill_d<DT, 64, 8>(p, st) : launch_prefill_d<DT, 64, 4>(p, st);
         case 128:
             return prefill_pick_waves(p) == 8 ? launch_prefill_d<DT, 128, 8>(p, st) : launch_prefill_d<DT, 128, 4>(p, st);
         case 256: return launch_prefill_d<DT, 256, 4>(p, st);

@@ -3,12 +3,12 @@
 // kv_write_token, inference.rs:1886-1917) on gfx950 MFMA.  Replaces the
 // token-serial attention of the prefill loop (inference.rs:2981-3017, one
 // attention_token per token) for Q8 run states: one launch per chunk, every
-// K / V tile read once per 128 (d128) or 64 (d256) query rows.
+// K / V tile read once per 128 (d64, d128) or 64 (d256) query rows.
 //
 // Workgroup = row groups of 32 query rows of one query head x 2 key halves,
 // wave (row group, half) taking the 32-key sub-tiles 2 j + half of every tile;
-// the two halves' (max, sum, O) merge through LDS at the end.  head_dim 128: 4
-// row groups, 128-key tiles, 8 waves (two per SIMD: the MFMAs of one overlap
+// the two halves' (max, sum, O) merge through LDS at the end.  head_dim 64 and
+// 128: 4 row groups, 128-key tiles, 8 waves (two per SIMD: the MFMAs of one overlap
 // the VALU work of the other).  head_dim 256: 2 row groups, 64-key tiles, 4
 // waves (one per SIMD, for the registers).  The tile goes global -> registers ->
 // LDS (the next tile's loads are in flight while the current one is computed),
@@ -44,14 +44,14 @@ constexpr float kQ8Lazy = 8.0f;   // lazy softmax rescale threshold (log2 units)
 
 // RG row groups of 32 query rows x KH key halves per workgroup (one wave each),
 // BN keys per tile (each wave takes BN / 32 / KH sub-tiles between barriers).
-// d128: 128 rows, 8 waves (two per SIMD).  d256: 64 rows, 4 waves (one per
+// d64 / d128: 128 rows, 8 waves (two per SIMD).  d256: 64 rows, 4 waves (one per
 // SIMD, which its registers need), so that 8-head models still launch one
 // workgroup per CU for a 2048-token chunk.
 template <int D>
 struct Q8Tile {
-    static constexpr int RG = D == 128 ? 4 : 2;
+    static constexpr int RG = D <= 128 ? 4 : 2;
     static constexpr int KH = 2;
-    static constexpr int BN = D == 128 ? 128 : 64;
+    static constexpr int BN = D <= 128 ? 128 : 64;
     static constexpr int BM = 32 * RG;
     static constexpr int NT = 64 * RG * KH;
 };
@@ -99,9 +99,15 @@ __device__ __forceinline__ float q8p_xsum32(float x) {
 // floor(log2 x) for a positive normal float
 __device__ __forceinline__ int q8p_ilog2(float x) { return (int)((__float_as_uint(x) >> 23) & 0xffu) - 127; }
 
-// Position of 16-byte chunk c of tile row r: c ^ q8p_swz(r & 15) (conflict-free
-// K operand reads of 16 rows and V transpose reads of 4 rows x 4 chunks).
-__device__ __forceinline__ int q8p_swz(int r) { return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15; }
+// Position of 16-byte chunk c of tile row r: c ^ q8p_swz<D>(r & 15) (conflict-free
+// K operand reads of 16 rows and V transpose reads of 4 rows x 4 chunks).  A
+// head_dim-64 row is 8 chunks (half the banks): a 3-bit swizzle whose bit 2 is
+// bit 1 of r keeps both read patterns conflict-free.
+template <int D>
+__device__ __forceinline__ int q8p_swz(int r) {
+    if constexpr (D == 64) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else return ((r << 2) ^ (r << 1) ^ (r >> 2)) & 15;
+}
 
 template <int D, bool BLOCK>
 __global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const PrefillQ8Launch p) {
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const Pref
 #pragma unroll
         for (int i = 0; i < KCH; i++) {
             const int c = tid + NT * i;
-            const int r = c / CPR, cc = c % CPR, z = q8p_swz(r & 15);
+            const int r = c / CPR, cc = c % CPR, z = q8p_swz<D>(r & 15);
             uint16_t* kd = Kt + r * D;
             uint16_t* vd = Vt + r * D;
             *(uint4*)(kd + ((2 * cc) ^ z) * 8) = q8p_cvt8(kreg[i].x, kreg[i].y);
@@ -269,9 +275,9 @@ __global__ __launch_bounds__(Q8Tile<D>::NT, 1) void prefill_q8_kernel(const Pref
     for (int b = 0; b < 2; b++) {
         const int r = 8 * b + 4 * lg + (gi >> 2);
         v_base[b] = r * D + (gi & 1) * 4;
-        v_swz[b] = q8p_swz(r & 15);
+        v_swz[b] = q8p_swz<D>(r & 15);
     }
-    const int swz_k = q8p_swz(ln & 15);
+    const int swz_k = q8p_swz<D>(ln & 15);
 
     f32x16 o[NB];
 #pragma unroll
@@ -515,6 +521,7 @@ hipError_t launch_q8_d(const PrefillQ8Launch& p, hipStream_t st) {
 hipError_t launch_prefill_q8(const PrefillQ8Launch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
     switch (p.head_dim) {
+        case 64: return p.block ? launch_q8_d<64, true>(p, st) : launch_q8_d<64, false>(p, st);
         case 128: return p.block ? launch_q8_d<128, true>(p, st) : launch_q8_d<128, false>(p, st);
         case 256: return p.block ? launch_q8_d<256, true>(p, st) : launch_q8_d<256, false>(p, st);
         default: return hipErrorInvalidValue;

@@ -159,7 +159,7 @@ typedef struct gr_prefill_args {
     int32_t base_pos;
     int32_t n_heads;
     int32_t n_kv_heads;   /* n_heads % n_kv_heads == 0 */
-    int32_t head_dim;     /* 128 or 256 */
+    int32_t head_dim;     /* 64, 128 or 256 */
     int32_t dtype;        /* GR_DTYPE_F16 or GR_DTYPE_BF16: q/k/v inputs and cache */
     int32_t window;       /* 0 = global causal, W > 0 = sliding window of W keys */
     int32_t rope_mode;    /* gr_rope_mode; GR_ROPE_ADJACENT needs rope_dim == head_dim */

@@ -245,7 +245,8 @@ def _image_block_case(orc, dev, *, hist, blk, n_heads, n_kv, d, fmt, seed, windo
 
 
 @pytest.mark.parametrize("d,fmt_name,window", [(128, "F16", 0), (128, "BF16", 64),
-                                               (256, "BF16", 96), (256, "F16", 0)])
+                                               (256, "BF16", 96), (256, "F16", 0),
+                                               (64, "F16", 0), (64, "BF16", 64)])
 def test_prefill_image_block_bidirectional(orc, dev, d, fmt_name, window):
     """bidirectional = 1: 150 causal history rows, then a 200-row image block whose rows see
     every block key (later ones included) plus their causal / window history
@@ -294,3 +295,28 @@ def test_bf16_prefill_values_outside_f16_take_the_exact_path(orc, dev, d, which,
     assert np.isfinite(ref).all()
     _assert_close(got, ref)
     _assert_cache(kc, vc, orc.BF16, orc)
+
+
+@pytest.mark.parametrize("fmt_name,window,chunks", [("F16", 0, [100, 200]), ("BF16", 37, [64, 236]),
+                                                   ("F16", 1, [300]), ("BF16", 0, [1, 127, 172])])
+def test_prefill_head_dim_64(orc, dev, fmt_name, window, chunks):
+    """head_dim 64 (the Qwen2-0.5B / SmolLM-class heads of qwen2.rs / smolvlm.rs) on the MFMA
+    flash kernel: 4-wave workgroups over 64-key tiles with the 8-chunk row swizzle, global,
+    window 37 and window 1 layers, chunked continuation, f16 and bf16 caches."""
+    from gguf_runner_amd import ffi
+    fmt = getattr(orc, fmt_name)
+    got, ref, kc, vc = _case(orc, dev, m=300, n_heads=14, n_kv=2, d=64, fmt=fmt, seed=640 + window,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6, window=window, norm=window == 37,
+                             base_chunks=chunks)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, fmt, orc)
+
+
+def test_prefill_head_dim_64_eight_wave_blocks(orc, dev):
+    """A 2048-token head_dim-64 chunk with 64 Q heads launches the 8-wave workgroups
+    (256-row query blocks over 128-key tiles, two workgroups per CU)."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=64, n_kv=8, d=64, fmt=orc.F16, seed=6464,
+                             rope_mode=ffi.ROPE_ADJACENT, theta=1e4)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)

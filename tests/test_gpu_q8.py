@@ -246,15 +246,17 @@ def test_q8_decode_layer_batch_slots(orc, dev, block):
 @pytest.mark.parametrize("block,d,window,image", [
     (False, 128, None, False), (True, 128, 100, False), (False, 256, None, False),
     (True, 256, 37, False), (False, 128, None, True), (True, 128, 60, True),
-    (False, 256, None, True), (True, 256, 60, True)])
+    (False, 256, None, True), (True, 256, 60, True), (False, 64, None, False),
+    (True, 64, 50, False), (False, 64, 70, True), (True, 64, None, True)])
 def test_q8_prefill_chunk_mfma(orc, dev, block, d, window, image):
     """One long gr_prefill_attention_chunk (or gr_prefill_image_block) over a Q8 cache
     after a 40-token history: 300 query rows of the MFMA prefill kernel (d128: 128-row
     query blocks over 128-key tiles; d256: 64-row blocks over 64-key tiles), global or
-    sliding-window layer, row or block scales.  Each output row == the oracle's
-    attention_token over the rows the device wrote, with that row's visible range (1e-5)."""
+    sliding-window layer, row or block scales; d64 as d128 with 8-chunk rows.  Each output
+    row == the oracle's attention_token over the rows the device wrote, with that row's
+    visible range (1e-5)."""
     from gguf_runner_amd import ffi, runtime as rt
-    n_heads, n_kv = (16, 8) if d == 128 else (8, 2)
+    n_heads, n_kv = {64: (12, 4), 128: (16, 8), 256: (8, 2)}[d]
     p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=512,
                   kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE,
                   layer_windows=[window, window])
@@ -284,7 +286,7 @@ def test_q8_prefill_chunk_mfma(orc, dev, block, d, window, image):
     assert worst <= TOL, worst
 
 
-@pytest.mark.parametrize("d", [128, 256])
+@pytest.mark.parametrize("d", [64, 128, 256])
 @pytest.mark.parametrize("block,m,window,hist", [
     (False, 1, None, 7), (True, 31, 1, 0), (False, 33, 5, 90), (True, 97, None, 415)])
 def test_q8_prefill_chunk_edges(orc, dev, block, m, window, hist, d):
@@ -293,7 +295,7 @@ def test_q8_prefill_chunk_edges(orc, dev, block, m, window, hist, d):
     (each row sees only itself, so one key half of a workgroup is empty) and 5, a chunk
     that ends exactly at seq_len (history 415 + 97 = 512)."""
     from gguf_runner_amd import ffi, runtime as rt
-    n_heads, n_kv = (16, 8) if d == 128 else (8, 2)
+    n_heads, n_kv = {64: (12, 4), 128: (16, 8), 256: (8, 2)}[d]
     p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=512,
                   kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE,
                   layer_windows=[window])
