@@ -461,6 +461,22 @@ def run_one(args, dev, stream, lens) -> int:
         call, flops, keep = prefill_workload(dev, S, 8)
         ms, _ = _timed(call, args.steps, args.warmup, stream)
         res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "decode_c1":
+        # config 1: Qwen3-0.6B-shaped single-layer decode, f32 KV, 1024 keys
+        call, nbytes, keep = rotating(
+            lambda sd: decode_workload(dev, [1024], sd, n_heads=16, n_kv=8, kv_dtype=torch.float32), 41)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, gbs=nbytes / (ms * 1e-3) / 1e9, bytes=nbytes)
+    elif args.only == "decode_c4":
+        # config 4: one decode step after the 8192-token prefill, 5 local + 1 global layer
+        for key, (b, e) in (("local", (8193 - 1024, 8193)), ("global", (0, 8193))):
+            call, nbytes, keep = rotating(
+                lambda sd: decode_workload(dev, [e], sd, n_heads=8, n_kv=4, d=256, kv_dtype=torch.bfloat16,
+                                           starts=[b]), 43)
+            ms, _ = _timed(call, args.steps, args.warmup, stream)
+            res[key] = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes}
+            del keep, call
+        res["step_ms"] = 5 * res["local"]["ms"] + res["global"]["ms"]
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -509,7 +525,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
+                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")

@@ -225,8 +225,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(cons
         const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
         const int col = (h / kv_mul) * n_sub + (n_sub > 1 ? (h % kv_mul) / p.sub_heads : 0);
         nv = stream_partials(p, s, col);
-    } else {
-        nv = len > 0 ? (len + p.split_keys - 1) / p.split_keys : 0;
+    } else {  // the splits the grid has (keys past them are dropped, as on the stream schedule)
+        nv = len > 0 ? min(p.n_splits, (len + p.split_keys - 1) / p.split_keys) : 0;
     }
     const size_t base = ((size_t)s * p.n_heads + h) * p.n_splits;
     float* out = p.out + ((size_t)s * p.n_heads + h) * D;
