@@ -25,8 +25,8 @@ int check_encoder(float* out, const float* q, const float* k, const float* v, in
     if (total > INT32_MAX) return fail(GR_ERR_ARG, "encoder attention token count overflow");
     if (total * dim > ((int64_t)1 << 40)) return fail(GR_ERR_ARG, "encoder attention buffer size overflow");
     if (total * dim == 0) return GR_OK;
-    if (head_dim > 128)
-        return fail(GR_ERR_ARG, "gr_encoder_self_attention: head_dim %d unsupported (<= 128)", head_dim);
+    if (head_dim > 256)
+        return fail(GR_ERR_ARG, "gr_encoder_self_attention: head_dim %d unsupported (<= 256)", head_dim);
     if (!out || !q || !k || !v)
         return fail(GR_ERR_ARG, "encoder attention shape mismatch: sequences=%d tokens=%d heads=%d head_dim=%d",
                     n_seq, tokens, heads, head_dim);

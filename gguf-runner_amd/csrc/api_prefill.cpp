@@ -40,6 +40,10 @@ int check_prefill(const gr_prefill_args* a) {
     }
     if ((a->q_norm == nullptr) != (a->k_norm == nullptr))
         return fail(GR_ERR_ARG, "gr_prefill_attention: q_norm and k_norm must be both set or both NULL");
+    if ((a->q_bias == nullptr) != (a->k_bias == nullptr) || (a->q_bias == nullptr) != (a->v_bias == nullptr))
+        return fail(GR_ERR_ARG, "gr_prefill_attention: q_bias, k_bias and v_bias must be all set or all NULL");
+    if (((uintptr_t)a->q_bias | (uintptr_t)a->k_bias | (uintptr_t)a->v_bias) % 16)
+        return fail(GR_ERR_ARG, "gr_prefill_attention: q_bias, k_bias and v_bias must be 16-byte aligned");
     if (((uintptr_t)a->q_norm | (uintptr_t)a->k_norm) % 16)
         return fail(GR_ERR_ARG, "gr_prefill_attention: q_norm and k_norm must be 16-byte aligned");
     if (a->n_tokens > 0 && (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache || !a->out ||
@@ -135,6 +139,9 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
     pp.rope_freqs = a->rope_freqs;
     pp.q_norm = a->q_norm;
     pp.k_norm = a->k_norm;
+    pp.q_bias = a->q_bias;
+    pp.k_bias = a->k_bias;
+    pp.v_bias = a->v_bias;
     pp.eps = a->norm_eps;
     pp.gemma_q_scale = a->is_gemma3;
     pp.q = a->q;
@@ -208,6 +215,7 @@ int prefill_enqueue_ex(const gr_prefill_args* a, int in_dtype, hipStream_t st) {
         pf.q_raw = a->q;
         pf.q_in_dtype = in_dtype;
         pf.q_row_stride = (int64_t)a->n_heads * a->head_dim;
+        pf.q_bias = a->q_bias;
         pf.q_norm = a->q_norm;
         pf.norm_eps = a->norm_eps;
         pf.rope_mode = a->rope_mode;

@@ -9,8 +9,9 @@
 // through LDS in tiles of 32 and every lane reads the same row (broadcast, no
 // bank conflicts).  Per tile: 32 scores in registers, the tile maximum raises
 // the running maximum (O and the sum rescaled), then P = 2^(s - m) and
-// O += P V.  Head dims up to 128; a dim that is not one of the compiled sizes
-// runs zero-padded in the next one (zeros add nothing to dots or outputs).
+// O += P V.  Head dims up to 128 here, up to 256 on the MFMA kernel; a dim that
+// is not one of the compiled sizes runs zero-padded in the next one (zeros add
+// nothing to dots or outputs).
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -118,7 +119,7 @@ typedef float em_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kEmThreads = 256;
 constexpr int kEmBM = 128;         // queries per workgroup
-constexpr int kEmBN = 64;          // keys per tile
+constexpr int kEmBN = 64;          // keys per tile (32 for head dims above 128)
 constexpr int kEmMinTokens = 64;   // shorter sequences take the VALU kernel
 constexpr float kEmLazy = 8.0f;    // log2 units
 
@@ -131,9 +132,11 @@ __device__ __forceinline__ float em_xsum32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Head dims above 128 (DP 192, 256): one wave per SIMD and 32-key tiles (Q
+// operands, O and the tile staging then fit the 512 registers of a lone wave).
 template <int DP>
-__global__ __launch_bounds__(kEmThreads, 2) void encoder_mfma_kernel(const EncoderLaunch p) {
-    constexpr int BN = kEmBN;
+__global__ __launch_bounds__(kEmThreads, (DP <= 128 ? 2 : 1)) void encoder_mfma_kernel(const EncoderLaunch p) {
+    constexpr int BN = DP <= 128 ? kEmBN : 32;
     constexpr int KS = DP / 2;           // k-steps over the head dim
     constexpr int DT = (DP + 31) / 32;   // O^T tiles of 32 dims
     constexpr int DP32 = DT * 32;
@@ -293,13 +296,18 @@ __global__ __launch_bounds__(kEmThreads, 2) void encoder_mfma_kernel(const Encod
 
 template <int DP>
 static hipError_t launch_encoder_dp(const EncoderLaunch& p, hipStream_t st) {
-    if (p.tokens >= kEmMinTokens) {
-        dim3 grid((p.tokens + kEmBM - 1) / kEmBM, p.heads, p.n_seq);
-        encoder_mfma_kernel<DP><<<grid, kEmThreads, 0, st>>>(p);
-    } else {
-        dim3 grid((p.tokens + kEncThreads - 1) / kEncThreads, p.heads, p.n_seq);
-        encoder_attention_kernel<DP><<<grid, kEncThreads, 0, st>>>(p);
+    // head dims above 128 take the MFMA kernel at every length (the VALU kernel's
+    // per-lane query and output rows would not fit its registers); it masks the keys
+    // past a short sequence's end and skips its query rows
+    if constexpr (DP <= 128) {
+        if (p.tokens < kEmMinTokens) {
+            dim3 grid((p.tokens + kEncThreads - 1) / kEncThreads, p.heads, p.n_seq);
+            encoder_attention_kernel<DP><<<grid, kEncThreads, 0, st>>>(p);
+            return hipGetLastError();
+        }
     }
+    dim3 grid((p.tokens + kEmBM - 1) / kEmBM, p.heads, p.n_seq);
+    encoder_mfma_kernel<DP><<<grid, kEmThreads, 0, st>>>(p);
     return hipGetLastError();
 }
 
@@ -311,6 +319,8 @@ hipError_t launch_encoder_attention(const EncoderLaunch& p, hipStream_t st) {
     if (d <= 80) return launch_encoder_dp<80>(p, st);
     if (d <= 96) return launch_encoder_dp<96>(p, st);
     if (d <= 128) return launch_encoder_dp<128>(p, st);
+    if (d <= 192) return launch_encoder_dp<192>(p, st);
+    if (d <= 256) return launch_encoder_dp<256>(p, st);
     return hipErrorInvalidValue;
 }
 

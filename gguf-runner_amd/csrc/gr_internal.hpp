@@ -106,6 +106,11 @@ struct QkvPrepLaunch {
     const float* rope_freqs;
     const float* q_norm;
     const float* k_norm;
+    // Qwen2 biases added to the loaded q / k / v rows before the norm (nullable;
+    // [n_heads*head_dim] / [n_kv_heads*head_dim])
+    const float* q_bias;
+    const float* k_bias;
+    const float* v_bias;
     float eps;
     int gemma_q_scale;
     const void* q;
@@ -269,6 +274,7 @@ struct PrefillLaunch {
     const void* q_raw;
     int q_in_dtype;
     int64_t q_row_stride;
+    const float* q_bias;  // Qwen2 q bias [n_heads][head_dim] added to the raw row, or null
     const float* q_norm;
     float norm_eps;
     int rope_mode, rope_dim;

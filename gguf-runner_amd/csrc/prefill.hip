@@ -181,6 +181,15 @@ __device__ __forceinline__ void pf_prepare_q(const PrefillLaunch& p, int row, in
     const size_t base = (size_t)row * p.q_row_stride + (size_t)h * D + 8 * lg;
 #pragma unroll
     for (int c = 0; c < NC; c++) pf_load8(p.q_raw, base + 16 * c, p.q_in_dtype, x[c]);
+    if (p.q_bias) {  // Qwen2 q bias, before the norm (inference.rs:2545-2559)
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            float bv[8];
+            pf_load8(p.q_bias, (size_t)h * D + 16 * c + 8 * lg, GR_DTYPE_F32, bv);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[c][e] += bv[e];
+        }
+    }
     if (p.q_norm) {
         float ss = 0.0f;
 #pragma unroll

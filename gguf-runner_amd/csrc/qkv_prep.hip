@@ -95,6 +95,14 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
         else
 #pragma unroll
             for (int e = 0; e < 8; e++) x[e] = 0.0f;
+        // Qwen2 attention biases, before the norm (qkv_bias_and_norm, inference.rs:2545-2559)
+        const float* bias = kind == 0 ? p.q_bias : (kind == 1 ? p.k_bias : p.v_bias);
+        if (bias && !skip) {
+            float bv[8];
+            load8(bias, (size_t)head * D + c8, GR_DTYPE_F32, bv);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] += bv[e];
+        }
         if (kind != 2) {
             // QK RMSNorm: ss = sum(x^2)/d + eps; x = w * ((1/sqrt(ss)) * x).
             const float* w = kind == 0 ? p.q_norm : p.k_norm;

@@ -60,6 +60,7 @@ class PrefillArgs(ctypes.Structure):
         ("k_cache", _p), ("v_cache", _p), ("cache_row_stride", _i64), ("out", _p),
         ("workspace", _p), ("bidirectional", _i32),
         ("out_gate", _p), ("out_gate_row_stride", _i64), ("out_gate_head_stride", _i32),
+        ("q_bias", _p), ("k_bias", _p), ("v_bias", _p),
     ]
 
 

@@ -181,7 +181,8 @@ class PrefillCall:
     def __init__(self, q, k, v, k_cache, v_cache, out, *, base_pos=0, window=0,
                  rope_mode=ffi.ROPE_NONE, rope_dim=0, rope_scale=1.0, rope_freqs=None,
                  q_norm=None, k_norm=None, norm_eps=1e-6, is_gemma3=False, bidirectional=False,
-                 out_gate=None, out_gate_row_stride=0, out_gate_head_stride=0):
+                 out_gate=None, out_gate_row_stride=0, out_gate_head_stride=0, q_bias=None, k_bias=None,
+                 v_bias=None):
         m, n_heads, d = q.shape
         _, n_kv, d2 = k.shape
         assert d2 == d and v.shape == k.shape and out.shape == (m, n_heads, d)
@@ -189,7 +190,7 @@ class PrefillCall:
         assert out.dtype == torch.float32
         for t in (q, k, v, k_cache, v_cache, out):
             assert t.is_contiguous()
-        self._keep = (q, k, v, k_cache, v_cache, out, rope_freqs, q_norm, k_norm, out_gate)
+        self._keep = (q, k, v, k_cache, v_cache, out, rope_freqs, q_norm, k_norm, out_gate, q_bias, k_bias, v_bias)
         a = ffi.PrefillArgs()
         a.n_tokens, a.base_pos, a.n_heads, a.n_kv_heads, a.head_dim = m, base_pos, n_heads, n_kv, d
         a.dtype = _DT[q.dtype]
@@ -197,6 +198,7 @@ class PrefillCall:
         a.rope_mode, a.rope_dim, a.rope_scale = int(rope_mode), int(rope_dim), float(rope_scale)
         a.rope_freqs = _ptr(rope_freqs)
         a.q_norm, a.k_norm = _ptr(q_norm), _ptr(k_norm)
+        a.q_bias, a.k_bias, a.v_bias = _ptr(q_bias), _ptr(k_bias), _ptr(v_bias)
         a.norm_eps = float(norm_eps)
         a.is_gemma3 = int(bool(is_gemma3))
         a.bidirectional = int(bool(bidirectional))

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define GR_ATTN_ABI_VERSION 4
+#define GR_ATTN_ABI_VERSION 5
 
 /* Status codes. */
 #define GR_OK 0
@@ -195,6 +195,13 @@ typedef struct gr_prefill_args {
     const float* out_gate;
     int64_t out_gate_row_stride;
     int32_t out_gate_head_stride;
+    /* Qwen2 attention biases (qkv_bias_and_norm, inference.rs:2545-2559): device f32
+     * q_bias [n_heads*head_dim], k_bias and v_bias [n_kv_heads*head_dim] of this layer,
+     * added to every q / k / v row before the QK norm and RoPE.  All three or none
+     * (NULL); 16-byte aligned. */
+    const float* q_bias;
+    const float* k_bias;
+    const float* v_bias;
 } gr_prefill_args;
 
 size_t gr_prefill_workspace_size(const gr_prefill_args* a);
@@ -217,7 +224,7 @@ int gr_rope_freqs(float theta, int32_t rope_dim, float* freqs_out);
  * mod.rs:145-256), the attention of the vision / audio encoders.  q, k, v, out
  * are device f32 rows [n_seq * tokens][heads * head_dim]; each token attends to
  * every token of its own sequence (no mask, no cache), scores scaled by
- * 1/sqrt(head_dim).  head_dim <= 128.  Sizes of 0 are a no-op, like the
+ * 1/sqrt(head_dim).  head_dim <= 256.  Sizes of 0 are a no-op, like the
  * reference's required == 0 case; negative sizes fail with its "encoder
  * attention shape mismatch" message.  Enqueued on `stream`, allocates nothing.
  * ====================================================================== */

@@ -6,7 +6,7 @@
 #![allow(non_camel_case_types, dead_code)]
 use std::ffi::{c_char, c_void};
 
-pub const GR_ATTN_ABI_VERSION: i32 = 4;
+pub const GR_ATTN_ABI_VERSION: i32 = 5;
 
 pub const GR_OK: i32 = 0;
 pub const GR_DTYPE_F32: i32 = 0;
@@ -87,6 +87,9 @@ pub struct GrPrefillArgs {
     pub out_gate: *const f32,
     pub out_gate_row_stride: i64,
     pub out_gate_head_stride: i32,
+    pub q_bias: *const f32,
+    pub k_bias: *const f32,
+    pub v_bias: *const f32,
 }
 
 #[repr(C)]

@@ -27,7 +27,7 @@ def test_no_unexpected_exports(pkg):
 def test_abi_version_and_error_path(pkg):
     from gguf_runner_amd import ffi
     L = ffi.lib()
-    assert L.gr_abi_version() == 4
+    assert L.gr_abi_version() == 5
     a = ffi.DecodeArgs()
     a.n_seq, a.n_heads, a.n_kv_heads, a.head_dim = 1, 6, 4, 128
     rc = L.gr_decode_attention(ctypes.byref(a), None)

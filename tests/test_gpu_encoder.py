@@ -52,10 +52,12 @@ def test_encoder_attention_reference_fixture(orc, dev):
 
 @pytest.mark.parametrize("ns,tps,hc,hd", [(1, 1, 2, 64), (2, 17, 4, 72), (3, 300, 16, 80),
                                           (1, 1025, 16, 64), (2, 256, 8, 128), (1, 100, 3, 20),
-                                          (1, 50, 2, 100)])
+                                          (1, 50, 2, 100), (2, 5, 2, 256), (1, 333, 4, 256),
+                                          (2, 70, 3, 160), (1, 129, 2, 192), (1, 40, 2, 136)])
 def test_encoder_attention_matches_oracle(orc, dev, ns, tps, hc, hd):
-    """Sequences of 1 to 1025 tokens; head dims of the vision encoders (64, 72, 80) and
-    dims that run zero-padded (20 -> 32, 100 -> 128)."""
+    """Sequences of 1 to 1025 tokens; head dims of the vision encoders (64, 72, 80),
+    dims that run zero-padded (20 -> 32, 100 -> 128, 136 / 160 -> 192) and the 192 / 256
+    tilings (one wave per SIMD, 32-key tiles; every length on the MFMA kernel)."""
     rng = np.random.default_rng(ns * 1000 + tps + hd)
     q, k, v = (rng.standard_normal((ns * tps, hc * hd)).astype(np.float32) for _ in range(3))
     shape = dict(n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
@@ -66,16 +68,16 @@ def test_encoder_attention_matches_oracle(orc, dev, ns, tps, hc, hd):
 
 def test_encoder_attention_sizes(dev):
     """A zero size is a no-op (the reference returns Ok for required == 0); negative sizes
-    and head_dim > 128 are errors with a message."""
+    and head_dim > 256 are errors with a message."""
     from gguf_runner_amd import ffi
     L = ffi.lib()
     assert L.gr_encoder_self_attention(None, None, None, None, 0, 5, 2, 64, None) == 0
     assert L.gr_encoder_self_attention(None, None, None, None, -1, 5, 2, 64, None) < 0
     assert b"encoder attention shape mismatch" in ffi.lib().gr_last_error()
-    x = torch.zeros((4, 2 * 160), device=dev)
+    x = torch.zeros((4, 2 * 264), device=dev)
     assert L.gr_encoder_self_attention(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
-                                       1, 4, 2, 160, None) < 0
-    assert b"head_dim 160 unsupported" in ffi.lib().gr_last_error()
+                                       1, 4, 2, 264, None) < 0
+    assert b"head_dim 264 unsupported" in ffi.lib().gr_last_error()
 
 
 def test_encoder_attention_gemma3_siglip_shape(dev):

@@ -31,7 +31,7 @@ def _bits(x, fmt, orc):
 
 def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_scale=1.0,
           window=0, norm=False, is_gemma3=False, base_chunks=None, eps=1e-6, rope_dim=None,
-          attend_rows=None, patch=None):
+          attend_rows=None, patch=None, bias=None):
     from gguf_runner_amd import ffi, ops
     rng = np.random.default_rng(seed)
     qf = rng.standard_normal((m, n_heads, d), dtype=np.float32)
@@ -46,10 +46,13 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
         kn = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     rope_dim = d if rope_dim is None else rope_dim
     freqs = orc.rope_freqs(theta, rope_dim)
-    # oracle (token-serial, raw cache of the same 16-bit format)
+    # oracle (token-serial, raw cache of the same 16-bit format); Qwen2 biases are
+    # f32 additions to the rows before everything else (inference.rs:2545-2559)
+    qo, ko, vo = (orc.upcast(x, fmt).reshape(m, -1) for x in (qb, kb, vb))
+    if bias is not None:
+        qo, ko, vo = qo + bias[0][None, :], ko + bias[1][None, :], vo + bias[2][None, :]
     ref, kc_ref, vc_ref = orc.prefill_layer(
-        orc.upcast(qb, fmt).reshape(m, -1), orc.upcast(kb, fmt).reshape(m, -1),
-        orc.upcast(vb, fmt).reshape(m, -1), n_heads=n_heads, n_kv_heads=n_kv, head_size=d,
+        qo, ko, vo, n_heads=n_heads, n_kv_heads=n_kv, head_size=d,
         seq_len=m, fmt=fmt, rope_dim=(0 if rope_mode == ffi.ROPE_NONE else rope_dim), neox=(rope_mode == ffi.ROPE_NEOX), rope_freqs_tab=freqs,
         rope_scale=rope_scale, is_gemma3=is_gemma3, window=window, q_norm=qn, k_norm=kn, eps=eps,
         n_threads=orc.env_threads(), attend_rows=attend_rows)
@@ -62,6 +65,7 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
     knt = torch.from_numpy(kn).to(dev) if norm else None
     chunks = base_chunks or [m]
     out = torch.empty((m, n_heads, d), dtype=torch.float32, device=dev)
+    bt = [torch.from_numpy(x).to(dev) for x in bias] if bias is not None else [None] * 3
     b = 0
     for c in chunks:
         ops.PrefillCall(q[b:b + c].contiguous(), k[b:b + c].contiguous(), v[b:b + c].contiguous(),
@@ -69,7 +73,7 @@ def _case(orc, dev, *, m, n_heads, n_kv, d, fmt, seed, rope_mode, theta, rope_sc
                                                         device=dev),
                         base_pos=b, window=window, rope_mode=rope_mode, rope_dim=rope_dim,
                         rope_scale=rope_scale, rope_freqs=fr, q_norm=qnt, k_norm=knt,
-                        norm_eps=eps, is_gemma3=is_gemma3)()
+                        norm_eps=eps, is_gemma3=is_gemma3, q_bias=bt[0], k_bias=bt[1], v_bias=bt[2])()
         out[b:b + c] = out_view
         b += c
     torch.cuda.synchronize()
@@ -320,3 +324,18 @@ def test_prefill_head_dim_64_eight_wave_blocks(orc, dev):
                              rope_mode=ffi.ROPE_ADJACENT, theta=1e4)
     _assert_close(got, ref)
     _assert_cache(kc, vc, orc.F16, orc)
+
+
+@pytest.mark.parametrize("d,n_heads,n_kv,fmt_name", [(64, 14, 2, "BF16"), (128, 28, 4, "F16"), (128, 8, 2, "BF16")])
+def test_prefill_qwen2_attention_biases(orc, dev, d, n_heads, n_kv, fmt_name):
+    """Qwen2 q / k / v biases (qkv_bias_and_norm, inference.rs:2545-2559) added on the
+    device before RoPE: head_dim 64 (Qwen2-0.5B) through the staging pass, head_dim 128
+    (Qwen2-7B) with Q prepared inside the attention kernel, in two chunks."""
+    from gguf_runner_amd import ffi
+    rng = np.random.default_rng(2545 + d + n_heads)
+    bias = tuple((0.5 * rng.standard_normal(h * d)).astype(np.float32) for h in (n_heads, n_kv, n_kv))
+    fmt = getattr(orc, fmt_name)
+    got, ref, kc, vc = _case(orc, dev, m=260, n_heads=n_heads, n_kv=n_kv, d=d, fmt=fmt, seed=d + n_kv,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6, base_chunks=[100, 160], bias=bias)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, fmt, orc)
