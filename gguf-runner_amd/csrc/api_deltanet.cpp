@@ -9,16 +9,19 @@ namespace gr {
 
 namespace {
 
+// The chunked kernels are built for state size 128; other sizes run the token
+// recurrence whatever the algorithm asked for (the same results to fp32 rounding).
 bool use_chunked(const gr_deltanet_args* a) {
-    return a->algo == GR_DELTANET_CHUNKED || (a->algo == GR_DELTANET_AUTO && a->n_tokens >= 64);
+    return a->head_dim == 128 &&
+           (a->algo == GR_DELTANET_CHUNKED || (a->algo == GR_DELTANET_AUTO && a->n_tokens >= 64));
 }
 
 int check_deltanet(const gr_deltanet_args* a) {
     if (!a) return fail(GR_ERR_ARG, "gr_deltanet_attention: null args");
     if (a->n_tokens < 0 || a->n_heads <= 0)
         return fail(GR_ERR_ARG, "gr_deltanet_attention: n_tokens >= 0 and n_heads > 0 required");
-    if (a->head_dim != 128)
-        return fail(GR_ERR_ARG, "gr_deltanet_attention: head_dim %d unsupported (128)", a->head_dim);
+    if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+        return fail(GR_ERR_ARG, "gr_deltanet_attention: head_dim %d unsupported (64, 128, 256)", a->head_dim);
     if (a->in_dtype < GR_DTYPE_F32 || a->in_dtype > GR_DTYPE_BF16)
         return fail(GR_ERR_ARG, "gr_deltanet_attention: bad in_dtype %d", a->in_dtype);
     if (a->algo < GR_DELTANET_AUTO || a->algo > GR_DELTANET_CHUNKED)

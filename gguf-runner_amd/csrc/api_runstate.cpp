@@ -233,8 +233,9 @@ int validate_config(const gr_attn_config* c) {
         return fail(GR_ERR_ARG, "rope_theta must be finite and positive");
     if ((c->q_norm == nullptr) != (c->k_norm == nullptr))
         return fail(GR_ERR_ARG, "q_norm and k_norm must be both set or both NULL");
-    if (c->ssm_n_heads < 0 || (c->ssm_n_heads > 0 && c->ssm_head_dim != 128))
-        return fail(GR_ERR_ARG, "DeltaNet state needs ssm_head_dim 128");
+    if (c->ssm_n_heads < 0 ||
+        (c->ssm_n_heads > 0 && c->ssm_head_dim != 64 && c->ssm_head_dim != 128 && c->ssm_head_dim != 256))
+        return fail(GR_ERR_ARG, "DeltaNet state needs ssm_head_dim 64, 128 or 256");
     // One SSM state and conv history per layer, as one reference RunState holds:
     // the SSM entry points and the prefill-cache sections take no sequence slot.
     if (c->ssm_n_heads > 0 && c->n_seq != 1)

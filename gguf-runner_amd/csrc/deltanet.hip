@@ -857,13 +857,19 @@ size_t deltanet_chunked_ws_bytes(int n_tokens, int n_heads, int head_dim, int ch
     return dn_ws_head(n_heads) + n_chunks * n_heads * kTpBytes;
 }
 
+// The token recurrence at any supported state size (64, 128, 256: 32 value
+// columns per workgroup, D / 8 state rows per thread).
 hipError_t launch_deltanet_scan(const DeltaNetLaunch& p, hipStream_t st) {
     if (p.n_tokens <= 0) return hipSuccess;
-    if (p.head_dim != 128) return hipErrorInvalidValue;
     DeltaNetLaunch q = p;
     q.first_bad = nullptr;
-    dim3 grid(128 / kStepCols, p.n_heads);
-    deltanet_step_kernel<128><<<grid, kStepThreads, 0, st>>>(q);
+    const dim3 grid(p.head_dim / kStepCols, p.n_heads);
+    switch (p.head_dim) {
+        case 64: deltanet_step_kernel<64><<<grid, kStepThreads, 0, st>>>(q); break;
+        case 128: deltanet_step_kernel<128><<<grid, kStepThreads, 0, st>>>(q); break;
+        case 256: deltanet_step_kernel<256><<<grid, kStepThreads, 0, st>>>(q); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

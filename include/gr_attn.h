@@ -254,7 +254,8 @@ typedef enum gr_deltanet_algo {
 typedef struct gr_deltanet_args {
     int32_t n_tokens;     /* T */
     int32_t n_heads;      /* value heads H */
-    int32_t head_dim;     /* 128 */
+    int32_t head_dim;     /* state size d: 64, 128 or 256 (the chunked algorithm at 128;
+                           * other sizes run the token recurrence) */
     int32_t in_dtype;     /* gr_dtype of q/k/v */
     int32_t l2norm;       /* 1: fuse the q/k normalisation above */
     int32_t algo;         /* gr_deltanet_algo */
@@ -308,7 +309,7 @@ typedef struct gr_attn_config {
     const float* k_norm;        /* host [n_layers][head_dim], or NULL */
     const uint8_t* qk_norm_present; /* host [n_layers] or NULL (= every layer when q_norm is set) */
     int32_t ssm_n_heads;        /* DeltaNet value heads, 0 = no SSM state */
-    int32_t ssm_head_dim;       /* 128 */
+    int32_t ssm_head_dim;       /* 64, 128 or 256 (ssm_state_size) */
     int32_t q8_block_scales;    /* Q8 cache: 1 = one scale per 32 elements (GGUF_Q8_BLOCK_SCALES,
                                  * inference.rs:1883), 0 = one scale per row */
     /* Qwen3.5 SSM layer weights for gr_qwen3next_ssm_layer (NULL when unused),

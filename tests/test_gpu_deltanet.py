@@ -151,3 +151,15 @@ def test_deltanet_16bit_inputs_chunked(orc, dev, fmt, l2norm):
     got, S = out.cpu().numpy(), st.cpu().numpy()
     assert float(np.abs(got - ref).max()) <= TOL, np.abs(got - ref).max()
     assert float(np.abs(S - Sref).max()) <= TOL, np.abs(S - Sref).max()
+
+
+@pytest.mark.parametrize("d,algo,fmt_name", [(64, 1, "F32"), (64, 0, "BF16"), (256, 1, "F32"), (256, 2, "F16")])
+def test_deltanet_state_sizes_64_and_256(orc, dev, d, algo, fmt_name):
+    """State sizes other than 128 (the reference takes any ssm_state_size, math.rs:566):
+    the token recurrence at d = 64 and 256, also when the chunked or automatic algorithm
+    is asked for (the chunked kernels are built for 128), in two calls that carry the
+    state."""
+    fmt = getattr(orc, fmt_name)
+    got, ref, S, Sref = _run(orc, dev, 150, 3, d, 900 + d + algo, fmt, algo, chunks=[70, 80])
+    assert float(np.abs(got - ref).max()) <= TOL
+    assert float(np.abs(S - Sref).max()) <= TOL

@@ -34,13 +34,15 @@ def _weights(rng, n_layers, nk, nv, d, K):
         ssm_norm=(1 + 0.1 * rng.standard_normal((n_layers, d))).astype(np.float32))
 
 
-@pytest.mark.parametrize("nk,fused,chunks", [(8, True, (300, 37)), (16, False, (37, 130))])
-def test_qwen3next_ssm_layer_matches_token_loop(orc, dev, nk, fused, chunks):
+@pytest.mark.parametrize("nk,fused,chunks,d", [(8, True, (300, 37), 128), (16, False, (37, 130), 128),
+                                                (4, True, (90, 20), 64), (2, False, (70, 3), 256)])
+def test_qwen3next_ssm_layer_matches_token_loop(orc, dev, nk, fused, chunks, d):
     """Config-5 shape (16 value heads, d128, conv kernel 4): two consecutive calls
-    (chunked and recurrent DeltaNet paths) carry the conv history and the state."""
+    (chunked and recurrent DeltaNet paths) carry the conv history and the state; state
+    sizes 64 and 256 (ssm_state_size, math.rs:566) on the token recurrence."""
     from gguf_runner_amd import runtime as rt
-    rng = np.random.default_rng(500 + nk)
-    nv, d, K, layer, eps = 16, 128, 4, 1, 1e-6
+    rng = np.random.default_rng(500 + nk + d)
+    nv, K, layer, eps = 16, 4, 1, 1e-6
     W = _weights(rng, 2, nk, nv, d, K)
     p = rt.Config(n_layers=2, n_heads=2, n_kv_heads=1, head_dim=128, seq_len=16, ssm_n_heads=nv,
                   ssm_head_dim=d, ssm_n_k_heads=nk, ssm_conv_kernel=K, rms_norm_eps=eps, **W)
