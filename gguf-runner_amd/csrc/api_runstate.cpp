@@ -17,16 +17,13 @@
 namespace gr {
 
 int h2d(gr_run_state* s, void* dst, const void* src, size_t bytes) {
-    if (!bytes) return GR_OK;
-    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s->stream);
+    hipError_t e = xfer_h2d(s->xfer, s->stream, dst, src, bytes);
     return e == hipSuccess ? GR_OK : hip_fail(e, "host to device copy");
 }
 
 int d2h_sync(gr_run_state* s, void* dst, const void* src, size_t bytes) {
-    hipError_t e = bytes ? hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s->stream) : hipSuccess;
-    if (e != hipSuccess) return hip_fail(e, "device to host copy");
-    e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? GR_OK : hip_fail(e, "stream synchronize");
+    hipError_t e = xfer_d2h(s->xfer, s->stream, dst, src, bytes);
+    return e == hipSuccess ? GR_OK : hip_fail(e, "device to host copy");
 }
 
 namespace {
@@ -393,6 +390,7 @@ void gr_free_run_state(gr_run_state* s) {
                     (void*)s->ssm_a, (void*)s->ssm_dt, (void*)s->ssm_nw, (void*)s->ssm_hist, (void*)s->freqs,
                     (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn, (void*)s->ssm, s->stage})
         if (p) (void)hipFree(p);
+    xfer_release(s->xfer);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
 }

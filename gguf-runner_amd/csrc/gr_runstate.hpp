@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "gr_attn.h"
+#include "host_xfer.hpp"
 
 struct gr_run_state {
     gr_attn_config cfg{};
@@ -50,6 +51,7 @@ struct gr_run_state {
     float* ssm_hist = nullptr;    // [n_layers][K-1][conv_dim]
     void* stage = nullptr;
     size_t stage_bytes = 0;
+    gr::HostXfer xfer;  // pinned ring for the host rows of each call
 };
 
 namespace gr {

@@ -161,29 +161,39 @@ def attention_layer_token(p: Config, s: RunState, l: int, pos: int, seq: int = 0
                                                  _p(s.v), _p(s.xb)))
 
 
+def _out_rows(out, m: int, width: int) -> np.ndarray:
+    """The output rows: `out` when given (a reused [m][width] f32 buffer, like the
+    reference's run-state xb), else a new zeroed array."""
+    if out is None:
+        return np.zeros((m, width), np.float32)
+    if out.dtype != np.float32 or out.shape != (m, width) or not out.flags.c_contiguous:
+        raise ValueError(f"out must be a C-contiguous float32 array of shape {(m, width)}")
+    return out
+
+
 def prefill_attention_chunk(p: Config, s: RunState, l: int, base_pos: int, q, k, v,
-                            seq: int = 0) -> np.ndarray:
+                            seq: int = 0, out=None) -> np.ndarray:
     """The attention loop of transformer_prefill_batch (inference.rs:2981-3017) for
     rows q [m][q_dim], k/v [m][kv_dim]; returns xb rows [m][q_dim]."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
     m = q.shape[0]
-    xb = np.zeros((m, p.q_dim), np.float32)
+    xb = _out_rows(out, m, p.q_dim)
     ffi.check(ffi.lib().gr_prefill_attention_chunk(s.handle, seq, l, base_pos, m, _p(q), _p(k),
                                                    _p(v), _p(xb)))
     return xb
 
 
 def prefill_image_block(p: Config, s: RunState, l: int, base_pos: int, q, k, v,
-                        seq: int = 0) -> np.ndarray:
+                        seq: int = 0, out=None) -> np.ndarray:
     """The attention of transformer_prefill_image_block (media_prefill.rs:15-124) for
     one complete bidirectional image block at base_pos..base_pos+m-1; returns xb rows."""
     q = np.ascontiguousarray(q, np.float32)
     k = np.ascontiguousarray(k, np.float32)
     v = np.ascontiguousarray(v, np.float32)
     m = q.shape[0]
-    xb = np.zeros((m, p.q_dim), np.float32)
+    xb = _out_rows(out, m, p.q_dim)
     ffi.check(ffi.lib().gr_prefill_image_block(s.handle, seq, l, base_pos, m, _p(q), _p(k),
                                                _p(v), _p(xb)))
     return xb

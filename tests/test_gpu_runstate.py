@@ -277,3 +277,36 @@ def test_prefill_image_block_outside_context_is_rejected(dev):
     zk = np.zeros((10, p.kv_dim), np.float32)
     with pytest.raises(ffi.GrError, match="image-block prefill must evaluate one complete"):
         rt.prefill_image_block(p, s, 0, 60, z, zk, zk)
+
+
+def test_large_host_rows_through_the_pinned_ring(dev):
+    """Host rows above the staging threshold travel through the run state's pinned
+    ring (several 8 MB slots, a partial last slot, uploads after downloads): one
+    2600-row chunk over an f32 cache, twice with new rows into the same output
+    buffer; the K / V rows read back bit-exact and sampled output rows against a
+    float64 restatement of the causal softmax within 1e-5."""
+    from gguf_runner_amd import ffi, runtime as rt
+    m, H, G, d = 2600, 16, 8, 128
+    p = rt.Config(n_layers=1, n_heads=H, n_kv_heads=G, head_dim=d, seq_len=m,
+                  kv_dtype=ffi.DTYPE_F32, rope_mode=ffi.ROPE_NONE)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(77)
+    xb = np.zeros((m, p.q_dim), np.float32)
+    for rep in range(2):
+        q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+        k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+        v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+        got = rt.prefill_attention_chunk(p, s, 0, 0, q, k, v, out=xb)
+        assert got is xb
+        kd, vd = rt.read_kv_rows(p, s, 0, 0, m)
+        assert np.array_equal(kd, k) and np.array_equal(vd, v), rep
+        for t in (0, 1, 1000, 2047, 2048, m - 1):
+            for h in range(H):
+                g = h // (H // G)
+                kk = k[:t + 1, g * d:(g + 1) * d].astype(np.float64)
+                vv = v[:t + 1, g * d:(g + 1) * d].astype(np.float64)
+                sc = kk @ q[t, h * d:(h + 1) * d].astype(np.float64) / math.sqrt(d)
+                w = np.exp(sc - sc.max())
+                ref = (w / w.sum()) @ vv
+                err = np.abs(xb[t, h * d:(h + 1) * d] - ref).max()
+                assert err <= TOL_F32, (rep, t, h, err)
