@@ -138,7 +138,11 @@ int gr_decode_attention(const gr_decode_args* a, void* stream);
  * whose gr_decode_workspace_size exceeds the maximum fail with GR_ERR_ARG
  * before any launch.  Allocates nothing.  Every call on one GPU uses the same
  * array: calls that overlap on one GPU (other streams or threads) race, so
- * serialise them. */
+ * serialise them.  The first call of each head shape and cache type on a device
+ * also resolves the array's address and the kernels' occupancy (host-side
+ * queries): make it before a graph capture; captured calls then record kernel
+ * nodes only, and a replay reads q, the cache and kv_start / kv_end as they are
+ * at replay time (kv_end at most the max_kv_len the capture was made with). */
 #define GR_DECODE_NOALLOC_MAX_WORKSPACE (64u << 20)
 int gr_decode_attention_noalloc(const gr_decode_args* a, void* stream);
 

@@ -129,3 +129,44 @@ def test_noalloc_rejects_oversize_before_launch(dev):
     assert b"built-in scratch" in ffi.lib().gr_last_error()
     torch.cuda.synchronize()
     assert float(out.abs().max()) == 0.0
+
+
+def test_noalloc_decode_replays_under_graph_capture(dev):
+    """The first no-alloc call on a device resolves the scratch address and the launch
+    occupancy (host queries, outside any capture); after it the call records into a
+    HIP graph as kernel nodes only.  Each replay, with new kv_end contents written
+    between replays and eager work and synchronisations around them, matches
+    gr_decode_attention on the same contents (Q8 cache: the 1e-5 bar)."""
+    import torch
+    from gguf_runner_amd import ffi, ops
+    rng = np.random.default_rng(99)
+    lens = [3000, 17, 1200, 4096]
+    call, out_ref, out_na, keep = _case(torch, dev, rng, 4, 32, 4, 128, lens, torch.int8)
+    kv_end = keep[6]
+    _run_noalloc(call, out_na)  # first call on the device: before the capture
+    torch.cuda.synchronize()
+    a = ffi.DecodeArgs.from_buffer_copy(call.args)
+    a.workspace = None
+    a.out = out_na.data_ptr()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=s):
+        ffi.check(ffi.lib().gr_decode_attention_noalloc(ctypes.byref(a), ops._stream(s)))
+    torch.cuda.synchronize()
+    for i, ends in enumerate(([3000, 17, 1200, 4096], [5, 4096, 1, 2000], [4096] * 4)):
+        print(f"graph replay {i}: kv_end {ends}", flush=True)
+        kv_end.copy_(torch.tensor(ends, dtype=torch.int32))
+        out_na.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out_na.cpu().numpy()
+        out_ref.fill_(float("nan"))
+        call()
+        torch.cuda.synchronize()
+        ref = out_ref.cpu().numpy()
+        assert np.isfinite(ref).all() and np.isfinite(got).all()
+        err = float(np.abs(got - ref).max())
+        print(f"  max |replay - workspace| {err:.3e}", flush=True)
+        assert err <= 1e-5
