@@ -164,7 +164,11 @@ typedef struct gr_prefill_args {
     int32_t n_heads;
     int32_t n_kv_heads;   /* n_heads % n_kv_heads == 0 */
     int32_t head_dim;     /* 64, 128 or 256 */
-    int32_t dtype;        /* GR_DTYPE_F16 or GR_DTYPE_BF16: q/k/v inputs and cache */
+    int32_t dtype;        /* GR_DTYPE_F16 or GR_DTYPE_BF16: q/k/v inputs and cache.  The
+                           * prepared queries are staged as f16 for both, so
+                           * |q * score_scale * log2(e)| must stay below 65504; a bf16
+                           * cache is read through exact f16 copies of its rows (in
+                           * the workspace) unless a K / V value is beyond f16's range */
     int32_t window;       /* 0 = global causal, W > 0 = sliding window of W keys */
     int32_t rope_mode;    /* gr_rope_mode; GR_ROPE_ADJACENT needs rope_dim == head_dim */
     int32_t rope_dim;     /* rotated dims per head, even, <= head_dim */
