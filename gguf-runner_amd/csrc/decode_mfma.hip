@@ -135,16 +135,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t md_rsrc(const void* p) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)(((uint64_t)hi << 32) | lo), 0, (int)0xffffffff,
                                              0x00020000);
 }
+// soff is wave-uniform at every call site (whole-tile or tail offsets of a
+// wave-uniform tile); readfirstlane states it, so that a value the compiler
+// cannot prove uniform is not turned into a loop over its distinct values
+// around the load.
 __device__ __forceinline__ uint2 md_ld8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, __builtin_amdgcn_readfirstlane(soff), 0);
     return make_uint2(v[0], v[1]);
 }
 __device__ __forceinline__ uint4 md_ld16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, __builtin_amdgcn_readfirstlane(soff), 0);
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ float md_ldf(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, __builtin_amdgcn_readfirstlane(soff), 0));
 }
 
 // Waves per workgroup: 8 (one workgroup per CU, two waves per SIMD) where the
@@ -215,7 +219,8 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
     const int n_cols = p.n_kv_heads * n_sub;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int l16 = lane & 15, g4 = lane >> 4;
 
     // Segment = keys [t_begin, t_stop) of sequence s, column g (KV head g / n_sub); its partial
@@ -253,6 +258,10 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
         g = cur.col;
         __syncthreads();  // the previous segment is done with the LDS
     }
+    // The segment bounds are wave-uniform; in SGPRs the whole-tile / tail choices
+    // on them stay scalar branches instead of per-lane selects of load offsets.
+    t_begin = __builtin_amdgcn_readfirstlane(t_begin);
+    t_stop = __builtin_amdgcn_readfirstlane(t_stop);
     const int kvh = g / n_sub;                                     // KV head
     const int h0 = kvh * kv_mul + (g % n_sub) * 16;                // first query head
     const int nq = min(16, kvh * kv_mul + kv_mul - h0);            // query heads (MFMA columns)

@@ -468,10 +468,10 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
     const __amdgpu_buffer_rsrc_t ksh = buf_rsrc((const uint8_t*)p.k_sign + e0 / 8);
     const __amdgpu_buffer_rsrc_t vsh = buf_rsrc((const uint8_t*)p.v_sign + e0 / 8);
     const int64_t a0 = (int64_t)slot * p.scale_seq_stride + g;
-    const __amdgpu_buffer_rsrc_t ksig = buf_rsrc(p.k_scale + a0);
-    const __amdgpu_buffer_rsrc_t kgam = buf_rsrc(p.k_rnorm + a0);
-    const __amdgpu_buffer_rsrc_t vsig = buf_rsrc(p.v_scale + a0);
-    const __amdgpu_buffer_rsrc_t vgam = buf_rsrc(p.v_rnorm + a0);
+    const float* ksig_p = p.k_scale + a0;
+    const float* kgam_p = p.k_rnorm + a0;
+    const float* vsig_p = p.v_scale + a0;
+    const float* vgam_p = p.v_rnorm + a0;
     const uint32_t rsc = (uint32_t)(p.row_stride / 4), rss = (uint32_t)(p.row_stride / 8);
     const uint32_t ars = (uint32_t)p.scale_row_stride;
     const float rfac = sqrtf(tq::kFracPi2 / (float)D);
@@ -525,14 +525,12 @@ __global__ __launch_bounds__(kTsThreads, (D <= 128 ? 2 : 1)) void turbo_split_ke
             load_dwords<VSD>(vsh, (int)(key * rss + 4 * VSD * half), vsw);
         }
         {
-            const int off = (int)((uint32_t)min(t0 + (lane & 31), t_stop - 1) * ars * 4);
-            if (lane < 32) {
-                xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ksig, off, 0, 0));
-                xg = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(kgam, off, 0, 0));
-            } else {
-                xs = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vsig, off, 0, 0));
-                xg = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vgam, off, 0, 0));
-            }
+            // lanes 0..31: K sigma / gamma, 32..63: V; plain loads through a
+            // per-lane pointer (a per-lane choice of buffer descriptor would
+            // become a loop over the two descriptors around each load)
+            const size_t off = (size_t)min(t0 + (lane & 31), t_stop - 1) * ars;
+            xs = (lane < 32 ? ksig_p : vsig_p)[off];
+            xg = (lane < 32 ? kgam_p : vgam_p)[off];
         }
     };
 
