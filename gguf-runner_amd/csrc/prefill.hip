@@ -6,7 +6,10 @@
 // (LanguageAttentionPolicy::visible_keys, attention.rs:74-96).
 //
 // Workgroup = NW waves x 32 query rows of one query head (NW = 8 for large
-// launches, 4 for small ones).  K and V tiles of BN keys go from the cache
+// launches, 4 for small ones), or, with KH = 2 key halves (d64 launches of at
+// most one four-wave workgroup per CU), NW / 2 row groups of two waves that
+// take alternate 32-key sub-tiles of every tile and merge their online-softmax
+// states at the end.  K and V tiles of BN keys go from the cache
 // straight into LDS (buffer_load ... lds, no register staging), both row-major
 // with their 16-byte chunks XOR-swizzled per row so that every LDS read below
 // is free of bank conflicts.  Each wave computes
@@ -93,8 +96,10 @@ __device__ __forceinline__ int pf_swz(int r) {
 
 // Workgroup = NW waves of 32 query rows each.  Large launches use 8 waves
 // (256 query rows share every K / V tile, one workgroup per CU), small ones 4
-// waves (twice the workgroups, so short prompts still fill the GPU).
-template <int D, int NW>
+// waves (twice the workgroups, so short prompts still fill the GPU), or, at d64,
+// 8 waves as 4 row groups x 2 key halves (KH = 2: the four-wave kernel's
+// workgroups with twice the waves).
+template <int D, int NW, int KH = 1>
 struct PfTile;
 template <>
 struct PfTile<128, 8> {
@@ -115,6 +120,11 @@ template <>
 struct PfTile<64, 4> {
     static constexpr int BN = 64;
     static constexpr int kWaves = 4;    // four workgroups per CU
+};
+template <>
+struct PfTile<64, 8, 2> {
+    static constexpr int BN = 128;      // 4 sub-tiles, two per key half
+    static constexpr int kWaves = 4;    // two workgroups per CU
 };
 template <>
 struct PfTile<256, 4> {
@@ -251,12 +261,14 @@ __device__ __forceinline__ void pf_prepare_q(const PrefillLaunch& p, int row, in
 // double-buffered tiles (BN * D each) and Qlo the bf16 d256 Q residuals, all in
 // LDS and declared by the kernel (distinct arrays, so the compiler sees that the
 // DMA into one buffer never aliases the reads of another).
-template <typename DT, int D, int NW>
+template <typename DT, int D, int NW, int KH = 1>
 __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void* k_cache, const void* v_cache,
                                              const int64_t rs, const int64_t row0, uint16_t* Ks0, uint16_t* Ks1,
                                              uint16_t* Vs0, uint16_t* Vs1, uint4* Qlo) {
     constexpr int kPfThreads = NW * 64;
-    constexpr int BM = NW * 32, BN = PfTile<D, NW>::BN;
+    constexpr int RW = NW / KH;                 // row groups of 32 query rows
+    constexpr int BM = RW * 32, BN = PfTile<D, NW, KH>::BN;
+    static_assert(KH == 1 || (KH == 2 && D <= 128 && BN / 32 % 2 == 0), "key halves: d <= 128, even sub-tiles");
     constexpr int CPR = D / 8;                   // 16-byte chunks per cache row
     constexpr int LD = BN * CPR / kPfThreads;    // DMA chunks per thread per K (or V) tile
     constexpr int RPU = kPfThreads / CPR;        // tile rows filled by one DMA round
@@ -275,6 +287,7 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int rw = KH > 1 ? wave % RW : wave, kh = KH > 1 ? wave / RW : 0;  // row group, key half
     const int ln = lane & 31, lg = lane >> 5;
     const int m = p.n_tokens;
     const int P0 = (int)p.base_pos;
@@ -331,7 +344,7 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
         if (pass == 1 && qblk >= n_qb - 1 - j) break;
 
         const int q0 = qblk * BM;
-        const int wr0 = q0 + wave * 32;
+        const int wr0 = q0 + rw * 32;
         const int my_row = wr0 + ln;
         const bool row_ok = my_row < m;
         const int my_row_c = row_ok ? my_row : m - 1;
@@ -595,6 +608,7 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
 #pragma unroll
             for (int sb = 0; sb < BN / 32; sb++) {
                 const int ts = t0 + 32 * sb;
+                if (KH > 1 && sb % KH != kh) continue;  // the other key half's sub-tile
                 if (!(wave_active && ts <= hi_max && ts + 31 >= lo_min)) continue;
                 subtile(kb, vb, sb, ts);
             }
@@ -615,9 +629,40 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
             compute_tile(Ks1, Vs1, t0 + BN);
         }
 
+        if constexpr (KH > 1) {
+            // Key half 1 hands (O, m, l) of its rows to key half 0 through the tile
+            // buffers, free once every wave is past its last tile.  Both halves'
+            // O and l are relative to their own reference maxima m (the row's
+            // m_off of the folded S^T start is m once the row has seen a key,
+            // and O = l = 0 before), so O = O0 2^(m0 - M) + O1 2^(m1 - M), M = max.
+            constexpr int NO = D / 32 * 16;
+            static_assert(2 * NO * 64 * 4 <= BN * D * 2 && RW * 2 * 64 * 4 <= BN * D * 2, "merge buffers");
+            float* ob = (float*)(rw < 2 ? Ks0 : Ks1) + (size_t)(rw & 1) * NO * 64;
+            float* mlb = (float*)Vs0 + (size_t)rw * 2 * 64;
+            __syncthreads();
+            if (kh == 1) {
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) ob[(dt * 16 + e) * 64 + lane] = o[dt][e];
+                mlb[lane] = mrow;
+                mlb[64 + lane] = lrow;
+            }
+            __syncthreads();
+            if (kh == 0) {
+                const float m1 = mlb[lane], l1 = mlb[64 + lane];
+                const float mm = fmaxf(mrow, m1);
+                const float a0 = __builtin_amdgcn_exp2f(mrow - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+                lrow = lrow * a0 + l1 * a1;
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) o[dt][e] = o[dt][e] * a0 + ob[(dt * 16 + e) * 64 + lane] * a1;
+            }
+        }
         const float lsum = pf_xsum32(lrow);
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-        if (row_ok) {
+        if (row_ok && kh == 0) {
             float* orow = p.out + ((size_t)my_row * p.n_heads + h) * D;
             const float* gt = p.gate.at(my_row, h);  // Qwen3.5 output gate, or null
 #pragma unroll
@@ -644,57 +689,71 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
 
 // The LDS of one workgroup: double-buffered K and V tiles (four distinct
 // arrays) and, with QLO, the bf16 d256 Q residual fragments.
-#define GR_PF_LDS(D, NW, QLO)                                                          \
-    __shared__ __attribute__((aligned(16))) uint16_t Ks0[PfTile<D, NW>::BN * D];    \
-    __shared__ __attribute__((aligned(16))) uint16_t Ks1[PfTile<D, NW>::BN * D];    \
-    __shared__ __attribute__((aligned(16))) uint16_t Vs0[PfTile<D, NW>::BN * D];    \
-    __shared__ __attribute__((aligned(16))) uint16_t Vs1[PfTile<D, NW>::BN * D];    \
+#define GR_PF_LDS(D, NW, KH, QLO)                                                      \
+    __shared__ __attribute__((aligned(16))) uint16_t Ks0[PfTile<D, NW, KH>::BN * D];  \
+    __shared__ __attribute__((aligned(16))) uint16_t Ks1[PfTile<D, NW, KH>::BN * D];  \
+    __shared__ __attribute__((aligned(16))) uint16_t Vs0[PfTile<D, NW, KH>::BN * D];  \
+    __shared__ __attribute__((aligned(16))) uint16_t Vs1[PfTile<D, NW, KH>::BN * D];  \
     __shared__ __attribute__((aligned(16))) uint4 Qlo[(QLO) ? NW * (D / 16) * 64 : 1]
 
-template <typename DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kWaves)) void prefill_kernel(const PrefillLaunch p) {
-    GR_PF_LDS(D, NW, Mfma32<DT>::kSplit && D == 256);
-    prefill_body<DT, D, NW>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
+template <typename DT, int D, int NW, int KH>
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW, KH>::kWaves)) void prefill_kernel(const PrefillLaunch p) {
+    GR_PF_LDS(D, NW, KH, Mfma32<DT>::kSplit && D == 256);
+    prefill_body<DT, D, NW, KH>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
 }
 
 // bf16 cache with an exact f16 copy of its visible rows: the single-pass f16
 // path on the copy, or, when the copy could not hold every value (the flag
 // carries this launch's epoch), the bf16 hi + lo path on the cache itself.
-template <int D, int NW>
-__global__ __launch_bounds__(NW * 64, (PfTile<D, NW>::kWaves)) void prefill_bf16x_kernel(const PrefillLaunch p) {
-    GR_PF_LDS(D, NW, D == 256);
+template <int D, int NW, int KH>
+__global__ __launch_bounds__(NW * 64, (PfTile<D, NW, KH>::kWaves)) void prefill_bf16x_kernel(const PrefillLaunch p) {
+    GR_PF_LDS(D, NW, KH, D == 256);
     if (*p.f16_flag != p.f16_epoch)
-        prefill_body<F16, D, NW>(p, p.k_f16, p.v_f16, p.f16_row_stride, p.f16_row0, Ks0, Ks1, Vs0, Vs1, Qlo);
+        prefill_body<F16, D, NW, KH>(p, p.k_f16, p.v_f16, p.f16_row_stride, p.f16_row0, Ks0, Ks1, Vs0, Vs1, Qlo);
     else
-        prefill_body<BF16, D, NW>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
+        prefill_body<BF16, D, NW, KH>(p, p.k_cache, p.v_cache, p.cache_row_stride, 0, Ks0, Ks1, Vs0, Vs1, Qlo);
 }
 #undef GR_PF_LDS
 
-template <typename DT, int D, int NW>
+template <typename DT, int D, int NW, int KH = 1>
 static hipError_t launch_prefill_d(const PrefillLaunch& p, hipStream_t st) {
-    const int n_qb = (p.n_tokens + NW * 32 - 1) / (NW * 32);
+    constexpr int BM = NW / KH * 32;
+    const int n_qb = (p.n_tokens + BM - 1) / BM;
     const int n_items = p.n_heads * ((n_qb + 1) / 2);  // query blocks paired heavy + light
     dim3 grid(8 * ((n_items + 7) / 8));
     if (std::is_same<DT, BF16>::value && p.k_f16)
-        prefill_bf16x_kernel<D, NW><<<grid, NW * 64, 0, st>>>(p);
+        prefill_bf16x_kernel<D, NW, KH><<<grid, NW * 64, 0, st>>>(p);
     else
-        prefill_kernel<DT, D, NW><<<grid, NW * 64, 0, st>>>(p);
+        prefill_kernel<DT, D, NW, KH><<<grid, NW * 64, 0, st>>>(p);
     return hipGetLastError();
 }
 
-// Eight-wave workgroups once they alone fill every CU (256 on MI355X), else four.
-static int prefill_pick_waves(const PrefillLaunch& p) {
-    const int n_qb8 = (p.n_tokens + 255) / 256;
-    return p.head_dim <= 128 && p.n_heads * ((n_qb8 + 1) / 2) >= 256 ? 8 : 4;
+// Workgroup shape (d <= 128): eight waves of 256 rows once those workgroups
+// alone fill every CU (256 on MI355X); else four waves of 128 rows, or, at d64
+// while those number at most one per CU, the same 128-row blocks on eight waves
+// as two key halves.  Measured (MI355X): 14 / 2 heads, d64, S = 2048 (112
+// workgroups) 44.0 -> 36.4 us per call; at d128 (32 / 8 heads, S = 2048, 256
+// workgroups) the key halves were 1.5% slower than four waves.
+enum { kPfWaves8 = 8, kPfWaves4 = 4, kPfKeyHalves = 2 };
+static int prefill_pick(const PrefillLaunch& p) {
+    constexpr int kCUs = 256;
+    if (p.head_dim > 128) return kPfWaves4;
+    const int n_qb8 = (p.n_tokens + 255) / 256, n_qb4 = (p.n_tokens + 127) / 128;
+    if (p.n_heads * ((n_qb8 + 1) / 2) >= kCUs) return kPfWaves8;
+    return p.head_dim == 64 && p.n_heads * ((n_qb4 + 1) / 2) <= kCUs ? kPfKeyHalves : kPfWaves4;
 }
 
 template <typename DT>
 static hipError_t launch_prefill_dt(const PrefillLaunch& p, hipStream_t st) {
     switch (p.head_dim) {
         case 64:
-            return prefill_pick_waves(p) == 8 ? launch_prefill_d<DT, 64, 8>(p, st) : launch_prefill_d<DT, 64, 4>(p, st);
+            switch (prefill_pick(p)) {
+                case kPfWaves8: return launch_prefill_d<DT, 64, 8>(p, st);
+                case kPfKeyHalves: return launch_prefill_d<DT, 64, 8, 2>(p, st);
+                default: return launch_prefill_d<DT, 64, 4>(p, st);
+            }
         case 128:
-            return prefill_pick_waves(p) == 8 ? launch_prefill_d<DT, 128, 8>(p, st) : launch_prefill_d<DT, 128, 4>(p, st);
+            return prefill_pick(p) == kPfWaves8 ? launch_prefill_d<DT, 128, 8>(p, st) : launch_prefill_d<DT, 128, 4>(p, st);
         case 256: return launch_prefill_d<DT, 256, 4>(p, st);
         default: return hipErrorInvalidValue;
     }

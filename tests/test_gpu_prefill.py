@@ -305,7 +305,8 @@ def test_bf16_prefill_values_outside_f16_take_the_exact_path(orc, dev, d, which,
                                                    ("F16", 1, [300]), ("BF16", 0, [1, 127, 172])])
 def test_prefill_head_dim_64(orc, dev, fmt_name, window, chunks):
     """head_dim 64 (the Qwen2-0.5B / SmolLM-class heads of qwen2.rs / smolvlm.rs) on the MFMA
-    flash kernel: 4-wave workgroups over 64-key tiles with the 8-chunk row swizzle, global,
+    flash kernel: 128-row blocks on eight waves as two key halves (alternate 32-key
+    sub-tiles of 128-key tiles, merged at the end) with the 8-chunk row swizzle, global,
     window 37 and window 1 layers, chunked continuation, f16 and bf16 caches."""
     from gguf_runner_amd import ffi
     fmt = getattr(orc, fmt_name)
@@ -314,6 +315,17 @@ def test_prefill_head_dim_64(orc, dev, fmt_name, window, chunks):
                              base_chunks=chunks)
     _assert_close(got, ref)
     _assert_cache(kc, vc, fmt, orc)
+
+
+def test_prefill_head_dim_64_four_wave_blocks(orc, dev):
+    """A 2048-token head_dim-64 chunk with 60 Q / 4 KV heads (kv_mul 15): 240 eight-wave
+    items do not fill the CUs and 480 four-wave ones are more than one per CU, so the
+    launch takes the four-wave kernel (128-row blocks over 64-key tiles, no key halves)."""
+    from gguf_runner_amd import ffi
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=60, n_kv=4, d=64, fmt=orc.F16, seed=6460,
+                             rope_mode=ffi.ROPE_NEOX, theta=1e6)
+    _assert_close(got, ref)
+    _assert_cache(kc, vc, orc.F16, orc)
 
 
 def test_prefill_head_dim_64_eight_wave_blocks(orc, dev):
