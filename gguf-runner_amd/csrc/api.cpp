@@ -149,12 +149,22 @@ DecodePlan plan_decode(const gr_decode_args* a) {
         return pl;
     }
     if (split <= 0) {
+        // Fixed grid (VALU kernel, Turbo shapes off the stream schedule): about
+        // 2048 (sequence, KV head, split) units.  For the VALU kernel, splits of
+        // at least 256 keys once sequences reach 4096 keys: shorter splits of a
+        // long sequence cost more in partials and merging than their extra
+        // parallelism gains (MI355X, us per call, automatic split -> 256:
+        // f32 1 x 32768 keys, 8 KV heads 87.9 -> 65.6; f32 4 x 8192, 8 KV heads
+        // 76.6 -> 62.2; f16 d64 1 x 32768, 2 KV heads 91.3 -> 41.8), while short
+        // calls keep the small splits their latency needs (config 1, 1024 keys:
+        // 64; f32 4 x 2048 keys, 8 KV heads: 26.7 us at 64, 31.3 at 256).
         const long pairs = (long)a->n_seq * a->n_kv_heads;
         long want = (2048 + pairs - 1) / pairs;
         if (want < 1) want = 1;
         split = (int)((max_len + want - 1) / want);
         split = (split + 63) / 64 * 64;
         if (split < 64) split = 64;
+        if (!turbo && max_len >= 4096 && split < 256) split = 256;
     }
     pl.split_keys = split;
     pl.n_splits = (max_len + split - 1) / split;

@@ -11,6 +11,8 @@
 //
 // Scores are kept in the log2 domain: s2 = (q.k) * score_scale * log2(e), so
 // exp(s - m) == exp2(s2 - m2) with one v_exp_f32.
+#include <type_traits>
+
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 #include "stream_sched.hpp"
@@ -19,7 +21,14 @@ namespace gr {
 
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeWaves = kDecodeThreads / 64;
-constexpr int kDecodeUnroll = 4;  // rows per row-group per iteration (memory-level parallelism)
+// Rows per row group per iteration (memory-level parallelism): 4, or 8 for f32
+// splits that one 8-row iteration covers whole in grids of at most one
+// workgroup per CU (a short split then costs one round trip to HBM instead of
+// two: config 1, 1024 keys in 64-key splits, 128 workgroups, 11.9 -> 11.1 us
+// per call).  Larger grids measured slower with 8 (f32, 4 x 2048 keys, 8 KV
+// heads, 1024 workgroups: 26.7 -> 41 us), as did longer splits (4-5%).
+constexpr int kDecodeUnroll = 4;
+constexpr int64_t kDecodeUnroll8MaxWorkgroups = 256;
 
 // One lane owns 16 bytes (EPL elements) of a key row; LPR lanes cover a row of
 // D elements; a wave instruction covers RPW = 64 / LPR consecutive rows.
@@ -32,11 +41,11 @@ struct DecodeGeom {
 };
 
 // KVMUL: query heads per workgroup (the GQA group, or a slice of it: n_sub > 1).
-template <typename KV, int D, int KVMUL>
+template <typename KV, int D, int KVMUL, int U = kDecodeUnroll>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const DecodeLaunch p) {
     using G = DecodeGeom<KV, D>;
     constexpr int EPL = G::EPL, LPR = G::LPR, RPW = G::RPW;
-    constexpr int STEP = kDecodeWaves * kDecodeUnroll * RPW;  // rows per block iteration
+    constexpr int STEP = kDecodeWaves * U * RPW;  // rows per block iteration
 
     const int split = blockIdx.x;
     const int n_sub = p.n_sub > 0 ? p.n_sub : 1;
@@ -82,19 +91,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
     const size_t row_bytes = (size_t)p.row_stride * KV::bytes;
 
     for (int tb = t_begin; tb < t_stop; tb += STEP) {
-        uint4 kraw[kDecodeUnroll], vraw[kDecodeUnroll];
-        bool valid[kDecodeUnroll];
+        uint4 kraw[U], vraw[U];
+        bool valid[U];
 #pragma unroll
-        for (int u = 0; u < kDecodeUnroll; u++) {
-            const int t = tb + (wave * kDecodeUnroll + u) * RPW + rg;
+        for (int u = 0; u < U; u++) {
+            const int t = tb + (wave * U + u) * RPW + rg;
             valid[u] = t < t_stop;
             const int tt = valid[u] ? t : t_begin;  // clamp: never read past the split
             kraw[u] = *(const uint4*)(kbase + (size_t)tt * row_bytes);
             vraw[u] = *(const uint4*)(vbase + (size_t)tt * row_bytes);
         }
-        float sc[kDecodeUnroll][KVMUL];
+        float sc[U][KVMUL];
 #pragma unroll
-        for (int u = 0; u < kDecodeUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             float kf[EPL];
             unpack16<KV>(kraw[u], kf);
 #pragma unroll
@@ -108,7 +117,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
         // Reduce partial dots across the LPR lanes of a row (butterfly: every
         // lane of the row group ends with the full score).
 #pragma unroll
-        for (int u = 0; u < kDecodeUnroll; u++)
+        for (int u = 0; u < U; u++)
 #pragma unroll
             for (int j = 0; j < KVMUL; j++) {
                 float v = wave_sum<LPR>(sc[u][j]);
@@ -118,14 +127,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
         for (int j = 0; j < KVMUL; j++) {
             float mx = m[j];
 #pragma unroll
-            for (int u = 0; u < kDecodeUnroll; u++) mx = fmaxf(mx, sc[u][j]);
+            for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][j]);
             // mx is finite whenever any row of this group was valid.
             const float alpha = (mx == -INFINITY) ? 1.0f : exp2f(m[j] - mx);
             float lsum = l[j] * alpha;
 #pragma unroll
             for (int e = 0; e < EPL; e++) o[j][e] *= alpha;
 #pragma unroll
-            for (int u = 0; u < kDecodeUnroll; u++) {
+            for (int u = 0; u < U; u++) {
                 const float pu = (sc[u][j] == -INFINITY) ? 0.0f : exp2f(sc[u][j] - mx);
                 lsum += pu;
                 sc[u][j] = pu;
@@ -134,7 +143,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(const Deco
             m[j] = mx;
         }
 #pragma unroll
-        for (int u = 0; u < kDecodeUnroll; u++) {
+        for (int u = 0; u < U; u++) {
             float vf[EPL];
             unpack16<KV>(vraw[u], vf);
 #pragma unroll
@@ -329,12 +338,24 @@ static hipError_t launch_kvmul(const DecodeLaunch& p0, int kv_mul, hipStream_t s
     p.n_sub = (kv_mul + hb - 1) / hb;
     p.sub_heads = hb;
     dim3 grid(p.n_splits, p.n_kv_heads * p.n_sub, p.n_seq);
-    switch (hb) {
-        case 1: decode_split_kernel<KV, D, 1><<<grid, kDecodeThreads, 0, st>>>(p); break;
-        case 2: decode_split_kernel<KV, D, 2><<<grid, kDecodeThreads, 0, st>>>(p); break;
-        case 4: decode_split_kernel<KV, D, 4><<<grid, kDecodeThreads, 0, st>>>(p); break;
-        case 8: decode_split_kernel<KV, D, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
-        default: return hipErrorInvalidValue;
+    constexpr int kStep4 = kDecodeWaves * 4 * DecodeGeom<KV, D>::RPW;
+    if (std::is_same<KV, F32>::value && p.split_keys > kStep4 && p.split_keys <= 2 * kStep4 &&
+        (int64_t)grid.x * grid.y * grid.z <= kDecodeUnroll8MaxWorkgroups) {
+        switch (hb) {
+            case 1: decode_split_kernel<KV, D, 1, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 2: decode_split_kernel<KV, D, 2, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 4: decode_split_kernel<KV, D, 4, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 8: decode_split_kernel<KV, D, 8, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (hb) {
+            case 1: decode_split_kernel<KV, D, 1><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 2: decode_split_kernel<KV, D, 2><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 4: decode_split_kernel<KV, D, 4><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            case 8: decode_split_kernel<KV, D, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
