@@ -115,8 +115,7 @@ DecodePlan plan_decode(const gr_decode_args* a) {
                 (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16 || a->kv_dtype == GR_DTYPE_Q8 ||
                  (turbo && turbo_stream_ok(a->head_dim, turbo_split_pieces(kv_mul)))) &&
                 kv_mul >= 1 &&
-                (a->head_dim == 128 || a->head_dim == 256 ||
-                 (a->head_dim == 64 && (a->kv_dtype == GR_DTYPE_Q8 || turbo))) &&
+                (a->head_dim == 64 || a->head_dim == 128 || a->head_dim == 256) &&
                 a->n_seq <= kStreamMaxSeq &&
                 (int64_t)a->n_seq * (max_len + pl.stream_seg_cost) * a->n_kv_heads * ((kv_mul + 15) / 16) <
                     (int64_t)1 << 30;

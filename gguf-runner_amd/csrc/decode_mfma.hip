@@ -198,13 +198,18 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     // Q8 block mode: per-wave scale tile [K|V][block][32 keys] after the V^T tiles
     constexpr int kScBytes = kBlock ? kMdWaves * 2 * NB * TILE * 4 : 0;
     // 16-bit caches: per-wave K tile [TILE rows][DC chunks], 16-byte chunk c of
-    // row r at chunk c ^ (r & 15) (conflict-free for the row-slice writes and the
-    // 16-row MFMA operand reads), the rows fetched as full-line row slices like V.
+    // row r at chunk c ^ kswz(r), the rows fetched as full-line row slices like V.
+    // d >= 128 (16+ chunks a row): kswz(r) = r & 15, conflict-free for the
+    // row-slice writes and the 16-row MFMA operand reads.  d64 (8 chunks, two rows
+    // per 256 bytes): kswz(r) = (r >> 1) & 7 keeps the operand reads of 16
+    // consecutive rows on distinct bank groups (the row-slice writes, rows of one
+    // parity per instruction, take two passes).
     // Q8 reads K straight from HBM in the operand layout: staging its rows through
     // the same tile (codes converted on the way in) measured slower at 32k keys,
     // 4.40 -> 3.73 TB/s with row scales and 3.39 -> 2.71 with block scales.
     constexpr bool kKLds = !kQ8;
-    static_assert(!kKLds || DC >= 16, "the K tile swizzle c ^ (r & 15) needs 16 chunks a row");
+    static_assert(!kKLds || DC >= 16 || DC == 8, "K tile swizzle: 8 or 16+ chunks a row");
+    auto kswz = [](int r) { return DC >= 16 ? (r & 15) : ((r >> 1) & 7); };
     constexpr int kKBytes = kKLds ? kMdWaves * TILE * D * 2 : 0;
     constexpr int kLoopBytes = kVtBytes + kScBytes + kKBytes;
     constexpr int kMergeBytes = (kMdWaves * 16 * (D + 1) + 2 * kMdWaves * 16) * 4;
@@ -563,7 +568,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = 4 * kg + r;
-                    kst[row * DC + (dc ^ (row & 15))] = KV::to16(krs[u][r]);
+                    kst[row * DC + (dc ^ kswz(row))] = KV::to16(krs[u][r]);
                 }
             }
             __builtin_amdgcn_wave_barrier();
@@ -590,7 +595,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                 uint4 ka;
                 if constexpr (kKLds) {
                     const int row = 16 * sb + l16;
-                    ka = kst[row * DC + ((4 * k + g4) ^ (row & 15))];
+                    ka = kst[row * DC + ((4 * k + g4) ^ kswz(row))];
                 } else {
                     ka = KV::to16(kr[sb][k]);
                 }
@@ -836,9 +841,7 @@ static hipError_t launch_mfma_kv_d(const DecodeLaunch& p, hipStream_t st) {
 template <typename KV>
 static hipError_t launch_mfma_kv(const DecodeLaunch& p, hipStream_t st) {
     switch (p.head_dim) {
-        case 64:  // Q8 only: 16-bit caches at d64 take the VALU kernel (the K tile swizzle needs 16 chunks a row)
-            if constexpr (KV::kQ8) return launch_mfma_kv_d<KV, 64>(p, st);
-            return hipErrorInvalidValue;
+        case 64: return launch_mfma_kv_d<KV, 64>(p, st);
         case 128: return launch_mfma_kv_d<KV, 128>(p, st);
         case 256: return launch_mfma_kv_d<KV, 256>(p, st);
         default: return hipErrorInvalidValue;
@@ -849,7 +852,7 @@ bool decode_mfma_supported(const DecodeLaunch& p) {
     const int kv_mul = p.n_heads / p.n_kv_heads;
     return (p.kv_dtype == GR_DTYPE_F16 || p.kv_dtype == GR_DTYPE_BF16 || p.kv_dtype == GR_DTYPE_Q8) &&
            (kv_mul <= 16 || (p.n_sub > 0 && p.sub_heads == 16)) &&
-           (p.head_dim == 128 || p.head_dim == 256 || (p.head_dim == 64 && p.kv_dtype == GR_DTYPE_Q8));
+           (p.head_dim == 64 || p.head_dim == 128 || p.head_dim == 256);
 }
 
 hipError_t launch_decode_mfma_split(const DecodeLaunch& p, hipStream_t st) {

@@ -92,6 +92,19 @@ def test_config4_gemma3_decode_bf16(orc, dev, window):
     _assert_close(got, ref, orc.BF16, orc)
 
 
+@pytest.mark.parametrize("fmt_name", ["F16", "BF16"])
+@pytest.mark.parametrize("n_heads,n_kv,ends", [(14, 2, [1, 33, 700, 5000, 20000]), (9, 3, [1024]),
+                                               (14, 2, [4096, 300])])
+def test_decode_head_dim_64_16bit_mfma(orc, dev, fmt_name, n_heads, n_kv, ends):
+    """head_dim 64 over f16 / bf16 caches (Qwen2-0.5B 14 / 2 heads, SmolLM-135M 9 / 3) on
+    the MFMA decode kernel: a ragged batch on the stream schedule, and short calls on
+    the fixed grid of the small-call plan; the 8-chunk K tile swizzle (r >> 1) & 7."""
+    fmt = getattr(orc, fmt_name)
+    got, ref = _run_case(orc, dev, n_heads=n_heads, n_kv=n_kv, d=64, starts=[0] * len(ends), ends=ends,
+                         seq_len=max(ends), fmt=fmt, seed=6400 + sum(ends) % 97)
+    _assert_close(got, ref, fmt, orc)
+
+
 @pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 1000])
 def test_decode_edge_lengths(orc, dev, L):
     """Single key (out == v), lengths around the 64-row block step, f32."""
