@@ -339,16 +339,21 @@ static hipError_t launch_kvmul(const DecodeLaunch& p0, int kv_mul, hipStream_t s
     p.sub_heads = hb;
     dim3 grid(p.n_splits, p.n_kv_heads * p.n_sub, p.n_seq);
     constexpr int kStep4 = kDecodeWaves * 4 * DecodeGeom<KV, D>::RPW;
-    if (std::is_same<KV, F32>::value && p.split_keys > kStep4 && p.split_keys <= 2 * kStep4 &&
-        (int64_t)grid.x * grid.y * grid.z <= kDecodeUnroll8MaxWorkgroups) {
-        switch (hb) {
-            case 1: decode_split_kernel<KV, D, 1, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
-            case 2: decode_split_kernel<KV, D, 2, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
-            case 4: decode_split_kernel<KV, D, 4, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
-            case 8: decode_split_kernel<KV, D, 8, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
-            default: return hipErrorInvalidValue;
+    bool launched = false;
+    if constexpr (std::is_same<KV, F32>::value) {
+        if (p.split_keys > kStep4 && p.split_keys <= 2 * kStep4 &&
+            (int64_t)grid.x * grid.y * grid.z <= kDecodeUnroll8MaxWorkgroups) {
+            switch (hb) {
+                case 1: decode_split_kernel<KV, D, 1, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+                case 2: decode_split_kernel<KV, D, 2, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+                case 4: decode_split_kernel<KV, D, 4, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+                case 8: decode_split_kernel<KV, D, 8, 8><<<grid, kDecodeThreads, 0, st>>>(p); break;
+                default: return hipErrorInvalidValue;
+            }
+            launched = true;
         }
-    } else {
+    }
+    if (!launched) {
         switch (hb) {
             case 1: decode_split_kernel<KV, D, 1><<<grid, kDecodeThreads, 0, st>>>(p); break;
             case 2: decode_split_kernel<KV, D, 2><<<grid, kDecodeThreads, 0, st>>>(p); break;
