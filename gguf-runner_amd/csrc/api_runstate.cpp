@@ -391,6 +391,7 @@ void gr_free_run_state(gr_run_state* s) {
                     (void*)s->freqs_swa, (void*)s->qn, (void*)s->kn, (void*)s->ssm, s->stage})
         if (p) (void)hipFree(p);
     xfer_release(s->xfer);
+    xfer_pipe_release(s->pipe);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
 }
@@ -515,9 +516,11 @@ static gr_decode_args turbo_pack_probe(const gr_run_state* s, int n, const Turbo
     return a;
 }
 
+// se_dev: the (start, end) arrays (or the pack's four arrays) already on the
+// device; null: uploaded here on the state's stream.
 static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, const int32_t* slots_dev, int seq,
                       const std::vector<int32_t>& starts, const std::vector<int32_t>& ends, float* xb_dev,
-                      Carve& cv, const TurboPack* pack = nullptr) {
+                      Carve& cv, const TurboPack* pack = nullptr, const int32_t* se_dev = nullptr) {
     std::vector<int32_t> host(2 * (size_t)n);
     int max_len = 1;
     for (int b = 0; b < n; b++) {
@@ -529,9 +532,13 @@ static int run_decode(gr_run_state* s, int layer, int n, const float* qdev, cons
         host = pack->host;
         max_len = pack->max_len;
     }
-    int32_t* se = cv.take<int32_t>(host.size());
-    int rc = h2d(s, se, host.data(), host.size() * 4);
-    if (rc) return rc;
+    const int32_t* se = se_dev;
+    if (!se) {
+        int32_t* up = cv.take<int32_t>(host.size());
+        const int rc = h2d(s, up, host.data(), host.size() * 4);
+        if (rc) return rc;
+        se = up;
+    }
     gr_decode_args a{};
     a.n_seq = n;
     a.n_heads = s->cfg.n_heads;
@@ -643,6 +650,38 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
 }
 
+// Large calls run their rows in pieces so that the uploads of piece p + 1, the
+// kernels of piece p and the downloads of piece p - 1 overlap (xfer_pipeline):
+// calls of at least kPipeMinBytes of host rows and two pieces' worth of rows.
+// The first and the last piece take half the rows of the others (256, then
+// pieces of ~512, then 256), which shortens the upload before the first kernel
+// and the kernels and download after the last upload.  Causal rows only: an
+// image block's rows see the whole block, so all of its K / V writes precede
+// its attention.  Over a Turbo cache every piece keeps >= 2048 (row group, KV
+// head) workgroups (equal pieces), so its split kernel still finishes the rows
+// itself.
+constexpr size_t kPipeMinBytes = size_t(16) << 20;
+
+static std::vector<int> row_pieces(const gr_run_state* s, int m, bool block, size_t bytes) {
+    const int kv_mul = s->cfg.n_heads / s->cfg.n_kv_heads;
+    const int tp = turbo_pack_rows(s->d, kv_mul);
+    const bool turbo_pack = is_turbo(s) && tp * kv_mul <= 16;
+    const int min_rows = turbo_pack ? std::max(512, (2048 + s->cfg.n_kv_heads - 1) / s->cfg.n_kv_heads * tp) : 512;
+    if (block || bytes < kPipeMinBytes || m < 2 * min_rows) return {0, m};
+    std::vector<int> cut;
+    if (turbo_pack) {
+        const int n = std::min(XferPipe::kMaxPieces, m / min_rows);
+        for (int i = 0; i <= n; i++) cut.push_back((int)((int64_t)m * i / n));
+        return cut;
+    }
+    const int half = min_rows / 2;
+    const int n_mid = std::max(1, std::min(XferPipe::kMaxPieces - 2, (m - 2 * half + min_rows / 2) / min_rows));
+    cut.push_back(0);
+    for (int i = 0; i <= n_mid; i++) cut.push_back(half + (int)((int64_t)(m - 2 * half) * i / n_mid));
+    cut.push_back(m);
+    return cut;
+}
+
 // The rows base_pos..base_pos+m-1 of one layer: QK-norm, RoPE and KV write of
 // every row, then attention of every row over its visible keys; block = the rows
 // are one bidirectional image block (attention.rs:87-94), else causal.
@@ -657,88 +696,137 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
                       (s->d == 64 || s->d == 128 || s->d == 256);
     const int64_t w = s->windows.empty() ? 0 : s->windows[layer];
     std::vector<int32_t> starts(m), ends(m);
-    int max_len = 1;
     for (int i = 0; i < m; i++) {
         visible(s, layer, base_pos + i, &starts[i], &ends[i]);
         if (block) {
             starts[i] = std::min(starts[i], (int32_t)base_pos);
             ends[i] = (int32_t)(base_pos + m);
         }
-        max_len = std::max(max_len, ends[i] - starts[i]);
     }
-    gr_decode_args probe{};
-    probe.n_seq = m;
-    probe.n_heads = s->cfg.n_heads;
-    probe.n_kv_heads = s->cfg.n_kv_heads;
-    probe.head_dim = s->d;
-    probe.kv_dtype = s->cfg.kv_dtype;
-    probe.max_kv_len = max_len;
-    TurboPack pack;  // tp = 0: rows decoded one query row each (GQA groups above 16 heads)
+    const std::vector<int> cut = row_pieces(s, m, block, 2 * qb + 2 * kb);
+    const int n_pieces = (int)cut.size() - 1;
     const int kv_mul = s->cfg.n_heads / s->cfg.n_kv_heads;
-    if (is_turbo(s) && turbo_pack_rows(s->d, kv_mul) * kv_mul <= 16) {
-        pack = plan_turbo_pack(s, m, starts, ends);
-        probe = turbo_pack_probe(s, m, pack);
+    // the MFMA prefill's arguments for n rows from position pos0 (sizes first: its
+    // workspace depends on them)
+    auto pf_args = [&](int n, int64_t pos0) {
+        gr_prefill_args a{};
+        a.n_tokens = n;
+        a.base_pos = (int32_t)pos0;
+        a.n_heads = s->cfg.n_heads;
+        a.n_kv_heads = s->cfg.n_kv_heads;
+        a.head_dim = s->d;
+        a.dtype = s->cfg.kv_dtype;
+        a.window = (int32_t)w;
+        a.rope_mode = s->cfg.rope_mode;
+        a.rope_dim = s->rope_dim;
+        return a;
+    };
+    // Per piece: its rows' key ranges, the decode path's range arrays (uploaded
+    // with the piece's rows) and the scratch its kernels carve; the pieces run in
+    // stream order, so they share one scratch region.
+    std::vector<std::vector<int32_t>> pst(n_pieces), pen(n_pieces), se(n_pieces);
+    std::vector<TurboPack> packs(n_pieces);
+    size_t scratch = 0, se_bytes = 0;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const int r0 = cut[pc], n = cut[pc + 1] - r0;
+        if (mfma) {
+            const gr_prefill_args a = pf_args(n, base_pos + r0);
+            scratch = std::max(scratch, prefill_ws_bytes(&a) + 256);
+            continue;
+        }
+        pst[pc].assign(starts.begin() + r0, starts.begin() + r0 + n);
+        pen[pc].assign(ends.begin() + r0, ends.begin() + r0 + n);
+        size_t need = 4 * (size_t)n * s->q_dim + q8_stage_bytes(s, n) + 4 * 256;
+        if (!is_q8(s)) {
+            gr_decode_args probe{};
+            probe.n_seq = n;
+            probe.n_heads = s->cfg.n_heads;
+            probe.n_kv_heads = s->cfg.n_kv_heads;
+            probe.head_dim = s->d;
+            probe.kv_dtype = s->cfg.kv_dtype;
+            probe.max_kv_len = 1;
+            for (int i = 0; i < n; i++) probe.max_kv_len = std::max(probe.max_kv_len, pen[pc][i] - pst[pc][i]);
+            if (is_turbo(s) && turbo_pack_rows(s->d, kv_mul) * kv_mul <= 16) {
+                packs[pc] = plan_turbo_pack(s, n, pst[pc], pen[pc]);
+                probe = turbo_pack_probe(s, n, packs[pc]);
+                se[pc] = packs[pc].host;
+            } else {  // tp = 0: rows decoded one query row each (GQA groups above 16 heads)
+                se[pc] = pst[pc];
+                se[pc].insert(se[pc].end(), pen[pc].begin(), pen[pc].end());
+            }
+            need += decode_ws_bytes(&probe) + 256;
+            se_bytes += align_up(4 * se[pc].size(), 256);
+        }
+        scratch = std::max(scratch, need);
     }
-    gr_prefill_args a{};  // the MFMA prefill's arguments (sizes first: its workspace depends on them)
-    a.n_tokens = m;
-    a.base_pos = (int32_t)base_pos;
-    a.n_heads = s->cfg.n_heads;
-    a.n_kv_heads = s->cfg.n_kv_heads;
-    a.head_dim = s->d;
-    a.dtype = s->cfg.kv_dtype;
-    a.window = (int32_t)w;
-    a.rope_mode = s->cfg.rope_mode;
-    a.rope_dim = s->rope_dim;
-    const size_t pf_ws = mfma ? prefill_ws_bytes(&a) : 0;
-    const size_t extra = mfma ? pf_ws : decode_ws_bytes(&probe) + qb + q8_stage_bytes(s, m) + 16 * (size_t)m;
-    if ((rc = ensure_stage(s, 2 * qb + 2 * kb + extra + 8 * (size_t)m + 16384))) return rc;
+    if ((rc = ensure_stage(s, 2 * qb + 2 * kb + se_bytes + scratch + 1024 * (size_t)n_pieces + 16384))) return rc;
+    // per piece, its q, k, v rows and range arrays back to back (one upload DMA)
     Carve cv(s->stage);
-    float* qin = cv.take<float>((size_t)m * s->q_dim);
-    float* kin = cv.take<float>((size_t)m * s->kv_dim);
-    float* vin = cv.take<float>((size_t)m * s->kv_dim);
+    std::vector<float*> qin(n_pieces), kin(n_pieces), vin(n_pieces);
+    std::vector<int32_t*> se_dev(n_pieces, nullptr);
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t n = (size_t)(cut[pc + 1] - cut[pc]);
+        qin[pc] = cv.take<float>(n * s->q_dim);
+        kin[pc] = cv.take<float>(n * s->kv_dim);
+        vin[pc] = cv.take<float>(n * s->kv_dim);
+        if (!se[pc].empty()) se_dev[pc] = cv.take<int32_t>(se[pc].size());
+    }
     float* xo = cv.take<float>((size_t)m * s->q_dim);
-    if ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb))) return rc;
+    const Carve scratch_base = cv;
     void* kc = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     void* vc = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
-    if (mfma) {
-        const bool swa = is_swa_layer(s, layer);
-        a.rope_scale = swa ? s->cfg.rope_scale_local : s->cfg.rope_scale_global;
-        a.rope_freqs = (s->cfg.is_gemma3 && swa) ? s->freqs_swa : s->freqs;
-        if (s->has_norm && s->norm_present[layer]) {
-            a.q_norm = s->qn + (size_t)layer * s->d;
-            a.k_norm = s->kn + (size_t)layer * s->d;
+
+    // the kernels of piece pc, on the state's stream, once its rows are on the device
+    auto enqueue = [&](int pc) -> int {
+        const int r0 = cut[pc], n = cut[pc + 1] - r0;
+        const int64_t pos0 = base_pos + r0;
+        Carve cw = scratch_base;
+        float* qi = qin[pc];
+        float* ki = kin[pc];
+        float* vi = vin[pc];
+        float* xi = xo + (size_t)r0 * s->q_dim;
+        if (mfma) {
+            gr_prefill_args a = pf_args(n, pos0);
+            const size_t ws = prefill_ws_bytes(&a);
+            const bool swa = is_swa_layer(s, layer);
+            a.rope_scale = swa ? s->cfg.rope_scale_local : s->cfg.rope_scale_global;
+            a.rope_freqs = (s->cfg.is_gemma3 && swa) ? s->freqs_swa : s->freqs;
+            if (s->has_norm && s->norm_present[layer]) {
+                a.q_norm = s->qn + (size_t)layer * s->d;
+                a.k_norm = s->kn + (size_t)layer * s->d;
+            }
+            a.norm_eps = s->eps;
+            a.is_gemma3 = s->cfg.is_gemma3;
+            a.q = qi;
+            a.k = ki;
+            a.v = vi;
+            a.k_cache = kc;
+            a.v_cache = vc;
+            a.cache_row_stride = s->kv_dim;
+            a.out = xi;
+            a.workspace = cw.take<char>(ws);
+            a.bidirectional = block ? 1 : 0;
+            return prefill_enqueue_ex(&a, GR_DTYPE_F32, s->stream);
         }
-        a.norm_eps = s->eps;
-        a.is_gemma3 = s->cfg.is_gemma3;
-        a.q = qin;
-        a.k = kin;
-        a.v = vin;
-        a.k_cache = kc;
-        a.v_cache = vc;
-        a.cache_row_stride = s->kv_dim;
-        a.out = xo;
-        a.workspace = cv.take<char>(pf_ws);
-        a.bidirectional = block ? 1 : 0;
-        if ((rc = prefill_enqueue_ex(&a, GR_DTYPE_F32, s->stream))) return rc;
-    } else {
-        float* qp = cv.take<float>((size_t)m * s->q_dim);
-        QkvPrepLaunch p = prep_for(s, layer, m, true, true);
-        p.pos0 = base_pos;
-        p.q = qin;
-        p.k = kin;
-        p.v = vin;
+        float* qp = cw.take<float>((size_t)n * s->q_dim);
+        QkvPrepLaunch p = prep_for(s, layer, n, true, true);
+        p.pos0 = pos0;
+        p.q = qi;
+        p.k = ki;
+        p.v = vi;
         p.q_out = qp;
         p.k_cache = kc;
         p.v_cache = vc;
-        if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
+        int r = prep_and_store(s, layer, seq, p, cw);
+        if (r) return r;
         if (is_q8(s)) {
-            // one MFMA flash pass over the int8 rows (all m queries share each K / V tile)
+            // one MFMA flash pass over the int8 rows (all n queries share each K / V tile)
             PrefillQ8Launch pq{};
-            pq.n_tokens = m;
+            pq.n_tokens = n;
             pq.n_heads = s->cfg.n_heads;
             pq.n_kv_heads = s->cfg.n_kv_heads;
             pq.head_dim = s->d;
-            pq.base_pos = base_pos;
+            pq.base_pos = pos0;
             pq.window = (int)w;
             pq.bidirectional = block ? 1 : 0;
             pq.block = s->cfg.q8_block_scales ? 1 : 0;
@@ -751,14 +839,33 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
             pq.k_scale = s->k_scale + so;
             pq.v_scale = s->v_scale + so;
             pq.scale_row_stride = (int64_t)s->sc_per_row;
-            pq.out = xo;
+            pq.out = xi;
             const hipError_t e = launch_prefill_q8(pq, s->stream);
-            if (e != hipSuccess) return hip_fail(e, "q8 prefill launch");
-        } else if ((rc = run_decode(s, layer, m, qp, nullptr, seq, starts, ends, xo, cv, pack.tp > 0 ? &pack : nullptr))) {
-            return rc;
+            return e == hipSuccess ? GR_OK : hip_fail(e, "q8 prefill launch");
         }
+        return run_decode(s, layer, n, qp, nullptr, seq, pst[pc], pen[pc], xi, cw,
+                          packs[pc].tp > 0 ? &packs[pc] : nullptr, se_dev[pc]);
+    };
+
+    if (n_pieces == 1) {
+        if ((rc = h2d(s, qin[0], q, qb)) || (rc = h2d(s, kin[0], k, kb)) || (rc = h2d(s, vin[0], v, kb))) return rc;
+        if (se_dev[0] && (rc = h2d(s, se_dev[0], se[0].data(), 4 * se[0].size()))) return rc;
+        if ((rc = enqueue(0))) return rc;
+        return d2h_sync(s, xb, xo, qb);
     }
-    return d2h_sync(s, xb, xo, qb);
+    std::vector<XferRange> ups, downs;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t r0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+        ups.push_back({(char*)qin[pc], (char*)(q + r0 * s->q_dim), 4 * n * s->q_dim, pc});
+        ups.push_back({(char*)kin[pc], (char*)(k + r0 * s->kv_dim), 4 * n * s->kv_dim, pc});
+        ups.push_back({(char*)vin[pc], (char*)(v + r0 * s->kv_dim), 4 * n * s->kv_dim, pc});
+        if (se_dev[pc]) ups.push_back({(char*)se_dev[pc], (char*)se[pc].data(), 4 * se[pc].size(), pc});
+        downs.push_back({(char*)(xo + r0 * s->q_dim), (char*)(xb + r0 * s->q_dim), 4 * n * s->q_dim, pc});
+    }
+    int status = GR_OK;
+    const hipError_t e = xfer_pipeline(s->xfer, s->pipe, s->stream, n_pieces, ups, downs, enqueue, &status);
+    if (status) return status;
+    return e == hipSuccess ? GR_OK : hip_fail(e, "pipelined host transfers");
 }
 
 int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,

@@ -52,6 +52,7 @@ struct gr_run_state {
     void* stage = nullptr;
     size_t stage_bytes = 0;
     gr::HostXfer xfer;  // pinned ring for the host rows of each call
+    gr::XferPipe pipe;  // streams and download ring of the pipelined large calls
 };
 
 namespace gr {

@@ -372,3 +372,44 @@ def test_quantised_prefill_into_a_middle_sequence_slot(orc, dev, kv):
         else:
             assert np.array_equal(after[0][0], before[sq][0][0]) and np.array_equal(after[0][1], before[sq][0][1])
             assert np.array_equal(after[1][0], before[sq][1][0]) and np.array_equal(after[1][1], before[sq][1][1])
+
+
+@pytest.mark.parametrize("block,window", [(False, None), (True, 700)])
+def test_q8_large_chunks_run_in_overlapped_pieces(orc, dev, block, window):
+    """Chunks of 2048 and 1024 rows at the config-2 shape (32 / 8 heads, d128): above
+    16 MB of host rows the run-state call cuts its rows into pieces of >= 512 rows (4,
+    then 2) whose uploads, kernels and downloads overlap, each piece written to the
+    cache before the next one's queries read it.  The K / V codes and scales of every
+    row == the oracle's quantize_row_q8 (bit-exact); sampled output rows of both chunks
+    (piece edges included) == the oracle's attention_token over those rows (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv, d = 32, 8, 128
+    m1, m2 = 2048, 1024
+    n = m1 + m2
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=n,
+                  kv_dtype=ffi.DTYPE_Q8, q8_block_scales=block, rope_mode=ffi.ROPE_NONE,
+                  layer_windows=[window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(2048 + (window or 0))
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    out1 = rt.prefill_attention_chunk(p, s, 0, 0, q[:m1], k[:m1], v[:m1]).copy()
+    out2 = rt.prefill_attention_chunk(p, s, 0, m1, q[m1:], k[m1:], v[m1:]).copy()
+    got = np.concatenate([out1, out2])
+    kq, vq = rt.read_kv_rows(p, s, 0, 0, n)
+    ks, vs = rt.read_kv_scales(p, s, 0, 0, n)
+    ck, sk = _quantize_cache(orc, k[None], block)
+    cv, sv = _quantize_cache(orc, v[None], block)
+    assert np.array_equal(kq, ck[0]) and np.array_equal(vq, cv[0])
+    assert np.array_equal(ks.reshape(sk[0].shape), sk[0]) and np.array_equal(vs.reshape(sv[0].shape), sv[0])
+    fmt = orc.Q8B if block else orc.Q8
+    rows = sorted({0, 1, 511, 512, 1023, 1024, 1535, 1536, 2047, 2048, 2559, 2560, n - 1}
+                  | set(rng.integers(0, n, 10).tolist()))
+    worst = 0.0
+    for t in rows:
+        start = max(0, t + 1 - window) if window else 0
+        ref = orc.attention_token(q[t], kq, vq, fmt, n_heads, n_kv, d, start, t + 1,
+                                  key_scale=ks.reshape(-1), value_scale=vs.reshape(-1))
+        worst = max(worst, float(np.abs(got[t] - ref).max()))
+    assert worst <= TOL, worst

@@ -281,10 +281,12 @@ def test_prefill_image_block_outside_context_is_rejected(dev):
 
 def test_large_host_rows_through_the_pinned_ring(dev):
     """Host rows above the staging threshold travel through the run state's pinned
-    ring (several 8 MB slots, a partial last slot, uploads after downloads): one
-    2600-row chunk over an f32 cache, twice with new rows into the same output
-    buffer; the K / V rows read back bit-exact and sampled output rows against a
-    float64 restatement of the causal softmax within 1e-5."""
+    rings: one 2600-row chunk over an f32 cache runs as six overlapped pieces (256,
+    four of ~522, 256 rows; uploads, kernels and downloads of neighbouring pieces at
+    once), twice with new rows into the same output buffer; the K / V rows read back
+    bit-exact (single 16 MB slot reads after the pipelined call) and sampled output
+    rows, piece edges included, against a float64 restatement of the causal softmax
+    within 1e-5."""
     from gguf_runner_amd import ffi, runtime as rt
     m, H, G, d = 2600, 16, 8, 128
     p = rt.Config(n_layers=1, n_heads=H, n_kv_heads=G, head_dim=d, seq_len=m,
@@ -300,7 +302,7 @@ def test_large_host_rows_through_the_pinned_ring(dev):
         assert got is xb
         kd, vd = rt.read_kv_rows(p, s, 0, 0, m)
         assert np.array_equal(kd, k) and np.array_equal(vd, v), rep
-        for t in (0, 1, 1000, 2047, 2048, m - 1):
+        for t in (0, 1, 255, 256, 777, 778, 1000, 2047, 2048, 2343, 2344, m - 1):
             for h in range(H):
                 g = h // (H // G)
                 kk = k[:t + 1, g * d:(g + 1) * d].astype(np.float64)
@@ -310,3 +312,32 @@ def test_large_host_rows_through_the_pinned_ring(dev):
                 ref = (w / w.sum()) @ vv
                 err = np.abs(xb[t, h * d:(h + 1) * d] - ref).max()
                 assert err <= TOL_F32, (rep, t, h, err)
+
+
+@pytest.mark.parametrize("kv_dtype,window", [(1, None), (2, 300)])
+def test_large_f16_chunk_runs_in_overlapped_pieces(dev, orc, kv_dtype, window):
+    """A 2048-row chunk over an f16 / bf16 cache (32 / 8 heads, d128, global or
+    window-300 layer) is cut into four overlapped pieces of 512 rows; the MFMA
+    prefill of each piece sees the rows the pieces before it wrote.  The cache rows
+    == the host rows rounded to the cache type (bit-exact) and sampled output rows
+    (piece edges included) == the oracle's attention_token over the device's rows,
+    to the 16-bit MFMA bar."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv, d, m = 32, 8, 128, 2048
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=m,
+                  kv_dtype=kv_dtype, rope_mode=ffi.ROPE_NONE, layer_windows=[window])
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(512 + kv_dtype)
+    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+    got = rt.prefill_attention_chunk(p, s, 0, 0, q, k, v)
+    kd, vd = rt.read_kv_rows(p, s, 0, 0, m)
+    cast = orc.c_f32_to_f16 if kv_dtype == ffi.DTYPE_F16 else orc.c_f32_to_bf16
+    assert np.array_equal(kd.reshape(-1), cast(k)) and np.array_equal(vd.reshape(-1), cast(v))
+    fmt = orc.F16 if kv_dtype == ffi.DTYPE_F16 else orc.BF16
+    rows = sorted({0, 1, 511, 512, 1023, 1024, 1535, 1536, m - 1} | set(rng.integers(0, m, 8).tolist()))
+    for t in rows:
+        start = max(0, t + 1 - window) if window else 0
+        ref = orc.attention_token(q[t], kd, vd, fmt, n_heads, n_kv, d, start, t + 1)
+        assert (np.abs(got[t] - ref) <= ATOL_16 + RTOL_16 * np.abs(ref)).all(), (t, float(np.abs(got[t] - ref).max()))

@@ -363,3 +363,37 @@ def test_turbo_decode_stream_sequence_limit(orc, dev, n_seq):
                             seq_len=int(ends.max()), seed=1500 + n_seq)
     assert float(np.abs(got - ref).max()) <= TOL, float(np.abs(got - ref).max())
     assert not got[lens == 0].any()
+
+
+def test_turbo_large_chunk_runs_in_overlapped_pieces(orc, dev):
+    """A 2048-row chunk at the config-2 shape over a Turbo cache, then a 1024-row
+    one: the first is cut into two overlapped pieces of 1024 rows (each keeps one
+    split kernel workgroup per (row group, KV head) and finishes its rows itself),
+    the second stays whole.  Every row's Turbo encoding == the oracle's
+    (bit-exact); sampled output rows of both chunks == the oracle's
+    attention_token_turbo (1e-5)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    n_heads, n_kv, d, layer = 32, 8, 128, 0
+    m1, m2 = 2048, 1024
+    n = m1 + m2
+    p = rt.Config(n_layers=1, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=n,
+                  kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(3072)
+    q = rng.standard_normal((n, p.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, p.kv_dim)).astype(np.float32)
+    out1 = rt.prefill_attention_chunk(p, s, layer, 0, q[:m1], k[:m1], v[:m1]).copy()
+    out2 = rt.prefill_attention_chunk(p, s, layer, m1, q[m1:], k[m1:], v[m1:]).copy()
+    got = np.concatenate([out1, out2])
+    table = orc.turbo_sign_table(1, n_kv, d)
+    c = orc.TurboCache(n, n_kv, d)
+    for t in range(n):
+        orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
+    _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 0, n), c, 0, n, n_kv, d)
+    rows = sorted({0, 1, 1023, 1024, 1025, 2047, 2048, n - 1} | set(rng.integers(0, n, 10).tolist()))
+    worst = 0.0
+    for t in rows:
+        ref = orc.attention_token_turbo(q[t], c, table, layer, n_heads, 0, t + 1)
+        worst = max(worst, float(np.abs(got[t] - ref).max()))
+    assert worst <= TOL, worst
