@@ -22,8 +22,11 @@
 //    deltanet_chunk_prep_kernel (chunk, head): T, P and per-row scales; the
 //    Gram products on v_mfma_f32_16x16x4_f32, T by forward substitution.
 //    deltanet_chunk_scan_kernel (head, 16 state columns): the sequential chunk
-//    steps, every product on v_mfma_f32_16x16x4_f32 with the raw q / k rows as
-//    operands and their row scales applied to the products' rows.
+//    steps with the raw q / k rows as operands and their row scales applied to
+//    the products' rows; T X and P Delta on v_mfma_f32_16x16x4_f32, and K S0,
+//    Q S0 and the state update too for f32 / f16 rows, while bf16 rows (exact
+//    bf16 operands) run those three on v_mfma_f32_16x16x32_bf16 against the f32
+//    state / Delta cut into three exact bf16 pieces.
 //    Non-finite values: the prep flags a chunk whose inputs, T or P are not all
 //    finite, the scan one whose X, Delta, O or new state are not.  The scan stops
 //    before such a chunk, keeping the state it started from, and the step kernel
@@ -208,6 +211,7 @@ __device__ __forceinline__ float dn_h2f(uint32_t b) {
 }
 
 typedef _Float16 dn_h8 __attribute__((ext_vector_type(8)));
+typedef short dn_s4 __attribute__((ext_vector_type(4)));  // ds_read_b64_tr_b16 result
 typedef __bf16 dn_b8 __attribute__((ext_vector_type(8)));
 
 // 16x16x32 MFMA on 16-bit operands (8 consecutive reduction indices per lane,
@@ -221,6 +225,27 @@ __device__ __forceinline__ dn_f32x4 mfma32(const uint4& a, const uint4& b, dn_f3
     else
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dn_b8, a), __builtin_bit_cast(dn_b8, b), c,
                                                        0, 0, 0);
+}
+
+// f32 x == hi + mid + lo exactly for three bf16 values made by truncation: hi
+// keeps x's first 8 significant bits, mid the next 8 of the exact residual and
+// lo the (at most 8) bits left.  (Normal values; the scan stops before a chunk
+// whose state is not finite.)  Returned as the upper halves of three words.
+__device__ __forceinline__ void dn_split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+    hi = __float_as_uint(x) & 0xffff0000u;
+    const float r1 = x - __uint_as_float(hi);
+    mid = __float_as_uint(r1) & 0xffff0000u;
+    lo = __float_as_uint(r1 - __uint_as_float(mid)) & 0xffff0000u;
+}
+// four floats as the three bf16 pieces of four consecutive B-operand slots
+// (two words each); piece pc at out[pc]
+__device__ __forceinline__ void dn_split3x4(const float* x, uint2* out) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) dn_split3(x[i], h[i], m[i], l[i]);
+    out[0] = make_uint2((h[0] >> 16) | h[1], (h[2] >> 16) | h[3]);
+    out[1] = make_uint2((m[0] >> 16) | m[1], (m[2] >> 16) | m[3]);
+    out[2] = make_uint2((l[0] >> 16) | l[1], (l[2] >> 16) | l[3]);
 }
 
 template <int DT>
@@ -573,6 +598,15 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
     __shared__ __attribute__((aligned(16))) float Sl[D * NC];
     __shared__ __attribute__((aligned(16))) float Xl[C * NC];
     __shared__ __attribute__((aligned(16))) float Dl[C * NC];
+    // bf16 rows (raw k / q exact as bf16): the K S0, Q S0 and state-update products
+    // run on v_mfma_f32_16x16x32_bf16 with the f32 operand as three exact bf16
+    // pieces (hi + mid + lo, three MFMAs), a third of the matrix-core time of the
+    // f32 MFMA.  The pieces in B-operand order: Sp[piece][k-step q][lane 16 g + n]
+    // = state rows 32 q + 8 g .. + 7 of column n; Dp the same for the scaled Delta
+    // rows (tokens).
+    constexpr bool BF = DT == GR_DTYPE_BF16;
+    __shared__ __attribute__((aligned(16))) uint4 Sp[BF ? 3 * (D / 32) * 64 : 1];
+    __shared__ __attribute__((aligned(16))) uint4 Dp[BF ? 3 * (C / 32) * 64 : 1];
     __shared__ int flag;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l16 = lane & 15, g = lane >> 4;
@@ -591,6 +625,30 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
         Sl[e] = Sh[(size_t)(16 * q + 4 * gg + i) * D + c0 + n];
     }
     if (tid == 0) flag = 0;
+    // this wave's state rows 32 w + 16 tt + 4 g + (0..3) (an MFMA result's rows) as
+    // bf16 pieces: k-step w, lane 16 (2 tt + g / 2) + n, slots 4 (g % 2) ..
+    auto store_state_pieces = [&](const float* v0, const float* v1) {
+        if constexpr (BF) {
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                uint2 pcs[3];
+                dn_split3x4(tt ? v1 : v0, pcs);
+#pragma unroll
+                for (int pc = 0; pc < 3; pc++)
+                    *(uint2*)((char*)&Sp[(pc * (D / 32) + wave) * 64 + 16 * (2 * tt + (g >> 1)) + l16] + 8 * (g & 1)) =
+                        pcs[pc];
+            }
+        }
+    };
+    if constexpr (BF) {
+        __syncthreads();  // Sl complete
+        float v0[4], v1[4];
+        const float4 a = *(const float4*)(Sl + ((2 * wave) * 64 + lane) * 4);
+        const float4 b = *(const float4*)(Sl + ((2 * wave + 1) * 64 + lane) * 4);
+        v0[0] = a.x, v0[1] = a.y, v0[2] = a.z, v0[3] = a.w;
+        v1[0] = b.x, v1[1] = b.y, v1[2] = b.z, v1[3] = b.w;
+        store_state_pieces(v0, v1);
+    }
 
     // DMA round k of this wave for a K / Q tile: round I = wave + 4 k (1 KB) fills
     // position l % PPR of row I * RPK + l / PPR (lane l) with the piece that
@@ -694,7 +752,30 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
         // b: K S0, Q S0 for rows 16 w + (0..15); four chains (K / Q x even / odd i);
         //    the next chunk's K (and 16-bit Q) rounds between the MFMAs
         dn_f32x4 ak0 = {0.0f, 0.0f, 0.0f, 0.0f}, ak1 = ak0, aq0 = ak0, aq1 = ak0;
-        {
+        if constexpr (BF) {
+            // bf16: A = the raw row piece (k-step q: dims 32 q + 8 g .. + 7), B = the
+            // state's three pieces; ak1 / aq1 stay zero
+            const dn_i32x4 rk = rows_rsrc(p.k, more ? c + 1 : c);
+            const dn_i32x4 rq = rows_rsrc(p.q, more ? c + 1 : c);
+            const int ta = 16 * wave + l16;
+#pragma unroll
+            for (int q = 0; q < D / 32; q++) {
+                const int pos = (4 * q + g) ^ (ta & 15);
+                const uint4 ka = *(const uint4*)(kt + ta * 256 + pos * 16);
+                const uint4 qa = *(const uint4*)(qt + ta * 256 + pos * 16);
+#pragma unroll
+                for (int pc = 0; pc < 3; pc++) {
+                    const uint4 sb = Sp[(pc * (D / 32) + q) * 64 + lane];
+                    ak0 = mfma32<DT>(ka, sb, ak0);
+                    aq0 = mfma32<DT>(qa, sb, aq0);
+                }
+                if (more && q < KR) {
+                    dma_row_round(rk, kn, q);
+                    if (Q2) dma_row_round(rq, qn, q);
+                }
+            }
+            static_assert(!BF || KR <= D / 32, "the DMA rounds fit the k-steps");
+        } else {
             const dn_i32x4 rk = rows_rsrc(p.k, more ? c + 1 : c);
             const dn_i32x4 rq = rows_rsrc(p.q, more ? c + 1 : c);
             const int ta = 16 * wave + l16;
@@ -757,6 +838,19 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
 #pragma unroll
         for (int i = 0; i < 4; i++) nf |= !is_finite_f(dl[i]);
         *(float4*)(Dl + (wave * 64 + lane) * 4) = make_float4(dl[0], dl[1], dl[2], dl[3]);
+        if constexpr (BF) {
+            // the state update's B operand: Delta rows t = 16 w + 4 g + i scaled by
+            // (gamma_last / gamma_t) / |k_t|, as pieces at k-step t / 32, lane
+            // 16 ((t % 32) / 8) + n, slots t % 8
+            const float4 sk = *(const float4*)(scl + 3 * C + 16 * wave + 4 * g);
+            const float xs[4] = {dl[0] * sk.x, dl[1] * sk.y, dl[2] * sk.z, dl[3] * sk.w};
+            uint2 pcs[3];
+            dn_split3x4(xs, pcs);
+#pragma unroll
+            for (int pc = 0; pc < 3; pc++)
+                *(uint2*)((char*)&Dp[(pc * (C / 32) + (wave >> 1)) * 64 + 16 * (2 * (wave & 1) + (g >> 1)) + l16] +
+                          8 * (g & 1)) = pcs[pc];
+        }
         if (nf) flag = 1;
         dn_lds_barrier();  // Delta complete
         if (!Q2 && more) {  // the single f32 Q buffer: its reads ended with step b
@@ -797,6 +891,38 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
             dn_f32x4 a0 = gl * s0own[0], a1 = gl * s0own[1];
             dn_f32x4 b0 = {0.0f, 0.0f, 0.0f, 0.0f}, b1 = b0;
             const int j0 = 32 * wave + l16, j1 = j0 + 16;
+            if constexpr (BF) {
+                // A = K^T (state rows 32 w + 16 tt + 0..15, tokens 32 ks + 8 g .. + 7):
+                // two transposing reads of 4 tokens x 16 dims each (lane i of a
+                // 16-lane group supplies token k0 + i / 4, dims d0 + 4 (i % 4) .. + 3,
+                // and receives dims d0 + i of tokens k0 .. k0 + 3); B = the pieces of
+                // the scaled Delta
+#pragma unroll
+                for (int ks = 0; ks < C / 32; ks++) {
+                    uint4 at[2];
+#pragma unroll
+                    for (int tt = 0; tt < 2; tt++) {
+                        dn_s4 part[2];
+#pragma unroll
+                        for (int hf = 0; hf < 2; hf++) {
+                            const int t = 32 * ks + 8 * g + 4 * hf + (l16 >> 2);
+                            const int e = 32 * wave + 16 * tt + 4 * (l16 & 3);
+                            const int pos = (e >> 3) ^ (t & 15);
+                            part[hf] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (__attribute__((address_space(3))) dn_s4*)(kt + t * 256 + pos * 16 + (e & 7) * 2));
+                        }
+                        const uint2 lo2 = __builtin_bit_cast(uint2, part[0]);
+                        const uint2 hi2 = __builtin_bit_cast(uint2, part[1]);
+                        at[tt] = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
+                    }
+#pragma unroll
+                    for (int pc = 0; pc < 3; pc++) {
+                        const uint4 db = Dp[(pc * (C / 32) + ks) * 64 + lane];
+                        a0 = mfma32<DT>(at[0], db, a0);
+                        a1 = mfma32<DT>(at[1], db, a1);
+                    }
+                }
+            } else {
 #pragma unroll
             for (int q = 0; q < C / 16; q++) {
                 const float4 b = *(const float4*)(Dl + (q * 64 + lane) * 4);
@@ -812,12 +938,17 @@ __global__ __launch_bounds__(kChunkThreads, 1) void deltanet_chunk_scan_kernel(c
                 b0 = mfma4(dn_elem<DT>(kt, s + 3, j0), bs[3], b0);
                 b1 = mfma4(dn_elem<DT>(kt, s + 3, j1), bs[3], b1);
             }
+            }
             a0 += b0;
             a1 += b1;
 #pragma unroll
             for (int i = 0; i < 4; i++) nf |= !is_finite_f(a0[i]) || !is_finite_f(a1[i]);
             *(float4*)srow0 = make_float4(a0[0], a0[1], a0[2], a0[3]);
             *(float4*)srow1 = make_float4(a1[0], a1[1], a1[2], a1[3]);
+            if constexpr (BF) {
+                const float v0[4] = {a0[0], a0[1], a0[2], a0[3]}, v1[4] = {a1[0], a1[1], a1[2], a1[3]};
+                store_state_pieces(v0, v1);
+            }
         }
         if (nf) flag = 1;
 #pragma unroll
