@@ -73,6 +73,7 @@ struct DecodePlan {
     size_t ws_ml_bytes;
     size_t ws_q_bytes;      // Turbo: rotated / projected queries
     size_t ws_sched_bytes;  // stream: pair offsets per sequence + range size
+    bool valu = false;      // 16-bit cache on the VALU split kernel (small calls, GQA groups <= 2)
 };
 
 // Stream schedule of the MFMA split kernel (16-bit and Q8 caches).  Keys per
@@ -126,7 +127,11 @@ DecodePlan plan_decode(const gr_decode_args* a) {
     // Measured (MI355X, us per call): Gemma-3-4B window layer (1024 keys, 4 KV
     // heads, bf16 d256) 20.5 stream -> 13.9 with 64-key splits; 4 x 2048 keys, 32 / 4
     // heads, f16 d128: 18.1 -> 15.0 with 128-key splits; the 8193-key global layer
-    // stays faster on the stream schedule (25 vs 30 us).
+    // stays faster on the stream schedule (25 vs 30 us).  With at most two query
+    // heads per KV head those splits run faster on the VALU kernel, whose lanes
+    // serve the group's heads without the MFMA kernel's 16-column tiles: window
+    // layer 16.9 -> 13.4 us, 2 x 1024 keys, 16 / 8 heads, bf16 d128 15.5 -> 12.9-14.5;
+    // larger groups are slower there (4 x 2048 keys, 32 / 4 heads: 15.2 -> 36.7).
     if (pl.stream && split <= 0 && (a->kv_dtype == GR_DTYPE_F16 || a->kv_dtype == GR_DTYPE_BF16) &&
         max_len <= kSmallCallMaxLen) {
         const int sk = std::max(64, (max_len + 16 * 64 - 1) / (16 * 64) * 64);
@@ -134,6 +139,7 @@ DecodePlan plan_decode(const gr_decode_args* a) {
         if (wgs <= kSmallCallMaxWorkgroups) {
             pl.stream = false;
             split = sk;
+            pl.valu = kv_mul <= 2;
         }
     }
     const size_t per_part = turbo ? 2 : 1;  // Turbo: base + residual
@@ -269,7 +275,7 @@ int decode_enqueue_ex(const gr_decode_args* a, const int32_t* seq_slot, hipStrea
     p.gate.head_stride = a->out_gate_head_stride;
     p.ws_o = (float*)a->workspace;
     p.ws_ml = (float*)((char*)a->workspace + pl.ws_o_bytes);
-    p.use_mfma = 1;
+    p.use_mfma = pl.valu ? 0 : 1;
     if (pl.stream) {  // workspace: partials o | (m, l) | Turbo queries | schedule
         p.stream_sched = (int*)((char*)a->workspace + pl.ws_o_bytes + pl.ws_ml_bytes + pl.ws_q_bytes);
         p.stream_min_keys = pl.stream_min_keys;
