@@ -478,6 +478,20 @@ def run_one(args, dev, stream, lens) -> int:
             res[key] = {"ms": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes}
             del keep, call
         res["step_ms"] = 5 * res["local"]["ms"] + res["global"]["ms"]
+    elif args.only == "decode_small":
+        # small 16-bit decode calls (the fixed-grid plan for short contexts): us per call
+        shapes = (("1x1024 bf16 8/4 d256", [1024], 8, 4, 256, torch.bfloat16),
+                  ("2x1024 bf16 16/8 d128", [1024] * 2, 16, 8, 128, torch.bfloat16),
+                  ("1x512 f16 16/8 d128", [512], 16, 8, 128, torch.float16),
+                  ("8x1024 f16 32/8 d128", [1024] * 8, 32, 8, 128, torch.float16),
+                  ("1x4096 f16 32/8 d128", [4096], 32, 8, 128, torch.float16),
+                  ("4x2048 f16 32/4 d128", [2048] * 4, 32, 4, 128, torch.float16))
+        for name, ls, H, G, d, dt in shapes:
+            call, nbytes, keep = rotating(
+                lambda sd: decode_workload(dev, ls, sd, n_heads=H, n_kv=G, d=d, kv_dtype=dt), 5)
+            ms, _ = _timed(call, args.steps, args.warmup, stream)
+            res[name] = round(ms * 1e3, 2)
+            del keep, call
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -526,7 +540,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
+                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
