@@ -847,11 +847,19 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
                           packs[pc].tp > 0 ? &packs[pc] : nullptr, se_dev[pc]);
     };
 
-    if (n_pieces == 1) {
-        if ((rc = h2d(s, qin[0], q, qb)) || (rc = h2d(s, kin[0], k, kb)) || (rc = h2d(s, vin[0], v, kb))) return rc;
-        if (se_dev[0] && (rc = h2d(s, se_dev[0], se[0].data(), 4 * se[0].size()))) return rc;
-        if ((rc = enqueue(0))) return rc;
-        return d2h_sync(s, xb, xo, qb);
+    if (n_pieces == 1 || !xfer_pipe_prepare(s->xfer, s->pipe)) {
+        // one piece, or no pinned memory for the pipeline: the pieces in turn
+        for (int pc = 0; pc < n_pieces; pc++) {
+            const size_t r0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+            if ((rc = h2d(s, qin[pc], q + r0 * s->q_dim, 4 * n * s->q_dim)) ||
+                (rc = h2d(s, kin[pc], k + r0 * s->kv_dim, 4 * n * s->kv_dim)) ||
+                (rc = h2d(s, vin[pc], v + r0 * s->kv_dim, 4 * n * s->kv_dim)))
+                return rc;
+            if (se_dev[pc] && (rc = h2d(s, se_dev[pc], se[pc].data(), 4 * se[pc].size()))) return rc;
+            if ((rc = enqueue(pc))) return rc;
+            if ((rc = d2h_sync(s, xb + r0 * s->q_dim, xo + r0 * s->q_dim, 4 * n * s->q_dim))) return rc;
+        }
+        return GR_OK;
     }
     std::vector<XferRange> ups, downs;
     for (int pc = 0; pc < n_pieces; pc++) {

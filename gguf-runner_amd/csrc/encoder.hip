@@ -297,12 +297,12 @@ __global__ __launch_bounds__(kEmThreads, (DP <= 128 ? 2 : 1)) void encoder_mfma_
 // ---------------------------------------------------------------- bf16-piece MFMA path
 //
 // Head dims up to 128: the same tiling on v_mfma_f32_32x32x16_bf16 with every f32
-// operand cut into three exact bf16 pieces (x = hi + mid + lo: hi keeps the first 8
-// significant bits by truncation, mid the next 8 of the exact residual, lo the rest)
-// and each product taken as the six piece products whose weight is at least 2^-16
-// of hi * hi (the three dropped ones are below 2^-24 relative, under the f32
-// rounding of the sum): products of bf16 values are exact and the MFMA sums them
-// in fp32.  Six bf16 MFMAs of 16 dims cost 3/8 of the f32 MFMA time for the same
+// operand cut into three exact bf16 pieces (x = hi + mid + lo, each the
+// round-to-nearest bf16 of what the pieces before it leave: |mid| <= 2^-8 |x|,
+// |lo| <= 2^-16 |x|, and lo holds the rest exactly) and each product taken as the
+// six piece products hi hi, hi mid, mid hi, hi lo, mid mid, lo hi (the three
+// dropped ones add at most ~2^-23 of |x y|, the size of the f32 rounding of the
+// sum): products of bf16 values are exact and the MFMA sums them in fp32.  Six bf16 MFMAs of 16 dims cost 3/8 of the f32 MFMA time for the same
 // dims (bf16 runs 16 x the f32 matrix rate on this part).  K and V tiles sit in
 // LDS as pieces, row-major [key][dim]; the V^T operand comes from transposing
 // reads (ds_read_b64_tr_b16); Q is cut once per query row, P once per sub-tile.
@@ -324,23 +324,25 @@ __device__ __forceinline__ em_f32x16 em_mma6(const uint4* a, const uint4* b, em_
     c = em_mma(a[2], b[0], c);
     return c;
 }
-__device__ __forceinline__ void em_split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
-    hi = __float_as_uint(x) & 0xffff0000u;
-    const float r1 = x - __uint_as_float(hi);
-    mid = __float_as_uint(r1) & 0xffff0000u;
-    lo = __float_as_uint(r1 - __uint_as_float(mid)) & 0xffff0000u;
+typedef __bf16 em_b2 __attribute__((ext_vector_type(2)));
+typedef float em_f2 __attribute__((ext_vector_type(2)));
+// two floats as a word of two round-to-nearest bf16 (v_cvt_pk_bf16_f32), and back
+__device__ __forceinline__ uint32_t em_bf2(em_f2 v) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, em_b2));
+}
+__device__ __forceinline__ em_f2 em_unbf2(uint32_t w) {
+    return em_f2{__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
 }
 // pieces of 2 n floats as n words each (two bf16 per word, element 2 i low)
 template <int N>
 __device__ __forceinline__ void em_split_words(const float* x, uint32_t* hi, uint32_t* mid, uint32_t* lo) {
 #pragma unroll
     for (int i = 0; i < N; i++) {
-        uint32_t h0, m0, l0, h1, m1, l1;
-        em_split3(x[2 * i], h0, m0, l0);
-        em_split3(x[2 * i + 1], h1, m1, l1);
-        hi[i] = (h0 >> 16) | h1;
-        mid[i] = (m0 >> 16) | m1;
-        lo[i] = (l0 >> 16) | l1;
+        const em_f2 v = {x[2 * i], x[2 * i + 1]};
+        hi[i] = em_bf2(v);
+        const em_f2 r1 = v - em_unbf2(hi[i]);  // exact
+        mid[i] = em_bf2(r1);
+        lo[i] = em_bf2(r1 - em_unbf2(mid[i]));  // exact (at most 8 significant bits left)
     }
 }
 

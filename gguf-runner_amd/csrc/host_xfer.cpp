@@ -262,6 +262,8 @@ void xfer_release(HostXfer& x) {
     x.ring = nullptr;
 }
 
+bool xfer_pipe_prepare(HostXfer& upr, XferPipe& pp) { return ensure_ring(upr) && pipe_init(pp); }
+
 hipError_t xfer_pipeline(HostXfer& upr, XferPipe& pp, hipStream_t work, int n_pieces,
                          const std::vector<XferRange>& ups, const std::vector<XferRange>& downs,
                          const std::function<int(int)>& enqueue, int* status) {

@@ -78,6 +78,11 @@ hipError_t xfer_pipeline(HostXfer& up_ring, XferPipe& pipe, hipStream_t work, in
                          const std::vector<XferRange>& ups, const std::vector<XferRange>& downs,
                          const std::function<int(int)>& enqueue, int* status);
 
+// Allocates what xfer_pipeline needs (both rings, the streams, the events) if it
+// is not there yet; false when that fails (no pinned memory), and the caller
+// then moves its pieces one after another with xfer_h2d / xfer_d2h.
+bool xfer_pipe_prepare(HostXfer& up_ring, XferPipe& pipe);
+
 // Destroys the pipe's streams, events and ring (after its work has finished).
 void xfer_pipe_release(XferPipe& pipe);
 

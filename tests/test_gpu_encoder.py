@@ -18,6 +18,7 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
+TOL_STRESS = 1e-4  # inputs scaled by 3-4 (see test_encoder_attention_matches_oracle)
 
 
 def _within(got, ref, tol=TOL):
@@ -50,20 +51,44 @@ def test_encoder_attention_reference_fixture(orc, dev):
     assert np.all(got[:tps] < 10.0) and np.all(got[tps:] > 90.0)
 
 
-@pytest.mark.parametrize("ns,tps,hc,hd", [(1, 1, 2, 64), (2, 17, 4, 72), (3, 300, 16, 80),
-                                          (1, 1025, 16, 64), (2, 256, 8, 128), (1, 100, 3, 20),
-                                          (1, 50, 2, 100), (2, 5, 2, 256), (1, 333, 4, 256),
-                                          (2, 70, 3, 160), (1, 129, 2, 192), (1, 40, 2, 136)])
-def test_encoder_attention_matches_oracle(orc, dev, ns, tps, hc, hd):
+@pytest.mark.parametrize("ns,tps,hc,hd,mag", [(1, 1, 2, 64, 1), (2, 17, 4, 72, 1), (3, 300, 16, 80, 1),
+                                              (1, 1025, 16, 64, 1), (2, 256, 8, 128, 1), (1, 100, 3, 20, 1),
+                                              (1, 50, 2, 100, 1), (2, 5, 2, 256, 1), (1, 333, 4, 256, 1),
+                                              (2, 70, 3, 160, 1), (1, 129, 2, 192, 1), (1, 40, 2, 136, 1),
+                                              (1, 200, 4, 96, 1), (2, 150, 2, 88, 1), (1, 300, 4, 72, 4),
+                                              (1, 200, 2, 128, 3)])
+def test_encoder_attention_matches_oracle(orc, dev, ns, tps, hc, hd, mag):
     """Sequences of 1 to 1025 tokens; head dims of the vision encoders (64, 72, 80),
-    dims that run zero-padded (20 -> 32, 100 -> 128, 136 / 160 -> 192) and the 192 / 256
-    tilings (one wave per SIMD, 32-key tiles; every length on the MFMA kernel)."""
-    rng = np.random.default_rng(ns * 1000 + tps + hd)
-    q, k, v = (rng.standard_normal((ns * tps, hc * hd)).astype(np.float32) for _ in range(3))
+    dims that run zero-padded (20 -> 32, 88 -> 96, 100 -> 128, 136 / 160 -> 192) and the
+    192 / 256 tilings (one wave per SIMD, 32-key tiles; every length on the MFMA
+    kernel).  Up to head_dim 128 the products run as bf16 piece products; inputs scaled
+    by mag = 3, 4 give scores up to ~100 (peaked softmax rows, outputs dominated by a
+    few keys).  At those magnitudes the fp32 summation order alone moves outputs by
+    several 1e-5 (scores |q.k| ~ 100 carry ~1e-5 absolute rounding, amplified by the
+    peaked softmax): the f32 MFMA kernel this one replaced measured 5.5e-5 from a
+    float64 evaluation where the oracle's sequential sums measured 1.0e-5, and this
+    kernel 4.0e-5.  There the device is held to the oracle's own distance from float64
+    plus 1e-4 (TOL_STRESS)."""
+    rng = np.random.default_rng(ns * 1000 + tps + hd + mag)
+    q, k, v = (mag * rng.standard_normal((ns * tps, hc * hd)).astype(np.float32) for _ in range(3))
     shape = dict(n_seq=ns, tokens=tps, heads=hc, head_dim=hd)
     got = _run(dev, q, k, v, **shape)
     ref = orc.encoder_self_attention(q, k, v, n_threads=orc.env_threads(), **shape)
-    assert _within(got, ref), f"max abs {np.abs(got - ref).max():.3e}"
+    if mag == 1:
+        assert _within(got, ref), f"max abs {np.abs(got - ref).max():.3e}"
+        return
+    exact = np.empty((ns * tps, hc * hd))
+    for sq in range(ns):
+        rows = slice(sq * tps, (sq + 1) * tps)
+        for h in range(hc):
+            sl = slice(h * hd, (h + 1) * hd)
+            sc = (q[rows, sl].astype(np.float64) @ k[rows, sl].astype(np.float64).T) / np.sqrt(hd)
+            w = np.exp(sc - sc.max(axis=1, keepdims=True))
+            exact[rows, sl] = (w / w.sum(axis=1, keepdims=True)) @ v[rows, sl].astype(np.float64)
+    scale = np.maximum(np.abs(exact), 1.0)
+    e_gpu = float((np.abs(got - exact) / scale).max())
+    e_orc = float((np.abs(ref - exact) / scale).max())
+    assert e_gpu <= e_orc + TOL_STRESS, f"device {e_gpu:.3e} vs oracle {e_orc:.3e} from float64"
 
 
 def test_encoder_attention_sizes(dev):
