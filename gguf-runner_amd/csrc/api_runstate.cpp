@@ -652,32 +652,23 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
 
 // Large calls run their rows in pieces so that the uploads of piece p + 1, the
 // kernels of piece p and the downloads of piece p - 1 overlap (xfer_pipeline):
-// calls of at least kPipeMinBytes of host rows and two pieces' worth of rows.
-// The first and the last piece take half the rows of the others (256, then
-// pieces of ~512, then 256), which shortens the upload before the first kernel
-// and the kernels and download after the last upload.  Causal rows only: an
-// image block's rows see the whole block, so all of its K / V writes precede
-// its attention.  Over a Turbo cache every piece keeps >= 2048 (row group, KV
-// head) workgroups (equal pieces), so its split kernel still finishes the rows
-// itself.
+// calls of at least kPipeMinBytes of host rows and 1024 rows.  The first and the
+// last piece take 256 rows, the ones between ~512 or more (at most eight pieces),
+// which shortens the upload before the first kernel and the kernels and download
+// after the last upload.  (Over a Turbo cache a piece of >= 2048 (row group, KV
+// head) workgroups gets one split per group, finished in the split kernel; the
+// smaller ones a few splits and the combine kernel.  Measured, 2048 rows, 32 / 8
+// heads: 2.06-2.34 ms as two 1024-row single-split pieces, 1.81-1.97 ms as 256,
+// 512, 512, 512, 256.)  Causal rows only: an image block's rows see the whole
+// block, so all of its K / V writes precede its attention.
 constexpr size_t kPipeMinBytes = size_t(16) << 20;
 
-static std::vector<int> row_pieces(const gr_run_state* s, int m, bool block, size_t bytes) {
-    const int kv_mul = s->cfg.n_heads / s->cfg.n_kv_heads;
-    const int tp = turbo_pack_rows(s->d, kv_mul);
-    const bool turbo_pack = is_turbo(s) && tp * kv_mul <= 16;
-    const int min_rows = turbo_pack ? std::max(512, (2048 + s->cfg.n_kv_heads - 1) / s->cfg.n_kv_heads * tp) : 512;
-    if (block || bytes < kPipeMinBytes || m < 2 * min_rows) return {0, m};
-    std::vector<int> cut;
-    if (turbo_pack) {
-        const int n = std::min(XferPipe::kMaxPieces, m / min_rows);
-        for (int i = 0; i <= n; i++) cut.push_back((int)((int64_t)m * i / n));
-        return cut;
-    }
-    const int half = min_rows / 2;
-    const int n_mid = std::max(1, std::min(XferPipe::kMaxPieces - 2, (m - 2 * half + min_rows / 2) / min_rows));
-    cut.push_back(0);
-    for (int i = 0; i <= n_mid; i++) cut.push_back(half + (int)((int64_t)(m - 2 * half) * i / n_mid));
+static std::vector<int> row_pieces(int m, bool block, size_t bytes) {
+    constexpr int kEdge = 256, kMid = 512;
+    if (block || bytes < kPipeMinBytes || m < 2 * kMid) return {0, m};
+    const int n_mid = std::max(1, std::min(XferPipe::kMaxPieces - 2, (m - 2 * kEdge + kMid / 2) / kMid));
+    std::vector<int> cut = {0};
+    for (int i = 0; i <= n_mid; i++) cut.push_back(kEdge + (int)((int64_t)(m - 2 * kEdge) * i / n_mid));
     cut.push_back(m);
     return cut;
 }
@@ -703,7 +694,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
             ends[i] = (int32_t)(base_pos + m);
         }
     }
-    const std::vector<int> cut = row_pieces(s, m, block, 2 * qb + 2 * kb);
+    const std::vector<int> cut = row_pieces(m, block, 2 * qb + 2 * kb);
     const int n_pieces = (int)cut.size() - 1;
     const int kv_mul = s->cfg.n_heads / s->cfg.n_kv_heads;
     // the MFMA prefill's arguments for n rows from position pos0 (sizes first: its

@@ -377,8 +377,8 @@ def test_quantised_prefill_into_a_middle_sequence_slot(orc, dev, kv):
 @pytest.mark.parametrize("block,window", [(False, None), (True, 700)])
 def test_q8_large_chunks_run_in_overlapped_pieces(orc, dev, block, window):
     """Chunks of 2048 and 1024 rows at the config-2 shape (32 / 8 heads, d128): above
-    16 MB of host rows the run-state call cuts its rows into pieces of >= 512 rows (4,
-    then 2) whose uploads, kernels and downloads overlap, each piece written to the
+    16 MB of host rows the run-state call cuts its rows into pieces (256, 512, 512, 512,
+    256 rows, then 256, 512, 256) whose uploads, kernels and downloads overlap, each piece written to the
     cache before the next one's queries read it.  The K / V codes and scales of every
     row == the oracle's quantize_row_q8 (bit-exact); sampled output rows of both chunks
     (piece edges included) == the oracle's attention_token over those rows (1e-5)."""
@@ -404,7 +404,7 @@ def test_q8_large_chunks_run_in_overlapped_pieces(orc, dev, block, window):
     assert np.array_equal(kq, ck[0]) and np.array_equal(vq, cv[0])
     assert np.array_equal(ks.reshape(sk[0].shape), sk[0]) and np.array_equal(vs.reshape(sv[0].shape), sv[0])
     fmt = orc.Q8B if block else orc.Q8
-    rows = sorted({0, 1, 511, 512, 1023, 1024, 1535, 1536, 2047, 2048, 2559, 2560, n - 1}
+    rows = sorted({0, 1, 255, 256, 767, 768, 1279, 1280, 1791, 1792, 2047, 2048, 2303, 2304, 2815, 2816, n - 1}
                   | set(rng.integers(0, n, 10).tolist()))
     worst = 0.0
     for t in rows:

@@ -317,8 +317,8 @@ def test_large_host_rows_through_the_pinned_ring(dev):
 @pytest.mark.parametrize("kv_dtype,window", [(1, None), (2, 300)])
 def test_large_f16_chunk_runs_in_overlapped_pieces(dev, orc, kv_dtype, window):
     """A 2048-row chunk over an f16 / bf16 cache (32 / 8 heads, d128, global or
-    window-300 layer) is cut into four overlapped pieces of 512 rows; the MFMA
-    prefill of each piece sees the rows the pieces before it wrote.  The cache rows
+    window-300 layer) is cut into overlapped pieces of 256, 512, 512, 512 and 256
+    rows; the MFMA prefill of each piece sees the rows the pieces before it wrote.  The cache rows
     == the host rows rounded to the cache type (bit-exact) and sampled output rows
     (piece edges included) == the oracle's attention_token over the device's rows,
     to the 16-bit MFMA bar."""
@@ -336,7 +336,7 @@ def test_large_f16_chunk_runs_in_overlapped_pieces(dev, orc, kv_dtype, window):
     cast = orc.c_f32_to_f16 if kv_dtype == ffi.DTYPE_F16 else orc.c_f32_to_bf16
     assert np.array_equal(kd.reshape(-1), cast(k)) and np.array_equal(vd.reshape(-1), cast(v))
     fmt = orc.F16 if kv_dtype == ffi.DTYPE_F16 else orc.BF16
-    rows = sorted({0, 1, 511, 512, 1023, 1024, 1535, 1536, m - 1} | set(rng.integers(0, m, 8).tolist()))
+    rows = sorted({0, 1, 255, 256, 767, 768, 1279, 1280, 1791, 1792, m - 1} | set(rng.integers(0, m, 8).tolist()))
     for t in rows:
         start = max(0, t + 1 - window) if window else 0
         ref = orc.attention_token(q[t], kd, vd, fmt, n_heads, n_kv, d, start, t + 1)

@@ -270,15 +270,17 @@ def test_turbo_prefill_chunk_token_packed(orc, dev, n_heads, n_kv, window, image
     assert worst <= TOL, worst
 
 
-@pytest.mark.parametrize("n_heads,n_kv,d,m,window", [(32, 8, 128, 1100, None), (32, 8, 128, 1100, 300),
-                                                     (16, 8, 256, 1100, None), (16, 8, 64, 2100, None)])
+@pytest.mark.parametrize("n_heads,n_kv,d,m,window", [(32, 8, 128, 6656, None), (32, 8, 128, 6656, 300),
+                                                     (16, 8, 256, 6656, None), (16, 8, 64, 12800, None)])
 def test_turbo_prefill_chunk_single_split_finished_in_split_kernel(orc, dev, n_heads, n_kv, d, m, window):
-    """Chunks with at least 2048 (row group, KV head) workgroups get one split per
-    group (1100 rows in groups of 4 x 8 KV heads = 2200; d64: 2100 rows in groups of
-    8 = 2104), and the split kernel finishes those rows itself (1/l, the inverse
-    rotations, the output store) with no partials and no combine launch.  Sampled
-    rows (the first two groups, the middle, the end and 12 random rows) == the
-    oracle's attention_token_turbo with each row's causal or window range (1e-5)."""
+    """A chunk runs as overlapped pieces of 256 rows, six middle pieces and 256 rows;
+    a piece with at least 2048 (row group, KV head) workgroups gets one split per
+    group (the middle pieces here: 1024 rows in groups of 4 x 8 KV heads = 2048; d64:
+    2048 rows in groups of 8), and the split kernel finishes those rows itself (1/l,
+    the inverse rotations, the output store) with no partials and no combine launch;
+    the 256-row edge pieces take several splits and the combine.  Sampled rows (the
+    first two groups, every piece edge, the end and 12 random rows) == the oracle's
+    attention_token_turbo with each row's causal or window range (1e-5)."""
     from gguf_runner_amd import ffi, runtime as rt
     p = rt.Config(n_layers=2, n_heads=n_heads, n_kv_heads=n_kv, head_dim=d, seq_len=m + 8,
                   kv_dtype=ffi.DTYPE_TURBO, rope_mode=ffi.ROPE_NONE, layer_windows=[window, window])
@@ -293,7 +295,9 @@ def test_turbo_prefill_chunk_single_split_finished_in_split_kernel(orc, dev, n_h
     c = orc.TurboCache(m, n_kv, d)
     for t in range(m):
         orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
-    rows = sorted(set(range(8)) | {m // 2, m // 2 + 1, m - 2, m - 1} | set(rng.integers(0, m, 12).tolist()))
+    edges = [256 + (m - 512) * i // 6 for i in range(7)]
+    rows = sorted(set(range(8)) | {e + o for e in edges for o in (-1, 0)} | {m - 2, m - 1}
+                  | set(rng.integers(0, m, 12).tolist()))
     worst = 0.0
     for i in rows:
         start = max(0, i + 1 - window) if window else 0
@@ -367,11 +371,10 @@ def test_turbo_decode_stream_sequence_limit(orc, dev, n_seq):
 
 def test_turbo_large_chunk_runs_in_overlapped_pieces(orc, dev):
     """A 2048-row chunk at the config-2 shape over a Turbo cache, then a 1024-row
-    one: the first is cut into two overlapped pieces of 1024 rows (each keeps one
-    split kernel workgroup per (row group, KV head) and finishes its rows itself),
-    the second stays whole.  Every row's Turbo encoding == the oracle's
-    (bit-exact); sampled output rows of both chunks == the oracle's
-    attention_token_turbo (1e-5)."""
+    one: overlapped pieces of 256, 512, 512, 512, 256 and of 256, 512, 256 rows,
+    each piece's keys written before the next piece's queries read them.  Every
+    row's Turbo encoding == the oracle's (bit-exact); sampled output rows of both
+    chunks == the oracle's attention_token_turbo (1e-5)."""
     from gguf_runner_amd import ffi, runtime as rt
     n_heads, n_kv, d, layer = 32, 8, 128, 0
     m1, m2 = 2048, 1024
@@ -391,7 +394,8 @@ def test_turbo_large_chunk_runs_in_overlapped_pieces(orc, dev):
     for t in range(n):
         orc.kv_write_turbo(c, t, k[t], v[t], table, layer)
     _assert_rows_equal(rt.read_turbo_rows(p, s, layer, 0, n), c, 0, n, n_kv, d)
-    rows = sorted({0, 1, 1023, 1024, 1025, 2047, 2048, n - 1} | set(rng.integers(0, n, 10).tolist()))
+    rows = sorted({0, 1, 255, 256, 767, 768, 1279, 1280, 1791, 1792, 2047, 2048, 2303, 2304, 2815, 2816, n - 1}
+                  | set(rng.integers(0, n, 10).tolist()))
     worst = 0.0
     for t in rows:
         ref = orc.attention_token_turbo(q[t], c, table, layer, n_heads, 0, t + 1)
