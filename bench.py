@@ -438,6 +438,32 @@ def deltanet_workload(dev, T, seed, H=16, d=128):
     return call, (q, k, v, beta, gate, state, out)
 
 
+def ssm_runstate_workload(T, seed, H=16, d=128, K=4):
+    """Config 5's heads through the run-state DeltaNet calls with host rows, T tokens
+    per call: gr_qwen3next_ssm_layer (conv + SiLU, q / k normalisation, gates, the
+    chunked scan, gated RMSNorm; host qkv / z / gate rows in, ssm_proj rows out) and
+    gr_qwen3next_prefill (host q / k / v / gate / beta rows in, outputs out)."""
+    from gguf_runner_amd import runtime as rt
+    rng = np.random.default_rng(seed)
+    conv_dim = 3 * H * d
+    p = rt.Config(n_layers=1, n_heads=1, n_kv_heads=1, head_dim=128, seq_len=8, ssm_n_heads=H,
+                  ssm_head_dim=d, ssm_n_k_heads=H, ssm_conv_kernel=K, rms_norm_eps=1e-6,
+                  ssm_conv1d=(0.3 * rng.standard_normal((1, conv_dim, K))).astype(np.float32),
+                  ssm_a=-rng.uniform(0.2, 1.2, (1, H)).astype(np.float32),
+                  ssm_dt_bias=(0.1 * rng.standard_normal((1, H))).astype(np.float32),
+                  ssm_norm=(1 + 0.1 * rng.standard_normal((1, d))).astype(np.float32))
+    s = rt.malloc_run_state(p)
+    qkv = rng.standard_normal((T, conv_dim)).astype(np.float32)
+    z = rng.standard_normal((T, H * d)).astype(np.float32)
+    ga = rng.standard_normal((T, 2 * H)).astype(np.float32)
+    q, k, v = (rng.standard_normal((T, H * d)).astype(np.float32) for _ in range(3))
+    gate = rng.uniform(-0.1, 0, (T, H)).astype(np.float32)
+    beta = rng.uniform(0, 1, (T, H)).astype(np.float32)
+    layer = lambda: rt.qwen3next_ssm_layer(p, s, 0, qkv, z, ga)
+    prefill = lambda: rt.qwen3next_prefill(p, s, 0, q, k, v, gate, beta)
+    return layer, prefill, (p, s)
+
+
 def run_one(args, dev, stream, lens) -> int:
     """A single workload, for rocprofv3 runs; prints one short JSON line."""
     import torch
@@ -504,6 +530,12 @@ def run_one(args, dev, stream, lens) -> int:
                                                 turbo=args.only.endswith("turbo"))
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "ssm2k":
+        # synchronous host-buffer calls, 2048 tokens each (wall time incl. PCIe copies)
+        layer, prefill, keep = ssm_runstate_workload(2048, 9)
+        _, lw = _timed(layer, args.steps, args.warmup, stream)
+        _, pw = _timed(prefill, args.steps, args.warmup, stream)
+        res.update(ssm_layer_call_ms=lw, prefill_call_ms=pw, tokens=2048)
     elif args.only == "prefill8k_d256":
         # config 4 shape (Gemma-3-4B): the sliding-window (1024) and the global layer
         for W, key in ((1024, "local"), (0, "global")):
@@ -541,7 +573,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet",
+                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <vector>
 
@@ -663,14 +664,38 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
 // block, so all of its K / V writes precede its attention.
 constexpr size_t kPipeMinBytes = size_t(16) << 20;
 
-static std::vector<int> row_pieces(int m, bool block, size_t bytes) {
+static std::vector<int> row_pieces(int m, bool block, size_t bytes, int align = 1) {
     constexpr int kEdge = 256, kMid = 512;
     if (block || bytes < kPipeMinBytes || m < 2 * kMid) return {0, m};
     const int n_mid = std::max(1, std::min(XferPipe::kMaxPieces - 2, (m - 2 * kEdge + kMid / 2) / kMid));
     std::vector<int> cut = {0};
-    for (int i = 0; i <= n_mid; i++) cut.push_back(kEdge + (int)((int64_t)(m - 2 * kEdge) * i / n_mid));
+    for (int i = 0; i <= n_mid; i++)
+        cut.push_back((kEdge + (int)((int64_t)(m - 2 * kEdge) * i / n_mid)) / align * align);
     cut.push_back(m);
     return cut;
+}
+
+// The pieces of a call: each piece's host rows `ups` go up, enqueue(pc) adds its
+// kernels to the state's stream and its output rows `downs` come back.  Several
+// pieces run pipelined (xfer_pipeline) when the pinned rings can be had, else
+// one after another through the state's own copies.
+static int run_pieces(gr_run_state* s, int n_pieces, const std::vector<XferRange>& ups,
+                      const std::vector<XferRange>& downs, const std::function<int(int)>& enqueue) {
+    int rc = GR_OK;
+    if (n_pieces > 1 && xfer_pipe_prepare(s->xfer, s->pipe)) {
+        const hipError_t e = xfer_pipeline(s->xfer, s->pipe, s->stream, n_pieces, ups, downs, enqueue, &rc);
+        if (rc) return rc;
+        return e == hipSuccess ? GR_OK : hip_fail(e, "pipelined host transfers");
+    }
+    size_t iu = 0, id = 0;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        for (; iu < ups.size() && ups[iu].piece == pc; iu++)
+            if ((rc = h2d(s, ups[iu].dev, ups[iu].host, ups[iu].bytes))) return rc;
+        if ((rc = enqueue(pc))) return rc;
+        for (; id < downs.size() && downs[id].piece == pc; id++)
+            if ((rc = d2h_sync(s, downs[id].host, downs[id].dev, downs[id].bytes))) return rc;
+    }
+    return GR_OK;
 }
 
 // The rows base_pos..base_pos+m-1 of one layer: QK-norm, RoPE and KV write of
@@ -838,20 +863,6 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
                           packs[pc].tp > 0 ? &packs[pc] : nullptr, se_dev[pc]);
     };
 
-    if (n_pieces == 1 || !xfer_pipe_prepare(s->xfer, s->pipe)) {
-        // one piece, or no pinned memory for the pipeline: the pieces in turn
-        for (int pc = 0; pc < n_pieces; pc++) {
-            const size_t r0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
-            if ((rc = h2d(s, qin[pc], q + r0 * s->q_dim, 4 * n * s->q_dim)) ||
-                (rc = h2d(s, kin[pc], k + r0 * s->kv_dim, 4 * n * s->kv_dim)) ||
-                (rc = h2d(s, vin[pc], v + r0 * s->kv_dim, 4 * n * s->kv_dim)))
-                return rc;
-            if (se_dev[pc] && (rc = h2d(s, se_dev[pc], se[pc].data(), 4 * se[pc].size()))) return rc;
-            if ((rc = enqueue(pc))) return rc;
-            if ((rc = d2h_sync(s, xb + r0 * s->q_dim, xo + r0 * s->q_dim, 4 * n * s->q_dim))) return rc;
-        }
-        return GR_OK;
-    }
     std::vector<XferRange> ups, downs;
     for (int pc = 0; pc < n_pieces; pc++) {
         const size_t r0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
@@ -861,10 +872,7 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         if (se_dev[pc]) ups.push_back({(char*)se_dev[pc], (char*)se[pc].data(), 4 * se[pc].size(), pc});
         downs.push_back({(char*)(xo + r0 * s->q_dim), (char*)(xb + r0 * s->q_dim), 4 * n * s->q_dim, pc});
     }
-    int status = GR_OK;
-    const hipError_t e = xfer_pipeline(s->xfer, s->pipe, s->stream, n_pieces, ups, downs, enqueue, &status);
-    if (status) return status;
-    return e == hipSuccess ? GR_OK : hip_fail(e, "pipelined host transfers");
+    return run_pieces(s, n_pieces, ups, downs, enqueue);
 }
 
 int gr_prefill_attention_chunk(gr_run_state* s, int32_t seq, int32_t layer, int64_t base_pos, int32_t m,
@@ -996,37 +1004,65 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
     if (!q || !k || !v || !gate || !beta || !out) return fail(GR_ERR_ARG, "null buffer");
     DeviceScope dsc(s->device);
     const int H = s->cfg.ssm_n_heads, D = s->cfg.ssm_head_dim;
-    const size_t rb = 4 * (size_t)T * H * D, gb = 4 * (size_t)T * H;
-    gr_deltanet_args a{};
-    a.n_tokens = T;
-    a.n_heads = H;
-    a.head_dim = D;
-    a.in_dtype = GR_DTYPE_F32;
-    a.l2norm = 1;
-    a.algo = GR_DELTANET_AUTO;
-    a.eps = s->eps;
-    const size_t ws = deltanet_ws(&a);
-    if ((rc = ensure_stage(s, 4 * rb + 2 * gb + ws + 8192))) return rc;
+    const size_t rw = (size_t)H * D;  // floats per token row
+    // Pieces at multiples of the chunked scan's 64 tokens (the state carries
+    // over in device memory, in stream order): the chunks are those of one call.
+    const std::vector<int> cut = row_pieces(T, false, 4 * (size_t)T * (4 * rw + 2 * H), 64);
+    const int n_pieces = (int)cut.size() - 1;
+    auto args = [&](int n) {
+        gr_deltanet_args a{};
+        a.n_tokens = n;
+        a.n_heads = H;
+        a.head_dim = D;
+        a.in_dtype = GR_DTYPE_F32;
+        a.l2norm = 1;
+        a.algo = GR_DELTANET_AUTO;
+        a.eps = s->eps;
+        return a;
+    };
+    size_t ws = 0, in_bytes = 0;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const gr_deltanet_args a = args(cut[pc + 1] - cut[pc]);
+        ws = std::max(ws, deltanet_ws(&a));
+        in_bytes += align_up(4 * (size_t)(cut[pc + 1] - cut[pc]) * (3 * rw + 2 * H) + 4 * 256, 256);
+    }
+    if ((rc = ensure_stage(s, in_bytes + 4 * (size_t)T * rw + ws + 8192))) return rc;
+    // per piece, its q, k, v, gate and beta rows back to back (one upload DMA)
     Carve cv(s->stage);
-    float* qd = cv.take<float>((size_t)T * H * D);
-    float* kd = cv.take<float>((size_t)T * H * D);
-    float* vd = cv.take<float>((size_t)T * H * D);
-    float* od = cv.take<float>((size_t)T * H * D);
-    float* gd = cv.take<float>((size_t)T * H);
-    float* bd = cv.take<float>((size_t)T * H);
-    if ((rc = h2d(s, qd, q, rb)) || (rc = h2d(s, kd, k, rb)) || (rc = h2d(s, vd, v, rb)) ||
-        (rc = h2d(s, gd, gate, gb)) || (rc = h2d(s, bd, beta, gb)))
-        return rc;
-    a.q = qd;
-    a.k = kd;
-    a.v = vd;
-    a.gate = gd;
-    a.beta = bd;
-    a.state = s->ssm + (size_t)layer * s->ssm_layer;
-    a.out = od;
-    a.workspace = ws ? cv.take<char>(ws) : nullptr;
-    if ((rc = deltanet_enqueue(&a, s->stream))) return rc;
-    return d2h_sync(s, out, od, rb);
+    std::vector<XferRange> ups, downs;
+    std::vector<float*> qd(n_pieces), kd(n_pieces), vd(n_pieces), gd(n_pieces), bd(n_pieces);
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+        qd[pc] = cv.take<float>(n * rw);
+        kd[pc] = cv.take<float>(n * rw);
+        vd[pc] = cv.take<float>(n * rw);
+        gd[pc] = cv.take<float>(n * H);
+        bd[pc] = cv.take<float>(n * H);
+        ups.push_back({(char*)qd[pc], (char*)(q + t0 * rw), 4 * n * rw, pc});
+        ups.push_back({(char*)kd[pc], (char*)(k + t0 * rw), 4 * n * rw, pc});
+        ups.push_back({(char*)vd[pc], (char*)(v + t0 * rw), 4 * n * rw, pc});
+        ups.push_back({(char*)gd[pc], (char*)(gate + t0 * H), 4 * n * H, pc});
+        ups.push_back({(char*)bd[pc], (char*)(beta + t0 * H), 4 * n * H, pc});
+    }
+    float* od = cv.take<float>((size_t)T * rw);
+    char* wsp = ws ? cv.take<char>(ws) : nullptr;  // shared by the pieces (stream order)
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+        downs.push_back({(char*)(od + t0 * rw), (char*)(out + t0 * rw), 4 * n * rw, pc});
+    }
+    auto enqueue = [&](int pc) {
+        gr_deltanet_args a = args(cut[pc + 1] - cut[pc]);
+        a.q = qd[pc];
+        a.k = kd[pc];
+        a.v = vd[pc];
+        a.gate = gd[pc];
+        a.beta = bd[pc];
+        a.state = s->ssm + (size_t)layer * s->ssm_layer;
+        a.out = od + (size_t)cut[pc] * rw;
+        a.workspace = deltanet_ws(&a) ? wsp : nullptr;
+        return deltanet_enqueue(&a, s->stream);
+    };
+    return run_pieces(s, n_pieces, ups, downs, enqueue);
 }
 
 int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const float* qkv, const float* z,
@@ -1042,70 +1078,104 @@ int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const floa
     const int nv = s->cfg.ssm_n_heads, d = s->cfg.ssm_head_dim, K = s->cfg.ssm_conv_kernel;
     const size_t cd = (size_t)s->ssm_conv_dim, di = (size_t)nv * d;
     const size_t ga_rows = gate_b ? (size_t)nv : 2 * (size_t)nv;
-    gr_deltanet_args a{};
-    a.n_tokens = T;
-    a.n_heads = nv;
-    a.head_dim = d;
-    a.in_dtype = GR_DTYPE_F32;
-    a.l2norm = 1;
-    a.algo = GR_DELTANET_AUTO;
-    a.eps = s->eps;
-    const size_t ws = deltanet_ws(&a);
-    const size_t need = 4 * ((size_t)T * (cd + 6 * di + ga_rows + 3 * nv)) + ws + 16384;
-    if ((rc = ensure_stage(s, need))) return rc;
+    const size_t gb_rows = gate_b ? (size_t)nv : 0;
+    // Pieces at multiples of the chunked scan's 64 tokens; each piece's launches
+    // read and update the conv history and the state like a call of their own.
+    const std::vector<int> cut = row_pieces(T, false, 4 * (size_t)T * (cd + 2 * di + ga_rows + gb_rows), 64);
+    const int n_pieces = (int)cut.size() - 1;
+    auto args = [&](int n) {
+        gr_deltanet_args a{};
+        a.n_tokens = n;
+        a.n_heads = nv;
+        a.head_dim = d;
+        a.in_dtype = GR_DTYPE_F32;
+        a.l2norm = 1;
+        a.algo = GR_DELTANET_AUTO;
+        a.eps = s->eps;
+        return a;
+    };
+    size_t ws = 0, in_bytes = 0;
+    int max_n = 0;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const int n = cut[pc + 1] - cut[pc];
+        const gr_deltanet_args a = args(n);
+        ws = std::max(ws, deltanet_ws(&a));
+        max_n = std::max(max_n, n);
+        in_bytes += align_up(4 * (size_t)n * (cd + di + ga_rows + gb_rows) + 4 * 256, 256);
+    }
+    const size_t mid = 4 * ((size_t)max_n * (4 * di + 2 * nv)) + 8 * 256;  // one piece's q, k, v, o, beta, gate
+    if ((rc = ensure_stage(s, in_bytes + mid + 4 * (size_t)T * di + ws + 16384))) return rc;
     Carve cv(s->stage);
-    float* qkv_d = cv.take<float>((size_t)T * cd);
-    float* z_d = cv.take<float>((size_t)T * di);
-    float* ga_d = cv.take<float>((size_t)T * ga_rows);
-    float* gb_d = gate_b ? cv.take<float>((size_t)T * nv) : nullptr;
-    float* q_d = cv.take<float>((size_t)T * di);
-    float* k_d = cv.take<float>((size_t)T * di);
-    float* v_d = cv.take<float>((size_t)T * di);
-    float* beta_d = cv.take<float>((size_t)T * nv);
-    float* gate_d = cv.take<float>((size_t)T * nv);
-    float* o_d = cv.take<float>((size_t)T * di);
+    std::vector<XferRange> ups, downs;
+    std::vector<float*> qkv_d(n_pieces), z_d(n_pieces), ga_d(n_pieces), gb_d(n_pieces, nullptr);
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+        qkv_d[pc] = cv.take<float>(n * cd);
+        z_d[pc] = cv.take<float>(n * di);
+        ga_d[pc] = cv.take<float>(n * ga_rows);
+        ups.push_back({(char*)qkv_d[pc], (char*)(qkv + t0 * cd), 4 * n * cd, pc});
+        ups.push_back({(char*)z_d[pc], (char*)(z + t0 * di), 4 * n * di, pc});
+        ups.push_back({(char*)ga_d[pc], (char*)(gate_a + t0 * ga_rows), 4 * n * ga_rows, pc});
+        if (gate_b) {
+            gb_d[pc] = cv.take<float>(n * gb_rows);
+            ups.push_back({(char*)gb_d[pc], (char*)(gate_b + t0 * gb_rows), 4 * n * gb_rows, pc});
+        }
+    }
+    // the intermediates of one piece, reused piece after piece (stream order)
+    float* q_d = cv.take<float>((size_t)max_n * di);
+    float* k_d = cv.take<float>((size_t)max_n * di);
+    float* v_d = cv.take<float>((size_t)max_n * di);
+    float* beta_d = cv.take<float>((size_t)max_n * nv);
+    float* gate_d = cv.take<float>((size_t)max_n * nv);
+    float* o_d = cv.take<float>((size_t)max_n * di);
     float* out_d = cv.take<float>((size_t)T * di);
-    if ((rc = h2d(s, qkv_d, qkv, 4 * (size_t)T * cd)) || (rc = h2d(s, z_d, z, 4 * (size_t)T * di)) ||
-        (rc = h2d(s, ga_d, gate_a, 4 * (size_t)T * ga_rows)) ||
-        (gate_b && (rc = h2d(s, gb_d, gate_b, 4 * (size_t)T * nv))))
-        return rc;
-    SsmLaunch p{};
-    p.n_tokens = T;
-    p.n_k_heads = s->cfg.ssm_n_k_heads;
-    p.n_v_heads = nv;
-    p.head_dim = d;
-    p.conv_kernel = K;
-    p.eps = s->eps;
-    p.qkv = qkv_d;
-    p.z = z_d;
-    p.gate_a = ga_d;
-    p.gate_b = gb_d;
-    p.conv_w = s->ssm_conv_w + (size_t)layer * cd * K;
-    p.dt_bias = s->ssm_dt + (size_t)layer * nv;
-    p.ssm_a = s->ssm_a + (size_t)layer * nv;
-    p.ssm_norm = s->ssm_nw + (size_t)layer * d;
-    p.conv_hist = s->ssm_hist + (size_t)layer * (K - 1) * cd;
-    p.q_out = q_d;
-    p.k_out = k_d;
-    p.v_out = v_d;
-    p.beta_out = beta_d;
-    p.gate_out = gate_d;
-    p.o = o_d;
-    p.out = out_d;
-    hipError_t e = launch_ssm_pre(p, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "ssm pre launch");
-    a.q = q_d;
-    a.k = k_d;
-    a.v = v_d;
-    a.gate = gate_d;
-    a.beta = beta_d;
-    a.state = s->ssm + (size_t)layer * s->ssm_layer;
-    a.out = o_d;
-    a.workspace = ws ? cv.take<char>(ws) : nullptr;
-    if ((rc = deltanet_enqueue(&a, s->stream))) return rc;
-    e = launch_ssm_post(p, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "ssm post launch");
-    return d2h_sync(s, out, out_d, 4 * (size_t)T * di);
+    char* wsp = ws ? cv.take<char>(ws) : nullptr;
+    for (int pc = 0; pc < n_pieces; pc++) {
+        const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
+        downs.push_back({(char*)(out_d + t0 * di), (char*)(out + t0 * di), 4 * n * di, pc});
+    }
+    auto enqueue = [&](int pc) {
+        const int n = cut[pc + 1] - cut[pc];
+        SsmLaunch p{};
+        p.n_tokens = n;
+        p.n_k_heads = s->cfg.ssm_n_k_heads;
+        p.n_v_heads = nv;
+        p.head_dim = d;
+        p.conv_kernel = K;
+        p.eps = s->eps;
+        p.qkv = qkv_d[pc];
+        p.z = z_d[pc];
+        p.gate_a = ga_d[pc];
+        p.gate_b = gb_d[pc];
+        p.conv_w = s->ssm_conv_w + (size_t)layer * cd * K;
+        p.dt_bias = s->ssm_dt + (size_t)layer * nv;
+        p.ssm_a = s->ssm_a + (size_t)layer * nv;
+        p.ssm_norm = s->ssm_nw + (size_t)layer * d;
+        p.conv_hist = s->ssm_hist + (size_t)layer * (K - 1) * cd;
+        p.q_out = q_d;
+        p.k_out = k_d;
+        p.v_out = v_d;
+        p.beta_out = beta_d;
+        p.gate_out = gate_d;
+        p.o = o_d;
+        p.out = out_d + (size_t)cut[pc] * di;
+        hipError_t e = launch_ssm_pre(p, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "ssm pre launch");
+        gr_deltanet_args a = args(n);
+        a.q = q_d;
+        a.k = k_d;
+        a.v = v_d;
+        a.gate = gate_d;
+        a.beta = beta_d;
+        a.state = s->ssm + (size_t)layer * s->ssm_layer;
+        a.out = o_d;
+        a.workspace = deltanet_ws(&a) ? wsp : nullptr;
+        int r = deltanet_enqueue(&a, s->stream);
+        if (r) return r;
+        e = launch_ssm_post(p, s->stream);
+        return e == hipSuccess ? GR_OK : hip_fail(e, "ssm post launch");
+    };
+    return run_pieces(s, n_pieces, ups, downs, enqueue);
 }
 
 int gr_read_ssm_conv_state(gr_run_state* s, int32_t layer, float* out) {

@@ -241,6 +241,30 @@ def test_qwen3next_prefill_matches_oracle_scan(dev, orc):
     assert float(np.abs(rt.read_ssm_state(p, s, 1) - Sref).max()) <= TOL_F32
 
 
+def test_qwen3next_prefill_in_overlapped_pieces(dev, orc):
+    """2000 tokens of 16 heads (65 MB of host rows): the call runs as overlapped pieces
+    of 256, 448, 512, 512 and 272 tokens (cut at multiples of the chunked scan's 64), the
+    state carried from piece to piece on the device; outputs and the final state ==
+    the oracle's token scan (1e-5)."""
+    from gguf_runner_amd import runtime as rt
+    H, d, T = 16, 128, 2000
+    p = rt.Config(n_layers=1, n_heads=1, n_kv_heads=1, head_dim=128, seq_len=8,
+                  ssm_n_heads=H, ssm_head_dim=d, rms_norm_eps=1e-6)
+    s = rt.malloc_run_state(p)
+    rng = np.random.default_rng(2000)
+    q = rng.standard_normal((T, H, d)).astype(np.float32)
+    k = rng.standard_normal((T, H, d)).astype(np.float32)
+    v = rng.standard_normal((T, H, d)).astype(np.float32)
+    gate = rng.uniform(-0.1, 0, (T, H)).astype(np.float32)
+    beta = rng.uniform(0, 1, (T, H)).astype(np.float32)
+    out = rt.qwen3next_prefill(p, s, 0, q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1),
+                               gate, beta).reshape(T, H, d)
+    ref, Sref = orc.deltanet_scan(q, k, v, gate, beta, np.zeros((H, d, d), np.float32),
+                                  eps=1e-6, n_threads=orc.env_threads())
+    assert float(np.abs(out - ref).max()) <= TOL_F32
+    assert float(np.abs(rt.read_ssm_state(p, s, 0) - Sref).max()) <= TOL_F32
+
+
 @pytest.mark.parametrize("kv_dtype", [1, 3])
 def test_prefill_image_block_runstate(dev, orc, kv_dtype):
     """gr_prefill_image_block (transformer_prefill_image_block's attention) after 40 causal

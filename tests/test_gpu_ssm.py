@@ -35,11 +35,15 @@ def _weights(rng, n_layers, nk, nv, d, K):
 
 
 @pytest.mark.parametrize("nk,fused,chunks,d", [(8, True, (300, 37), 128), (16, False, (37, 130), 128),
-                                                (4, True, (90, 20), 64), (2, False, (70, 3), 256)])
+                                                (4, True, (90, 20), 64), (2, False, (70, 3), 256),
+                                                (8, True, (1500, 1100), 128)])
 def test_qwen3next_ssm_layer_matches_token_loop(orc, dev, nk, fused, chunks, d):
     """Config-5 shape (16 value heads, d128, conv kernel 4): two consecutive calls
     (chunked and recurrent DeltaNet paths) carry the conv history and the state; state
-    sizes 64 and 256 (ssm_state_size, math.rs:566) on the token recurrence."""
+    sizes 64 and 256 (ssm_state_size, math.rs:566) on the token recurrence.  Calls of
+    1500 and 1100 tokens (over 16 MB of host rows) run as overlapped pieces cut at
+    multiples of 64 tokens (256, 448, 512, 284 and 256, 576, 268), each piece's
+    launches carrying the conv history and the state to the next."""
     from gguf_runner_amd import runtime as rt
     rng = np.random.default_rng(500 + nk + d)
     nv, K, layer, eps = 16, 4, 1, 1e-6
