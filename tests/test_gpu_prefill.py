@@ -198,15 +198,18 @@ def test_prefill_eight_wave_blocks_f16(orc, dev):
     _assert_cache(kc, vc, orc.F16, orc)
 
 
-def test_prefill_eight_wave_blocks_window_chunked_bf16(orc, dev):
+@pytest.mark.parametrize("fmt_name", ["BF16", "F16"])
+def test_prefill_eight_wave_blocks_window_chunked(orc, dev, fmt_name):
     """8-wave workgroups with a sliding window and a continuation chunk (base_pos 700,
-    1348 tokens, 96 heads: 96 x 3 pairs), bf16 hi/lo path, ragged last block."""
+    1348 tokens, 96 heads: 96 x 3 pairs), ragged last block: bf16 (f16 copy of the
+    rows), f16 (the split-role kernel: score and value waves)."""
     from gguf_runner_amd import ffi
-    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=96, n_kv=8, d=128, fmt=orc.BF16,
+    fmt = getattr(orc, fmt_name)
+    got, ref, kc, vc = _case(orc, dev, m=2048, n_heads=96, n_kv=8, d=128, fmt=fmt,
                              seed=96, rope_mode=ffi.ROPE_NEOX, theta=1e4, window=300,
                              base_chunks=[700, 1348])
     _assert_close(got, ref)
-    _assert_cache(kc, vc, orc.BF16, orc)
+    _assert_cache(kc, vc, fmt, orc)
 
 
 def _image_block_case(orc, dev, *, hist, blk, n_heads, n_kv, d, fmt, seed, window, rope_mode,
