@@ -452,7 +452,10 @@ __global__ __launch_bounds__(kChunkThreads, DT == GR_DTYPE_F32 ? 2 : 4) void del
             }
             const float sum = quad_sum((su[0] + su[1]) + (su[2] + su[3]));
             const float val = (t == col ? 1.0f : 0.0f) - sum;
-            if (((t >> 2) & 3) == part) x[(t >> 4) * 4 + (t & 3)] = val;
+            // a select, not a branch: under a lane-dependent branch the compiler
+            // copied the whole x array at every step
+            const int xi = (t >> 4) * 4 + (t & 3);
+            x[xi] = ((t >> 2) & 3) == part ? val : x[xi];
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
