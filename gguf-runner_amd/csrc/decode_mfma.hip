@@ -516,6 +516,15 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
     constexpr int NPB = kBlock ? NB : 1;   // P operands (one per V scale block)
     float pw[kQ8 ? NPB : 1];
     bool pw_set = false;
+    // O *= f inside the rarely taken rescale branches.  With block scales O lives
+    // in AGPRs (the MFMAs accumulate there); the empty asm statements move a tile
+    // to VGPRs for the multiply and back inside the branch, where otherwise the
+    // compiler reads all of O out of the AGPRs before the branch on every tile.
+    auto scale_o = [&](int dt, float f) {
+        if constexpr (kBlock) asm volatile("" : "+v"(o[dt]));
+        o[dt] *= f;
+        if constexpr (kBlock) asm volatile("" : "+a"(o[dt]));
+    };
 
     while (it < n_tiles) {
         const int t0 = t_begin + it * TILE;
@@ -655,7 +664,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
             mrow = mnew;
             lrow *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < D / 16; dt++) o[dt] *= alpha;
+            for (int dt = 0; dt < D / 16; dt++) scale_o(dt, alpha);
         }
         float pv[4 * NS16];
         float psum = 0.0f;
@@ -699,7 +708,7 @@ __global__ __launch_bounds__((MdWaves<KV, D>::value * 64),
                     if (pw_set && npw < pw[pb]) {
                         const float f = npw / pw[pb];
 #pragma unroll
-                        for (int dd = 0; dd < (D / 16) / NPB; dd++) o[pb * ((D / 16) / NPB) + dd] *= f;
+                        for (int dd = 0; dd < (D / 16) / NPB; dd++) scale_o(pb * ((D / 16) / NPB) + dd, f);
                         pw[pb] = npw;
                     } else if (!pw_set) {
                         pw[pb] = npw;
