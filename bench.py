@@ -528,6 +528,18 @@ def run_one(args, dev, stream, lens) -> int:
             ms, _ = _timed(call, args.steps, args.warmup, stream)
             res[name] = round(ms * 1e3, 2)
             del keep, call
+    elif args.only in ("decode_small_q8", "decode_small_q8b"):
+        # small decode calls over a Q8 cache (row or block scales): us per call
+        blk = args.only.endswith("b")
+        shapes = (("1x1024 16/8", [1024], 16, 8, 128), ("1x4096 16/8", [4096], 16, 8, 128),
+                  ("1x8192 32/8", [8192], 32, 8, 128), ("4x2048 32/4", [2048] * 4, 32, 4, 128),
+                  ("1x1024 8/4 d256", [1024], 8, 4, 256))
+        for name, ls, H, G, d in shapes:
+            call, nbytes, keep = rotating(
+                lambda sd: decode_q8_workload(dev, ls, sd, n_heads=H, n_kv=G, d=d, block=blk), 3)
+            ms, _ = _timed(call, args.steps, args.warmup, stream)
+            res[name] = round(ms * 1e3, 2)
+            del keep, call
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -582,7 +594,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
+                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")

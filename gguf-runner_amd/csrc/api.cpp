@@ -97,10 +97,9 @@ constexpr int kTurboStreamSegCost = 512;
 // need at most this many fixed-grid workgroups run the fixed grid (plan_decode).
 constexpr int kSmallCallMaxLen = 4096;
 constexpr int64_t kSmallCallMaxWorkgroups = 512;
-// The same for Turbo caches, whose stream ranges are at least 1024 keys: calls up
-// to 8192 keys per sequence on at most 512 fixed-grid workgroups take splits of
-// max(128, max_len / 32) keys.
-constexpr int kTurboSmallCallMaxLen = 8192;
+// The same for Q8 and Turbo caches: calls up to 8192 keys per sequence on at most
+// 512 fixed-grid workgroups take splits of max(128, max_len / 32) keys.
+constexpr int kQuantSmallCallMaxLen = 8192;
 
 // Split size: aim for ~2048 (sequence, KV head, split) work units so the 256
 // CUs stay fed even when sequences are ragged; never below 64 keys.
@@ -146,13 +145,15 @@ DecodePlan plan_decode(const gr_decode_args* a) {
             pl.valu = kv_mul <= 2;
         }
     }
-    // Small Turbo calls (batch-1 decode, the reference's default cache format):
-    // the stream schedule's 1024-key ranges leave a handful of workgroups.
-    // Measured (MI355X, us per call, stream -> fixed grid with these splits):
-    // 1 x 1024 keys, 16 / 8 heads 27.4 -> 17.2; 1 x 4096, 16 / 8 38.1 -> 19.4;
-    // 1 x 8192, 32 / 8 29.9 -> 22.2; 4 x 2048, 32 / 4 30.4 -> 20.4 (the best of
-    // splits 64 ... 512 in each case, within 0.2 us).
-    if (pl.stream && split <= 0 && turbo && max_len <= kTurboSmallCallMaxLen) {
+    // Small Q8 and Turbo calls (batch-1 decode over the reference's own storage
+    // formats): the stream schedule's ranges (1024 keys for Turbo, 256 for Q8)
+    // leave few workgroups.  Measured (MI355X, us per call, stream -> fixed grid
+    // with these splits): Turbo 1 x 1024 keys, 16 / 8 heads 27.4 -> 17.2;
+    // 1 x 4096, 16 / 8 38.1 -> 19.4; 1 x 8192, 32 / 8 29.9 -> 22.2; 4 x 2048,
+    // 32 / 4 30.4 -> 20.4 (the best of splits 64 ... 512 in each case, within
+    // 0.2 us); Q8 rows 1 x 1024, 16 / 8 15.1 -> 11.7; 1 x 8192, 32 / 8 20.7 ->
+    // 18.1; 4 x 2048, 32 / 4 18.3 -> 14.6.
+    if (pl.stream && split <= 0 && (turbo || a->kv_dtype == GR_DTYPE_Q8) && max_len <= kQuantSmallCallMaxLen) {
         const int sk = std::max(128, (max_len + 32 * 64 - 1) / (32 * 64) * 64);
         const int64_t wgs = (int64_t)a->n_seq * a->n_kv_heads * ((kv_mul + 15) / 16) * ((max_len + sk - 1) / sk);
         if (wgs <= kSmallCallMaxWorkgroups) {
