@@ -540,6 +540,30 @@ def run_one(args, dev, stream, lens) -> int:
             ms, _ = _timed(call, args.steps, args.warmup, stream)
             res[name] = round(ms * 1e3, 2)
             del keep, call
+    elif args.only == "runstate_token":
+        # the drop-in per-token call gr_attention_layer_token (QK norm, RoPE, KV write,
+        # attention of one token over 1024 cached keys, host rows in and out), config-1
+        # heads over each cache format: us per call (host wall clock, synchronous calls)
+        from gguf_runner_amd import ffi, runtime as rt
+        for name, kv in (("f32", ffi.DTYPE_F32), ("f16", ffi.DTYPE_F16), ("q8", ffi.DTYPE_Q8),
+                         ("turbo", ffi.DTYPE_TURBO)):
+            p = rt.Config(n_layers=1, n_heads=16, n_kv_heads=8, head_dim=128, seq_len=2048, kv_dtype=kv,
+                          rope_mode=ffi.ROPE_NEOX, rope_dim=128, rope_theta=1e6)
+            s = rt.malloc_run_state(p)
+            rng = np.random.default_rng(1)
+            for a in (s.q, s.k, s.v):
+                a[:] = rng.standard_normal(a.shape).astype(np.float32)
+            for pos in range(1024):
+                rt.attention_layer_token(p, s, 0, pos)
+            best = None
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    rt.attention_layer_token(p, s, 0, 1023)
+                us = (time.perf_counter() - t0) / args.steps * 1e6
+                best = us if best is None else min(best, us)
+            res[name] = round(best, 1)
+            del s
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -594,7 +618,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
+                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "runstate_token", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")

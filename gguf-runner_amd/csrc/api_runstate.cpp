@@ -6,8 +6,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <functional>
 #include <cmath>
+#include <cstring>
+#include <functional>
+#include <initializer_list>
 #include <vector>
 
 #include "gr_api_util.hpp"
@@ -28,6 +30,78 @@ int d2h_sync(gr_run_state* s, void* dst, const void* src, size_t bytes) {
 }
 
 namespace {
+
+// The small per-token calls (a few KB of rows) pay more for the runtime's
+// pageable copies (a staging copy and a DMA per row array, each ~10 us) than
+// for their kernels.  Their rows go through the state's device-mapped pinned
+// buffer instead: the host copies the inputs in, the kernels read them and
+// write the outputs there over PCIe, and after the stream synchronises the host
+// copies the outputs out.  The buffer is reused call after call: every call
+// returns only after its kernels have finished.
+constexpr size_t kMappedBytes = size_t(256) << 10;
+
+bool mapped_ready(gr_run_state* s) {
+    if (s->mapped) return true;
+    if (s->mapped_failed) return false;
+    void* h = nullptr;
+    void* d = nullptr;
+    if (hipHostMalloc(&h, kMappedBytes, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
+        (void)hipGetLastError();
+        s->mapped_failed = true;
+        return false;
+    }
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipHostFree(h);
+        s->mapped_failed = true;
+        return false;
+    }
+    s->mapped = (char*)h;
+    s->mapped_dev = (char*)d;
+    return true;
+}
+
+// The rows of one small call in the mapped buffer: in() copies host rows in and
+// returns their device address, out() reserves output rows; finish() waits for
+// the stream and copies the reserved outputs to their host destinations.
+struct MappedRows {
+    gr_run_state* s;
+    size_t off = 0;
+    struct Out {
+        void* dst;
+        size_t off, bytes;
+    };
+    std::vector<Out> outs;
+    explicit MappedRows(gr_run_state* st) : s(st) {}
+    template <typename T>
+    T* in(const T* src, size_t n) {
+        std::memcpy(s->mapped + off, src, n * sizeof(T));
+        T* d = (T*)(s->mapped_dev + off);
+        off = align_up(off + n * sizeof(T), 256);
+        return d;
+    }
+    template <typename T>
+    T* out(T* dst, size_t n) {
+        outs.push_back({dst, off, n * sizeof(T)});
+        T* d = (T*)(s->mapped_dev + off);
+        off = align_up(off + n * sizeof(T), 256);
+        return d;
+    }
+    int finish() {
+        const hipError_t e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "stream synchronize");
+        for (const Out& o : outs) std::memcpy(o.dst, s->mapped + o.off, o.bytes);
+        return GR_OK;
+    }
+};
+
+// Whether a call with these row bytes (inputs + outputs, each array rounded up
+// to 256 B) takes the mapped buffer.
+bool use_mapped(gr_run_state* s, std::initializer_list<size_t> arrays) {
+    size_t total = 0;
+    for (size_t b : arrays) total += align_up(b, 256);
+    return total <= kMappedBytes && mapped_ready(s);
+}
 
 // Staging arena: grows (never shrinks) and is carved per call.
 struct Carve {
@@ -393,6 +467,7 @@ void gr_free_run_state(gr_run_state* s) {
         if (p) (void)hipFree(p);
     xfer_release(s->xfer);
     xfer_pipe_release(s->pipe);
+    if (s->mapped) (void)hipHostFree(s->mapped);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
 }
@@ -406,12 +481,15 @@ static int norm_or_rope(gr_run_state* s, int32_t layer, int64_t pos, float* q, f
     rc = ensure_stage(s, 4 * ((size_t)s->q_dim * 2 + (size_t)s->kv_dim * 2) + 4096);
     if (rc) return rc;
     Carve cv(s->stage);
-    float* qin = cv.take<float>(s->q_dim);
-    float* kin = cv.take<float>(s->kv_dim);
-    float* qout = cv.take<float>(s->q_dim);
-    float* kout = cv.take<float>(s->kv_dim);
+    const size_t qb = 4 * (size_t)s->q_dim, kb = 4 * (size_t)s->kv_dim;
+    const bool mp = use_mapped(s, {qb, kb, qb, kb});
+    MappedRows mr(s);
+    float* qin = mp ? mr.in(q, s->q_dim) : cv.take<float>(s->q_dim);
+    float* kin = mp ? mr.in(k, s->kv_dim) : cv.take<float>(s->kv_dim);
+    float* qout = mp ? mr.out(q, s->q_dim) : cv.take<float>(s->q_dim);
+    float* kout = mp ? mr.out(k, s->kv_dim) : cv.take<float>(s->kv_dim);
     float* vdump = cv.take<float>(s->kv_dim);
-    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim)) || (rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim))) return rc;
+    if (!mp && ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)))) return rc;
     QkvPrepLaunch p = prep_for(s, layer, 1, norm, rope);
     p.pos0 = pos;
     p.q = qin;
@@ -424,8 +502,9 @@ static int norm_or_rope(gr_run_state* s, int32_t layer, int64_t pos, float* q, f
     p.cache_row_stride = 0;  // single row: ignore the position as a row index
     hipError_t e = launch_qkv_prep(p, s->stream);
     if (e != hipSuccess) return hip_fail(e, "prep launch");
-    if ((rc = d2h_sync(s, q, qout, 4 * (size_t)s->q_dim))) return rc;
-    return d2h_sync(s, k, kout, 4 * (size_t)s->kv_dim);
+    if (mp) return mr.finish();
+    if ((rc = d2h_sync(s, q, qout, qb))) return rc;
+    return d2h_sync(s, k, kout, kb);
 }
 
 int gr_qkv_norm(gr_run_state* s, int32_t layer, float* q, float* k) {
@@ -447,9 +526,12 @@ int gr_kv_write_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, 
     DeviceScope dsc(s->device);
     if ((rc = ensure_stage(s, 8 * (size_t)s->kv_dim + q8_stage_bytes(s, 1) + 1024))) return rc;
     Carve cv(s->stage);
-    float* kin = cv.take<float>(s->kv_dim);
-    float* vin = cv.take<float>(s->kv_dim);
-    if ((rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim)) || (rc = h2d(s, vin, v, 4 * (size_t)s->kv_dim))) return rc;
+    const size_t kb = 4 * (size_t)s->kv_dim;
+    const bool mp = use_mapped(s, {kb, kb});
+    MappedRows mr(s);
+    float* kin = mp ? mr.in(k, s->kv_dim) : cv.take<float>(s->kv_dim);
+    float* vin = mp ? mr.in(v, s->kv_dim) : cv.take<float>(s->kv_dim);
+    if (!mp && ((rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)))) return rc;
     QkvPrepLaunch p = prep_for(s, layer, 1, false, false);
     p.pos0 = pos;
     p.q = kin;
@@ -603,11 +685,16 @@ int gr_attention_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos,
     probe.max_kv_len = en - st;
     if ((rc = ensure_stage(s, 8 * (size_t)s->q_dim + decode_ws_bytes(&probe) + 4096))) return rc;
     Carve cv(s->stage);
-    float* qin = cv.take<float>(s->q_dim);
-    float* xo = cv.take<float>(s->q_dim);
-    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim))) return rc;
-    if ((rc = run_decode(s, layer, 1, qin, nullptr, seq, {st}, {en}, xo, cv))) return rc;
-    return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
+    const size_t qb = 4 * (size_t)s->q_dim;
+    const bool mp = use_mapped(s, {qb, 8, qb});
+    MappedRows mr(s);
+    const int32_t se[2] = {st, en};
+    float* qin = mp ? mr.in(q, s->q_dim) : cv.take<float>(s->q_dim);
+    const int32_t* se_dev = mp ? mr.in(se, 2) : nullptr;
+    float* xo = mp ? mr.out(xb, s->q_dim) : cv.take<float>(s->q_dim);
+    if (!mp && (rc = h2d(s, qin, q, qb))) return rc;
+    if ((rc = run_decode(s, layer, 1, qin, nullptr, seq, {st}, {en}, xo, cv, nullptr, se_dev))) return rc;
+    return mp ? mr.finish() : d2h_sync(s, xb, xo, qb);
 }
 
 int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_t pos, const float* q,
@@ -630,14 +717,17 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
                                   q8_stage_bytes(s, 1) + 8192)))
         return rc;
     Carve cv(s->stage);
-    float* qin = cv.take<float>(s->q_dim);
-    float* kin = cv.take<float>(s->kv_dim);
-    float* vin = cv.take<float>(s->kv_dim);
+    const size_t qb = 4 * (size_t)s->q_dim, kb = 4 * (size_t)s->kv_dim;
+    const bool mp = use_mapped(s, {qb, kb, kb, 8, qb});
+    MappedRows mr(s);
+    const int32_t se[2] = {st, en};
+    float* qin = mp ? mr.in(q, s->q_dim) : cv.take<float>(s->q_dim);
+    float* kin = mp ? mr.in(k, s->kv_dim) : cv.take<float>(s->kv_dim);
+    float* vin = mp ? mr.in(v, s->kv_dim) : cv.take<float>(s->kv_dim);
+    const int32_t* se_dev = mp ? mr.in(se, 2) : nullptr;
     float* qp = cv.take<float>(s->q_dim);
-    float* xo = cv.take<float>(s->q_dim);
-    if ((rc = h2d(s, qin, q, 4 * (size_t)s->q_dim)) || (rc = h2d(s, kin, k, 4 * (size_t)s->kv_dim)) ||
-        (rc = h2d(s, vin, v, 4 * (size_t)s->kv_dim)))
-        return rc;
+    float* xo = mp ? mr.out(xb, s->q_dim) : cv.take<float>(s->q_dim);
+    if (!mp && ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)))) return rc;
     QkvPrepLaunch p = prep_for(s, layer, 1, true, true);
     p.pos0 = pos;
     p.q = qin;
@@ -647,8 +737,8 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     p.k_cache = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     p.v_cache = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     if ((rc = prep_and_store(s, layer, seq, p, cv))) return rc;
-    if ((rc = run_decode(s, layer, 1, qp, nullptr, seq, {st}, {en}, xo, cv))) return rc;
-    return d2h_sync(s, xb, xo, 4 * (size_t)s->q_dim);
+    if ((rc = run_decode(s, layer, 1, qp, nullptr, seq, {st}, {en}, xo, cv, nullptr, se_dev))) return rc;
+    return mp ? mr.finish() : d2h_sync(s, xb, xo, qb);
 }
 
 // Large calls run their rows in pieces so that the uploads of piece p + 1, the
@@ -922,15 +1012,23 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
                                   16384)))
         return rc;
     Carve cv(s->stage);
-    float* qin = cv.take<float>((size_t)n * s->q_dim);
-    float* kin = cv.take<float>((size_t)n * s->kv_dim);
-    float* vin = cv.take<float>((size_t)n * s->kv_dim);
+    const bool mp = use_mapped(s, {qb, kb, kb, 4 * (size_t)n, 4 * (size_t)n, 8 * (size_t)n, qb});
+    MappedRows mr(s);
+    std::vector<int32_t> se(2 * (size_t)n);
+    for (int b = 0; b < n; b++) {
+        se[b] = starts[b];
+        se[n + b] = ends[b];
+    }
+    float* qin = mp ? mr.in(q, (size_t)n * s->q_dim) : cv.take<float>((size_t)n * s->q_dim);
+    float* kin = mp ? mr.in(k, (size_t)n * s->kv_dim) : cv.take<float>((size_t)n * s->kv_dim);
+    float* vin = mp ? mr.in(v, (size_t)n * s->kv_dim) : cv.take<float>((size_t)n * s->kv_dim);
+    int32_t* slot_d = mp ? mr.in(seqs, n) : cv.take<int32_t>(n);
+    int32_t* pos_d = mp ? mr.in(pos32.data(), n) : cv.take<int32_t>(n);
+    const int32_t* se_dev = mp ? mr.in(se.data(), se.size()) : nullptr;
     float* qp = cv.take<float>((size_t)n * s->q_dim);
-    float* xo = cv.take<float>((size_t)n * s->q_dim);
-    int32_t* slot_d = cv.take<int32_t>(n);
-    int32_t* pos_d = cv.take<int32_t>(n);
-    if ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)) ||
-        (rc = h2d(s, slot_d, seqs, 4 * (size_t)n)) || (rc = h2d(s, pos_d, pos32.data(), 4 * (size_t)n)))
+    float* xo = mp ? mr.out(xb, (size_t)n * s->q_dim) : cv.take<float>((size_t)n * s->q_dim);
+    if (!mp && ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)) ||
+                (rc = h2d(s, slot_d, seqs, 4 * (size_t)n)) || (rc = h2d(s, pos_d, pos32.data(), 4 * (size_t)n))))
         return rc;
     QkvPrepLaunch p = prep_for(s, layer, n, true, true);
     p.pos = pos_d;
@@ -943,8 +1041,8 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     p.cache_seq = slot_d;
     p.cache_seq_stride = (int64_t)s->seq_stride;
     if ((rc = prep_and_store(s, layer, 0, p, cv))) return rc;
-    if ((rc = run_decode(s, layer, n, qp, slot_d, 0, starts, ends, xo, cv))) return rc;
-    return d2h_sync(s, xb, xo, qb);
+    if ((rc = run_decode(s, layer, n, qp, slot_d, 0, starts, ends, xo, cv, nullptr, se_dev))) return rc;
+    return mp ? mr.finish() : d2h_sync(s, xb, xo, qb);
 }
 
 static int check_ssm(gr_run_state* s, int layer) {
@@ -965,14 +1063,17 @@ int gr_qwen3next_state_step(gr_run_state* s, int32_t layer, const float* q, cons
     const size_t rb = 4 * (size_t)H * D;
     if ((rc = ensure_stage(s, 4 * rb + 8 * (size_t)H + 4096))) return rc;
     Carve cv(s->stage);
-    float* qd = cv.take<float>((size_t)H * D);
-    float* kd = cv.take<float>((size_t)H * D);
-    float* vd = cv.take<float>((size_t)H * D);
-    float* od = cv.take<float>((size_t)H * D);
-    float* gd = cv.take<float>(H);
-    float* bd = cv.take<float>(H);
-    if ((rc = h2d(s, qd, q, rb)) || (rc = h2d(s, kd, k, rb)) || (rc = h2d(s, vd, v, rb)) ||
-        (rc = h2d(s, gd, g, 4 * (size_t)H)) || (rc = h2d(s, bd, beta, 4 * (size_t)H)))
+    const bool mp = use_mapped(s, {rb, rb, rb, 4 * (size_t)H, 4 * (size_t)H, rb});
+    MappedRows mr(s);
+    const size_t hd = (size_t)H * D;
+    float* qd = mp ? mr.in(q, hd) : cv.take<float>(hd);
+    float* kd = mp ? mr.in(k, hd) : cv.take<float>(hd);
+    float* vd = mp ? mr.in(v, hd) : cv.take<float>(hd);
+    float* gd = mp ? mr.in(g, (size_t)H) : cv.take<float>(H);
+    float* bd = mp ? mr.in(beta, (size_t)H) : cv.take<float>(H);
+    float* od = mp ? mr.out(out, hd) : cv.take<float>(hd);
+    if (!mp && ((rc = h2d(s, qd, q, rb)) || (rc = h2d(s, kd, k, rb)) || (rc = h2d(s, vd, v, rb)) ||
+                (rc = h2d(s, gd, g, 4 * (size_t)H)) || (rc = h2d(s, bd, beta, 4 * (size_t)H))))
         return rc;
     DeltaNetLaunch p{};
     p.n_tokens = 1;
@@ -991,7 +1092,7 @@ int gr_qwen3next_state_step(gr_run_state* s, int32_t layer, const float* q, cons
     p.gate_is_log = 0;
     hipError_t e = launch_deltanet_scan(p, s->stream);
     if (e != hipSuccess) return hip_fail(e, "deltanet step launch");
-    return d2h_sync(s, out, od, rb);
+    return mp ? mr.finish() : d2h_sync(s, out, od, rb);
 }
 
 int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float* q, const float* k,

@@ -53,6 +53,12 @@ struct gr_run_state {
     size_t stage_bytes = 0;
     gr::HostXfer xfer;  // pinned ring for the host rows of each call
     gr::XferPipe pipe;  // streams and download ring of the pipelined large calls
+    // Pinned, device-mapped host buffer for the rows of the small per-token calls:
+    // their kernels read the inputs and write the outputs there directly, with no
+    // DMA copy on either side (allocated on first use, kMappedBytes).
+    char* mapped = nullptr;      // host address
+    char* mapped_dev = nullptr;  // the same memory's device address
+    bool mapped_failed = false;  // allocation refused once: the copy path is used
 };
 
 namespace gr {
