@@ -7,6 +7,8 @@
 // multiplied by the softmax scale * log2(e) for the MFMA prefill kernel), or
 // skipped, with each token's RoPE (cos, sin) pairs written out instead for a
 // consumer that prepares Q itself.
+#include <algorithm>
+
 #include "gr_common.hpp"
 #include "gr_internal.hpp"
 
@@ -79,7 +81,8 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
             sincosf(val, &sn, &cs);
             cs_t[f] = cs;
             sn_t[f] = sn;
-            if (p.rope_cs_out && tok_ok) *(float2*)(p.rope_cs_out + ((size_t)i * half + f) * 2) = make_float2(cs, sn);
+            if (p.rope_cs_out && tok_ok && blockIdx.y == 0)
+                *(float2*)(p.rope_cs_out + ((size_t)i * half + f) * 2) = make_float2(cs, sn);
         }
     }
     __syncthreads();
@@ -90,8 +93,10 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
 
     // Without a Q staging buffer the Q rows are left to the consumer (the MFMA
     // prefill kernel prepares them itself from rope_cs_out).
+    // workgroup y of gridDim.y takes every gridDim.y-th group of WPT * RPW rows
     const int row0 = p.q_out ? 0 : p.n_heads;
-    for (int hr0 = row0 + wt * RPW; hr0 < rows_per_token; hr0 += WPT * RPW) {
+    for (int hr0 = row0 + ((int)blockIdx.y * WPT + wt) * RPW; hr0 < rows_per_token;
+         hr0 += (int)gridDim.y * WPT * RPW) {
         const int hr = hr0 + rsub;
         const bool valid = hr < rows_per_token;
         const int hrc = valid ? hr : rows_per_token - 1;
@@ -269,7 +274,16 @@ constexpr int kPrepWaveTokens = 1024;
 
 template <int T>
 static hipError_t launch_qkv_prep_t(const QkvPrepLaunch& p, hipStream_t st) {
-    const unsigned blocks = (unsigned)((p.n_tokens + T - 1) / T);
+    // A few tokens (decode, short chunks): the rows of a token spread over
+    // workgroups of one row step per wave each, so every wave issues its loads
+    // once (the inputs may sit in host memory, a PCIe round trip per step).
+    int ygroups = 1;
+    if (T == 1 && p.n_tokens <= 64) {
+        const int rows = p.n_heads + 2 * p.n_kv_heads - (p.q_out ? 0 : p.n_heads);
+        const int per_wg = kPrepRowsPerBlock * (64 / (p.head_dim / 8));  // waves x rows per wave step
+        ygroups = std::max(1, (rows + per_wg - 1) / per_wg);
+    }
+    const dim3 blocks((unsigned)((p.n_tokens + T - 1) / T), (unsigned)ygroups);
     switch (p.head_dim) {
         case 64: qkv_prep_kernel<64, T><<<blocks, kPrepThreads, 0, st>>>(p); break;
         case 128: qkv_prep_kernel<128, T><<<blocks, kPrepThreads, 0, st>>>(p); break;
