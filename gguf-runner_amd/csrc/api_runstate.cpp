@@ -724,11 +724,17 @@ int gr_attention_layer_token(gr_run_state* s, int32_t seq, int32_t layer, int64_
     float* qin = mp ? mr.in(q, s->q_dim) : cv.take<float>(s->q_dim);
     float* kin = mp ? mr.in(k, s->kv_dim) : cv.take<float>(s->kv_dim);
     float* vin = mp ? mr.in(v, s->kv_dim) : cv.take<float>(s->kv_dim);
-    const int32_t* se_dev = mp ? mr.in(se, 2) : nullptr;
+    const int32_t* se_host = mp ? mr.in(se, 2) : nullptr;
+    int32_t* se_dev = mp ? cv.take<int32_t>(2) : nullptr;  // the prep copies the range here
     float* qp = cv.take<float>(s->q_dim);
     float* xo = mp ? mr.out(xb, s->q_dim) : cv.take<float>(s->q_dim);
     if (!mp && ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)))) return rc;
     QkvPrepLaunch p = prep_for(s, layer, 1, true, true);
+    if (mp) {
+        p.copy_src = se_host;
+        p.copy_dst = se_dev;
+        p.n_copy = 2;
+    }
     p.pos0 = pos;
     p.q = qin;
     p.k = kin;
@@ -1022,15 +1028,29 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     float* qin = mp ? mr.in(q, (size_t)n * s->q_dim) : cv.take<float>((size_t)n * s->q_dim);
     float* kin = mp ? mr.in(k, (size_t)n * s->kv_dim) : cv.take<float>((size_t)n * s->kv_dim);
     float* vin = mp ? mr.in(v, (size_t)n * s->kv_dim) : cv.take<float>((size_t)n * s->kv_dim);
-    int32_t* slot_d = mp ? mr.in(seqs, n) : cv.take<int32_t>(n);
+    // mapped: [slots | starts | ends] in one array, which the prep copies to the
+    // device for the decode kernels (read by every workgroup)
+    std::vector<int32_t> sse;
+    if (mp) {
+        sse.assign(seqs, seqs + n);
+        sse.insert(sse.end(), se.begin(), se.end());
+    }
+    const int32_t* sse_host = mp ? mr.in(sse.data(), sse.size()) : nullptr;
+    int32_t* sse_dev = mp ? cv.take<int32_t>(3 * (size_t)n) : nullptr;
+    int32_t* slot_d = mp ? sse_dev : cv.take<int32_t>(n);
     int32_t* pos_d = mp ? mr.in(pos32.data(), n) : cv.take<int32_t>(n);
-    const int32_t* se_dev = mp ? mr.in(se.data(), se.size()) : nullptr;
+    const int32_t* se_dev = mp ? sse_dev + n : nullptr;
     float* qp = cv.take<float>((size_t)n * s->q_dim);
     float* xo = mp ? mr.out(xb, (size_t)n * s->q_dim) : cv.take<float>((size_t)n * s->q_dim);
     if (!mp && ((rc = h2d(s, qin, q, qb)) || (rc = h2d(s, kin, k, kb)) || (rc = h2d(s, vin, v, kb)) ||
                 (rc = h2d(s, slot_d, seqs, 4 * (size_t)n)) || (rc = h2d(s, pos_d, pos32.data(), 4 * (size_t)n))))
         return rc;
     QkvPrepLaunch p = prep_for(s, layer, n, true, true);
+    if (mp) {
+        p.copy_src = sse_host;
+        p.copy_dst = sse_dev;
+        p.n_copy = 3 * n;
+    }
     p.pos = pos_d;
     p.q = qin;
     p.k = kin;
@@ -1038,7 +1058,7 @@ int gr_decode_layer_batch(gr_run_state* s, int32_t layer, int32_t n, const int32
     p.q_out = qp;
     p.k_cache = layer_k(s, layer);
     p.v_cache = layer_v(s, layer);
-    p.cache_seq = slot_d;
+    p.cache_seq = mp ? sse_host : slot_d;  // the prep's own reads: the device copy is not there yet
     p.cache_seq_stride = (int64_t)s->seq_stride;
     if ((rc = prep_and_store(s, layer, 0, p, cv))) return rc;
     if ((rc = run_decode(s, layer, n, qp, slot_d, 0, starts, ends, xo, cv, nullptr, se_dev))) return rc;

@@ -140,6 +140,12 @@ struct QkvPrepLaunch {
     int64_t f16_row0, f16_row_stride;
     uint32_t* f16_flag;
     uint32_t f16_epoch;
+    // n_copy int32 values copied from copy_src to copy_dst by workgroup 0, for a
+    // kernel launched after this one (the decode's sequence slots and key ranges
+    // when the caller's copies sit in host memory); n_copy = 0: none.
+    const int32_t* copy_src;
+    int32_t* copy_dst;
+    int n_copy;
 };
 
 hipError_t launch_qkv_prep(const QkvPrepLaunch& p, hipStream_t st);

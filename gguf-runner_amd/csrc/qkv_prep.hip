@@ -70,6 +70,8 @@ __global__ __launch_bounds__(kPrepThreads) void qkv_prep_kernel(const QkvPrepLau
     const int i = tok_ok ? i_raw : p.n_tokens - 1;
     float* cs_t = cs_all[tsub];
     float* sn_t = sn_all[tsub];
+    if (p.n_copy > 0 && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int t = threadIdx.x; t < p.n_copy; t += kPrepThreads) p.copy_dst[t] = p.copy_src[t];
     const int rows_per_token = p.n_heads + 2 * p.n_kv_heads;
     const int64_t pos = p.pos ? (int64_t)p.pos[i] : p.pos0 + i;
     const bool rope = p.rope_mode != GR_ROPE_NONE;
