@@ -38,7 +38,7 @@ namespace {
 // write the outputs there over PCIe, and after the stream synchronises the host
 // copies the outputs out.  The buffer is reused call after call: every call
 // returns only after its kernels have finished.
-constexpr size_t kMappedBytes = size_t(256) << 10;
+constexpr size_t kMappedBytes = size_t(4) << 20;
 
 bool mapped_ready(gr_run_state* s) {
     if (s->mapped) return true;
@@ -75,7 +75,7 @@ struct MappedRows {
     explicit MappedRows(gr_run_state* st) : s(st) {}
     template <typename T>
     T* in(const T* src, size_t n) {
-        std::memcpy(s->mapped + off, src, n * sizeof(T));
+        host_copy(s->mapped + off, src, n * sizeof(T));
         T* d = (T*)(s->mapped_dev + off);
         off = align_up(off + n * sizeof(T), 256);
         return d;
@@ -90,7 +90,7 @@ struct MappedRows {
     int finish() {
         const hipError_t e = hipStreamSynchronize(s->stream);
         if (e != hipSuccess) return hip_fail(e, "stream synchronize");
-        for (const Out& o : outs) std::memcpy(o.dst, s->mapped + o.off, o.bytes);
+        for (const Out& o : outs) host_copy(o.dst, s->mapped + o.off, o.bytes);
         return GR_OK;
     }
 };
@@ -884,6 +884,19 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         if (!se[pc].empty()) se_dev[pc] = cv.take<int32_t>(se[pc].size());
     }
     float* xo = cv.take<float>((size_t)m * s->q_dim);
+    // One piece whose rows fit the mapped buffer (the reference's 64-token chunks):
+    // the kernels read q / k / v and write xb in host memory; the decode's range
+    // arrays reach the device through the prep pass's copy.
+    const bool mp = n_pieces == 1 && use_mapped(s, {qb, kb, kb, 4 * se[0].size(), qb});
+    MappedRows mr(s);
+    const int32_t* se_host = nullptr;
+    if (mp) {
+        qin[0] = mr.in(q, (size_t)m * s->q_dim);
+        kin[0] = mr.in(k, (size_t)m * s->kv_dim);
+        vin[0] = mr.in(v, (size_t)m * s->kv_dim);
+        if (!se[0].empty()) se_host = mr.in(se[0].data(), se[0].size());
+        xo = mr.out(xb, (size_t)m * s->q_dim);
+    }
     const Carve scratch_base = cv;
     void* kc = (char*)layer_k(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
     void* vc = (char*)layer_v(s, layer) + cache_bytes_at(s, (size_t)seq * s->seq_stride);
@@ -929,6 +942,11 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
         p.q_out = qp;
         p.k_cache = kc;
         p.v_cache = vc;
+        if (se_host && se_dev[pc]) {
+            p.copy_src = se_host;
+            p.copy_dst = se_dev[pc];
+            p.n_copy = (int)se[pc].size();
+        }
         int r = prep_and_store(s, layer, seq, p, cw);
         if (r) return r;
         if (is_q8(s)) {
@@ -959,6 +977,10 @@ static int prefill_rows(gr_run_state* s, int32_t seq, int32_t layer, int64_t bas
                           packs[pc].tp > 0 ? &packs[pc] : nullptr, se_dev[pc]);
     };
 
+    if (mp) {
+        if ((rc = enqueue(0))) return rc;
+        return mr.finish();
+    }
     std::vector<XferRange> ups, downs;
     for (int pc = 0; pc < n_pieces; pc++) {
         const size_t r0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);

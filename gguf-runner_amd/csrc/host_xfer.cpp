@@ -198,6 +198,8 @@ void pack_loads(const std::vector<XferRange>& chunks, std::vector<SlotLoad>& loa
 
 }  // namespace
 
+void host_copy(void* dst, const void* src, size_t bytes) { CopyPool::get().copy(dst, src, bytes); }
+
 hipError_t xfer_h2d(HostXfer& x, hipStream_t st, void* dst, const void* src, size_t bytes) {
     if (!bytes) return hipSuccess;
     if (bytes < HostXfer::kMinStaged || !ensure_ring(x))

@@ -43,6 +43,10 @@ hipError_t xfer_d2h(HostXfer& x, hipStream_t st, void* dst, const void* src, siz
 // Releases the ring (after the caller synchronised `st`).
 void xfer_release(HostXfer& x);
 
+// Host memcpy, split over the process-wide copy threads from 1 MB on (below
+// that, waking the threads costs more than the copy on the calling thread).
+void host_copy(void* dst, const void* src, size_t bytes);
+
 // One contiguous host <-> device range of a piece.
 struct XferRange {
     char* dev;
