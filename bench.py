@@ -564,6 +564,32 @@ def run_one(args, dev, stream, lens) -> int:
                 best = us if best is None else min(best, us)
             res[name] = round(best, 1)
             del s
+    elif args.only == "runstate_chunk":
+        # gr_prefill_attention_chunk with the reference's short chunks (16 and 64 rows at
+        # base_pos 1024, host rows in and out), 16 / 8 and 32 / 8 heads, d128: us per call
+        from gguf_runner_amd import ffi, runtime as rt
+        for name, kv in (("f16", ffi.DTYPE_F16), ("q8", ffi.DTYPE_Q8), ("turbo", ffi.DTYPE_TURBO)):
+            for H, G in ((16, 8), (32, 8)):
+                p = rt.Config(n_layers=1, n_heads=H, n_kv_heads=G, head_dim=128, seq_len=2048, kv_dtype=kv,
+                              rope_mode=ffi.ROPE_NEOX, rope_dim=128, rope_theta=1e6)
+                s = rt.malloc_run_state(p)
+                rng = np.random.default_rng(1)
+                for m in (16, 64):
+                    q = rng.standard_normal((m, p.q_dim)).astype(np.float32)
+                    k = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+                    v = rng.standard_normal((m, p.kv_dim)).astype(np.float32)
+                    xb = np.zeros((m, p.q_dim), np.float32)
+                    for _ in range(3):
+                        rt.prefill_attention_chunk(p, s, 0, 1024, q, k, v, out=xb)
+                    best = None
+                    for _ in range(3):
+                        t0 = time.perf_counter()
+                        for _ in range(args.steps):
+                            rt.prefill_attention_chunk(p, s, 0, 1024, q, k, v, out=xb)
+                        us = (time.perf_counter() - t0) / args.steps * 1e6
+                        best = us if best is None else min(best, us)
+                    res[f"{name} {H}/{G} m{m}"] = round(best, 1)
+                del s
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -618,7 +644,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "runstate_token", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
+                    choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "runstate_token", "runstate_chunk", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
                              "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
