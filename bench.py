@@ -602,6 +602,30 @@ def run_one(args, dev, stream, lens) -> int:
                                                 turbo=args.only.endswith("turbo"))
         _, wall = _timed(call, args.steps, args.warmup, stream)
         res.update(call_ms=wall, call_tflops=flops / (wall * 1e-3) / 1e12, gflop=flops / 1e9)
+    elif args.only == "ssm_token":
+        # per-token run-state DeltaNet calls (config 5 heads): the SSM layer with one
+        # token (conv, gates, the state step, gated RMSNorm) and the bare state step;
+        # us per call (host wall clock, synchronous calls)
+        from gguf_runner_amd import runtime as rt
+        layer, _, keep = ssm_runstate_workload(1, 9)
+        p, s = keep
+        rng = np.random.default_rng(3)
+        H, d = p.ssm_n_heads, p.ssm_head_dim
+        q, k, v = (rng.standard_normal(H * d).astype(np.float32) for _ in range(3))
+        gq = rng.uniform(0.9, 1.0, H).astype(np.float32)
+        bq = rng.uniform(0, 1, H).astype(np.float32)
+        step = lambda: rt.qwen3next_state_step(p, s, 0, q, k, v, gq, bq)
+        for name, fn in (("ssm_layer_T1", layer), ("state_step", step)):
+            for _ in range(5):
+                fn()
+            best = None
+            for _ in range(3):
+                t0 = time.perf_counter()
+                for _ in range(args.steps):
+                    fn()
+                us = (time.perf_counter() - t0) / args.steps * 1e6
+                best = us if best is None else min(best, us)
+            res[name] = round(best, 1)
     elif args.only == "ssm2k":
         # synchronous host-buffer calls, 2048 tokens each (wall time incl. PCIe copies)
         layer, prefill, keep = ssm_runstate_workload(2048, 9)
@@ -645,7 +669,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "runstate_token", "runstate_chunk", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k",
+                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k", "ssm_token",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()

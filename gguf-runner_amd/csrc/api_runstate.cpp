@@ -1189,6 +1189,18 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
     }
     float* od = cv.take<float>((size_t)T * rw);
     char* wsp = ws ? cv.take<char>(ws) : nullptr;  // shared by the pieces (stream order)
+    // one piece that fits the mapped buffer: rows read and written in host memory
+    const size_t tb = 4 * (size_t)T * rw, gb = 4 * (size_t)T * H;
+    const bool mp = n_pieces == 1 && use_mapped(s, {tb, tb, tb, gb, gb, tb});
+    MappedRows mr(s);
+    if (mp) {
+        qd[0] = mr.in(q, (size_t)T * rw);
+        kd[0] = mr.in(k, (size_t)T * rw);
+        vd[0] = mr.in(v, (size_t)T * rw);
+        gd[0] = mr.in(gate, (size_t)T * H);
+        bd[0] = mr.in(beta, (size_t)T * H);
+        od = mr.out(out, (size_t)T * rw);
+    }
     for (int pc = 0; pc < n_pieces; pc++) {
         const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
         downs.push_back({(char*)(od + t0 * rw), (char*)(out + t0 * rw), 4 * n * rw, pc});
@@ -1205,6 +1217,10 @@ int gr_qwen3next_prefill(gr_run_state* s, int32_t layer, int32_t T, const float*
         a.workspace = deltanet_ws(&a) ? wsp : nullptr;
         return deltanet_enqueue(&a, s->stream);
     };
+    if (mp) {
+        if ((rc = enqueue(0))) return rc;
+        return mr.finish();
+    }
     return run_pieces(s, n_pieces, ups, downs, enqueue);
 }
 
@@ -1273,6 +1289,18 @@ int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const floa
     float* o_d = cv.take<float>((size_t)max_n * di);
     float* out_d = cv.take<float>((size_t)T * di);
     char* wsp = ws ? cv.take<char>(ws) : nullptr;
+    // one piece that fits the mapped buffer (decode: T = 1): rows read and
+    // written in host memory
+    const bool mp = n_pieces == 1 && use_mapped(s, {4 * (size_t)T * cd, 4 * (size_t)T * di, 4 * (size_t)T * ga_rows,
+                                                   4 * (size_t)T * gb_rows, 4 * (size_t)T * di});
+    MappedRows mr(s);
+    if (mp) {
+        qkv_d[0] = mr.in(qkv, (size_t)T * cd);
+        z_d[0] = mr.in(z, (size_t)T * di);
+        ga_d[0] = mr.in(gate_a, (size_t)T * ga_rows);
+        if (gate_b) gb_d[0] = mr.in(gate_b, (size_t)T * gb_rows);
+        out_d = mr.out(out, (size_t)T * di);
+    }
     for (int pc = 0; pc < n_pieces; pc++) {
         const size_t t0 = (size_t)cut[pc], n = (size_t)(cut[pc + 1] - cut[pc]);
         downs.push_back({(char*)(out_d + t0 * di), (char*)(out + t0 * di), 4 * n * di, pc});
@@ -1318,6 +1346,10 @@ int gr_qwen3next_ssm_layer(gr_run_state* s, int32_t layer, int32_t T, const floa
         e = launch_ssm_post(p, s->stream);
         return e == hipSuccess ? GR_OK : hip_fail(e, "ssm post launch");
     };
+    if (mp) {
+        if ((rc = enqueue(0))) return rc;
+        return mr.finish();
+    }
     return run_pieces(s, n_pieces, ups, downs, enqueue);
 }
 
