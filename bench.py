@@ -27,6 +27,9 @@ Also reported in the same line:
   encoder_siglip -- encoder self-attention at the Gemma 3 SigLIP shape (4096
                   patches, 16 heads, d72, f32)
   config1_decode -- config 1 (Qwen3-0.6B-shaped decode, f32 KV, 1024 keys)
+  runstate_token_us -- the drop-in per-token call (gr_attention_layer_token: QK
+                  norm, RoPE, KV write and attention over 1024 keys with host rows),
+                  config 1's heads over f32 / f16 / Q8 / Turbo caches, us per call
   config4      -- config 4 (Gemma-3-4B-shaped, d256, bf16): the 8192-token prefill
                   of a sliding-window (1024) and the global layer, the 5 : 1 stack
                   of six layers, and one decode step over the six layers after it
@@ -464,6 +467,35 @@ def ssm_runstate_workload(T, seed, H=16, d=128, K=4):
     return layer, prefill, (p, s)
 
 
+def runstate_token_us(steps):
+    """The drop-in per-token call gr_attention_layer_token (QK norm, RoPE, KV write and
+    attention of one token over 1024 cached keys; host q / k / v rows in, xb out) at
+    config 1's heads (16 / 8, d128) over each cache format: us per call, host wall
+    clock of synchronous calls (the best of three runs of `steps` calls)."""
+    from gguf_runner_amd import ffi, runtime as rt
+    out = {}
+    for name, kv in (("f32", ffi.DTYPE_F32), ("f16", ffi.DTYPE_F16), ("q8", ffi.DTYPE_Q8),
+                     ("turbo", ffi.DTYPE_TURBO)):
+        p = rt.Config(n_layers=1, n_heads=16, n_kv_heads=8, head_dim=128, seq_len=2048, kv_dtype=kv,
+                      rope_mode=ffi.ROPE_NEOX, rope_dim=128, rope_theta=1e6)
+        s = rt.malloc_run_state(p)
+        rng = np.random.default_rng(1)
+        for a in (s.q, s.k, s.v):
+            a[:] = rng.standard_normal(a.shape).astype(np.float32)
+        for pos in range(1024):
+            rt.attention_layer_token(p, s, 0, pos)
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                rt.attention_layer_token(p, s, 0, 1023)
+            us = (time.perf_counter() - t0) / steps * 1e6
+            best = us if best is None else min(best, us)
+        out[name] = round(best, 1)
+        del s
+    return out
+
+
 def run_one(args, dev, stream, lens) -> int:
     """A single workload, for rocprofv3 runs; prints one short JSON line."""
     import torch
@@ -541,29 +573,7 @@ def run_one(args, dev, stream, lens) -> int:
             res[name] = round(ms * 1e3, 2)
             del keep, call
     elif args.only == "runstate_token":
-        # the drop-in per-token call gr_attention_layer_token (QK norm, RoPE, KV write,
-        # attention of one token over 1024 cached keys, host rows in and out), config-1
-        # heads over each cache format: us per call (host wall clock, synchronous calls)
-        from gguf_runner_amd import ffi, runtime as rt
-        for name, kv in (("f32", ffi.DTYPE_F32), ("f16", ffi.DTYPE_F16), ("q8", ffi.DTYPE_Q8),
-                         ("turbo", ffi.DTYPE_TURBO)):
-            p = rt.Config(n_layers=1, n_heads=16, n_kv_heads=8, head_dim=128, seq_len=2048, kv_dtype=kv,
-                          rope_mode=ffi.ROPE_NEOX, rope_dim=128, rope_theta=1e6)
-            s = rt.malloc_run_state(p)
-            rng = np.random.default_rng(1)
-            for a in (s.q, s.k, s.v):
-                a[:] = rng.standard_normal(a.shape).astype(np.float32)
-            for pos in range(1024):
-                rt.attention_layer_token(p, s, 0, pos)
-            best = None
-            for _ in range(3):
-                t0 = time.perf_counter()
-                for _ in range(args.steps):
-                    rt.attention_layer_token(p, s, 0, 1023)
-                us = (time.perf_counter() - t0) / args.steps * 1e6
-                best = us if best is None else min(best, us)
-            res[name] = round(best, 1)
-            del s
+        res.update(runstate_token_us(args.steps))
     elif args.only == "runstate_chunk":
         # gr_prefill_attention_chunk with the reference's short chunks (16 and 64 rows at
         # base_pos 1024, host rows in and out), 16 / 8 and 32 / 8 heads, d128: us per call
@@ -830,6 +840,8 @@ def main() -> int:
     e_ms, _ = _timed(ecall, max(5, args.steps // 5), 2, stream)
     line["encoder_siglip"] = {"ms": round(e_ms, 4), "tflops": round(eflops / (e_ms * 1e-3) / 1e12, 2)}
     del _keep_e, ecall
+
+    line["runstate_token_us"] = runstate_token_us(max(50, args.steps))
 
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(lens)
