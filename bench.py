@@ -191,15 +191,16 @@ def decode_turbo_workload(dev, lens, seed, n_heads=32, n_kv=4, d=128):
     return call, nbytes, (q, kb, vb, ks_, vs_, sig_k, sig_v, gam_k, gam_v, table, st, en, out)
 
 
-def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
+def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128, dtype=None):
     import torch
     from gguf_runner_amd import ffi, ops
+    dtype = dtype or torch.float16
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=torch.float16)
-    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
-    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
-    kc = torch.empty((S, n_kv, d), device=dev, dtype=torch.float16)
+    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=dtype)
+    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=dtype)
+    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=dtype)
+    kc = torch.empty((S, n_kv, d), device=dev, dtype=dtype)
     vc = torch.empty_like(kc)
     out = torch.empty((S, n_heads, d), device=dev, dtype=torch.float32)
     fr = torch.tensor(ops.rope_freqs(5e5, d), dtype=torch.float32, device=dev)
@@ -209,16 +210,17 @@ def prefill_workload(dev, S, seed, n_heads=32, n_kv=8, d=128):
     return call, flops, (q, k, v, kc, vc, out, fr)
 
 
-def prefill_d64_workload(dev, S, seed, n_heads=14, n_kv=2, d=64):
-    """head_dim-64 causal prefill at the Qwen2-0.5B shape (14 Q / 2 KV heads, f16 Q/K/V,
-    NeoX RoPE theta 1e6 fused on load)."""
+def prefill_d64_workload(dev, S, seed, n_heads=14, n_kv=2, d=64, dtype=None):
+    """head_dim-64 causal prefill at the Qwen2-0.5B shape (14 Q / 2 KV heads, f16 (or
+    `dtype`) Q/K/V, NeoX RoPE theta 1e6 fused on load)."""
     import torch
     from gguf_runner_amd import ffi, ops
+    dtype = dtype or torch.float16
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
-    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=torch.float16)
-    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
-    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=torch.float16)
+    q = torch.randn((S, n_heads, d), generator=g, device=dev, dtype=dtype)
+    k = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=dtype)
+    v = torch.randn((S, n_kv, d), generator=g, device=dev, dtype=dtype)
     kc, vc = torch.empty_like(k), torch.empty_like(v)
     out = torch.empty((S, n_heads, d), device=dev, dtype=torch.float32)
     fr = torch.tensor(ops.rope_freqs(1e6, d), dtype=torch.float32, device=dev)
@@ -600,6 +602,14 @@ def run_one(args, dev, stream, lens) -> int:
                         best = us if best is None else min(best, us)
                     res[f"{name} {H}/{G} m{m}"] = round(best, 1)
                 del s
+    elif args.only in ("prefill8k_bf16", "prefill8k_d64_bf16"):
+        # bf16 caches (the f16 MFMA path on an exact f16 copy of the rows)
+        if args.only == "prefill8k_bf16":
+            call, flops, keep = prefill_workload(dev, 8192, 8, dtype=torch.bfloat16)
+        else:
+            call, flops, keep = prefill_d64_workload(dev, 8192, 64, dtype=torch.bfloat16)
+        ms, _ = _timed(call, args.steps, args.warmup, stream)
+        res.update(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, gflop=flops / 1e9)
     elif args.only in ("prefill2k_d64", "prefill8k_d64"):
         S = 2048 if args.only == "prefill2k_d64" else 8192
         call, flops, keep = prefill_d64_workload(dev, S, 64)
@@ -679,7 +689,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="all",
                     choices=["all", "decode3", "decode32k", "decode_c1", "decode_c4", "decode_small", "decode_small_turbo", "decode_small_q8", "decode_small_q8b", "runstate_token", "runstate_chunk", "decode32k_q8", "decode32k_q8b", "decode32k_turbo",
-                             "prefill2k", "prefill8k", "prefill2k_d64", "prefill8k_d64", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k", "ssm_token",
+                             "prefill2k", "prefill8k", "prefill8k_bf16", "prefill2k_d64", "prefill8k_d64", "prefill8k_d64_bf16", "prefill2k_q8", "prefill2k_q8b", "prefill2k_turbo", "prefill8k_d256", "encoder", "deltanet", "ssm2k", "ssm_token",
                              "copy"],
                     help="run one workload (for profiling); prints a short JSON line")
     args = ap.parse_args()
