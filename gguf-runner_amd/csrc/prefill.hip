@@ -464,6 +464,13 @@ __device__ __forceinline__ void prefill_body(const PrefillLaunch& p, const void*
         auto subtile = [&](const uint16_t* kb, const uint16_t* vb, int sb, int ts) {
             const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                                  0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            // Scheduling hint for the S^T region: LLVM's single-wave MFMA
+            // interleave (iglp strategy 1) places the K fragment reads between
+            // the MFMAs.  MI355X, A/B on one box, ms: d128 S = 2048 (one wave
+            // per SIMD) 0.0655 -> 0.0640, S = 8192 unchanged; d256 window-1024
+            // layer 0.147 -> 0.140, global 0.348 -> 0.333.  At d64 it made the
+            // S = 8192 launch slower (0.167 -> 0.173), so d64 goes without it.
+            if constexpr (D != 64) __builtin_amdgcn_iglp_opt(1);
             // S^T = K Q^T.  The waves raise their priority over their MFMA
             // groups (s_setprio 1) so the SIMD's arbiter favours the wave that has
             // matrix work ready while the other computes its softmax.
